@@ -1,0 +1,162 @@
+/*
+ * strata_hip.h -- C ABI of libstrata_hip.so, the MI355X (gfx950) quantized
+ * weight compute path for strata-rs.
+ *
+ * The library replaces the matvec/matmul half of strata-core's
+ * `trait ComputeBackend` (crates/strata-core/src/backend.rs:20-51) for the
+ * GGUF types Q8_0, Q4_K and Q6_K. Weights stay packed in device memory in
+ * their GGUF block layout; kernels dequantize in registers.
+ *
+ * Conventions
+ *  - Every function returns int: SH_OK (0) or a negative SH_ERR_* code, and
+ *    never aborts the process. sh_last_error() gives a message for the last
+ *    failure on the calling thread.
+ *  - Host-slice entry points (sh_gemv, sh_expert_gemv, ...) are synchronous:
+ *    on return the output slice is written. A context serialises its calls
+ *    with an internal lock, so one context may be shared by many threads
+ *    (the trait is `Send + Sync`, backend.rs:20).
+ *  - Weights are identified by a caller-chosen 64-bit key (the Rust shim
+ *    hashes the tensor name, as the wgpu backend keys its cache by name,
+ *    crates/strata-backend-wgpu/src/gpu.rs:271,287). The first call with a
+ *    key copies the packed bytes to the device; later calls reuse them. The
+ *    resident set is bounded by the context's byte budget and evicted
+ *    least-recently-used (gpu.rs:61-113). Host pointers are not retained
+ *    after a call returns (weights are borrowed mmap slices, engine.rs:77-79).
+ *  - *_dev entry points take device pointers and a hipStream_t (as void*),
+ *    enqueue work and return without synchronising.
+ *  - No CPU fallback exists inside the library: without a usable device,
+ *    sh_create fails with SH_ERR_NO_DEVICE and the caller keeps its CPU
+ *    backend, as strata_backend_wgpu::select does
+ *    (crates/strata-backend-wgpu/src/lib.rs:36-43).
+ */
+#ifndef STRATA_HIP_H
+#define STRATA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SH_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define SH_OK 0
+#define SH_ERR_INVALID_ARGUMENT (-1) /* null pointer, zero batch, bad mode   */
+#define SH_ERR_SHAPE (-2)            /* length mismatch: ops.rs:15-17 asserts */
+#define SH_ERR_TRUNCATED (-3)        /* dequant.rs:50-55 Error::Truncated     */
+#define SH_ERR_UNSUPPORTED_QUANT (-4) /* type the device path does not read   */
+#define SH_ERR_UNSUPPORTED_SHAPE (-5) /* a shape the kernels do not take      */
+#define SH_ERR_NO_DEVICE (-6)        /* no usable HIP device                  */
+#define SH_ERR_DEVICE (-7)           /* HIP runtime failure                   */
+#define SH_ERR_OUT_OF_MEMORY (-8)    /* device or pinned allocation failed    */
+
+/* ---- quant type ids (Strata's scheme, crates/strata-gguf/src/quant.rs:15-43) */
+#define SH_QUANT_F32 0u
+#define SH_QUANT_F16 1u
+#define SH_QUANT_Q8_0 8u
+#define SH_QUANT_Q4_K 12u
+#define SH_QUANT_Q6_K 14u
+#define SH_QUANT_BF16 30u
+
+/* ---- tensor flags ------------------------------------------------------ */
+/* Q6_K sub-block scales as ggml's int8_t instead of strata-gguf's u8 reading
+ * (crates/strata-gguf/src/dequant.rs:211,224-227 reads them as u8). */
+#define SH_FLAG_Q6K_SIGNED_SCALES 1u
+
+/* ---- matmul modes ------------------------------------------------------ */
+#define SH_MATMUL_BF16 0u /* bf16 activations, dequant-to-bf16 LDS tiles, bf16 MFMA */
+#define SH_MATMUL_Q8 1u   /* activations quantized to Q8 blocks, int8 MFMA */
+
+typedef struct sh_context sh_context;
+
+/* A quantized matrix: QuantTensor (crates/strata-core/src/backend.rs:117-153).
+ * `rows` rows of `cols` elements, row-major packed blocks of `quant`; a row
+ * is ceil(cols / block) * block_bytes long (backend.rs:139-152). */
+typedef struct sh_quant_tensor {
+  uint64_t key;
+  uint32_t quant;
+  uint32_t flags;
+  uint64_t rows;
+  uint64_t cols;
+  const uint8_t* data;
+  uint64_t nbytes;
+} sh_quant_tensor;
+
+/* A 3-D expert tensor: ExpertView (crates/strata-core/src/weights.rs:14-34).
+ * Expert-major [n_expert][rows = in][cols = out]; quant blocks run along the
+ * output axis. */
+typedef struct sh_expert_view {
+  uint64_t key;
+  uint32_t quant;
+  uint32_t flags;
+  uint64_t n_expert;
+  uint64_t rows;
+  uint64_t cols;
+  const uint8_t* data;
+  uint64_t nbytes;
+} sh_expert_view;
+
+/* ---- library and context ----------------------------------------------- */
+int sh_abi_version(void);
+/* Message for the last failure on this thread ("" if none). */
+const char* sh_last_error(void);
+/* Number of visible HIP devices (0 is not an error). */
+int sh_device_count(int* count);
+/* Block geometry of a quant id: quant.rs:125-164 (block_size, type_size). */
+int sh_quant_geometry(uint32_t quant, uint32_t* block_size, uint32_t* type_size);
+
+/* Opens `device` with a resident-weight budget in bytes; 0 means 4 GiB, the
+ * wgpu backend's default (crates/strata-backend-wgpu/src/gpu.rs:227-230). */
+int sh_create(int device, uint64_t weight_budget_bytes, sh_context** out);
+int sh_destroy(sh_context* ctx);
+/* ComputeBackend::name (backend.rs:22): "hip". */
+const char* sh_name(const sh_context* ctx);
+/* Bytes of resident weights (WgpuBackend::resident_bytes, gpu.rs:238-241). */
+int sh_resident_bytes(sh_context* ctx, uint64_t* bytes);
+/* Drops one resident weight (no-op when absent). */
+int sh_evict(sh_context* ctx, uint64_t key);
+
+/* ---- the trait's quantized primitives (host slices, synchronous) ------- */
+
+/* ComputeBackend::gemv (backend.rs:25), semantics of ops::gemv
+ * (crates/strata-core/src/ops.rs:14-28): y[r] = sum_c W[r][c] * x[c].
+ * x_len must equal cols and y_len rows. */
+int sh_gemv(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint64_t x_len, float* y,
+            uint64_t y_len);
+
+/* `batch` independent gemvs against one weight read: x is [batch][cols],
+ * y is [batch][rows]; batch 1..8. No reference counterpart; equal to
+ * `batch` calls of ops::gemv. */
+int sh_gemv_batch(sh_context* ctx, const sh_quant_tensor* w, const float* x, float* y,
+                  uint32_t batch);
+
+/* ComputeBackend::expert_gemv (backend.rs:28-35), semantics of
+ * ops::expert_gemv (ops.rs:169-195): y[c] = sum_i x[i] * W_e[i][c].
+ * x_len must equal rows and y_len cols; e < n_expert. */
+int sh_expert_gemv(sh_context* ctx, const sh_expert_view* w, uint64_t e, const float* x,
+                   uint64_t x_len, float* y, uint64_t y_len);
+
+/* dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device:
+ * `n` f32 values from `nbytes` packed bytes, bit-exact. SH_ERR_TRUNCATED
+ * when n is not a whole number of blocks or the buffer is short. */
+int sh_dequantize_row(sh_context* ctx, uint32_t quant, uint32_t flags, const uint8_t* block,
+                      uint64_t nbytes, float* out, uint64_t n);
+
+/* ---- device-pointer variants (asynchronous on `stream`) ---------------- */
+
+/* rows x cols of packed blocks at `w` -> out[rows][cols] f32, bit-exact. */
+int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                   float* out, void* stream);
+
+/* y[b][r] = sum_c W[r][c] x[b][c], b < batch (1..8); w at least 2-byte
+ * aligned (4 for Q8_0), x 16-byte aligned. */
+int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                const float* x, float* y, uint32_t batch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATA_HIP_H */

@@ -1,0 +1,486 @@
+/*
+ * CPU oracle: plain-C restatement of the reference's scalar quantized
+ * matvec path. TEST INFRASTRUCTURE ONLY -- see oracle.h. Build with
+ * -O2 -ffp-contract=off (oracle/Makefile); never with -ffast-math.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- f16 <-> f32 -------------------------------------------------------
+ * The reference converts with the `half` crate 2.7.1 (dequant.rs:34-36,
+ * Cargo.lock:764-766): the exact IEEE binary16 -> binary32 widening; NaNs
+ * come out quiet with the payload kept in the top mantissa bits.
+ * Written here from the binary16 definition:
+ *   normal    (-1)^s * 2^(e-15) * (1 + m/1024)
+ *   subnormal (-1)^s * m * 2^-24                                        */
+float sho_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) & 1u;
+  uint32_t e = (uint32_t)(h >> 10) & 0x1Fu;
+  uint32_t m = (uint32_t)h & 0x3FFu;
+  float v;
+  if (e == 0x1F) {
+    uint32_t bits;
+    if (m == 0) {
+      bits = 0x7F800000u;
+    } else {
+      bits = 0x7FC00000u | (m << 13);
+    }
+    bits |= sign << 31;
+    memcpy(&v, &bits, 4);
+    return v;
+  }
+  if (e == 0) {
+    v = ldexpf((float)m, -24); /* exact: m < 2^10 */
+  } else {
+    v = ldexpf((float)(1024u + m), (int)e - 25); /* exact */
+  }
+  return sign ? -v : v;
+}
+
+/* binary32 -> binary16, round to nearest even (half::f16::from_f32). Used
+ * only by the synthetic block generators and the known-answer tests. */
+uint16_t sho_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) { /* inf or NaN */
+    if (ax == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+  }
+  float a;
+  memcpy(&a, &ax, 4);
+  if (a >= 65520.0f) return (uint16_t)(sign | 0x7C00u); /* rounds to inf */
+  if (a < ldexpf(1.0f, -14)) {
+    /* subnormal (or zero): value = k * 2^-24, k = rne(a * 2^24). The
+     * scaling by 2^24 is exact; nearbyintf rounds half to even. */
+    float k = nearbyintf(ldexpf(a, 24));
+    return (uint16_t)(sign | (uint16_t)k); /* k == 1024 is the min normal */
+  }
+  int e;
+  float fr = frexpf(a, &e); /* a = fr * 2^e, fr in [0.5, 1) */
+  /* significand with 11 bits: rne(fr * 2^11) in [1024, 2048] */
+  float s = nearbyintf(ldexpf(fr, 11));
+  int be = e - 1 + 15; /* biased exponent of 2^(e-1) */
+  uint32_t si = (uint32_t)s;
+  if (si == 2048u) {
+    si = 1024u;
+    be += 1;
+  }
+  if (be >= 31) return (uint16_t)(sign | 0x7C00u);
+  return (uint16_t)(sign | (uint16_t)(be << 10) | (uint16_t)(si - 1024u));
+}
+
+/* bf16 round trip, round to nearest even (half::bf16::from_f32; used by the
+ * router input rounding, hyper.rs:22-24). */
+float sho_bf16_round(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) {
+    x = (x | 0x00400000u) & 0xFFFF0000u;
+  } else {
+    uint32_t lsb = (x >> 16) & 1u;
+    x = (x + 0x7FFFu + lsb) & 0xFFFF0000u;
+  }
+  float r;
+  memcpy(&r, &x, 4);
+  return r;
+}
+
+/* ---- geometry (quant.rs:125-181), for the types this path handles ------ */
+int64_t sho_block_size(uint32_t quant) {
+  switch (quant) {
+    case SHO_F32:
+    case SHO_F16:
+    case SHO_BF16:
+      return 1;
+    case SHO_Q8_0:
+      return 32;
+    case SHO_Q4_K:
+    case SHO_Q6_K:
+      return 256;
+    default:
+      return -1;
+  }
+}
+
+int64_t sho_type_size(uint32_t quant) {
+  switch (quant) {
+    case SHO_F32:
+      return 4;
+    case SHO_F16:
+    case SHO_BF16:
+      return 2;
+    case SHO_Q8_0:
+      return 34;
+    case SHO_Q4_K:
+      return 144;
+    case SHO_Q6_K:
+      return 210;
+    default:
+      return -1;
+  }
+}
+
+/* n_blocks = ceil(n / block_size); byte_size = n_blocks * type_size. */
+int64_t sho_byte_size(uint32_t quant, int64_t n_elements) {
+  int64_t bs = sho_block_size(quant), ts = sho_type_size(quant);
+  if (bs <= 0 || ts <= 0 || n_elements < 0) return -1;
+  return ((n_elements + bs - 1) / bs) * ts;
+}
+
+static uint16_t rd16(const uint8_t* b) { return (uint16_t)(b[0] | (b[1] << 8)); }
+
+/* ---- block decoders ----------------------------------------------------- */
+
+/* dequant.rs:123-128: out[j] = (i8)q[j] as f32 * d. */
+static void dq_q8_0(const uint8_t* b, float* out) {
+  float d = sho_f16_to_f32(rd16(b));
+  for (int j = 0; j < 32; ++j) out[j] = (float)(int8_t)b[2 + j] * d;
+}
+
+/* dequant.rs:237-245: the packed 6-bit (scale, min) of sub-block j. */
+void sho_get_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *sc = (uint8_t)((q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4));
+    *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+  }
+}
+
+/* dequant.rs:247-270. d1 = d*sc and m1 = dmin*m are rounded to f32 first;
+ * each output is (d1*q) - m1 with two roundings (no fused multiply-add). */
+static void dq_q4_k(const uint8_t* b, float* out) {
+  float d = sho_f16_to_f32(rd16(b));
+  float mn = sho_f16_to_f32(rd16(b + 2));
+  const uint8_t* scales = b + 4;
+  const uint8_t* q = b + 16;
+  for (int grp = 0; grp < 4; ++grp) {
+    uint8_t sc, m;
+    sho_get_scale_min_k4(2 * grp, scales, &sc, &m);
+    float d1 = d * (float)sc;
+    float m1 = mn * (float)m;
+    sho_get_scale_min_k4(2 * grp + 1, scales, &sc, &m);
+    float d2 = d * (float)sc;
+    float m2 = mn * (float)m;
+    const uint8_t* qq = q + 32 * grp;
+    float* o = out + 64 * grp;
+    for (int l = 0; l < 32; ++l) {
+      float p1 = d1 * (float)(qq[l] & 0x0F);
+      o[l] = p1 - m1;
+      float p2 = d2 * (float)(qq[l] >> 4);
+      o[32 + l] = p2 - m2;
+    }
+  }
+}
+
+/* dequant.rs:208-234. Two halves of 128 elements; q = 6-bit code - 32 and
+ * out = (d * sc) * q. The reference reads sc as u8 (F4); SHO_Q6K_SCALE_I8
+ * gives ggml's int8_t reading for comparison. */
+static void dq_q6_k(const uint8_t* b, float* out, int scale_mode) {
+  const uint8_t* ql = b;
+  const uint8_t* qh = b + 128;
+  const uint8_t* sc = b + 192;
+  float d = sho_f16_to_f32(rd16(b + 208));
+  for (int half = 0; half < 2; ++half) {
+    const uint8_t* l0 = ql + 64 * half;
+    const uint8_t* h0 = qh + 32 * half;
+    const uint8_t* s0 = sc + 8 * half;
+    float* o = out + 128 * half;
+    for (int l = 0; l < 32; ++l) {
+      int is = l / 16;
+      int q1 = ((l0[l] & 0x0F) | ((h0[l] & 3) << 4)) - 32;
+      int q2 = ((l0[l + 32] & 0x0F) | (((h0[l] >> 2) & 3) << 4)) - 32;
+      int q3 = ((l0[l] >> 4) | (((h0[l] >> 4) & 3) << 4)) - 32;
+      int q4 = ((l0[l + 32] >> 4) | (((h0[l] >> 6) & 3) << 4)) - 32;
+      float s[4];
+      for (int t = 0; t < 4; ++t) {
+        uint8_t raw = s0[is + 2 * t];
+        s[t] = scale_mode == SHO_Q6K_SCALE_I8 ? (float)(int8_t)raw : (float)raw;
+      }
+      float a;
+      a = d * s[0];
+      o[l] = a * (float)q1;
+      a = d * s[1];
+      o[l + 32] = a * (float)q2;
+      a = d * s[2];
+      o[l + 64] = a * (float)q3;
+      a = d * s[3];
+      o[l + 96] = a * (float)q4;
+    }
+  }
+}
+
+static int dq_block(uint32_t quant, const uint8_t* b, float* out, int q6_mode) {
+  switch (quant) {
+    case SHO_F32:
+      memcpy(out, b, 4);
+      return SHO_OK;
+    case SHO_F16:
+      out[0] = sho_f16_to_f32(rd16(b));
+      return SHO_OK;
+    case SHO_BF16: {
+      uint32_t bits = (uint32_t)rd16(b) << 16;
+      memcpy(out, &bits, 4);
+      return SHO_OK;
+    }
+    case SHO_Q8_0:
+      dq_q8_0(b, out);
+      return SHO_OK;
+    case SHO_Q4_K:
+      dq_q4_k(b, out);
+      return SHO_OK;
+    case SHO_Q6_K:
+      dq_q6_k(b, out, q6_mode);
+      return SHO_OK;
+    default:
+      return SHO_UNSUPPORTED;
+  }
+}
+
+/* dequant.rs:45-61: Truncated when n is not a whole number of blocks or the
+ * buffer is short; otherwise block by block. */
+static int dequant_row_mode(uint32_t quant, const uint8_t* block, size_t nbytes,
+                            float* out, size_t n, int q6_mode) {
+  int64_t bs = sho_block_size(quant), ts = sho_type_size(quant);
+  if (bs <= 0) return SHO_UNSUPPORTED;
+  size_t n_blocks = (n + (size_t)bs - 1) / (size_t)bs;
+  if (n % (size_t)bs != 0 || nbytes < n_blocks * (size_t)ts) return SHO_TRUNCATED;
+  for (size_t i = 0; i < n_blocks; ++i) {
+    int rc = dq_block(quant, block + i * (size_t)ts, out + i * (size_t)bs, q6_mode);
+    if (rc) return rc;
+  }
+  return SHO_OK;
+}
+
+int sho_dequantize_row(uint32_t quant, const uint8_t* block, size_t nbytes,
+                       float* out, size_t n) {
+  return dequant_row_mode(quant, block, nbytes, out, n, SHO_Q6K_SCALE_U8);
+}
+
+int sho_dequantize_row_q6k_mode(const uint8_t* block, size_t nbytes, float* out,
+                                size_t n, int scale_mode) {
+  return dequant_row_mode(SHO_Q6_K, block, nbytes, out, n, scale_mode);
+}
+
+/* ---- gemv (ops.rs:14-28) -----------------------------------------------
+ * For each row: dequantize into scratch, then a sequential f64 dot, cast to
+ * f32 at the end. Rows [r0, r1) only, so the threaded variant reuses it. */
+static int gemv_rows(uint32_t quant, int64_t r0, int64_t r1, int64_t cols,
+                     const uint8_t* data, size_t nbytes, const float* x,
+                     float* y, int q6_mode) {
+  int64_t rb = sho_byte_size(quant, cols);
+  if (rb < 0) return SHO_UNSUPPORTED;
+  float* row = (float*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(float));
+  if (!row) return SHO_UNSUPPORTED;
+  int rc = SHO_OK;
+  for (int64_t r = r0; r < r1; ++r) {
+    size_t off = (size_t)(r * rb);
+    if (off + (size_t)rb > nbytes) {
+      rc = SHO_TRUNCATED;
+      break;
+    }
+    rc = dequant_row_mode(quant, data + off, (size_t)rb, row, (size_t)cols, q6_mode);
+    if (rc) break;
+    double acc = 0.0;
+    for (int64_t c = 0; c < cols; ++c) acc += (double)row[c] * (double)x[c];
+    y[r] = (float)acc;
+  }
+  free(row);
+  return rc;
+}
+
+int sho_gemv(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+             size_t nbytes, const float* x, float* y) {
+  return gemv_rows(quant, 0, rows, cols, data, nbytes, x, y, SHO_Q6K_SCALE_U8);
+}
+
+int sho_gemv_q6k_mode(int64_t rows, int64_t cols, const uint8_t* data,
+                      size_t nbytes, const float* x, float* y, int scale_mode) {
+  return gemv_rows(SHO_Q6_K, 0, rows, cols, data, nbytes, x, y, scale_mode);
+}
+
+/* Row-parallel gemv: the same per-row arithmetic on n_threads threads, so
+ * its output is bit-identical to sho_gemv. This is the all-cores CPU
+ * baseline the reference's backend description promises
+ * (crates/strata-backend-cpu/Cargo.toml:3) but never runs. */
+typedef struct {
+  uint32_t quant;
+  int64_t r0, r1, cols;
+  const uint8_t* data;
+  size_t nbytes;
+  const float* x;
+  float* y;
+  int rc;
+} gemv_job;
+
+static void* gemv_worker(void* p) {
+  gemv_job* j = (gemv_job*)p;
+  j->rc = gemv_rows(j->quant, j->r0, j->r1, j->cols, j->data, j->nbytes, j->x,
+                    j->y, SHO_Q6K_SCALE_U8);
+  return NULL;
+}
+
+int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
+                     const uint8_t* data, size_t nbytes, const float* x,
+                     float* y, int n_threads) {
+  if (n_threads <= 1 || rows < 2) return sho_gemv(quant, rows, cols, data, nbytes, x, y);
+  if (n_threads > 256) n_threads = 256;
+  pthread_t th[256];
+  int started[256];
+  gemv_job jobs[256];
+  int64_t per = (rows + n_threads - 1) / n_threads;
+  int n_jobs = 0;
+  for (int t = 0; t < n_threads; ++t) {
+    int64_t r0 = t * per;
+    if (r0 >= rows) break;
+    int64_t r1 = r0 + per < rows ? r0 + per : rows;
+    jobs[t] = (gemv_job){quant, r0, r1, cols, data, nbytes, x, y, 0};
+    started[t] = pthread_create(&th[t], NULL, gemv_worker, &jobs[t]) == 0;
+    if (!started[t]) gemv_worker(&jobs[t]); /* could not start: run inline */
+    ++n_jobs;
+  }
+  int rc = SHO_OK;
+  for (int t = 0; t < n_jobs; ++t) {
+    if (started[t]) pthread_join(th[t], NULL);
+    if (jobs[t].rc) rc = jobs[t].rc;
+  }
+  return rc;
+}
+
+/* ---- expert_gemv (ops.rs:169-195) --------------------------------------
+ * Expert-major [n_expert][rows = in][cols = out] (weights.rs:14-34):
+ * acc[c] += x[i] * W_e[i][c] in f64 over input rows i, skipping x[i] == 0,
+ * then cast to f32. */
+int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
+                    int64_t cols, const uint8_t* data, size_t nbytes,
+                    int64_t e, const float* x, float* y) {
+  int64_t rb = sho_byte_size(quant, cols);
+  if (rb < 0) return SHO_UNSUPPORTED;
+  if (e < 0 || e >= n_expert) return SHO_TRUNCATED;
+  double* acc = (double*)calloc((size_t)(cols > 0 ? cols : 1), sizeof(double));
+  float* row = (float*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(float));
+  if (!acc || !row) {
+    free(acc);
+    free(row);
+    return SHO_UNSUPPORTED;
+  }
+  int rc = SHO_OK;
+  size_t base = (size_t)(e * rows * rb);
+  for (int64_t i = 0; i < rows; ++i) {
+    double xi = (double)x[i];
+    if (xi == 0.0) continue;
+    size_t off = base + (size_t)(i * rb);
+    if (off + (size_t)rb > nbytes) {
+      rc = SHO_TRUNCATED;
+      break;
+    }
+    rc = sho_dequantize_row(quant, data + off, (size_t)rb, row, (size_t)cols);
+    if (rc) break;
+    for (int64_t c = 0; c < cols; ++c) acc[c] += xi * (double)row[c];
+  }
+  if (rc == SHO_OK)
+    for (int64_t c = 0; c < cols; ++c) y[c] = (float)acc[c];
+  free(acc);
+  free(row);
+  return rc;
+}
+
+/* ops.rs:85-87 */
+float sho_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* ---- MoE routing (moe.rs:58-90), from the router logits ---------------
+ * softmax: max-shift, f32 exp, f64 sum, inv = (f32)(1/sum), p *= inv;
+ * top-k by descending p, ties by ascending id; ids returned ascending;
+ * weights renormalised as (f32)((f64)p / max(sum_f64, 2^-14)).
+ * Returns k = min(top_k, n_expert). */
+static const float* g_rank_p;
+static int rank_cmp(const void* a, const void* b) {
+  int64_t ia = *(const int64_t*)a, ib = *(const int64_t*)b;
+  float pa = g_rank_p[ia], pb = g_rank_p[ib];
+  if (pa > pb) return -1;
+  if (pa < pb) return 1;
+  return ia < ib ? -1 : (ia > ib ? 1 : 0);
+}
+static int id_cmp(const void* a, const void* b) {
+  int64_t ia = *(const int64_t*)a, ib = *(const int64_t*)b;
+  return ia < ib ? -1 : (ia > ib ? 1 : 0);
+}
+
+int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
+                  int64_t* ids, float* weights) {
+  if (n_expert <= 0 || top_k <= 0) return 0;
+  float* p = (float*)malloc((size_t)n_expert * sizeof(float));
+  int64_t* idx = (int64_t*)malloc((size_t)n_expert * sizeof(int64_t));
+  float mx = -INFINITY;
+  for (int64_t i = 0; i < n_expert; ++i) mx = fmaxf(mx, logits[i]);
+  double sum = 0.0;
+  for (int64_t i = 0; i < n_expert; ++i) {
+    p[i] = expf(logits[i] - mx);
+    sum += (double)p[i];
+  }
+  float inv = (float)(1.0 / sum);
+  for (int64_t i = 0; i < n_expert; ++i) p[i] *= inv;
+  for (int64_t i = 0; i < n_expert; ++i) idx[i] = i;
+  int64_t k = top_k < n_expert ? top_k : n_expert;
+  g_rank_p = p; /* the comparator is a total order: the k-set is unique */
+  qsort(idx, (size_t)n_expert, sizeof(int64_t), rank_cmp);
+  qsort(idx, (size_t)k, sizeof(int64_t), id_cmp);
+  double ws = 0.0;
+  for (int64_t j = 0; j < k; ++j) {
+    ids[j] = idx[j];
+    weights[j] = p[idx[j]];
+    ws += (double)weights[j];
+  }
+  double s = ws > ldexp(1.0, -14) ? ws : ldexp(1.0, -14);
+  for (int64_t j = 0; j < k; ++j) weights[j] = (float)((double)weights[j] / s);
+  free(p);
+  free(idx);
+  return (int)k;
+}
+
+/* ---- routed combine (moe.rs:108-127) -----------------------------------
+ * For each selected expert in the given (ascending) order with w != 0:
+ *   h = gate_e . x, p = up_e . x, h = silu(h) * p, d = down_e . h,
+ *   out += w * d   (f32, product then sum).
+ * gate/up: [n_expert][n_embd][n_ff]; down: [n_expert][n_ff][n_embd].
+ * out (n_embd) is overwritten. The shared expert (moe.rs:129-143) is not
+ * part of this op. */
+int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                   int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                   const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                   size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                   const int64_t* ids, const float* weights, int64_t k,
+                   const float* x, float* out) {
+  float* h = (float*)malloc((size_t)n_ff * sizeof(float));
+  float* part = (float*)malloc((size_t)n_ff * sizeof(float));
+  float* d = (float*)malloc((size_t)n_embd * sizeof(float));
+  int rc = SHO_OK;
+  for (int64_t i = 0; i < n_embd; ++i) out[i] = 0.0f;
+  for (int64_t j = 0; j < k && rc == SHO_OK; ++j) {
+    float w = weights[j];
+    if (w == 0.0f) continue;
+    int64_t e = ids[j];
+    rc = sho_expert_gemv(gate_quant, n_expert, n_embd, n_ff, gate, gate_bytes, e, x, h);
+    if (rc) break;
+    rc = sho_expert_gemv(up_quant, n_expert, n_embd, n_ff, up, up_bytes, e, x, part);
+    if (rc) break;
+    for (int64_t i = 0; i < n_ff; ++i) h[i] = sho_silu(h[i]) * part[i];
+    rc = sho_expert_gemv(down_quant, n_expert, n_ff, n_embd, down, down_bytes, e, h, d);
+    if (rc) break;
+    for (int64_t i = 0; i < n_embd; ++i) {
+      float t = w * d[i];
+      out[i] = out[i] + t;
+    }
+  }
+  free(h);
+  free(part);
+  free(d);
+  return rc;
+}

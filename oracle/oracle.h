@@ -1,0 +1,92 @@
+/*
+ * CPU oracle for the quantized-weight matvec/matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product library links this file;
+ * only the tests, the smoke check and the CPU-baseline leg of the benchmark
+ * load it, and only as the checker / the timed CPU reference.
+ *
+ * It restates, in plain C, the reference's scalar CPU path:
+ *   - block geometry          crates/strata-gguf/src/quant.rs:125-181
+ *   - f16 -> f32, row dequant crates/strata-gguf/src/dequant.rs:28-61,123-128,208-270
+ *   - gemv / expert_gemv      crates/strata-core/src/ops.rs:14-28,169-195
+ *   - silu                    crates/strata-core/src/ops.rs:85-87
+ *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
+ * Compiled with -ffp-contract=off and no fast-math so every f32 product and
+ * difference rounds exactly as the Rust source (which never fuses), and the
+ * f64 dot products are summed in the same sequential order.
+ */
+#ifndef STRATA_ORACLE_H
+#define STRATA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Strata QuantType ids (crates/strata-gguf/src/quant.rs:15-43). */
+enum {
+  SHO_F32 = 0,
+  SHO_F16 = 1,
+  SHO_Q8_0 = 8,
+  SHO_Q4_K = 12,
+  SHO_Q6_K = 14,
+  SHO_BF16 = 30,
+};
+
+/* Status codes. */
+enum {
+  SHO_OK = 0,
+  SHO_TRUNCATED = -1,   /* dequant.rs:50-55 Error::Truncated */
+  SHO_UNSUPPORTED = -2, /* quant.rs:47-80 Error::UnsupportedQuant */
+};
+
+/* Q6_K sub-block scale semantics: the reference reads the 16 scale bytes as
+ * u8 (dequant.rs:211,224-227); ggml declares them int8_t. */
+enum { SHO_Q6K_SCALE_U8 = 0, SHO_Q6K_SCALE_I8 = 1 };
+
+float sho_f16_to_f32(uint16_t h);
+uint16_t sho_f32_to_f16(float f);
+float sho_bf16_round(float f);
+
+int64_t sho_block_size(uint32_t quant);
+int64_t sho_type_size(uint32_t quant);
+int64_t sho_byte_size(uint32_t quant, int64_t n_elements);
+
+void sho_get_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m);
+
+int sho_dequantize_row(uint32_t quant, const uint8_t* block, size_t nbytes,
+                       float* out, size_t n);
+int sho_dequantize_row_q6k_mode(const uint8_t* block, size_t nbytes, float* out,
+                                size_t n, int scale_mode);
+
+int sho_gemv(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+             size_t nbytes, const float* x, float* y);
+int sho_gemv_q6k_mode(int64_t rows, int64_t cols, const uint8_t* data,
+                      size_t nbytes, const float* x, float* y, int scale_mode);
+int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
+                     const uint8_t* data, size_t nbytes, const float* x,
+                     float* y, int n_threads);
+
+int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
+                    int64_t cols, const uint8_t* data, size_t nbytes,
+                    int64_t e, const float* x, float* y);
+
+float sho_silu(float x);
+
+int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
+                  int64_t* ids, float* weights);
+
+int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                   int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                   const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                   size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                   const int64_t* ids, const float* weights, int64_t k,
+                   const float* x, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

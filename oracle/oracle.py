@@ -1,0 +1,184 @@
+"""ctypes binding of the CPU oracle (liboracle.so, built by oracle/Makefile).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke check and the CPU
+baseline leg of bench.py, as the checker or the timed CPU reference. The
+product library never loads it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
+SCALE_U8, SCALE_I8 = 0, 1
+OK, TRUNCATED, UNSUPPORTED = 0, -1, -2
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run `make -C oracle`)")
+        L = C.CDLL(LIB_PATH)
+        u8p, f32p, i64p = C.c_void_p, C.c_void_p, C.c_void_p
+        L.sho_f16_to_f32.argtypes = [C.c_uint16]
+        L.sho_f16_to_f32.restype = C.c_float
+        L.sho_f32_to_f16.argtypes = [C.c_float]
+        L.sho_f32_to_f16.restype = C.c_uint16
+        L.sho_bf16_round.argtypes = [C.c_float]
+        L.sho_bf16_round.restype = C.c_float
+        for fn in ("sho_block_size", "sho_type_size"):
+            getattr(L, fn).argtypes = [C.c_uint32]
+            getattr(L, fn).restype = C.c_int64
+        L.sho_byte_size.argtypes = [C.c_uint32, C.c_int64]
+        L.sho_byte_size.restype = C.c_int64
+        L.sho_get_scale_min_k4.argtypes = [C.c_int, u8p, C.POINTER(C.c_uint8), C.POINTER(C.c_uint8)]
+        L.sho_dequantize_row.argtypes = [C.c_uint32, u8p, C.c_size_t, f32p, C.c_size_t]
+        L.sho_dequantize_row_q6k_mode.argtypes = [u8p, C.c_size_t, f32p, C.c_size_t, C.c_int]
+        L.sho_gemv.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p]
+        L.sho_gemv_q6k_mode.argtypes = [C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p, C.c_int]
+        L.sho_gemv_threads.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p,
+                                       C.c_int]
+        L.sho_expert_gemv.argtypes = [C.c_uint32, C.c_int64, C.c_int64, C.c_int64, u8p, C.c_size_t,
+                                      C.c_int64, f32p, f32p]
+        L.sho_silu.argtypes = [C.c_float]
+        L.sho_silu.restype = C.c_float
+        L.sho_moe_route.argtypes = [f32p, C.c_int64, C.c_int64, i64p, f32p]
+        L.sho_moe_routed.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
+                                     C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
+                                     i64p, f32p, C.c_int64, f32p, f32p]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(np.frombuffer(bytes(a), np.uint8) if isinstance(a, (bytes, bytearray))
+                                else a, dtype=np.uint8)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, rc: int, what: str):
+        name = {TRUNCATED: "truncated", UNSUPPORTED: "unsupported quant"}.get(rc, str(rc))
+        super().__init__(f"{what}: {name}")
+        self.rc = rc
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise OracleError(rc, what)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().sho_f16_to_f32(h)
+
+
+def f32_to_f16(f: float) -> int:
+    return lib().sho_f32_to_f16(f)
+
+
+def block_size(q: int) -> int:
+    return lib().sho_block_size(q)
+
+
+def type_size(q: int) -> int:
+    return lib().sho_type_size(q)
+
+
+def byte_size(q: int, n: int) -> int:
+    return lib().sho_byte_size(q, n)
+
+
+def get_scale_min_k4(j: int, scales) -> tuple[int, int]:
+    s = _u8(scales)
+    sc, m = C.c_uint8(), C.c_uint8()
+    lib().sho_get_scale_min_k4(j, _ptr(s), C.byref(sc), C.byref(m))
+    return sc.value, m.value
+
+
+def dequantize_row(quant: int, block, n: int, scale_mode: int = SCALE_U8) -> np.ndarray:
+    b = _u8(block)
+    out = np.zeros(n, dtype=np.float32)
+    if quant == Q6_K:
+        rc = lib().sho_dequantize_row_q6k_mode(_ptr(b), b.nbytes, _ptr(out), n, scale_mode)
+    else:
+        rc = lib().sho_dequantize_row(quant, _ptr(b), b.nbytes, _ptr(out), n)
+    _check(rc, "dequantize_row")
+    return out
+
+
+def dequantize(quant: int, data, rows: int, cols: int, scale_mode: int = SCALE_U8) -> np.ndarray:
+    """All rows of a ``rows x cols`` matrix, row by row through dequantize_row."""
+    b = _u8(data)
+    rb = byte_size(quant, cols)
+    out = np.empty((rows, cols), dtype=np.float32)
+    for r in range(rows):
+        out[r] = dequantize_row(quant, b[r * rb:(r + 1) * rb], cols, scale_mode)
+    return out
+
+
+def gemv(quant: int, rows: int, cols: int, data, x, scale_mode: int = SCALE_U8,
+         threads: int = 1) -> np.ndarray:
+    b, xv = _u8(data), _f32(x)
+    assert xv.size == cols
+    y = np.empty(rows, dtype=np.float32)
+    if quant == Q6_K and scale_mode != SCALE_U8:
+        rc = lib().sho_gemv_q6k_mode(rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y), scale_mode)
+    elif threads > 1:
+        rc = lib().sho_gemv_threads(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y), threads)
+    else:
+        rc = lib().sho_gemv(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y))
+    _check(rc, "gemv")
+    return y
+
+
+def expert_gemv(quant: int, n_expert: int, rows: int, cols: int, data, e: int, x) -> np.ndarray:
+    b, xv = _u8(data), _f32(x)
+    assert xv.size == rows
+    y = np.empty(cols, dtype=np.float32)
+    _check(lib().sho_expert_gemv(quant, n_expert, rows, cols, _ptr(b), b.nbytes, e, _ptr(xv), _ptr(y)),
+           "expert_gemv")
+    return y
+
+
+def silu(x: float) -> float:
+    return lib().sho_silu(x)
+
+
+def moe_route(logits, top_k: int) -> tuple[np.ndarray, np.ndarray]:
+    lg = _f32(logits)
+    ids = np.zeros(top_k, dtype=np.int64)
+    w = np.zeros(top_k, dtype=np.float32)
+    k = lib().sho_moe_route(_ptr(lg), lg.size, top_k, _ptr(ids), _ptr(w))
+    return ids[:k], w[:k]
+
+
+def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, n_ff: int,
+               gate, up, down, ids, weights, x) -> np.ndarray:
+    g, u, d = _u8(gate), _u8(up), _u8(down)
+    idv = np.ascontiguousarray(ids, dtype=np.int64)
+    wv, xv = _f32(weights), _f32(x)
+    out = np.empty(n_embd, dtype=np.float32)
+    _check(lib().sho_moe_routed(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
+                                _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
+                                _ptr(xv), _ptr(out)), "moe_routed")
+    return out

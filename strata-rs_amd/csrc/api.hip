@@ -1,0 +1,456 @@
+// C ABI of libstrata_hip: context, resident weight store, entry points.
+//
+// Host-side mirror of the reference's device backend behaviour
+// (crates/strata-backend-wgpu/src/gpu.rs): a name-keyed weight cache
+// bounded by a byte budget with least-recently-used eviction (gpu.rs:61-113),
+// reusable scratch buffers grown on demand (gpu.rs:126-150,244-262), one lock
+// per context (gpu.rs:122-124). Unlike the wgpu backend the weights are
+// uploaded packed (GGUF blocks), not dequantized to f32 on the host.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/strata_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string t_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  t_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  if (e == hipErrorOutOfMemory) return fail(SH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+    return fail(SH_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  return fail(SH_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                  \
+  do {                                       \
+    hipError_t e_ = (expr);                  \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+struct Resident {
+  void* dev = nullptr;
+  uint64_t bytes = 0;
+  uint64_t used = 0;
+  uint32_t quant = 0;
+  uint64_t rows = 0, cols = 0, n_expert = 0;
+};
+
+// A device buffer that only grows.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t need, const char* what) {
+    if (need <= cap && p) return SH_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    size_t sz = (need + 4095) & ~size_t(4095);
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return hip_fail(e, what);
+    }
+    cap = sz;
+    return SH_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+// Pinned host staging (hipHostMalloc: page-locked, allocated as such).
+struct HostBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t need, const char* what) {
+    if (need <= cap && p) return SH_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+    size_t sz = (need + 4095) & ~size_t(4095);
+    hipError_t e = hipHostMalloc(&p, sz, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return hip_fail(e, what);
+    }
+    cap = sz;
+    return SH_OK;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+}  // namespace
+
+struct sh_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint64_t budget = 0;
+  uint64_t bytes = 0;
+  uint64_t clock = 0;
+  std::unordered_map<uint64_t, Resident> weights;
+  DevBuf d_in, d_out, d_blk;
+  HostBuf h_in, h_out;
+  std::mutex mu;
+};
+
+namespace {
+
+void free_resident(Resident& r) {
+  if (r.dev) (void)hipFree(r.dev);
+  r.dev = nullptr;
+}
+
+// Evicts least-recently-used entries until `incoming` more bytes fit, or the
+// store is empty (gpu.rs:88-112): a single tensor larger than the budget is
+// still admitted, alone.
+void make_room(sh_context* c, uint64_t incoming) {
+  while (!c->weights.empty() && c->bytes + incoming > c->budget) {
+    auto victim = c->weights.begin();
+    for (auto it = c->weights.begin(); it != c->weights.end(); ++it)
+      if (it->second.used < victim->second.used) victim = it;
+    c->bytes -= victim->second.bytes;
+    free_resident(victim->second);
+    c->weights.erase(victim);
+  }
+}
+
+// The device copy of a weight, uploading the packed bytes on first use.
+int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uint64_t rows,
+             uint64_t cols, const uint8_t* data, uint64_t nbytes, Resident** out) {
+  auto it = c->weights.find(key);
+  if (it != c->weights.end()) {
+    Resident& r = it->second;
+    if (r.quant == quant && r.rows == rows && r.cols == cols && r.n_expert == n_expert &&
+        r.bytes == nbytes) {
+      r.used = ++c->clock;
+      *out = &r;
+      return SH_OK;
+    }
+    // same key, different tensor: replace it
+    c->bytes -= r.bytes;
+    free_resident(r);
+    c->weights.erase(it);
+  }
+  if (!data) return fail(SH_ERR_INVALID_ARGUMENT, "weight %llu: null data", (unsigned long long)key);
+  make_room(c, nbytes);
+  Resident r;
+  r.quant = quant;
+  r.rows = rows;
+  r.cols = cols;
+  r.n_expert = n_expert;
+  r.bytes = nbytes;
+  hipError_t e = hipMalloc(&r.dev, nbytes ? nbytes : 1);
+  if (e != hipSuccess) return hip_fail(e, "uploading weight");
+  e = hipMemcpyAsync(r.dev, data, nbytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(r.dev);
+    return hip_fail(e, "uploading weight");
+  }
+  r.used = ++c->clock;
+  c->bytes += nbytes;
+  auto ins = c->weights.emplace(key, r);
+  *out = &ins.first->second;
+  return SH_OK;
+}
+
+// Shape checks shared by the matrix entry points; mirrors what the
+// reference asserts (ops.rs:15-17) or reports (dequant.rs:50-55).
+int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert, uint64_t nbytes) {
+  sh::Geometry g = sh::geometry(quant);
+  if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
+  if (!sh::device_quant(quant))
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u has no device matvec", quant);
+  if (cols % uint64_t(g.block) != 0)
+    return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of %lld-element blocks",
+                (unsigned long long)cols, (long long)g.block);
+  uint64_t need = n_expert * rows * (cols / uint64_t(g.block)) * uint64_t(g.bytes);
+  if (nbytes < need)
+    return fail(SH_ERR_TRUNCATED, "%llu bytes for a tensor that needs %llu", (unsigned long long)nbytes,
+                (unsigned long long)need);
+  return SH_OK;
+}
+
+struct Guard {
+  sh_context* c;
+  std::lock_guard<std::mutex> lk;
+  explicit Guard(sh_context* ctx) : c(ctx), lk(ctx->mu) {}
+};
+
+}  // namespace
+
+extern "C" {
+
+int sh_abi_version(void) { return SH_ABI_VERSION; }
+
+const char* sh_last_error(void) { return t_error.c_str(); }
+
+int sh_device_count(int* count) {
+  if (!count) return fail(SH_ERR_INVALID_ARGUMENT, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) n = 0;
+  else if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  *count = n;
+  return SH_OK;
+}
+
+int sh_quant_geometry(uint32_t quant, uint32_t* block_size, uint32_t* type_size) {
+  sh::Geometry g = sh::geometry(quant);
+  if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
+  if (block_size) *block_size = uint32_t(g.block);
+  if (type_size) *type_size = uint32_t(g.bytes);
+  return SH_OK;
+}
+
+int sh_create(int device, uint64_t weight_budget_bytes, sh_context** out) {
+  if (!out) return fail(SH_ERR_INVALID_ARGUMENT, "null out");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) return fail(SH_ERR_NO_DEVICE, "no HIP device available");
+  if (device < 0 || device >= n)
+    return fail(SH_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, n);
+  HIP_TRY(hipSetDevice(device), "hipSetDevice");
+  sh_context* c = new sh_context();
+  c->device = device;
+  c->budget = weight_budget_bytes ? weight_budget_bytes : (uint64_t(4) << 30);
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  *out = c;
+  return SH_OK;
+}
+
+int sh_destroy(sh_context* c) {
+  if (!c) return SH_OK;
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto& kv : c->weights) free_resident(kv.second);
+    c->weights.clear();
+    c->d_in.release();
+    c->d_out.release();
+    c->d_blk.release();
+    c->h_in.release();
+    c->h_out.release();
+    (void)hipStreamDestroy(c->stream);
+  }
+  delete c;
+  return SH_OK;
+}
+
+const char* sh_name(const sh_context*) { return "hip"; }
+
+int sh_resident_bytes(sh_context* c, uint64_t* bytes) {
+  if (!c || !bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  std::lock_guard<std::mutex> lk(c->mu);
+  *bytes = c->bytes;
+  return SH_OK;
+}
+
+int sh_evict(sh_context* c, uint64_t key) {
+  if (!c) return fail(SH_ERR_INVALID_ARGUMENT, "null context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->weights.find(key);
+  if (it != c->weights.end()) {
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    c->bytes -= it->second.bytes;
+    free_resident(it->second);
+    c->weights.erase(it);
+  }
+  return SH_OK;
+}
+
+// Host x -> device, kernel, device -> host y; all on the context stream.
+static int run_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, float* y,
+                    uint32_t batch) {
+  const uint64_t rows = w->rows, cols = w->cols;
+  if (rows == 0) return SH_OK;
+  if (cols == 0) {  // ops::gemv: every row sums nothing
+    memset(y, 0, sizeof(float) * rows * batch);
+    return SH_OK;
+  }
+  if (!sh::gemv_shape_ok(w->quant, int64_t(rows), int64_t(cols), int(batch)))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "gemv %llux%llu of type %u (batch %u) is not supported",
+                (unsigned long long)rows, (unsigned long long)cols, w->quant, batch);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident* r = nullptr;
+  const uint64_t need = rows * uint64_t(sh::byte_size(w->quant, int64_t(cols)));
+  int rc = resident(c, w->key, w->quant, 1, rows, cols, w->data, need, &r);
+  if (rc) return rc;
+  const size_t xb = sizeof(float) * cols * batch, yb = sizeof(float) * rows * batch;
+  if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(yb, "y buffer")) ||
+      (rc = c->h_in.ensure(xb, "x staging")) || (rc = c->h_out.ensure(yb, "y staging")))
+    return rc;
+  memcpy(c->h_in.p, x, xb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
+  HIP_TRY(sh::launch_gemv(w->quant, r->dev, int64_t(rows), int64_t(cols),
+                          static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
+                          int(batch), (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+          "gemv launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "gemv");
+  memcpy(y, c->h_out.p, yb);
+  return SH_OK;
+}
+
+int sh_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, uint64_t x_len, float* y,
+            uint64_t y_len) {
+  if (!c || !w || (!x && x_len) || (!y && y_len)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (x_len != w->cols) return fail(SH_ERR_SHAPE, "gemv: x has %llu elements, cols is %llu",
+                                    (unsigned long long)x_len, (unsigned long long)w->cols);
+  if (y_len != w->rows) return fail(SH_ERR_SHAPE, "gemv: y has %llu elements, rows is %llu",
+                                    (unsigned long long)y_len, (unsigned long long)w->rows);
+  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes);
+  if (rc) return rc;
+  Guard g(c);
+  return run_gemv(c, w, x, y, 1);
+}
+
+int sh_gemv_batch(sh_context* c, const sh_quant_tensor* w, const float* x, float* y, uint32_t batch) {
+  if (!c || !w || !x || !y) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);
+  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes);
+  if (rc) return rc;
+  Guard g(c);
+  return run_gemv(c, w, x, y, batch);
+}
+
+int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const float* x,
+                   uint64_t x_len, float* y, uint64_t y_len) {
+  if (!c || !w || (!x && x_len) || (!y && y_len)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (x_len != w->rows) return fail(SH_ERR_SHAPE, "expert_gemv: x has %llu elements, rows is %llu",
+                                    (unsigned long long)x_len, (unsigned long long)w->rows);
+  if (y_len != w->cols) return fail(SH_ERR_SHAPE, "expert_gemv: y has %llu elements, cols is %llu",
+                                    (unsigned long long)y_len, (unsigned long long)w->cols);
+  if (e >= w->n_expert) return fail(SH_ERR_SHAPE, "expert %llu of %llu", (unsigned long long)e,
+                                    (unsigned long long)w->n_expert);
+  int rc = check_matrix(w->quant, w->rows, w->cols, w->n_expert, w->nbytes);
+  if (rc) return rc;
+  const uint64_t rows = w->rows, cols = w->cols;
+  if (cols == 0) return SH_OK;
+  if (rows == 0) {  // ops::expert_gemv: no input rows, all sums zero
+    memset(y, 0, sizeof(float) * cols);
+    return SH_OK;
+  }
+  if (!sh::expert_shape_ok(w->quant, int64_t(rows), int64_t(cols)))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "expert_gemv %llux%llu of type %u is not supported",
+                (unsigned long long)rows, (unsigned long long)cols, w->quant);
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident* r = nullptr;
+  const uint64_t need = w->n_expert * rows * uint64_t(sh::byte_size(w->quant, int64_t(cols)));
+  rc = resident(c, w->key, w->quant, w->n_expert, rows, cols, w->data, need, &r);
+  if (rc) return rc;
+  const size_t xb = sizeof(float) * rows, yb = sizeof(float) * cols;
+  const size_t ws = sh::expert_workspace_bytes(int64_t(rows), int64_t(cols));
+  if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(yb, "y buffer")) ||
+      (rc = c->d_blk.ensure(ws, "workspace")) || (rc = c->h_in.ensure(xb, "x staging")) ||
+      (rc = c->h_out.ensure(yb, "y staging")))
+    return rc;
+  const uint8_t* we = static_cast<const uint8_t*>(r->dev) +
+                      e * rows * uint64_t(sh::byte_size(w->quant, int64_t(cols)));
+  memcpy(c->h_in.p, x, xb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
+  HIP_TRY(sh::launch_expert_gemv(w->quant, we, int64_t(rows), int64_t(cols),
+                                 static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
+                                 static_cast<float*>(c->d_blk.p),
+                                 (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+          "expert_gemv launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "expert_gemv");
+  memcpy(y, c->h_out.p, yb);
+  return SH_OK;
+}
+
+int sh_dequantize_row(sh_context* c, uint32_t quant, uint32_t flags, const uint8_t* block,
+                      uint64_t nbytes, float* out, uint64_t n) {
+  if (!c || (!block && nbytes) || (!out && n)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  sh::Geometry g = sh::geometry(quant);
+  if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
+  const uint64_t nb = (n + uint64_t(g.block) - 1) / uint64_t(g.block);
+  if (n % uint64_t(g.block) != 0 || nbytes < nb * uint64_t(g.bytes))
+    return fail(SH_ERR_TRUNCATED, "truncated block: expected %llu bytes, found %llu",
+                (unsigned long long)(nb * uint64_t(g.bytes)), (unsigned long long)nbytes);
+  if (n == 0) return SH_OK;
+  Guard gd(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  const size_t in_b = nb * size_t(g.bytes), out_b = sizeof(float) * n;
+  int rc;
+  if ((rc = c->d_blk.ensure(in_b, "block buffer")) || (rc = c->d_out.ensure(out_b, "out buffer")) ||
+      (rc = c->h_out.ensure(out_b, "out staging")))
+    return rc;
+  HIP_TRY(hipMemcpyAsync(c->d_blk.p, block, in_b, hipMemcpyHostToDevice, c->stream), "block upload");
+  HIP_TRY(sh::launch_dequant(quant, c->d_blk.p, 1, int64_t(n), static_cast<float*>(c->d_out.p),
+                             (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+          "dequant launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, out_b, hipMemcpyDeviceToHost, c->stream), "readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "dequant");
+  memcpy(out, c->h_out.p, out_b);
+  return SH_OK;
+}
+
+int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                   float* out, void* stream) {
+  sh::Geometry g = sh::geometry(quant);
+  if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
+  if (cols % uint64_t(g.block) != 0)
+    return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of blocks", (unsigned long long)cols);
+  if (rows && cols && (!w || !out)) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  HIP_TRY(sh::launch_dequant(quant, w, int64_t(rows), int64_t(cols), out,
+                             (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                             static_cast<hipStream_t>(stream)),
+          "dequant launch");
+  return SH_OK;
+}
+
+int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                const float* x, float* y, uint32_t batch, void* stream) {
+  if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);
+  int rc = check_matrix(quant, rows, cols, 1, ~uint64_t(0));
+  if (rc) return rc;
+  if (rows == 0 || cols == 0)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "empty matrix on the device path");
+  if (!w || !x || !y) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if (!sh::gemv_shape_ok(quant, int64_t(rows), int64_t(cols), int(batch)))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "gemv %llux%llu of type %u (batch %u) is not supported",
+                (unsigned long long)rows, (unsigned long long)cols, quant, batch);
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
+      (quant == SH_QUANT_Q8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0; x 16)");
+  HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
+                          (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
+          "gemv launch");
+  return SH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Shared definitions for the CDNA4 (gfx950) quantized-weight kernels.
+//
+// Block layouts read directly from HBM, exactly as GGUF stores them
+// (crates/strata-gguf/src/quant.rs:125-164):
+//   Q8_0  32 elements /  34 B: [d: f16][q: i8 x 32]
+//   Q4_K 256 elements / 144 B: [d: f16][dmin: f16][scales: 12 B][qs: 128 B]
+//   Q6_K 256 elements / 210 B: [ql: 128 B][qh: 64 B][sc: 16 B][d: f16]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sh {
+
+enum QuantId : uint32_t {
+  kF32 = 0,
+  kF16 = 1,
+  kQ8_0 = 8,
+  kQ4_K = 12,
+  kQ6_K = 14,
+  kBF16 = 30,
+};
+
+struct Geometry {
+  int64_t block;  // elements per block
+  int64_t bytes;  // bytes per block
+};
+
+// quant.rs:125-164 for the ids this path accepts; {0, 0} otherwise.
+inline Geometry geometry(uint32_t q) {
+  switch (q) {
+    case kF32: return {1, 4};
+    case kF16: return {1, 2};
+    case kBF16: return {1, 2};
+    case kQ8_0: return {32, 34};
+    case kQ4_K: return {256, 144};
+    case kQ6_K: return {256, 210};
+    default: return {0, 0};
+  }
+}
+
+// quant.rs:173-181: ceil(n / block) * bytes.
+inline int64_t byte_size(uint32_t q, int64_t n) {
+  Geometry g = geometry(q);
+  if (g.block == 0 || n < 0) return -1;
+  return (n + g.block - 1) / g.block * g.bytes;
+}
+
+// The quantized matvec kernels accept these.
+inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ6_K; }
+
+constexpr int kWave = 64;
+
+// A 16-byte vector that only promises 4-byte alignment: GGUF blocks of 34 and
+// 210 bytes start at 2-byte boundaries, so every wide load below goes through
+// a dword-aligned address and a realignment.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// Non-temporal 16-byte weight load: the packed weights are streamed exactly
+// once per launch, so they should not displace x or the partial sums in L2.
+__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ uint32_t ld4_stream(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
+// bytes [shift, shift + 4) of the 8-byte little-endian pair (lo, hi).
+__device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
+  return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
+}
+
+// IEEE binary16 bits -> f32 through the hardware conversion (exact, f16
+// denormals preserved under the default FP16 denorm mode).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16 & 0xFFFFu));
+  return static_cast<float>(h);
+}
+
+// Byte k of w as an exact float (v_cvt_f32_ubyte{0..3}).
+template <int K>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+  return static_cast<float>((w >> (8 * K)) & 0xFFu);
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+}  // namespace sh

@@ -1,0 +1,325 @@
+"""Python host mirror of strata-core's ComputeBackend over libstrata_hip.
+
+Names and argument meanings follow the reference interface
+(crates/strata-core/src/backend.rs:20-51 and :117-153,
+crates/strata-core/src/weights.rs:14-34):
+
+* ``QuantTensor(name, quant, rows, cols, data)`` -- a packed row-major matrix;
+* ``ExpertView(name, quant, n_expert, rows, cols, data)`` -- expert-major
+  ``[n_expert][rows = in][cols = out]``;
+* ``HipBackend.gemv(w, x, y, scratch)`` / ``expert_gemv(w, e, x, y, scratch)``
+  write ``y`` in place, like the trait methods; ``scratch`` is accepted and
+  ignored, as a device backend may (crates/strata-backend-wgpu/src/gpu.rs:270).
+
+Errors raise ``BackendError`` (the trait's ``Error::Backend``), with
+``ShapeError`` for the length mismatches the reference asserts on
+(crates/strata-core/src/ops.rs:15-17) and ``TruncatedError`` for
+strata-gguf's ``Error::Truncated`` (crates/strata-gguf/src/dequant.rs:50-55).
+
+Every call goes through the C ABI in ``include/strata_hip.h``; there is no
+fallback: if the library is not built or no device exists, construction
+fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libstrata_hip.so")
+
+SH_OK = 0
+SH_ERR_INVALID_ARGUMENT = -1
+SH_ERR_SHAPE = -2
+SH_ERR_TRUNCATED = -3
+SH_ERR_UNSUPPORTED_QUANT = -4
+SH_ERR_UNSUPPORTED_SHAPE = -5
+SH_ERR_NO_DEVICE = -6
+SH_ERR_DEVICE = -7
+SH_ERR_OUT_OF_MEMORY = -8
+
+FLAG_Q6K_SIGNED_SCALES = 1
+MATMUL_BF16 = 0
+MATMUL_Q8 = 1
+
+# Every symbol include/strata_hip.h declares (kept in step with the header).
+EXPORTS = (
+    "sh_abi_version", "sh_last_error", "sh_device_count", "sh_quant_geometry",
+    "sh_create", "sh_destroy", "sh_name", "sh_resident_bytes", "sh_evict",
+    "sh_gemv", "sh_gemv_batch", "sh_expert_gemv", "sh_dequantize_row",
+    "sh_dequant_dev", "sh_gemv_dev",
+)
+
+
+class QuantType(enum.IntEnum):
+    """Strata's ggml type ids (crates/strata-gguf/src/quant.rs:15-43)."""
+    F32 = 0
+    F16 = 1
+    Q8_0 = 8
+    Q4_K = 12
+    Q6_K = 14
+    BF16 = 30
+
+
+class BackendError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"backend error ({code}): {message}")
+        self.code = code
+
+
+class ShapeError(BackendError):
+    pass
+
+
+class TruncatedError(BackendError):
+    pass
+
+
+class UnsupportedQuantError(BackendError):
+    pass
+
+
+class NoDeviceError(BackendError):
+    pass
+
+
+_ERRORS = {
+    SH_ERR_SHAPE: ShapeError,
+    SH_ERR_TRUNCATED: TruncatedError,
+    SH_ERR_UNSUPPORTED_QUANT: UnsupportedQuantError,
+    SH_ERR_NO_DEVICE: NoDeviceError,
+}
+
+
+class _QuantTensorC(C.Structure):
+    _fields_ = [("key", C.c_uint64), ("quant", C.c_uint32), ("flags", C.c_uint32),
+                ("rows", C.c_uint64), ("cols", C.c_uint64), ("data", C.c_void_p),
+                ("nbytes", C.c_uint64)]
+
+
+class _ExpertViewC(C.Structure):
+    _fields_ = [("key", C.c_uint64), ("quant", C.c_uint32), ("flags", C.c_uint32),
+                ("n_expert", C.c_uint64), ("rows", C.c_uint64), ("cols", C.c_uint64),
+                ("data", C.c_void_p), ("nbytes", C.c_uint64)]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load_library() -> C.CDLL:
+    """The C-ABI library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() "
+                           f"(or make -C strata-rs_amd)")
+    L = C.CDLL(LIB_PATH)
+    vp, u32, u64, f32p = C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p
+    L.sh_abi_version.restype = C.c_int
+    L.sh_last_error.restype = C.c_char_p
+    L.sh_device_count.argtypes = [C.POINTER(C.c_int)]
+    L.sh_quant_geometry.argtypes = [u32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
+    L.sh_create.argtypes = [C.c_int, u64, C.POINTER(vp)]
+    L.sh_destroy.argtypes = [vp]
+    L.sh_name.argtypes = [vp]
+    L.sh_name.restype = C.c_char_p
+    L.sh_resident_bytes.argtypes = [vp, C.POINTER(C.c_uint64)]
+    L.sh_evict.argtypes = [vp, u64]
+    L.sh_gemv.argtypes = [vp, C.POINTER(_QuantTensorC), f32p, u64, f32p, u64]
+    L.sh_gemv_batch.argtypes = [vp, C.POINTER(_QuantTensorC), f32p, f32p, u32]
+    L.sh_expert_gemv.argtypes = [vp, C.POINTER(_ExpertViewC), u64, f32p, u64, f32p, u64]
+    L.sh_dequantize_row.argtypes = [vp, u32, u32, vp, u64, f32p, u64]
+    L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
+    L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load_library().sh_last_error().decode()
+
+
+def check(rc: int) -> None:
+    if rc != SH_OK:
+        raise _ERRORS.get(rc, BackendError)(rc, last_error())
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(load_library().sh_device_count(C.byref(n)))
+    return n.value
+
+
+def quant_geometry(quant: int) -> tuple[int, int]:
+    bs, ts = C.c_uint32(), C.c_uint32()
+    check(load_library().sh_quant_geometry(int(quant), C.byref(bs), C.byref(ts)))
+    return bs.value, ts.value
+
+
+def byte_size(quant: int, n: int) -> int:
+    """QuantType::byte_size (crates/strata-gguf/src/quant.rs:173-181)."""
+    bs, ts = quant_geometry(quant)
+    return (n + bs - 1) // bs * ts
+
+
+def name_key(name: str) -> int:
+    """64-bit FNV-1a of a tensor name: the key the Rust shim derives."""
+    h = 0xCBF29CE484222325
+    for b in name.encode():
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def _bytes(data) -> np.ndarray:
+    if isinstance(data, (bytes, bytearray, memoryview)):
+        return np.frombuffer(data, dtype=np.uint8)
+    return np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+
+
+@dataclass
+class QuantTensor:
+    """backend.rs:117-153: ``rows`` rows of ``cols`` elements in ``quant``."""
+    name: str
+    quant: int
+    rows: int
+    cols: int
+    data: object
+    flags: int = 0
+    _buf: np.ndarray = field(init=False, repr=False)
+
+    def __post_init__(self):
+        self._buf = _bytes(self.data)
+
+    def row_bytes(self) -> int:
+        return byte_size(self.quant, self.cols)
+
+    def _c(self) -> _QuantTensorC:
+        return _QuantTensorC(name_key(self.name), int(self.quant), self.flags, self.rows, self.cols,
+                             self._buf.ctypes.data, self._buf.nbytes)
+
+
+@dataclass
+class ExpertView:
+    """weights.rs:14-34: expert-major ``[n_expert][rows = in][cols = out]``."""
+    name: str
+    quant: int
+    n_expert: int
+    rows: int
+    cols: int
+    data: object
+    flags: int = 0
+    _buf: np.ndarray = field(init=False, repr=False)
+
+    def __post_init__(self):
+        self._buf = _bytes(self.data)
+
+    def _c(self) -> _ExpertViewC:
+        return _ExpertViewC(name_key(self.name), int(self.quant), self.flags, self.n_expert, self.rows,
+                            self.cols, self._buf.ctypes.data, self._buf.nbytes)
+
+
+def _f32_in(a, n: int | None = None) -> np.ndarray:
+    v = np.ascontiguousarray(a, dtype=np.float32)
+    return v
+
+
+def _f32_out(y) -> np.ndarray:
+    if not (isinstance(y, np.ndarray) and y.dtype == np.float32 and y.flags.c_contiguous):
+        raise TypeError("output must be a C-contiguous float32 numpy array")
+    return y
+
+
+class HipBackend:
+    """The HIP backend: the quantized primitives of ComputeBackend on one GPU.
+
+    ``weight_budget`` bounds resident packed weights (LRU eviction), like
+    ``WgpuBackend::probe_with_budget`` (crates/strata-backend-wgpu/src/gpu.rs:164).
+    """
+
+    def __init__(self, device: int = 0, weight_budget: int = 0):
+        L = load_library()
+        ctx = C.c_void_p()
+        check(L.sh_create(device, weight_budget, C.byref(ctx)))
+        self._ctx = ctx
+        self._L = L
+
+    def close(self) -> None:
+        if self._ctx:
+            self._L.sh_destroy(self._ctx)
+            self._ctx = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def name(self) -> str:
+        return self._L.sh_name(self._ctx).decode()
+
+    def resident_bytes(self) -> int:
+        v = C.c_uint64()
+        check(self._L.sh_resident_bytes(self._ctx, C.byref(v)))
+        return v.value
+
+    def evict(self, name: str) -> None:
+        check(self._L.sh_evict(self._ctx, name_key(name)))
+
+    def gemv(self, w: QuantTensor, x, y: np.ndarray, scratch=None) -> None:
+        """``y = W x`` (backend.rs:25; ops.rs:14-28)."""
+        xv, yv = _f32_in(x), _f32_out(y)
+        wc = w._c()
+        check(self._L.sh_gemv(self._ctx, C.byref(wc), xv.ctypes.data, xv.size, yv.ctypes.data, yv.size))
+
+    def gemv_batch(self, w: QuantTensor, x, batch: int) -> np.ndarray:
+        """``batch`` gemvs sharing one weight read: x ``[batch][cols]``."""
+        xv = _f32_in(x)
+        if xv.size != batch * w.cols:
+            raise ShapeError(SH_ERR_SHAPE, f"x has {xv.size} elements, want {batch}x{w.cols}")
+        y = np.empty((batch, w.rows), dtype=np.float32)
+        wc = w._c()
+        check(self._L.sh_gemv_batch(self._ctx, C.byref(wc), xv.ctypes.data, y.ctypes.data, batch))
+        return y
+
+    def expert_gemv(self, w: ExpertView, e: int, x, y: np.ndarray, scratch=None) -> None:
+        """``y = W_e x`` in the in-major orientation (backend.rs:28-35; ops.rs:169-195)."""
+        xv, yv = _f32_in(x), _f32_out(y)
+        wc = w._c()
+        check(self._L.sh_expert_gemv(self._ctx, C.byref(wc), e, xv.ctypes.data, xv.size,
+                                     yv.ctypes.data, yv.size))
+
+    def dequantize_row(self, quant: int, block, out: np.ndarray, flags: int = 0) -> None:
+        """dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device."""
+        b = _bytes(block)
+        o = _f32_out(out)
+        check(self._L.sh_dequantize_row(self._ctx, int(quant), flags, b.ctypes.data, b.nbytes,
+                                        o.ctypes.data, o.size))
+
+
+# ---- device-pointer entry points (pointers and a hipStream_t as ints) ------
+
+def dequant_dev(quant: int, w_ptr: int, rows: int, cols: int, out_ptr: int, stream: int = 0,
+                flags: int = 0) -> None:
+    check(load_library().sh_dequant_dev(int(quant), flags, w_ptr, rows, cols, out_ptr, stream or None))
+
+
+def gemv_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, y_ptr: int, batch: int = 1,
+             stream: int = 0, flags: int = 0) -> None:
+    check(load_library().sh_gemv_dev(int(quant), flags, w_ptr, rows, cols, x_ptr, y_ptr, batch,
+                                     stream or None))

@@ -1,0 +1,204 @@
+"""Pins the oracle's gemv, expert_gemv and MoE routing/combine.
+
+* the reference's unit tests: crates/strata-core/tests/ops_tests.rs:22-61,
+  crates/strata-backend-cpu/src/lib.rs:88-120, and the wgpu parity shapes
+  (crates/strata-backend-wgpu/src/gpu.rs:513-575) against manual dots;
+* brute force with exact rational arithmetic on tiny shapes: the oracle's
+  f64 sum may differ from the exact sum only by f64 rounding;
+* the sequential f64 order (ops.rs:22-26): the oracle equals a Python loop
+  of the same order bit for bit, and the threaded variant equals it too;
+* MoE routing invariants (crates/strata-core/src/moe.rs:58-90): weights sum
+  to one, ids ascending, ties to the lower id, uniform logits give uniform
+  weights; the routed combine equals its composition from expert_gemv.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import np_oracle as N
+from strata_hip import synth as S
+
+
+def f32_matrix(rows, cols, f):
+    return np.array([[f(r, c) for c in range(cols)] for r in range(rows)], np.float32)
+
+
+def test_gemv_matches_manual_dot(oracle):
+    # ops_tests.rs:22-42
+    rows, cols = 3, 4
+    w = f32_matrix(rows, cols, lambda r, c: float(r * cols + c) + 1.0)
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    y = oracle.gemv(oracle.F32, rows, cols, w.view(np.uint8), x)
+    for r in range(rows):
+        expect = sum(float(w[r, c]) * float(x[c]) for c in range(cols))
+        assert abs(float(y[r]) - expect) < 1e-4
+
+
+def test_cpu_backend_gemv_values(oracle):
+    # crates/strata-backend-cpu/src/lib.rs:88-100: y = [14, 32]
+    w = f32_matrix(2, 3, lambda r, c: float(r * 3 + c) + 1.0)
+    y = oracle.gemv(oracle.F32, 2, 3, w.view(np.uint8), np.array([1, 2, 3], np.float32))
+    assert abs(y[0] - 14.0) < 1e-4 and abs(y[1] - 32.0) < 1e-4
+
+
+def q8_single_block():
+    # ops_tests.rs:44-61 / lib.rs:102-120: d = 0.5, q = (j % 7) - 3
+    b = np.zeros(34, np.uint8)
+    b[:2] = np.array([0.5], np.float32).astype(np.float16).view(np.uint8)
+    for j in range(32):
+        b[2 + j] = np.uint8((j % 7 - 3) & 0xFF)
+    x = np.array([i * 0.25 - 1.0 for i in range(32)], np.float32)
+    return b, x
+
+
+def test_gemv_q8_0_matches_dequant_dot(oracle):
+    b, x = q8_single_block()
+    y = oracle.gemv(oracle.Q8_0, 1, 32, b, x)
+    expect = sum(float(j % 7 - 3) * 0.5 * float(x[j]) for j in range(32))
+    assert abs(float(y[0]) - expect) < 1e-4
+
+
+def test_expert_gemv_matches_transposed_dot(oracle):
+    # gpu.rs:537-575: two experts of [rows = 5][cols = 8]
+    n_expert, rows, cols = 2, 5, 8
+    data = np.array([[[((e * 100 + r * 10 + c) % 13) * 0.2 - 1.0 for c in range(cols)]
+                      for r in range(rows)] for e in range(n_expert)], np.float32)
+    x = np.array([(i % 3) - 0.5 for i in range(rows)], np.float32)
+    for e in range(n_expert):
+        y = oracle.expert_gemv(oracle.F32, n_expert, rows, cols, data.view(np.uint8), e, x)
+        for c in range(cols):
+            expect = sum(float(data[e, i, c]) * float(x[i]) for i in range(rows))
+            assert abs(float(y[c]) - expect) < 1e-6
+
+
+def _exact_dot(wrow, x):
+    return sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(wrow, x))
+
+
+@pytest.mark.parametrize("quant,rows,cols", [(8, 5, 64), (12, 3, 256), (14, 3, 512)])
+def test_gemv_brute_force_exact(oracle, quant, rows, cols):
+    w = S.matrix(quant, 99 + quant, rows, cols)
+    x = S.normal_f32(5, cols)
+    y = oracle.gemv(quant, rows, cols, w, x)
+    deq = oracle.dequantize(quant, w, rows, cols)
+    for r in range(rows):
+        exact = _exact_dot(deq[r], x)
+        mag = sum(abs(Fraction(float(a)) * Fraction(float(b))) for a, b in zip(deq[r], x))
+        # f64 sequential sum of `cols` terms, then one f32 rounding
+        bound = float(mag) * cols * 2.0 ** -52 + abs(float(exact)) * 2.0 ** -24
+        assert abs(float(y[r]) - float(exact)) <= bound
+
+
+def test_gemv_sequential_f64_order(oracle):
+    rows, cols = 4, 512
+    w = S.matrix(12, 31, rows, cols)
+    x = S.normal_f32(32, cols)
+    y = oracle.gemv(12, rows, cols, w, x)
+    deq = oracle.dequantize(12, w, rows, cols)
+    for r in range(rows):
+        acc = 0.0
+        for c in range(cols):
+            acc += float(deq[r, c]) * float(x[c])
+        assert np.float32(acc) == y[r]
+
+
+@pytest.mark.parametrize("quant", [8, 12, 14])
+def test_gemv_threads_identical_and_numpy_close(oracle, quant):
+    rows, cols = 97, 1024
+    w = S.matrix(quant, 7 + quant, rows, cols)
+    x = S.normal_f32(8, cols)
+    y1 = oracle.gemv(quant, rows, cols, w, x)
+    y4 = oracle.gemv(quant, rows, cols, w, x, threads=4)
+    assert np.array_equal(y1, y4)
+    yn = N.gemv(quant, w, rows, cols, x)
+    assert np.abs(y1 - yn).max() <= 1e-6 * np.abs(yn).max()
+
+
+def test_expert_gemv_skips_zero_inputs(oracle):
+    # ops.rs:182-184: a row whose x is 0 is not read, so a NaN weight there
+    # does not poison the sum
+    rows, cols, n_expert = 4, 256, 1
+    w = S.matrix(12, 3, rows, cols).copy()
+    w[144 * 2: 144 * 2 + 2] = [0x00, 0x7E]  # row 2's d = f16 NaN
+    x = np.array([1.0, -2.0, 0.0, 0.5], np.float32)
+    y = oracle.expert_gemv(12, n_expert, rows, cols, w, 0, x)
+    assert np.all(np.isfinite(y))
+    x[2] = 1.0
+    assert np.all(np.isnan(oracle.expert_gemv(12, n_expert, rows, cols, w, 0, x)[:256]))
+
+
+@pytest.mark.parametrize("quant,rows,cols", [(12, 16, 512), (14, 8, 512), (8, 8, 64)])
+def test_expert_gemv_equals_transposed_gemv_exactly(oracle, quant, rows, cols):
+    # both sum the same f64 products; the expert sum runs over rows i in order
+    n_expert = 3
+    w = S.matrix(quant, 11, n_expert * rows, cols)
+    x = S.normal_f32(12, rows)
+    deq = oracle.dequantize(quant, w, n_expert * rows, cols).reshape(n_expert, rows, cols)
+    for e in range(n_expert):
+        y = oracle.expert_gemv(quant, n_expert, rows, cols, w, e, x)
+        for c in range(0, cols, 37):
+            acc = 0.0
+            for i in range(rows):
+                acc += float(x[i]) * float(deq[e, i, c])
+            assert np.float32(acc) == y[c]
+
+
+# ---- MoE routing --------------------------------------------------------------
+
+def test_route_invariants(oracle):
+    for seed in range(20):
+        logits = S.normal_f32(seed, 128)
+        ids, w = oracle.moe_route(logits, 8)
+        assert len(ids) == 8
+        assert np.all(np.diff(ids) > 0)
+        assert abs(float(np.sum(w.astype(np.float64))) - 1.0) < 1e-6
+        # the selected set is the 8 largest logits (softmax is monotone)
+        assert set(ids.tolist()) == set(np.argsort(-logits.astype(np.float64), kind="stable")[:8].tolist())
+
+
+def test_route_ties_go_to_lower_ids(oracle):
+    logits = np.zeros(16, np.float32)
+    logits[[3, 9, 12]] = 1.0
+    ids, w = oracle.moe_route(logits, 5)
+    # the three 1.0 logits, then the two lowest ids among the zero logits
+    assert ids.tolist() == [0, 1, 3, 9, 12]
+
+
+def test_route_uniform_logits_give_uniform_weights(oracle):
+    ids, w = oracle.moe_route(np.full(8, 0.3, np.float32), 8)
+    assert ids.tolist() == list(range(8))
+    assert np.all(w == np.float32(0.125))
+
+
+def test_route_hand_computed(oracle):
+    # logits [0, ln 3, ln 2] -> softmax [1/6, 1/2, 1/3]; top-2 ids [1, 2] with
+    # renormalised weights [3/5, 2/5]
+    logits = np.array([0.0, np.log(3.0), np.log(2.0)], np.float32)
+    ids, w = oracle.moe_route(logits, 2)
+    assert ids.tolist() == [1, 2]
+    assert abs(w[0] - 0.6) < 1e-6 and abs(w[1] - 0.4) < 1e-6
+
+
+def test_routed_combine_is_its_composition(oracle):
+    n_expert, n_embd, n_ff = 4, 256, 512
+    gate = S.matrix(12, 1, n_expert * n_embd, n_ff)
+    up = S.matrix(12, 2, n_expert * n_embd, n_ff)
+    down = S.matrix(14, 3, n_expert * n_ff, n_embd)
+    x = S.normal_f32(4, n_embd)
+    ids, w = oracle.moe_route(S.normal_f32(5, n_expert), 2)
+    out = oracle.moe_routed(12, 12, 14, n_expert, n_embd, n_ff, gate, up, down, ids, w, x)
+    want = np.zeros(n_embd, np.float32)
+    for e, we in zip(ids, w):
+        h = oracle.expert_gemv(12, n_expert, n_embd, n_ff, gate, int(e), x)
+        p = oracle.expert_gemv(12, n_expert, n_embd, n_ff, up, int(e), x)
+        a = np.array([np.float32(oracle.silu(float(v))) * p[i] for i, v in enumerate(h)], np.float32)
+        d = oracle.expert_gemv(14, n_expert, n_ff, n_embd, down, int(e), a)
+        want = (want + (np.float32(we) * d).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(out, want)
+
+
+def test_silu_closed_form(oracle):
+    for v in [-20.0, -1.0, 0.0, 0.5, 3.0, 40.0]:
+        ref = v / (1.0 + np.exp(-v))
+        assert abs(oracle.silu(v) - ref) <= 2e-7 * max(1.0, abs(ref))
