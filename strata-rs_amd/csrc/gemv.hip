@@ -72,6 +72,7 @@ __device__ __forceinline__ void stage_x(float* lds, const float* __restrict__ x,
 // nibbles sub-block 2g+1).
 struct FmtQ4K {
   static constexpr int kR = 2;
+  static constexpr int kRing = 4;
   struct Load {
     u32x4 h, a, b;
   };
@@ -119,6 +120,7 @@ struct FmtQ4K {
 // start is, which the launcher checks).
 struct FmtQ8 {
   static constexpr int kR = 2;
+  static constexpr int kRing = 3;
   struct Load {
     u32x4 a, b, c, d;
     uint32_t e;
@@ -169,6 +171,7 @@ struct FmtQ8 {
 // `shift` (0 or 2) bytes. No load leaves the block's own 210 bytes.
 struct FmtQ6K {
   static constexpr int kR = 1;
+  static constexpr int kRing = 4;
   struct Load {
     u32x4 l0, l1, l2, l3;
     uint32_t l4;
@@ -345,6 +348,549 @@ __global__ void __launch_bounds__(512) gemv_kernel(const uint8_t* __restrict__ w
   }
 }
 
+// ------------------------------------------------------- batch-1 kernel --
+// Each wave owns `rg_per_wave` consecutive row groups (F::kR rows each) and
+// walks their (row group, window) items in order. Loads are issued as early
+// as the hardware allows:
+//   1. the workgroup's share of x is loaded into registers,
+//   2. the weight loads of the wave's first D items are issued,
+//   3. x (and its per-16 sums) is written to LDS -- this waits only for the
+//      x loads, which were issued first -- and the workgroup synchronises,
+//   4. items are computed in order; the moment item i is consumed its D-slot
+//      register set is refilled with item i + D.
+// So every wave has D items of weight bytes in flight from the first cycle
+// on, and x staging overlaps the first weight fetches instead of preceding
+// them.
+constexpr int kXRounds = 3;  // x groups held in registers per thread
+
+// Loads are never under a branch: lanes past the last unit, items past the
+// wave's last one and x groups past the end re-load a valid address whose
+// result is discarded. Branch-free load sequences let the compiler count
+// outstanding loads exactly (s_waitcnt vmcnt(N) with N > 0) instead of
+// draining the whole queue at every control-flow merge.
+template <class F, int D>
+__global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ w, int rows,
+                                                    int cols, int64_t row_bytes,
+                                                    const float* __restrict__ x,
+                                                    float* __restrict__ y, int q6_signed,
+                                                    int rg_per_wave) {
+  constexpr int R = F::kR;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wpg = blockDim.x >> 6;
+  const int units = cols >> 6;
+  const int nwin = (units + 63) >> 6;
+  const int n_rg = (rows + R - 1) / R;
+  const int wave_id = blockIdx.x * wpg + (tid >> 6);
+  const int rg0 = wave_id * rg_per_wave;
+  const int my_rg = max(0, min(rg_per_wave, n_rg - rg0));
+  const int n_items = my_rg * nwin;  // wave-uniform
+
+  // 1. x loads (16-float groups, round-robin over the workgroup)
+  const int groups = cols >> 4;
+  f32x4 xr[kXRounds][4];
+#pragma unroll
+  for (int k = 0; k < kXRounds; ++k) {
+    const int g = min(tid + k * int(blockDim.x), groups - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + 16 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xr[k][j] = src[j];
+  }
+
+  // 2. weight loads of the first D items
+  typename F::Load slot[D][R];
+  const int last = max(n_items - 1, 0);
+  auto issue = [&](typename F::Load* L, int i) {
+    i = min(i, last);
+    const int q = i / nwin;
+    const int win = i - q * nwin;
+    const int u = min((win << 6) + lane, units - 1);
+    const int rgq = min(rg0 + q, n_rg - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(rgq * R + r, rows - 1);
+      typename F::Load v;
+      F::load(w + int64_t(row) * row_bytes, u, v);
+      L[r] = v;
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) issue(slot[s], s);
+
+  // 3. x -> LDS with per-16 sums (waits only for the x loads, issued first)
+  const int sum_base = cols + cols / 16;
+#pragma unroll
+  for (int k = 0; k < kXRounds; ++k) {
+    const int g = tid + k * int(blockDim.x);
+    const f32x4 a = xr[k][0], b = xr[k][1], c = xr[k][2], e = xr[k][3];
+    const float sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+                      (((c.x + c.y) + (c.z + c.w)) + ((e.x + e.y) + (e.z + e.w)));
+    if (g < groups) {
+      const int e0 = 16 * g;
+      f32x4* d = reinterpret_cast<f32x4*>(lds + e0 + 4 * (e0 >> 6));
+      d[0] = a;
+      d[1] = b;
+      d[2] = c;
+      d[3] = e;
+      lds[sum_base + g] = sum;
+    }
+  }
+  // rows wider than kXRounds * blockDim * 16 columns (none of the configs)
+  for (int g = tid + kXRounds * int(blockDim.x); g < groups; g += blockDim.x) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + 16 * g);
+    const f32x4 a = src[0], b = src[1], c = src[2], e = src[3];
+    const int e0 = 16 * g;
+    f32x4* d = reinterpret_cast<f32x4*>(lds + e0 + 4 * (e0 >> 6));
+    d[0] = a;
+    d[1] = b;
+    d[2] = c;
+    d[3] = e;
+    lds[sum_base + g] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+                        (((c.x + c.y) + (c.z + c.w)) + ((e.x + e.y) + (e.z + e.w)));
+  }
+  __syncthreads();
+  if (n_items == 0) return;
+
+  // 4. compute in order, refilling each slot as soon as it is consumed
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  XSlice xv;
+  int xwin = -1;
+  for (int base = 0; base < n_items; base += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int i = base + s;
+      const int q = i / nwin;
+      const int win = i - q * nwin;
+      const int u = (win << 6) + lane;
+      if (xwin != win) {
+        load_xslice(lds, cols, min(u, units - 1), xv);
+        xwin = win;
+      }
+      float part[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[r] = F::dot(slot[s][r], xv, u, q6_signed);
+      // keep the refill below the last use of the slot, so the new loads land
+      // in the same registers and the loop needs no register rotation (a
+      // rotating copy of a pending load would drain the whole load queue)
+      __builtin_amdgcn_sched_barrier(0);
+      issue(slot[s], i + D);
+      if (i < n_items) {
+        if (u < units) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r] += part[r];
+        }
+        if (win == nwin - 1) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const float t = wave_sum(acc[r]);
+            const int row = (rg0 + q) * R + r;
+            if (lane == 0 && row < rows) y[row] = t;
+            acc[r] = 0.f;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ================================================== batch-1 integer path ==
+// x as three int8 limbs. Each workgroup converts the f32 activations once:
+// per 32-column block a power-of-two scale 2^-k is chosen so that the block's
+// largest |x| times 2^k is below 2^22, and every element becomes the integer
+//   v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c,  a in [-64, 64], b, c in [0, 255]
+// (a is byte 2 of v, b byte 1, c byte 0, in two's complement). Each element
+// is represented to within 2^-23 of its block's maximum, as close to x as the
+// f32 activations themselves for elements near the maximum. Weight codes are
+// small non-negative integers, so the per-block dot products are exact
+// integer sums on v_dot4_i32_i8 (a) and v_dot4_u32_u8 (b, c), four weights
+// per instruction:
+//   sum_j q_j x_j = 2^-k (2^16 sum q a + (2^8 sum q b + sum q c)) + rounding of v
+// and only the per-block scale epilogue is f32.
+//
+// LDS layout for `cols` columns (bytes): three limb planes, each with a
+// 16-byte pad after every 64 bytes (so lanes reading 64-byte runs hit
+// distinct banks), then per 32-column block 16 bytes:
+//   {sum of x over columns 0-15, sum over 16-31, 2^-k, K}
+// with K = sum of (v & 0xFFFF) = sum 2^8 b + c (an integer, for the bias of
+// signed weights against the unsigned low limbs).
+__host__ __device__ inline int plane_stride(int cols) { return cols + cols / 4; }
+__host__ __device__ inline int limb_lds_bytes(int cols) { return 3 * plane_stride(cols) + (cols / 32) * 16; }
+
+// 4 int32 values -> their bytes `b` packed low to high (one v_perm each pair)
+__device__ __forceinline__ void transpose_bytes(uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                                uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u);  // v0b0 v1b0 v0b1 v1b1
+  const uint32_t t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
+  const uint32_t u01 = __builtin_amdgcn_perm(v1, v0, 0x07030602u);  // v0b2 v1b2 v0b3 v1b3
+  const uint32_t u23 = __builtin_amdgcn_perm(v3, v2, 0x07030602u);
+  p0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u);  // byte 0 of v0..v3
+  p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u);  // byte 1
+  p2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);  // byte 2
+}
+
+// Converts one 16-column group held in registers and writes it to LDS. The
+// thread handling group g ^ 1 (the other half of the 32-column block) is the
+// neighbouring lane, which shares the block maximum and sum.
+__device__ __forceinline__ void limb_group(uint8_t* lds, int cols, int g, bool valid, f32x4 a, f32x4 b,
+                                           f32x4 c, f32x4 d) {
+  const float xs[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w,
+                        c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+  float m = 0.f, s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    m = fmaxf(m, fabsf(xs[i]));
+    s += xs[i];
+  }
+  m = fmaxf(m, __shfl_xor(m, 1, kWave));
+  const float s_other = __shfl_xor(s, 1, kWave);
+  // k with m * 2^k < 2^22; for m == 0 any k works
+  // (clamped so 2^k stays finite for blocks whose maximum is below 2^-104)
+  int e = 0;
+  (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
+  const int k = m > 0.f ? min(22 - e, 126) : 0;
+  const float up = ldexpf(1.f, k);
+  // a NaN or infinite block keeps its NaN through the scale
+  const float down = (m - m == 0.f) ? ldexpf(1.f, -k) : __builtin_nanf("");
+  uint32_t v[16];
+  uint32_t low = 0;  // sum of (v & 0xFFFF) over the group
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
+    const float t = __builtin_fmaf(xs[i], up, 12582912.0f);
+    v[i] = __builtin_bit_cast(uint32_t, t) - 0x4B400000u;
+    low += v[i] & 0xFFFFu;
+  }
+  const uint32_t low_other = __shfl_xor(low, 1, kWave);
+  if (!valid) return;
+  const int e0 = 16 * g;
+  const int off = e0 + 16 * (e0 >> 6);
+  const int ps = plane_stride(cols);
+  uint32_t pc[4], pb[4], pa[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) transpose_bytes(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], pc[q], pb[q], pa[q]);
+  *reinterpret_cast<u32x4*>(lds + off) = u32x4{pa[0], pa[1], pa[2], pa[3]};
+  *reinterpret_cast<u32x4*>(lds + ps + off) = u32x4{pb[0], pb[1], pb[2], pb[3]};
+  *reinterpret_cast<u32x4*>(lds + 2 * ps + off) = u32x4{pc[0], pc[1], pc[2], pc[3]};
+  if ((g & 1) == 0) {
+    *reinterpret_cast<u32x4*>(lds + 3 * ps + 16 * (g >> 1)) =
+        u32x4{__builtin_bit_cast(uint32_t, s), __builtin_bit_cast(uint32_t, s_other),
+              __builtin_bit_cast(uint32_t, down), low + low_other};
+  }
+}
+
+// The lane's 64 columns: limb dwords for elements 4j..4j+3 and the two
+// 32-column blocks' {sum, scale}.
+struct XLimbs {
+  u32x4 a[4], b[4], c[4];
+  u32x4 i0, i1;  // the two 32-column blocks: {sum 0-15, sum 16-31, 2^-k, K} as raw words
+};
+
+__device__ __forceinline__ float fw(uint32_t bits) { return __builtin_bit_cast(float, bits); }
+
+__device__ __forceinline__ void load_limbs(const uint8_t* lds, int cols, int u, XLimbs& o) {
+  const int ps = plane_stride(cols);
+  const int off = 80 * u;  // 64 bytes + 16 pad per unit
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o.a[i] = *reinterpret_cast<const u32x4*>(lds + off + 16 * i);
+    o.b[i] = *reinterpret_cast<const u32x4*>(lds + ps + off + 16 * i);
+    o.c[i] = *reinterpret_cast<const u32x4*>(lds + 2 * ps + off + 16 * i);
+  }
+  o.i0 = *reinterpret_cast<const u32x4*>(lds + 3 * ps + 32 * u);
+  o.i1 = *reinterpret_cast<const u32x4*>(lds + 3 * ps + 32 * u + 16);
+}
+
+__device__ __forceinline__ uint32_t limb_word(const u32x4* p, int j) {
+  const u32x4 v = p[j >> 2];
+  return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
+}
+
+// Exact sum over 4 weights (bytes of `q`, each 0..127) times 4 x elements
+// (limb words a, b, c), accumulated into the three integer sums.
+__device__ __forceinline__ void dot_limbs(uint32_t q, uint32_t a, uint32_t b, uint32_t c, int& sa,
+                                          uint32_t& sb, uint32_t& sc) {
+  sa = __builtin_amdgcn_sdot4(int(q), int(a), sa, false);
+  sb = __builtin_amdgcn_udot4(q, b, sb, false);
+  sc = __builtin_amdgcn_udot4(q, c, sc, false);
+}
+
+// sum q*v = 2^16 sa + 2^8 sb + sc as f32 (2^8 sb + sc < 2^25 is exact in u32)
+__device__ __forceinline__ float limb_value(int sa, uint32_t sb, uint32_t sc) {
+  return __builtin_fmaf(float(sa), 65536.f, float(sb * 256u + sc));
+}
+
+// Sum over the 64 lanes with DPP: quad swaps, half-row and row mirrors,
+// then row broadcasts 15 and 31; lane 63 ends with the total.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)); // row_bcast15
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)); // row_bcast31
+  return v;
+}
+
+// Q4_K with integer dots: unit u = (super-block u/4, group g = u%4) as in
+// FmtQ4K; low nibbles are sub-block 2g (x block 2u), high nibbles 2g+1.
+struct LimbQ4K {
+  struct Load {
+    u32x4 h, a, b;
+  };
+  static constexpr int kWinBytes = 16 * 144;  // one 4096-column window of a row
+  struct Off {
+    int h, q;
+  };
+  // h: the super-block's byte offset (advances by kWinBytes per window);
+  // q: the lane's quant bytes relative to it
+  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 144, 16 + 32 * (u & 3)}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    L.h = ld16(row + o.h);
+    L.a = ld16(row + o.h + o.q);
+    L.b = ld16(row + o.h + o.q + 16);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
+    const int g = lane & 3;
+    const uint32_t sh = (g & 1) << 4;
+    const uint32_t t1 = L.h.y >> sh, t2 = L.h.z >> sh, t3 = L.h.w >> sh;
+    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
+    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
+    int a0 = 0, a1 = 0;
+    uint32_t b0 = 0, b1 = 0, c0 = 0, c1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t lo = q[k] & 0x0F0F0F0Fu;
+      const uint32_t hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+      dot_limbs(lo, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), a0, b0, c0);
+      dot_limbs(hi, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), a1, b1, c1);
+    }
+    const float s0 = limb_value(a0, b0, c0) * fw(x.i0.z);  // sum over sub-block 2g of q * x
+    const float s1 = limb_value(a1, b1, c1) * fw(x.i1.z);  // sub-block 2g + 1
+    const float qsum = ubyte<0>(scp) * s0 + ubyte<1>(scp) * s1;
+    const float msum = ubyte<0>(mp) * (fw(x.i0.x) + fw(x.i0.y)) + ubyte<1>(mp) * (fw(x.i1.x) + fw(x.i1.y));
+    return d * qsum - dm * msum;
+  }
+};
+
+// Q8_0 with integer dots: unit u = blocks 2u and 2u+1 (68 bytes from a
+// dword-aligned address). Codes are signed: the top limb (signed) takes them
+// as they are; against the unsigned low limbs they are biased to q + 128 and
+// the bias 128 * K is removed in integers before the one f32 conversion.
+struct LimbQ8 {
+  struct Load {
+    u32x4 a, b, c, d;
+    uint32_t e;
+  };
+  static constexpr int kWinBytes = 64 * 68;
+  struct Off {
+    int h, q;
+  };
+  __device__ static __forceinline__ Off offsets(int u) { return {u * 68, 0}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    const uint8_t* p = row + o.h;
+    L.a = ld16(p);
+    L.b = ld16(p + 16);
+    L.c = ld16(p + 32);
+    L.d = ld16(p + 48);
+    L.e = ld4(p + 64);
+  }
+  __device__ static __forceinline__ float block(const uint32_t* q, const u32x4* xa, const u32x4* xb,
+                                                const u32x4* xc, int j0, u32x4 info) {
+    int sa = 0;
+    uint32_t sb = 0, sc = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t qb = q[k] ^ 0x80808080u;  // q + 128
+      sa = __builtin_amdgcn_sdot4(int(q[k]), int(limb_word(xa, j0 + k)), sa, false);
+      sb = __builtin_amdgcn_udot4(qb, limb_word(xb, j0 + k), sb, false);
+      sc = __builtin_amdgcn_udot4(qb, limb_word(xc, j0 + k), sc, false);
+    }
+    const int bc = int(sb * 256u + sc) - 128 * int(info.w);
+    return __builtin_fmaf(float(sa), 65536.f, float(bc)) * fw(info.z);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int, int) {
+    const uint32_t D[17] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w, L.c.x,
+                            L.c.y, L.c.z, L.c.w, L.d.x, L.d.y, L.d.z, L.d.w, L.e};
+    uint32_t q0[8], q1[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      q0[k] = realign(D[k], D[k + 1], 2);
+      q1[k] = D[9 + k];
+    }
+    const float d0 = h2f(D[0]), d1 = h2f(D[8] >> 16);
+    return d0 * block(q0, x.a, x.b, x.c, 0, x.i0) + d1 * block(q1, x.a, x.b, x.c, 8, x.i1);
+  }
+};
+
+// Q6_K with integer dots: unit u = (super-block u/4, quarter j = u%4) as in
+// FmtQ6K; the 6-bit codes 0..63 go straight into the dots and the -32
+// offset is taken off with the per-16 sums of x.
+struct LimbQ6K {
+  using Load = FmtQ6K::Load;
+  static constexpr int kWinBytes = 16 * 210;
+  struct Off {
+    int h, q;
+  };
+  // h: the super-block's byte offset, q: the quarter 0..3
+  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 210, u & 3}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    FmtQ6K::load(row + o.h, o.q, L);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int q6_signed) {
+    const uint32_t tp = uint32_t(lane) & 1u;
+    const uint32_t s = L.shift;
+    const uint32_t qlr[17] = {L.l0.x, L.l0.y, L.l0.z, L.l0.w, L.l1.x, L.l1.y, L.l1.z, L.l1.w, L.l2.x,
+                              L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
+    const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
+    const uint32_t scw = realign(L.s0, L.s1, s);
+    const uint32_t nib = 4u * tp;
+    int sa[4] = {0, 0, 0, 0};
+    uint32_t sb[4] = {0, 0, 0, 0}, sc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
+      const uint32_t qs = tp ? qh : (qh << 4);
+      const uint32_t va = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
+      const uint32_t vb =
+          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+      const int ga = k >> 2, gb = 2 + (k >> 2);
+      dot_limbs(va, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), sa[ga], sb[ga], sc[ga]);
+      dot_limbs(vb, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), sa[gb], sb[gb], sc[gb]);
+    }
+    float scf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t byte = (scw >> (8 * i)) & 0xFFu;
+      scf[i] = q6_signed ? float(int8_t(byte)) : float(byte);
+    }
+    const float xs[4] = {fw(x.i0.x), fw(x.i0.y), fw(x.i1.x), fw(x.i1.y)};
+    const float ks[4] = {fw(x.i0.z), fw(x.i0.z), fw(x.i1.z), fw(x.i1.z)};
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t += scf[i] * (limb_value(sa[i], sb[i], sc[i]) * ks[i] - 32.f * xs[i]);
+    return h2f(L.d) * t;
+  }
+};
+
+// Batch-1 matvec on the integer path.
+//
+// Wave w owns row groups [w*per, w*per + per) of R rows. Items are
+// (row group, window) pairs taken window-major, so each wave reads its x
+// limbs from LDS once per window and keeps `per` (<= MAXQ) row sums per
+// row in registers. All item control is wave-uniform (scalar registers);
+// per-lane byte offsets within a row are computed once. Loads are
+// double-buffered (A/B ping-pong, both refills unconditional so the loop
+// latch never drains the load queue), and the first item is requested
+// before x is staged, so weight bytes are in flight from the first cycles.
+template <class F, int R, int MAXQ>
+__global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restrict__ w, int rows,
+                                                        int cols, int64_t row_bytes,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ y, int per, int flags) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
+  const int units = cols >> 6;
+  const int nwin = (units + 63) >> 6;
+  const int n_rg = (rows + R - 1) / R;
+  const int rg0 = wave * per;
+  const int my = max(0, min(per, n_rg - rg0));  // row groups of this wave
+  const int n_items = my * nwin;
+
+  // per-lane offsets: window 0, and the clamped unit of a partial last window
+  const typename F::Off off0 = F::offsets(lane);
+  const int ulast = min((nwin - 1) * 64 + lane, units - 1);
+  const typename F::Off offl = F::offsets(ulast);
+  const bool lane_valid_last = (nwin - 1) * 64 + lane < units;
+
+  // the item sequence: window-major, row groups inner
+  auto item_off = [&](int wn) -> typename F::Off {
+    if (wn == nwin - 1) return offl;
+    return {off0.h + wn * F::kWinBytes, off0.q};
+  };
+  int pw = 0, pq = 0;  // next item to request
+  auto issue = [&](typename F::Load* L) {
+    const bool past = pw >= nwin;  // past the end: re-request the last item
+    const int wn = past ? nwin - 1 : pw;
+    const int qq = past ? max(my - 1, 0) : pq;
+    const typename F::Off o = item_off(wn);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min((rg0 + qq) * R + r, rows - 1);
+      F::load(w + int64_t(row) * row_bytes, o, L[r]);
+    }
+    if (++pq == my) {
+      pq = 0;
+      ++pw;
+    }
+  };
+  typename F::Load A[R], B[R];
+  issue(A);
+
+  // stage x as limbs (a wave whose 64 groups all lie past the end skips the
+  // round: the last round is usually partial)
+  const int groups = cols >> 4;
+  const int wave_first = tid & ~63;
+  for (int g0 = 0; g0 < groups; g0 += blockDim.x) {
+    if (g0 + wave_first >= groups) break;
+    const int g = g0 + tid;
+    const int gl = min(g, groups - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + 16 * gl);
+    limb_group(lds8, cols, g, g < groups, src[0], src[1], src[2], src[3]);
+  }
+  __syncthreads();
+  if (n_items == 0) return;
+
+  float acc[MAXQ][R];
+#pragma unroll
+  for (int q = 0; q < MAXQ; ++q)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[q][r] = 0.f;
+  XLimbs xl;
+  int cw = 0, cq = 0;  // item being computed
+  auto step = [&](const typename F::Load* L) {
+    if (cq == 0) {
+      const int u = cw == nwin - 1 ? ulast : cw * 64 + lane;
+      load_limbs(lds8, cols, u, xl);
+    }
+    const bool ok = cw < nwin - 1 || lane_valid_last;
+#pragma unroll
+    for (int q = 0; q < MAXQ; ++q) {
+      if (q == cq) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float t = F::dot(L[r], xl, lane, flags);
+          acc[q][r] += ok ? t : 0.f;
+        }
+      }
+    }
+    if (++cq == my) {
+      cq = 0;
+      ++cw;
+    }
+  };
+  for (int i = 0; i < n_items; i += 2) {
+    issue(B);
+    step(A);
+    issue(A);
+    if (i + 1 < n_items) step(B);
+  }
+#pragma unroll
+  for (int q = 0; q < MAXQ; ++q) {
+    if (q < my) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float t = wave_sum_dpp(acc[q][r]);
+        const int row = (rg0 + q) * R + r;
+        if (lane == 63 && row < rows) y[row] = t;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- launch --
 static int g_cu_count = 0;
 
@@ -372,6 +918,45 @@ bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
   return lds_bytes(int(cols), 1) <= kMaxLds;
 }
 
+template <class F, int D>
+static hipError_t launch_one(const uint8_t* w, int rows, int cols, int64_t row_bytes,
+                             const float* x, float* y, int q6_signed, hipStream_t stream) {
+  constexpr int R = F::kR;
+  const int threads = 512, wpg = threads / 64;
+  const int n_rg = (rows + R - 1) / R;
+  // Spread the row groups over 8 waves per CU. For the decode shapes that is
+  // at most D items per wave, so each wave fills its ring once and never
+  // cycles; larger matrices (the lm_head) cycle the ring.
+  const int min_waves = cu_count() * 8;
+  const int per_wave = (n_rg + min_waves - 1) / min_waves;
+  const int waves = (n_rg + per_wave - 1) / per_wave;
+  const int blocks = (waves + wpg - 1) / wpg;
+  const size_t lds = lds_bytes(cols, 1);
+  hipLaunchKernelGGL((gemv1_kernel<F, D>), dim3(unsigned(blocks)), dim3(threads), lds, stream, w,
+                     rows, cols, row_bytes, x, y, q6_signed, per_wave);
+  return hipGetLastError();
+}
+
+// Row groups spread over `waves_per_cu` waves per CU; multi-window rows keep
+// at most MAXQ row groups per wave (their sums live in registers).
+template <class F, int R, int MAXQ>
+static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_bytes,
+                              const float* x, float* y, hipStream_t stream, int threads,
+                              int waves_per_cu, int flags = 0) {
+  const int wpg = threads / 64;
+  const int n_rg = (rows + R - 1) / R;
+  const int units = cols >> 6, nwin = (units + 63) >> 6;
+  const int min_waves = cu_count() * waves_per_cu;
+  int per = (n_rg + min_waves - 1) / min_waves;
+  if (nwin > 1 && per > MAXQ) per = MAXQ;
+  if (nwin == 1 && per > MAXQ) per = MAXQ;
+  const int waves = (n_rg + per - 1) / per;
+  const int blocks = (waves + wpg - 1) / wpg;
+  hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ>), dim3(unsigned(blocks)), dim3(threads),
+                     size_t(limb_lds_bytes(cols)), stream, w, rows, cols, row_bytes, x, y, per, flags);
+  return hipGetLastError();
+}
+
 template <class F, int NB>
 static hipError_t launch_fmt(const uint8_t* w, int rows, int cols, int64_t row_bytes,
                              const float* x, float* y, int q6_signed, hipStream_t stream) {
@@ -391,7 +976,7 @@ template <class F>
 static hipError_t launch_nb(int nb, const uint8_t* w, int rows, int cols, int64_t row_bytes,
                             const float* x, float* y, int q6_signed, hipStream_t s) {
   switch (nb) {
-    case 1: return launch_fmt<F, 1>(w, rows, cols, row_bytes, x, y, q6_signed, s);
+    case 1: return launch_one<F, F::kRing>(w, rows, cols, row_bytes, x, y, q6_signed, s);
     case 2: return launch_fmt<F, 2>(w, rows, cols, row_bytes, x, y, q6_signed, s);
     case 3: return launch_fmt<F, 3>(w, rows, cols, row_bytes, x, y, q6_signed, s);
     case 4: return launch_fmt<F, 4>(w, rows, cols, row_bytes, x, y, q6_signed, s);
@@ -422,9 +1007,18 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
     float* yb = y + int64_t(b0) * rows;
     hipError_t e;
     switch (quant) {
-      case kQ4_K: e = launch_nb<FmtQ4K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream); break;
-      case kQ8_0: e = launch_nb<FmtQ8>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream); break;
-      default: e = launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
+      case kQ4_K:
+        e = nb == 1 ? launch_limb<LimbQ4K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8)
+                    : launch_nb<FmtQ4K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
+        break;
+      case kQ8_0:
+        e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8)
+                    : launch_nb<FmtQ8>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
+        break;
+      default:
+        e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8,
+                                                  q6_signed)
+                    : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
     }
     if (e != hipSuccess) return e;
   }

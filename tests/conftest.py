@@ -16,6 +16,16 @@ for p in (os.path.join(ROOT, "strata-rs_amd"), os.path.join(ROOT, "oracle")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# torch bundles its own HIP runtime with the same soname (libamdhip64.so.7)
+# as the system one libstrata_hip links against; whichever is loaded first
+# serves the whole process, and torch only works with its own. Importing
+# torch before the library is loaded keeps one runtime for every test (the
+# benchmark imports torch first for the same reason).
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is part of the image
+    torch = None
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path)")
