@@ -144,7 +144,45 @@ int sh_expert_gemv(sh_context* ctx, const sh_expert_view* w, uint64_t e, const f
 int sh_dequantize_row(sh_context* ctx, uint32_t quant, uint32_t flags, const uint8_t* block,
                       uint64_t nbytes, float* out, uint64_t n);
 
+/* MoeLayer::route from router logits (crates/strata-core/src/moe.rs:58-90):
+ * softmax over all experts, top-k by descending probability (ties to the
+ * lower id), ids ascending, weights renormalised by max(sum, 2^-14).
+ * logits [n_tok][n_expert]; ids/weights [n_tok][top_k]. n_expert <= 1024,
+ * top_k <= min(32, n_expert), n_tok <= 256. */
+int sh_moe_route(sh_context* ctx, const float* logits, uint32_t n_tok, uint32_t n_expert,
+                 uint32_t top_k, int32_t* ids, float* weights);
+
+/* The routed half of MoeLayer::combine (moe.rs:108-127) for n_tok tokens,
+ * from router logits: out[t] = sum over t's top_k experts (ascending id) of
+ * w * down_e(silu(gate_e x_t) * up_e x_t). gate/up are [n_expert][n_embd]
+ * [n_ff], down [n_expert][n_ff][n_embd] (reference orientation); x and out
+ * are [n_tok][n_embd]. The shared expert (moe.rs:129-143) is not included.
+ * gate and up must have the same quant type. */
+int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view* up,
+               const sh_expert_view* down, const float* logits, uint32_t n_tok, uint32_t top_k,
+               const float* x, float* out);
+
 /* ---- device-pointer variants (asynchronous on `stream`) ---------------- */
+
+/* One expert tensor already in device memory. */
+typedef struct sh_expert_dev {
+  uint32_t quant;
+  uint32_t flags;
+  const void* data; /* [n_expert][rows][cols] packed, as in sh_expert_view */
+} sh_expert_dev;
+
+/* Bytes of device workspace sh_moe_ffn_dev needs for these shapes. */
+int sh_moe_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
+                           uint64_t n_ff, uint32_t quant_gate_up, uint32_t quant_down,
+                           uint64_t* bytes);
+
+/* sh_moe_ffn on device pointers; logits, x, out and workspace are device
+ * buffers, workspace at least sh_moe_workspace_bytes() long and 256-byte
+ * aligned. Calls sharing one workspace must not overlap in time. */
+int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_expert_dev* down,
+                   uint64_t n_expert, uint64_t n_embd, uint64_t n_ff, const float* logits,
+                   uint32_t n_tok, uint32_t top_k, const float* x, float* out, void* workspace,
+                   uint64_t workspace_bytes, void* stream);
 
 /* rows x cols of packed blocks at `w` -> out[rows][cols] f32, bit-exact. */
 int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,

@@ -392,6 +392,106 @@ int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const flo
   return SH_OK;
 }
 
+static int moe_check(uint64_t n_expert, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
+                     uint32_t top_k, uint32_t qa, uint32_t qb, sh::MoePlan* plan) {
+  if (n_expert == 0 || n_expert > uint64_t(sh::kMoeMaxExperts))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_expert %llu outside 1..%d", (unsigned long long)n_expert,
+                sh::kMoeMaxExperts);
+  if (top_k == 0 || top_k > uint32_t(sh::kMoeMaxTopK) || top_k > n_expert)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "top_k %u outside 1..min(%d, n_expert)", top_k, sh::kMoeMaxTopK);
+  if (n_tok == 0 || n_tok > uint32_t(sh::kMoeMaxTokens))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_tok %u outside 1..%d", n_tok, sh::kMoeMaxTokens);
+  if (n_embd > (1u << 20) || n_ff > (1u << 20))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "MoE widths too large");
+  if (!sh::moe_plan(int(n_tok), int(top_k), int(n_expert), int(n_embd), int(n_ff), qa, qb, plan))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "MoE %llu x %llu (types %u, %u) is not supported",
+                (unsigned long long)n_embd, (unsigned long long)n_ff, qa, qb);
+  return SH_OK;
+}
+
+int sh_moe_route(sh_context* c, const float* logits, uint32_t n_tok, uint32_t n_expert, uint32_t top_k,
+                 int32_t* ids, float* weights) {
+  if (!c || !logits || !ids || !weights) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  sh::MoePlan plan;
+  // routing needs no weights: plan with a minimal Q4_K shape for the layout
+  int rc = moe_check(n_expert, 256, 256, n_tok, top_k, sh::kQ4_K, sh::kQ4_K, &plan);
+  if (rc) return rc;
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  const size_t lb = sizeof(float) * n_tok * n_expert, ob = sizeof(float) * n_tok * top_k;
+  if ((rc = c->d_in.ensure(lb, "logits buffer")) || (rc = c->d_blk.ensure(plan.bytes, "workspace")) ||
+      (rc = c->h_in.ensure(lb, "logits staging")) || (rc = c->h_out.ensure(2 * ob, "route staging")))
+    return rc;
+  memcpy(c->h_in.p, logits, lb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, lb, hipMemcpyHostToDevice, c->stream), "logits upload");
+  HIP_TRY(sh::launch_moe_route(plan, static_cast<const float*>(c->d_in.p), c->d_blk.p, c->stream), "route");
+  uint8_t* ho = static_cast<uint8_t*>(c->h_out.p);
+  HIP_TRY(hipMemcpyAsync(ho, static_cast<uint8_t*>(c->d_blk.p) + plan.o_ids, ob, hipMemcpyDeviceToHost,
+                         c->stream), "ids readback");
+  HIP_TRY(hipMemcpyAsync(ho + ob, static_cast<uint8_t*>(c->d_blk.p) + plan.o_wts, ob,
+                         hipMemcpyDeviceToHost, c->stream), "weights readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "route");
+  memcpy(ids, ho, ob);
+  memcpy(weights, ho + ob, ob);
+  return SH_OK;
+}
+
+int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* up,
+               const sh_expert_view* down, const float* logits, uint32_t n_tok, uint32_t top_k,
+               const float* x, float* out) {
+  if (!c || !gate || !up || !down || !logits || !x || !out)
+    return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols;
+  if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
+      down->rows != n_ff || down->cols != n_embd)
+    return fail(SH_ERR_SHAPE, "MoE views disagree: gate/up [%llu][%llu][%llu], down [%llu][%llu][%llu]",
+                (unsigned long long)E, (unsigned long long)n_embd, (unsigned long long)n_ff,
+                (unsigned long long)down->n_expert, (unsigned long long)down->rows,
+                (unsigned long long)down->cols);
+  if (gate->quant != up->quant)
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", gate->quant, up->quant);
+  int rc;
+  if ((rc = check_matrix(gate->quant, n_embd, n_ff, E, gate->nbytes)) ||
+      (rc = check_matrix(up->quant, n_embd, n_ff, E, up->nbytes)) ||
+      (rc = check_matrix(down->quant, n_ff, n_embd, E, down->nbytes)))
+    return rc;
+  sh::MoePlan plan;
+  if ((rc = moe_check(E, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan))) return rc;
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident *rg = nullptr, *ru = nullptr, *rd = nullptr;
+  const uint64_t ga = E * n_embd * uint64_t(sh::byte_size(gate->quant, int64_t(n_ff)));
+  const uint64_t db = E * n_ff * uint64_t(sh::byte_size(down->quant, int64_t(n_embd)));
+  if ((rc = resident(c, gate->key, gate->quant, E, n_embd, n_ff, gate->data, ga, &rg))) return rc;
+  if ((rc = resident(c, up->key, up->quant, E, n_embd, n_ff, up->data, ga, &ru))) return rc;
+  if ((rc = resident(c, down->key, down->quant, E, n_ff, n_embd, down->data, db, &rd))) return rc;
+  // a budget eviction while admitting a later view may have dropped an earlier one
+  if ((rc = resident(c, gate->key, gate->quant, E, n_embd, n_ff, gate->data, ga, &rg))) return rc;
+  if ((rc = resident(c, up->key, up->quant, E, n_embd, n_ff, up->data, ga, &ru))) return rc;
+  const size_t lb = sizeof(float) * n_tok * E, xb = sizeof(float) * n_tok * n_embd;
+  const size_t lb_al = (lb + 255) & ~size_t(255);
+  if ((rc = c->d_in.ensure(lb_al + xb, "inputs")) || (rc = c->d_out.ensure(xb, "out buffer")) ||
+      (rc = c->d_blk.ensure(plan.bytes, "workspace")) || (rc = c->h_in.ensure(lb_al + xb, "staging")) ||
+      (rc = c->h_out.ensure(xb, "out staging")))
+    return rc;
+  uint8_t* hi = static_cast<uint8_t*>(c->h_in.p);
+  memcpy(hi, logits, lb);
+  memcpy(hi + lb_al, x, xb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, hi, lb_al + xb, hipMemcpyHostToDevice, c->stream), "input upload");
+  const uint8_t* di = static_cast<const uint8_t*>(c->d_in.p);
+  HIP_TRY(sh::launch_moe(plan, gate->quant, up->quant, down->quant, rg->dev, ru->dev, rd->dev,
+                         (gate->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         (up->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         (down->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         reinterpret_cast<const float*>(di), reinterpret_cast<const float*>(di + lb_al),
+                         static_cast<float*>(c->d_out.p), c->d_blk.p, c->stream),
+          "moe launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, xb, hipMemcpyDeviceToHost, c->stream), "out readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "moe");
+  memcpy(out, c->h_out.p, xb);
+  return SH_OK;
+}
+
 int sh_dequantize_row(sh_context* c, uint32_t quant, uint32_t flags, const uint8_t* block,
                       uint64_t nbytes, float* out, uint64_t n) {
   if (!c || (!block && nbytes) || (!out && n)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
@@ -450,6 +550,46 @@ int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, ui
   HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
                           (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
           "gemv launch");
+  return SH_OK;
+}
+
+int sh_moe_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
+                           uint64_t n_ff, uint32_t quant_gate_up, uint32_t quant_down, uint64_t* bytes) {
+  if (!bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null bytes");
+  sh::MoePlan plan;
+  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, quant_gate_up, quant_down, &plan);
+  if (rc) return rc;
+  *bytes = plan.bytes;
+  return SH_OK;
+}
+
+int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_expert_dev* down,
+                   uint64_t n_expert, uint64_t n_embd, uint64_t n_ff, const float* logits,
+                   uint32_t n_tok, uint32_t top_k, const float* x, float* out, void* workspace,
+                   uint64_t workspace_bytes, void* stream) {
+  if (!gate || !up || !down || !gate->data || !up->data || !down->data || !logits || !x || !out ||
+      !workspace)
+    return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (gate->quant != up->quant)
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", gate->quant, up->quant);
+  sh::MoePlan plan;
+  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan);
+  if (rc) return rc;
+  if (workspace_bytes < plan.bytes)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed",
+                (unsigned long long)workspace_bytes, (unsigned long long)plan.bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  for (const sh_expert_dev* t : {gate, up, down})
+    if ((reinterpret_cast<uintptr_t>(t->data) & 1u) ||
+        (t->quant == SH_QUANT_Q8_0 && (reinterpret_cast<uintptr_t>(t->data) & 3u)))
+      return fail(SH_ERR_INVALID_ARGUMENT, "misaligned expert tensor");
+  HIP_TRY(sh::launch_moe(plan, gate->quant, up->quant, down->quant, gate->data, up->data, down->data,
+                         (gate->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         (up->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         (down->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, logits, x, out, workspace,
+                         static_cast<hipStream_t>(stream)),
+          "moe launch");
   return SH_OK;
 }
 

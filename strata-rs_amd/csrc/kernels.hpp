@@ -27,4 +27,30 @@ hipError_t launch_expert_gemv(uint32_t quant, const void* w, int64_t rows, int64
                               const float* x, float* y, float* workspace, int q6_signed,
                               hipStream_t stream);
 
+// Routed MoE FFN (router logits -> top-k -> gate/up -> silu*up -> down ->
+// weighted combine). A plan fixes the launch shapes and the workspace layout
+// (byte offsets into one device buffer of `bytes` bytes).
+constexpr int kMoeMaxExperts = 1024;
+constexpr int kMoeMaxTopK = 32;
+constexpr int kMoeMaxTokens = 256;
+
+struct MoePlan {
+  int n_tok, top_k, n_expert, n_embd, n_ff;
+  int s_max;                     // most unique experts a call can route to
+  int nch_a, chunk_a;            // gate/up row chunks (rows = n_embd)
+  int nch_b, chunk_b;            // down row chunks (rows = n_ff)
+  int64_t rb_a, rb_b;            // row bytes of gate/up and of down
+  size_t o_ids, o_wts, o_meta, o_slot_e, o_slot_off, o_slot_cnt, o_pair_tok, o_pair_w, o_tokpair;
+  size_t o_part_a, o_part_b;
+  size_t bytes;
+};
+
+bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t q_gateup,
+              uint32_t q_down, MoePlan* plan);
+hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, const void* gate,
+                      const void* up, const void* down, int q6g, int q6u, int q6d,
+                      const float* logits, const float* x, float* out, void* workspace,
+                      hipStream_t s);
+hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
+
 }  // namespace sh

@@ -52,7 +52,8 @@ EXPORTS = (
     "sh_abi_version", "sh_last_error", "sh_device_count", "sh_quant_geometry",
     "sh_create", "sh_destroy", "sh_name", "sh_resident_bytes", "sh_evict",
     "sh_gemv", "sh_gemv_batch", "sh_expert_gemv", "sh_dequantize_row",
-    "sh_dequant_dev", "sh_gemv_dev",
+    "sh_moe_route", "sh_moe_ffn",
+    "sh_dequant_dev", "sh_gemv_dev", "sh_moe_workspace_bytes", "sh_moe_ffn_dev",
 )
 
 
@@ -102,6 +103,10 @@ class _QuantTensorC(C.Structure):
                 ("nbytes", C.c_uint64)]
 
 
+class _ExpertDevC(C.Structure):
+    _fields_ = [("quant", C.c_uint32), ("flags", C.c_uint32), ("data", C.c_void_p)]
+
+
 class _ExpertViewC(C.Structure):
     _fields_ = [("key", C.c_uint64), ("quant", C.c_uint32), ("flags", C.c_uint32),
                 ("n_expert", C.c_uint64), ("rows", C.c_uint64), ("cols", C.c_uint64),
@@ -139,6 +144,12 @@ def load_library() -> C.CDLL:
     L.sh_gemv_batch.argtypes = [vp, C.POINTER(_QuantTensorC), f32p, f32p, u32]
     L.sh_expert_gemv.argtypes = [vp, C.POINTER(_ExpertViewC), u64, f32p, u64, f32p, u64]
     L.sh_dequantize_row.argtypes = [vp, u32, u32, vp, u64, f32p, u64]
+    L.sh_moe_route.argtypes = [vp, f32p, u32, u32, u32, vp, f32p]
+    L.sh_moe_ffn.argtypes = [vp, C.POINTER(_ExpertViewC), C.POINTER(_ExpertViewC),
+                             C.POINTER(_ExpertViewC), f32p, u32, u32, f32p, f32p]
+    L.sh_moe_workspace_bytes.argtypes = [u32, u32, u64, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
+    L.sh_moe_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC),
+                                 u64, u64, u64, vp, u32, u32, vp, vp, vp, u64, vp]
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
     _lib = L
@@ -304,6 +315,34 @@ class HipBackend:
         check(self._L.sh_expert_gemv(self._ctx, C.byref(wc), e, xv.ctypes.data, xv.size,
                                      yv.ctypes.data, yv.size))
 
+    def moe_route(self, logits, top_k: int) -> tuple[np.ndarray, np.ndarray]:
+        """MoeLayer::route from router logits (crates/strata-core/src/moe.rs:58-90):
+        ids (ascending) and renormalised weights, ``[n_tok][top_k]`` each."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        if lg.ndim == 1:
+            lg = lg[None, :]
+        n_tok, n_expert = lg.shape
+        ids = np.empty((n_tok, top_k), np.int32)
+        w = np.empty((n_tok, top_k), np.float32)
+        check(self._L.sh_moe_route(self._ctx, lg.ctypes.data, n_tok, n_expert, top_k, ids.ctypes.data,
+                                   w.ctypes.data))
+        return ids, w
+
+    def moe_ffn(self, gate: ExpertView, up: ExpertView, down: ExpertView, logits, x,
+                top_k: int) -> np.ndarray:
+        """Routed MoE FFN (moe.rs:108-127) for ``x [n_tok][n_embd]`` from router
+        ``logits [n_tok][n_expert]``; returns ``[n_tok][n_embd]``."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        xv = np.ascontiguousarray(x, dtype=np.float32)
+        if xv.ndim == 1:
+            xv, lg = xv[None, :], lg.reshape(1, -1)
+        n_tok = xv.shape[0]
+        out = np.empty_like(xv)
+        g, u, d = gate._c(), up._c(), down._c()
+        check(self._L.sh_moe_ffn(self._ctx, C.byref(g), C.byref(u), C.byref(d), lg.ctypes.data, n_tok,
+                                 top_k, xv.ctypes.data, out.ctypes.data))
+        return out
+
     def dequantize_row(self, quant: int, block, out: np.ndarray, flags: int = 0) -> None:
         """dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device."""
         b = _bytes(block)
@@ -323,3 +362,21 @@ def gemv_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, y_ptr: in
              stream: int = 0, flags: int = 0) -> None:
     check(load_library().sh_gemv_dev(int(quant), flags, w_ptr, rows, cols, x_ptr, y_ptr, batch,
                                      stream or None))
+
+
+def moe_workspace_bytes(n_tok: int, top_k: int, n_expert: int, n_embd: int, n_ff: int,
+                        quant_gate_up: int, quant_down: int) -> int:
+    v = C.c_uint64()
+    check(load_library().sh_moe_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, int(quant_gate_up),
+                                                int(quant_down), C.byref(v)))
+    return v.value
+
+
+def moe_ffn_dev(gate: tuple, up: tuple, down: tuple, n_expert: int, n_embd: int, n_ff: int,
+                logits_ptr: int, n_tok: int, top_k: int, x_ptr: int, out_ptr: int, ws_ptr: int,
+                ws_bytes: int, stream: int = 0) -> None:
+    """gate/up/down: (quant, flags, device pointer)."""
+    g, u, d = (_ExpertDevC(int(q), f, p) for q, f, p in (gate, up, down))
+    check(load_library().sh_moe_ffn_dev(C.byref(g), C.byref(u), C.byref(d), n_expert, n_embd, n_ff,
+                                        logits_ptr, n_tok, top_k, x_ptr, out_ptr, ws_ptr, ws_bytes,
+                                        stream or None))

@@ -1,0 +1,128 @@
+"""Routed MoE FFN on the device vs the oracle (crates/strata-core/src/moe.rs).
+
+Routing: ids must equal the oracle's (softmax, stable top-k, ascending ids)
+and weights agree to f32 rounding (the device exp differs from glibc's by at
+most an ulp). The FFN output is checked with max|out - ref| / max|ref| <=
+1e-3 at the MoE config's shapes (128 experts, top-8, hidden 2048, expert
+intermediate 768; gate/up Q4_K, down Q6_K) for 1 and 16 tokens, and on a
+small Q8_0 / signed-scale variant.
+"""
+import numpy as np
+import pytest
+
+import strata_hip as H
+from conftest import elem_rel_err, rel_err
+from strata_hip import synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.mark.parametrize("n_tok,n_expert,top_k", [(1, 128, 8), (16, 128, 8), (5, 64, 4), (3, 8, 8),
+                                                  (2, 1000, 32)])
+def test_route_matches_oracle(backend, oracle, n_tok, n_expert, top_k):
+    say("route", n_tok, n_expert, top_k)
+    logits = S.router_logits(100 + n_tok + n_expert, n_tok, n_expert)
+    ids, w = backend.moe_route(logits, top_k)
+    for t in range(n_tok):
+        oid, ow = oracle.moe_route(logits[t], top_k)
+        assert ids[t].tolist() == oid.tolist()
+        assert np.abs(w[t] - ow).max() <= 4e-7
+        assert abs(float(w[t].astype(np.float64).sum()) - 1.0) < 1e-5
+
+
+def test_route_ties_and_uniform(backend, oracle):
+    say("route ties")
+    lg = np.zeros((2, 16), np.float32)
+    lg[0, [3, 9, 12]] = 1.0
+    ids, w = backend.moe_route(lg, 5)
+    assert ids[0].tolist() == [0, 1, 3, 9, 12]
+    assert ids[1].tolist() == [0, 1, 2, 3, 4]
+    assert np.all(w[1] == np.float32(0.2))
+
+
+def expert_tensors(n_expert, n_embd, n_ff, qg, qd, seed):
+    gate = S.matrix(qg, seed, n_expert * n_embd, n_ff)
+    up = S.matrix(qg, seed + 1, n_expert * n_embd, n_ff)
+    down = S.matrix(qd, seed + 2, n_expert * n_ff, n_embd)
+    return gate, up, down
+
+
+def oracle_moe(oracle, qg, qd, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k, q6_signed=False):
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        ids, w = oracle.moe_route(logits[t], top_k)
+        out[t] = oracle.moe_routed(qg, qg, qd, n_expert, n_embd, n_ff, gate, up, down, ids, w, x[t])
+    return out
+
+
+@pytest.fixture(scope="module")
+def moe_config_tensors():
+    # 128 experts, hidden 2048, expert intermediate 768 (about 26 s to synthesise)
+    return expert_tensors(128, 2048, 768, 12, 14, 4000)
+
+
+@pytest.mark.parametrize("n_tok", [1, 16])
+def test_moe_ffn_config_shapes(backend, oracle, moe_config_tensors, n_tok):
+    n_expert, n_embd, n_ff, top_k = 128, 2048, 768, 8
+    say("moe ffn", n_tok, "tokens", n_expert, n_embd, n_ff)
+    gate, up, down = moe_config_tensors
+    logits = S.router_logits(4100 + n_tok, n_tok, n_expert)
+    x = S.normal_f32(4200 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    g = H.ExpertView("blk.0.ffn_gate_exps.weight", 12, n_expert, n_embd, n_ff, gate)
+    u = H.ExpertView("blk.0.ffn_up_exps.weight", 12, n_expert, n_embd, n_ff, up)
+    d = H.ExpertView("blk.0.ffn_down_exps.weight", 14, n_expert, n_ff, n_embd, down)
+    out = backend.moe_ffn(g, u, d, logits, x, top_k)
+    ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    for t in range(n_tok):
+        assert rel_err(out[t], ref[t]) <= 1e-3, (t, rel_err(out[t], ref[t]))
+        assert elem_rel_err(out[t], ref[t], floor=1.0) <= 1e-3
+
+
+def test_moe_ffn_q8_gate_up_small(backend, oracle):
+    n_expert, n_embd, n_ff, top_k, n_tok = 16, 256, 128, 4, 6
+    say("moe ffn q8 small")
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 8, 14, 5000)
+    logits = S.router_logits(5100, n_tok, n_expert)
+    x = S.normal_f32(5200, n_tok * n_embd).reshape(n_tok, n_embd)
+    out = backend.moe_ffn(H.ExpertView("g8", 8, n_expert, n_embd, n_ff, gate),
+                          H.ExpertView("u8", 8, n_expert, n_embd, n_ff, up),
+                          H.ExpertView("d8", 14, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    ref = oracle_moe(oracle, 8, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    assert rel_err(out, ref) <= 1e-3
+
+
+def test_moe_ffn_dev_matches_host_path(backend):
+    import torch
+    n_expert, n_embd, n_ff, top_k, n_tok = 32, 512, 256, 8, 4
+    say("moe ffn dev")
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 6000)
+    logits = S.router_logits(6100, n_tok, n_expert)
+    x = S.normal_f32(6200, n_tok * n_embd).reshape(n_tok, n_embd)
+    host = backend.moe_ffn(H.ExpertView("gd", 12, n_expert, n_embd, n_ff, gate),
+                           H.ExpertView("ud", 12, n_expert, n_embd, n_ff, up),
+                           H.ExpertView("dd", 14, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    dev = torch.device("cuda:0")
+    tg, tu, td = (torch.from_numpy(a).to(dev) for a in (gate, up, down))
+    tl, tx = torch.from_numpy(logits).to(dev), torch.from_numpy(x).to(dev)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+    nb = H.moe_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, 12, 14)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    H.moe_ffn_dev((12, 0, tg.data_ptr()), (12, 0, tu.data_ptr()), (14, 0, td.data_ptr()), n_expert, n_embd,
+                  n_ff, tl.data_ptr(), n_tok, top_k, tx.data_ptr(), out.data_ptr(), ws.data_ptr(), nb,
+                  torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), host)
+
+
+def test_moe_errors(backend):
+    say("moe errors")
+    g = H.ExpertView("eg", 12, 4, 256, 256, S.matrix(12, 1, 4 * 256, 256))
+    d_bad = H.ExpertView("ed", 14, 4, 256, 512, S.matrix(14, 1, 4 * 256, 512))
+    with pytest.raises(H.ShapeError):
+        backend.moe_ffn(g, g, d_bad, np.zeros((1, 4), np.float32), np.zeros((1, 256), np.float32), 2)
+    with pytest.raises(H.BackendError):
+        backend.moe_route(np.zeros((1, 4), np.float32), 5)  # top_k > n_expert
