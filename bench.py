@@ -19,7 +19,12 @@ Prints ONE JSON line (rank 0):
                  single thread, sequential f64) timed on this host on a
                  bounded sample of the same workload
   extra          the other decode shapes (Q4_K 12288x4096 batch 1 and 8, Q8_0
-                 4096x4096, Q6_K 151936x4096) measured the same way
+                 4096x4096, Q6_K 151936x4096) measured the same way; the routed
+                 MoE FFN (128 experts, hidden 2048, expert FFN 768, top-8; 1 and
+                 16 tokens, routing varied per call, 3 copies of the expert
+                 set rotated); the prefill matmul (Q4_K 12288x4096 times 512
+                 tokens, bf16 and Q8 activation modes, activation pre-pass
+                 included)
 """
 from __future__ import annotations
 
@@ -93,6 +98,119 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
     del g, copies, base
     torch.cuda.empty_cache()
     return ms, n_copies, reps * n_copies
+
+
+def time_calls(torch, calls, steps, warmup):
+    """Mean ms per call of a list of enqueue functions f(stream_handle),
+    captured once in a HIP graph and replayed; calls are cycled in order."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for f in calls:
+            f(stream.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for f in calls:
+            f(torch.cuda.current_stream().cuda_stream)
+    n = len(calls)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, -(-warmup // n))):
+            g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, -(-steps // n))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (reps * n)
+    del g
+    return ms
+
+
+def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):
+    """Prefill matmul W[rows][cols] (Q4_K) x X[m][cols] -> Y[m][rows], both
+    activation modes; TFLOP/s of 2 * m * rows * cols per call."""
+    dev = torch.device("cuda:0")
+    w = torch.from_numpy(w_host).to(dev)
+    x = torch.from_numpy(S.normal_f32(0x5EED0006, m * cols)).to(dev)
+    y = torch.empty(m * rows, dtype=torch.float32, device=dev)
+    res = {}
+    flops = 2.0 * m * rows * cols
+    for mode, name, peak in ((H.MATMUL_BF16, "bf16", 2500.0), (H.MATMUL_Q8, "q8_int8", 5000.0)):
+        nb = H.matmul_workspace_bytes(S.Q4_K, rows, cols, m, mode)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        call = (lambda st, mode=mode, ws=ws, nb=nb:
+                H.matmul_dev(S.Q4_K, w.data_ptr(), rows, cols, x.data_ptr(), m, y.data_ptr(), mode,
+                             ws.data_ptr(), nb, st))
+        ms = time_calls(torch, [call], steps, 3)
+        tf = flops / (ms * 1e-3) / 1e12
+        res[f"prefill_q4k_12288x4096_m{m}_{name}"] = {
+            "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+            "peak_TFLOPs": peak, "frac_of_peak": round(tf / peak, 4)}
+        del ws
+    del w, x, y
+    return res
+
+
+def bench_moe(torch, H, S, steps):
+    """Routed MoE FFN at 128 experts, hidden 2048, expert FFN 768, top-8:
+    gate/up Q4_K, down Q6_K; GB/s of the packed bytes of the experts each
+    call routes to (each unique expert read once)."""
+    import numpy as np
+    E, n_embd, n_ff, top_k = 128, 2048, 768, 8
+    gate = S.matrix(S.Q4_K, 0x5EED0041, E * n_embd, n_ff)
+    up = S.matrix(S.Q4_K, 0x5EED0042, E * n_embd, n_ff)
+    down = S.matrix(S.Q6_K, 0x5EED0043, E * n_ff, n_embd)
+    per_expert = (gate.nbytes + up.nbytes + down.nbytes) // E
+    dev = torch.device("cuda:0")
+    sets = []
+    for k in range(3):  # 3 x 391 MB: more than the Infinity Cache holds
+        tg, tu, td = (torch.from_numpy(a).to(dev) for a in (gate, up, down))
+        sets.append((tg, tu, td))
+    del gate, up, down
+    res = {}
+    for n_tok in (1, 16):
+        variants = 8
+        logits = [S.router_logits(0x5EED0044 + 97 * v + n_tok, n_tok, E) for v in range(variants)]
+        uniq = []
+        for lg in logits:
+            # softmax preserves the order of the logits: the top-k ids are the
+            # k largest logits (ties to the lower id)
+            ids = set()
+            for t in range(n_tok):
+                ids.update(np.argsort(-lg[t], kind="stable")[:top_k].tolist())
+            uniq.append(len(ids))
+        tl = [torch.from_numpy(lg).to(dev) for lg in logits]
+        x = torch.from_numpy(S.normal_f32(0x5EED0045 + n_tok, n_tok * n_embd)).to(dev)
+        out = torch.empty(n_tok * n_embd, dtype=torch.float32, device=dev)
+        nb = H.moe_workspace_bytes(n_tok, top_k, E, n_embd, n_ff, S.Q4_K, S.Q6_K)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        calls = []
+        byts = 0
+        for v in range(variants * len(sets)):
+            tg, tu, td = sets[v % len(sets)]
+            lgv = tl[v % variants]
+            byts += uniq[v % variants] * per_expert
+            calls.append(lambda st, tg=tg, tu=tu, td=td, lgv=lgv:
+                         H.moe_ffn_dev((S.Q4_K, 0, tg.data_ptr()), (S.Q4_K, 0, tu.data_ptr()),
+                                       (S.Q6_K, 0, td.data_ptr()), E, n_embd, n_ff, lgv.data_ptr(), n_tok,
+                                       top_k, x.data_ptr(), out.data_ptr(), ws.data_ptr(), nb, st))
+        ms = time_calls(torch, calls, steps, len(calls))
+        mean_bytes = byts / len(calls)
+        res[f"moe_128x2048x768_top8_{n_tok}tok"] = {
+            "us_per_call": round(ms * 1e3, 2), "mean_unique_experts": round(sum(uniq) / variants, 2),
+            "expert_bytes_GBps": round(mean_bytes / (ms * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(100 * mean_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+        del ws, tl, x, out
+    del sets
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(w, x, rows, cols, seconds):
@@ -197,6 +315,7 @@ def main():
                   ("q4k_gate_12288x4096_b8", S.Q4_K, 12288, 4096, 8),
                   ("q8_0_4096x4096_b1", S.Q8_0, 4096, 4096, 1),
                   ("q6k_lm_head_151936x4096_b1", S.Q6_K, 151936, 4096, 1)]
+        prefill_w = None
         for name, q, r, c, b in shapes:
             wm = S.matrix(q, 0x5EED0000 + q + r, r, c)
             print(f"[bench] extra {name}", file=sys.stderr, flush=True)
@@ -205,7 +324,14 @@ def main():
             extra[name] = {"us_per_launch": round(t * 1e3, 3),
                            "weight_GBps": round(wm.nbytes / (t * 1e-3) / 1e9, 1),
                            "pct_hbm_peak": round(100 * wm.nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            if name == "q4k_gate_12288x4096_b1":
+                prefill_w = wm
             del wm
+        print("[bench] extra prefill matmul", file=sys.stderr, flush=True)
+        extra.update(bench_prefill(torch, H, S, prefill_w, 12288, 4096, 512, 50))
+        del prefill_w
+        print("[bench] extra moe", file=sys.stderr, flush=True)
+        extra.update(bench_moe(torch, H, S, 240))
         out["extra"] = extra
 
     if not args.no_cpu:

@@ -162,7 +162,38 @@ int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view
                const sh_expert_view* down, const float* logits, uint32_t n_tok, uint32_t top_k,
                const float* x, float* out);
 
+/* Batched prefill matmul: y[t][r] = sum_c W[r][c] * x[t][c] for t < m, x
+ * [m][cols] and y [m][rows] row-major f32. The reference has no matmul
+ * (prefill is one forward per token, crates/strata-core/src/generate.rs:
+ * 116-117); the result equals m calls of ops::gemv (ops.rs:14-28) up to the
+ * activation rounding of `mode`:
+ *   SH_MATMUL_BF16  x rounded to bf16, weights dequantized to bf16, f32
+ *                   accumulation (Q8_0, Q4_K, Q6_K);
+ *   SH_MATMUL_Q8    x quantized to 32-element blocks (scale max|x| / 127,
+ *                   int8 codes rounded to nearest even), int8 products
+ *                   (Q8_0, Q4_K).
+ * cols must be a multiple of 64. */
+int sh_matmul(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint32_t m, float* y,
+              uint32_t mode);
+
 /* ---- device-pointer variants (asynchronous on `stream`) ---------------- */
+
+/* Bytes of device workspace sh_matmul_dev needs. */
+int sh_matmul_workspace_bytes(uint32_t quant, uint64_t rows, uint64_t cols, uint32_t m, uint32_t mode,
+                              uint64_t* bytes);
+
+/* sh_matmul on device pointers: w (4-byte aligned), x [m][cols], y
+ * [m][rows], workspace at least sh_matmul_workspace_bytes() long and
+ * 256-byte aligned. Calls sharing one workspace must not overlap in time. */
+int sh_matmul_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                  const float* x, uint32_t m, float* y, uint32_t mode, void* workspace,
+                  uint64_t workspace_bytes, void* stream);
+
+/* The activation quantization of SH_MATMUL_Q8 on its own: n f32 (n a
+ * multiple of 32, x 16-byte aligned) -> n int8 codes, n / 32 scales
+ * (max|x| / 127 per block) and n / 32 values scale * sum(codes). */
+int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales, float* code_sums,
+                       void* stream);
 
 /* One expert tensor already in device memory. */
 typedef struct sh_expert_dev {

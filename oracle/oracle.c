@@ -484,3 +484,39 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
   free(d);
   return rc;
 }
+
+int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+               size_t nbytes, const float* x, int64_t m, float* y, int n_threads) {
+  if (m < 0) return SHO_UNSUPPORTED;
+  for (int64_t t = 0; t < m; ++t) {
+    int rc = n_threads > 1
+                 ? sho_gemv_threads(quant, rows, cols, data, nbytes, x + t * cols,
+                                    y + t * rows, n_threads)
+                 : sho_gemv(quant, rows, cols, data, nbytes, x + t * cols, y + t * rows);
+    if (rc != SHO_OK) return rc;
+  }
+  return SHO_OK;
+}
+
+int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,
+                    float* sums) {
+  if (n % 32 != 0) return SHO_TRUNCATED;
+  for (size_t b = 0; b < n / 32; ++b) {
+    const float* v = x + 32 * b;
+    float amax = 0.0f;
+    for (int k = 0; k < 32; ++k) {
+      const float a = fabsf(v[k]);
+      if (a > amax) amax = a;
+    }
+    const float s = amax / 127.0f;
+    int sum = 0;
+    for (int k = 0; k < 32; ++k) {
+      const int c = s > 0.0f ? (int)rintf(v[k] / s) : 0;
+      q[32 * b + k] = (int8_t)c;
+      sum += c;
+    }
+    scales[b] = s;
+    sums[b] = s * (float)sum;
+  }
+  return SHO_OK;
+}

@@ -11,6 +11,11 @@
  *   - gemv / expert_gemv      crates/strata-core/src/ops.rs:14-28,169-195
  *   - silu                    crates/strata-core/src/ops.rs:85-87
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
+ *   - prefill matmul          no reference op: m independent ops::gemv calls
+ *                             (crates/strata-core/src/generate.rs:116-117)
+ *   - Q8 activation blocks    the quantization the int8 prefill mode applies
+ *                             to activations (32 elements, scale max|x|/127,
+ *                             codes rounded to nearest even)
  * Compiled with -ffp-contract=off and no fast-math so every f32 product and
  * difference rounds exactly as the Rust source (which never fuses), and the
  * f64 dot products are summed in the same sequential order.
@@ -84,6 +89,17 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
                    size_t up_bytes, const uint8_t* down, size_t down_bytes,
                    const int64_t* ids, const float* weights, int64_t k,
                    const float* x, float* out);
+
+/* y[t][r] = gemv(W, x[t]) for t < m: m independent sho_gemv calls, each
+ * row-parallel over n_threads (bit-identical to the sequential loop). */
+int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+               size_t nbytes, const float* x, int64_t m, float* y, int n_threads);
+
+/* Activation blocks of 32 (n % 32 == 0): s = max|x| / 127 (f32 division),
+ * q = rint(x / s) (round to nearest even; 0 when s == 0), sums[b] =
+ * s * (float)sum(q). */
+int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,
+                    float* sums);
 
 #ifdef __cplusplus
 }

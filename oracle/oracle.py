@@ -59,6 +59,9 @@ def lib() -> C.CDLL:
         L.sho_moe_routed.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
                                      C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
                                      i64p, f32p, C.c_int64, f32p, f32p]
+        L.sho_matmul.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, C.c_int64, f32p,
+                                 C.c_int]
+        L.sho_quantize_q8.argtypes = [f32p, C.c_size_t, u8p, f32p, f32p]
         _lib = L
     return _lib
 
@@ -182,3 +185,37 @@ def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, 
                                 _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
                                 _ptr(xv), _ptr(out)), "moe_routed")
     return out
+
+
+def matmul(quant: int, rows: int, cols: int, data, x, threads: int = 1) -> np.ndarray:
+    """y[t] = gemv(W, x[t]) for every row t of x ([m][cols] -> [m][rows])."""
+    b, xv = _u8(data), _f32(x)
+    m = xv.size // cols
+    assert xv.size == m * cols
+    y = np.empty((m, rows), dtype=np.float32)
+    _check(lib().sho_matmul(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), m, _ptr(y), threads), "matmul")
+    return y
+
+
+def quantize_q8(x) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(codes int8 [n], scales f32 [n/32], scale * code sums f32 [n/32])."""
+    xv = _f32(x).reshape(-1)
+    q = np.empty(xv.size, dtype=np.int8)
+    s = np.empty(xv.size // 32, dtype=np.float32)
+    u = np.empty(xv.size // 32, dtype=np.float32)
+    _check(lib().sho_quantize_q8(_ptr(xv), xv.size, _ptr(q), _ptr(s), _ptr(u)), "quantize_q8")
+    return q, s, u
+
+
+def dequantize_q8_activations(x) -> np.ndarray:
+    """x rounded through Q8 blocks: scale * code per element (f32 product)."""
+    xv = _f32(x)
+    q, s, _ = quantize_q8(xv)
+    return (np.repeat(s, 32) * q.astype(np.float32)).astype(np.float32).reshape(xv.shape)
+
+
+def bf16_round_array(a) -> np.ndarray:
+    """Round f32 to bf16 (nearest even) and back, elementwise (matches sho_bf16_round for finite values)."""
+    u = _f32(a).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return r.view(np.float32).reshape(np.shape(a))

@@ -492,6 +492,52 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
   return SH_OK;
 }
 
+static int matmul_check(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t m, uint32_t mode) {
+  if (mode > SH_MATMUL_Q8) return fail(SH_ERR_INVALID_ARGUMENT, "matmul mode %u", mode);
+  if (!sh::device_quant(quant))
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: type %u has no device kernel", quant);
+  if (mode == SH_MATMUL_Q8 && quant == SH_QUANT_Q6_K)
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: Q6_K weights take SH_MATMUL_BF16 only");
+  if (!sh::matmul_shape_ok(quant, int64_t(rows), int64_t(cols), int64_t(m), mode))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "matmul %llux%llu (m %llu) of type %u is not supported",
+                (unsigned long long)rows, (unsigned long long)cols, (unsigned long long)m, quant);
+  return SH_OK;
+}
+
+int sh_matmul(sh_context* c, const sh_quant_tensor* w, const float* x, uint32_t m, float* y, uint32_t mode) {
+  if (!c || !w || (!x && m) || (!y && m)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes);
+  if (rc) return rc;
+  const uint64_t rows = w->rows, cols = w->cols;
+  if (m == 0 || rows == 0) return SH_OK;
+  if (cols == 0) {
+    memset(y, 0, sizeof(float) * rows * m);
+    return SH_OK;
+  }
+  if ((rc = matmul_check(w->quant, rows, cols, m, mode))) return rc;
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident* r = nullptr;
+  const uint64_t need = rows * uint64_t(sh::byte_size(w->quant, int64_t(cols)));
+  if ((rc = resident(c, w->key, w->quant, 1, rows, cols, w->data, need, &r))) return rc;
+  const size_t xb = sizeof(float) * cols * m, yb = sizeof(float) * rows * m;
+  const size_t ws = sh::matmul_workspace_bytes(int64_t(cols), int64_t(m), mode);
+  if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(yb, "y buffer")) ||
+      (rc = c->d_blk.ensure(ws, "workspace")) || (rc = c->h_in.ensure(xb, "x staging")) ||
+      (rc = c->h_out.ensure(yb, "y staging")))
+    return rc;
+  memcpy(c->h_in.p, x, xb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
+  HIP_TRY(sh::launch_matmul(w->quant, r->dev, int64_t(rows), int64_t(cols),
+                            static_cast<const float*>(c->d_in.p), int64_t(m), static_cast<float*>(c->d_out.p),
+                            mode, c->d_blk.p, (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+          "matmul launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "matmul");
+  memcpy(y, c->h_out.p, yb);
+  return SH_OK;
+}
+
 int sh_dequantize_row(sh_context* c, uint32_t quant, uint32_t flags, const uint8_t* block,
                       uint64_t nbytes, float* out, uint64_t n) {
   if (!c || (!block && nbytes) || (!out && n)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
@@ -594,3 +640,44 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
 }
 
 }  // extern "C"
+
+int sh_matmul_workspace_bytes(uint32_t quant, uint64_t rows, uint64_t cols, uint32_t m, uint32_t mode,
+                              uint64_t* bytes) {
+  if (!bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null bytes");
+  int rc = matmul_check(quant, rows, cols, m, mode);
+  if (rc) return rc;
+  *bytes = sh::matmul_workspace_bytes(int64_t(cols), int64_t(m), mode);
+  return SH_OK;
+}
+
+int sh_matmul_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
+                  const float* x, uint32_t m, float* y, uint32_t mode, void* workspace,
+                  uint64_t workspace_bytes, void* stream) {
+  if (!w || !x || !y || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  int rc = matmul_check(quant, rows, cols, m, mode);
+  if (rc) return rc;
+  const uint64_t need = sh::matmul_workspace_bytes(int64_t(cols), int64_t(m), mode);
+  if (workspace_bytes < need)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed",
+                (unsigned long long)workspace_bytes, (unsigned long long)need);
+  if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(x) & 15u) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 4 bytes, x 16, workspace 256)");
+  HIP_TRY(sh::launch_matmul(quant, w, int64_t(rows), int64_t(cols), x, int64_t(m), y, mode, workspace,
+                            (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
+          "matmul launch");
+  return SH_OK;
+}
+
+int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales, float* code_sums,
+                       void* stream) {
+  if (!x || !codes || !scales || !code_sums) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if (n == 0 || n % 32 != 0 || n > (uint64_t(1) << 40))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "quantize: %llu values (a positive multiple of 32 needed)",
+                (unsigned long long)n);
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(codes) & 15u))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (x and codes need 16 bytes)");
+  HIP_TRY(sh::launch_quantize_q8(x, int64_t(n), codes, scales, code_sums, static_cast<hipStream_t>(stream)),
+          "quantize launch");
+  return SH_OK;
+}

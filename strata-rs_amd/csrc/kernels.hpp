@@ -53,4 +53,17 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       hipStream_t s);
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
 
+// Prefill matmul Y[t][r] = sum_c W[r][c] X[t][c], t < m. mode 0: bf16
+// activations on bf16 MFMA; mode 1: Q8-quantized activations on int8 MFMA
+// (Q4_K and Q8_0 weights). `workspace` holds matmul_workspace_bytes().
+bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint32_t mode);
+size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode);
+hipError_t launch_matmul(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
+                         int64_t m, float* y, uint32_t mode, void* workspace, int q6_signed,
+                         hipStream_t stream);
+// Activation quantization of the int8 mode: n f32 (n % 32 == 0) -> int8
+// codes, per-32 scales and per-32 scale * sum of codes.
+hipError_t launch_quantize_q8(const float* x, int64_t n, int8_t* q, float* scales, float* usum,
+                              hipStream_t stream);
+
 }  // namespace sh

@@ -1,0 +1,686 @@
+// Batched prefill matmul on MFMA: Y[t][r] = sum_c W[r][c] * X[t][c] for m
+// tokens, W packed Q4_K / Q8_0 / Q6_K [rows][cols], X and Y f32 row-major.
+//
+// The reference has no matmul: prefill runs one forward per token
+// (crates/strata-core/src/generate.rs:116-117), so the op is defined as m
+// independent ops::gemv calls (crates/strata-core/src/ops.rs:14-28).
+//
+// Two modes:
+//   bf16  X is rounded to bf16; each workgroup dequantizes its weight rows
+//         chunk by chunk into a bf16 LDS tile and runs
+//         v_mfma_f32_32x32x16_bf16 with f32 accumulation.
+//   q8    X is quantized to Q8 blocks (32 elements, f32 scale max|x| / 127,
+//         int8 codes rounded to nearest even); the weight codes go to LDS as
+//         int8 and v_mfma_i32_32x32x32_i8 computes one exact integer dot per
+//         32-element block, which the VALU scales by the weight block's scale
+//         and the activation block's scale (and subtracts the Q4_K min term).
+//
+// Workgroup tile: 256 tokens x 96 weight rows, 4 waves stacked along the
+// tokens (wave w owns tokens [64w, 64w + 64) and all 96 rows: 2 x 3 MFMA
+// tiles of 32 x 32). Activations are private to a wave, so each wave loads
+// its A fragments straight from global memory (L2-resident) into registers;
+// only the weight tile, shared by the 4 waves, goes through LDS (double
+// buffered, one barrier per 64-element chunk of K). The MFMA's k order is
+// free as long as A and B agree, so lane half h of k-step s holds chunk
+// elements [32h + 8s, +8) (bf16) or [32s + 16h, +16) (int8) of both operands,
+// which keeps every fragment one 16-byte load. Tiles are numbered so that the
+// 8 XCDs (workgroup i runs on XCD i % 8) each get a contiguous run of weight
+// rows, and the token tiles of one weight tile share that XCD's L2.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace sh {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMmBM = 256;                  // tokens per workgroup
+constexpr int kMmBN = 96;                   // weight rows per workgroup
+constexpr int kMmKC = 64;                   // K elements per chunk
+constexpr int kMmThreads = 256;
+constexpr int kMmRowB = kMmKC * 2 + 16;     // bytes per bf16 LDS row (padded)
+constexpr int kMmRowQ = kMmKC + 16;         // bytes per int8 LDS row (padded)
+
+// Two floats -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  const bf16x2 v = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ------------------------------------------------------------ weight stagers --
+// A stager turns one row's 64-element chunk c of packed blocks into values
+// for the LDS tile. The chunk is split into kPieces pieces per row, each a
+// thread's task: `load` issues the global loads (so they can be in flight a
+// chunk ahead), `emit_bf16` writes two runs of 16 bf16 at chunk offsets
+// o0 and o1, `emit_q8` writes the same runs as int8 codes plus the block
+// scale (and min) for the int8 path.
+
+// Q4_K: chunk c is group g = c % 4 of super-block c / 4; piece hb holds qs
+// bytes [16hb, 16hb + 16) of the group, whose low nibbles are elements
+// [16hb, +16) (sub-block 2g) and high nibbles [32 + 16hb, +16) (sub-block
+// 2g + 1). dequant.rs:247-270 and get_scale_min_k4 (dequant.rs:237-245).
+struct StQ4K {
+  static constexpr int kPieces = 2;
+  static constexpr bool kQ8 = true;
+  static constexpr bool kMin = true;  // value d * q - m
+  struct Raw {
+    u32x4 h, q;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int c, int hb) {
+    const uint8_t* sb = row + (c >> 2) * 144;
+    return {ld16(sb), ld16(sb + 16 + 32 * (c & 3) + 16 * hb)};
+  }
+  // d * sc and dmin * m of sub-blocks 2g and 2g + 1
+  __device__ static __forceinline__ void scales(const u32x4& h, int g, float& d0, float& m0, float& d1,
+                                                float& m1) {
+    const uint32_t s = (g & 1) << 4;
+    const uint32_t t1 = h.y >> s, t2 = h.z >> s, t3 = h.w >> s;
+    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+    const float d = h2f(h.x), dm = h2f(h.x >> 16);
+    d0 = d * ubyte<0>(scp);
+    d1 = d * ubyte<1>(scp);
+    m0 = dm * ubyte<0>(mp);
+    m1 = dm * ubyte<1>(mp);
+  }
+  __device__ static __forceinline__ void emit_bf16(const Raw& r, int c, int hb, uint32_t* run0,
+                                                   uint32_t* run1, int& o0, int& o1, int) {
+    float d0, m0, d1, m1;
+    scales(r.h, c & 3, d0, m0, d1, m1);
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+      run0[2 * k] = pack_bf16(__builtin_fmaf(d0, ubyte<0>(lo), -m0), __builtin_fmaf(d0, ubyte<1>(lo), -m0));
+      run0[2 * k + 1] =
+          pack_bf16(__builtin_fmaf(d0, ubyte<2>(lo), -m0), __builtin_fmaf(d0, ubyte<3>(lo), -m0));
+      run1[2 * k] = pack_bf16(__builtin_fmaf(d1, ubyte<0>(hi), -m1), __builtin_fmaf(d1, ubyte<1>(hi), -m1));
+      run1[2 * k + 1] =
+          pack_bf16(__builtin_fmaf(d1, ubyte<2>(hi), -m1), __builtin_fmaf(d1, ubyte<3>(hi), -m1));
+    }
+    o0 = 16 * hb;
+    o1 = 32 + 16 * hb;
+  }
+  // int8 codes 0..15; run k lies in block jb_k of the chunk, whose values
+  // are dj[k] * q - mj[k]
+  __device__ static __forceinline__ void emit_q8(const Raw& r, int c, int hb, uint32_t* run0,
+                                                 uint32_t* run1, int& o0, int& o1, int& jb0, int& jb1,
+                                                 float* dj, float* mj) {
+    scales(r.h, c & 3, dj[0], mj[0], dj[1], mj[1]);
+    jb0 = 0;
+    jb1 = 1;
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      run0[k] = q[k] & 0x0F0F0F0Fu;
+      run1[k] = (q[k] >> 4) & 0x0F0F0F0Fu;
+    }
+    o0 = 16 * hb;
+    o1 = 32 + 16 * hb;
+  }
+};
+
+// Q8_0: chunk c is blocks 2c and 2c + 1 (68 bytes from 68c, 4-byte aligned);
+// piece hb is block hb, read through the aligned 36-byte window at
+// 68c + 32hb. dequant.rs:123-128: value = q * d (exact in f32).
+struct StQ8 {
+  static constexpr int kPieces = 2;
+  static constexpr bool kQ8 = true;
+  static constexpr bool kMin = false;  // value d * q
+  struct Raw {
+    u32x4 a, b;
+    uint32_t e;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int c, int hb) {
+    const uint8_t* p = row + 68 * c + 32 * hb;
+    return {ld16(p), ld16(p + 16), ld4(p + 32)};
+  }
+  __device__ static __forceinline__ void codes(const Raw& r, int hb, uint32_t* q, float& d) {
+    const uint32_t w[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.e};
+    d = h2f(hb ? (w[0] >> 16) : w[0]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = hb ? w[k + 1] : realign(w[k], w[k + 1], 2);
+  }
+  __device__ static __forceinline__ void emit_bf16(const Raw& r, int, int hb, uint32_t* run0,
+                                                   uint32_t* run1, int& o0, int& o1, int) {
+    uint32_t q[8];
+    float d;
+    codes(r, hb, q, d);
+    const float bias = -128.f * d;  // (q ^ 0x80) - 128 = q: d * q exactly
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t u = q[k] ^ 0x80808080u;
+      uint32_t* dst = k < 4 ? run0 + 2 * k : run1 + 2 * (k - 4);
+      dst[0] = pack_bf16(__builtin_fmaf(d, ubyte<0>(u), bias), __builtin_fmaf(d, ubyte<1>(u), bias));
+      dst[1] = pack_bf16(__builtin_fmaf(d, ubyte<2>(u), bias), __builtin_fmaf(d, ubyte<3>(u), bias));
+    }
+    o0 = 32 * hb;
+    o1 = 32 * hb + 16;
+  }
+  __device__ static __forceinline__ void emit_q8(const Raw& r, int, int hb, uint32_t* run0,
+                                                 uint32_t* run1, int& o0, int& o1, int& jb0, int& jb1,
+                                                 float* dj, float* mj) {
+    uint32_t q[8];
+    float d;
+    codes(r, hb, q, d);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      run0[k] = q[k];
+      run1[k] = q[k + 4];
+    }
+    // both runs are block hb
+    jb0 = jb1 = hb;
+    dj[0] = dj[1] = d;
+    mj[0] = mj[1] = 0.f;
+    o0 = 32 * hb;
+    o1 = 32 * hb + 16;
+  }
+};
+
+// Q6_K: chunk c is quarter j = c % 4 of super-block c / 4 (half h = j / 2,
+// nibble tp = j % 2); piece hb holds elements [16hb, +16) and
+// [32 + 16hb, +16) of the quarter. dequant.rs:208-234: value
+// d * sc * (q - 32) with q = (ql nibble) | (qh 2 bits << 4); sc read as u8
+// (dequant.rs:211,224-227) or, with the signed-scale flag, as i8.
+struct StQ6K {
+  static constexpr int kPieces = 2;
+  static constexpr bool kQ8 = false;  // 16-element scales do not fit 32-element int8 blocks
+  struct Raw {
+    u32x4 l0, l1, qh;
+    uint32_t l0e, l1e, qhe, s0, s1;
+    uint32_t d;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int c, int hb) {
+    const uint8_t* blk = row + (c >> 2) * 210;
+    const int j = c & 3, h = j >> 1, tp = j & 1;
+    const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    const uint8_t* base = blk - s;  // rows are 2-byte aligned: s is 0 or 2
+    const uint8_t* p0 = base + 64 * h + 16 * hb;
+    const uint8_t* p1 = p0 + 32;
+    const uint8_t* ph = base + 128 + 32 * h + 16 * hb;
+    const uint8_t* ps = base + 192 + 8 * h + 4 * tp;
+    Raw r;
+    r.l0 = ld16(p0);
+    r.l0e = ld4(p0 + 16);
+    r.l1 = ld16(p1);
+    r.l1e = ld4(p1 + 16);
+    r.qh = ld16(ph);
+    r.qhe = ld4(ph + 16);
+    r.s0 = ld4(ps);
+    r.s1 = s ? ld4(ps + 4) : 0u;  // ends at blk + 210; with s = 0 it is not needed
+    r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    return r;
+  }
+  // 6-bit codes of the two runs (4 per word) and the scale bytes of the piece
+  __device__ static __forceinline__ void decode(const Raw& r, int c, uint32_t shift, uint32_t* va,
+                                                uint32_t* vb, uint32_t& scw) {
+    const uint32_t tp = uint32_t(c & 1);
+    const uint32_t L0[5] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l0e};
+    const uint32_t L1[5] = {r.l1.x, r.l1.y, r.l1.z, r.l1.w, r.l1e};
+    const uint32_t QH[5] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w, r.qhe};
+    const uint32_t nib = 4u * tp;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t qh = realign(QH[k], QH[k + 1], shift);
+      const uint32_t qs = tp ? qh : (qh << 4);
+      va[k] = ((realign(L0[k], L0[k + 1], shift) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
+      vb[k] = ((realign(L1[k], L1[k + 1], shift) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+    }
+    scw = realign(r.s0, r.s1, shift);
+  }
+};
+
+// ----------------------------------------------------- activation pre-pass --
+// X f32 -> bf16 (round to nearest even), 8 elements per thread.
+__global__ void x_bf16_kernel(const float* __restrict__ x, uint32_t* __restrict__ xb, int64_t n8) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n8) return;
+  const f32x4 a = reinterpret_cast<const f32x4*>(x)[2 * i];
+  const f32x4 b = reinterpret_cast<const f32x4*>(x)[2 * i + 1];
+  reinterpret_cast<u32x4*>(xb)[i] = u32x4{pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y),
+                                          pack_bf16(b.z, b.w)};
+}
+
+// X f32 -> Q8 blocks of 32: s = max|x| / 127 (f32 division), q = rne(x / s)
+// (0 where s == 0), plus u = s * sum(q) for the Q4_K min term. One thread
+// per block; `blocks` = m * cols / 32, scales indexed [token][block].
+__global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s_out,
+                            float* __restrict__ u_out, int64_t blocks) {
+  const int64_t b = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (b >= blocks) return;
+  const f32x4* xv = reinterpret_cast<const f32x4*>(x + 32 * b);
+  float v[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const f32x4 t = xv[k];
+    v[4 * k] = t.x;
+    v[4 * k + 1] = t.y;
+    v[4 * k + 2] = t.z;
+    v[4 * k + 3] = t.w;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
+  const float s = __fdiv_rn(amax, 127.f);
+  uint32_t w[8];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = s > 0.f ? int(__builtin_rintf(__fdiv_rn(v[4 * k + e], s))) : 0;
+      sum += c;
+      word |= (uint32_t(c) & 0xFFu) << (8 * e);
+    }
+    w[k] = word;
+  }
+  u32x4* qv = reinterpret_cast<u32x4*>(q + 32 * b);
+  qv[0] = u32x4{w[0], w[1], w[2], w[3]};
+  qv[1] = u32x4{w[4], w[5], w[6], w[7]};
+  s_out[b] = s;
+  u_out[b] = s * float(sum);
+}
+
+// --------------------------------------------------------------- tile order --
+__device__ __forceinline__ void tile_of(int n_tiles_m, int& r0, int& t0) {
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  r0 = (bid / n_tiles_m) * kMmBN;
+  t0 = (bid % n_tiles_m) * kMmBM;
+}
+
+// Q6_K piece -> bf16 runs (scale bytes of the runs: hb and 2 + hb)
+__device__ __forceinline__ void q6k_emit_bf16(const StQ6K::Raw& r, int c, int hb, uint32_t shift,
+                                              uint32_t* run0, uint32_t* run1, int& o0, int& o1, int q6s) {
+  uint32_t va[4], vb[4], scw;
+  StQ6K::decode(r, c, shift, va, vb, scw);
+  const uint32_t b0 = (scw >> (8 * hb)) & 0xFFu, b1 = (scw >> (8 * (2 + hb))) & 0xFFu;
+  const float sc0 = q6s ? float(int8_t(b0)) : float(b0), sc1 = q6s ? float(int8_t(b1)) : float(b1);
+  const float d = h2f(r.d);
+  const float ds0 = d * sc0, ds1 = d * sc1;
+  const float z0 = -32.f * ds0, z1 = -32.f * ds1;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    run0[2 * k] = pack_bf16(__builtin_fmaf(ds0, ubyte<0>(va[k]), z0), __builtin_fmaf(ds0, ubyte<1>(va[k]), z0));
+    run0[2 * k + 1] =
+        pack_bf16(__builtin_fmaf(ds0, ubyte<2>(va[k]), z0), __builtin_fmaf(ds0, ubyte<3>(va[k]), z0));
+    run1[2 * k] = pack_bf16(__builtin_fmaf(ds1, ubyte<0>(vb[k]), z1), __builtin_fmaf(ds1, ubyte<1>(vb[k]), z1));
+    run1[2 * k + 1] =
+        pack_bf16(__builtin_fmaf(ds1, ubyte<2>(vb[k]), z1), __builtin_fmaf(ds1, ubyte<3>(vb[k]), z1));
+  }
+  o0 = 16 * hb;
+  o1 = 32 + 16 * hb;
+}
+
+template <class S>
+struct Bf16Emit {
+  __device__ static __forceinline__ void run(const typename S::Raw& r, int c, int hb, uint32_t,
+                                             uint32_t* run0, uint32_t* run1, int& o0, int& o1, int q6s) {
+    S::emit_bf16(r, c, hb, run0, run1, o0, o1, q6s);
+  }
+};
+template <>
+struct Bf16Emit<StQ6K> {
+  __device__ static __forceinline__ void run(const StQ6K::Raw& r, int c, int hb, uint32_t shift,
+                                             uint32_t* run0, uint32_t* run1, int& o0, int& o1, int q6s) {
+    q6k_emit_bf16(r, c, hb, shift, run0, run1, o0, o1, q6s);
+  }
+};
+
+// Alignment shift of the block a Q6_K piece reads (0 for the other formats).
+template <class S>
+__device__ __forceinline__ uint32_t block_shift(const uint8_t*, int) {
+  return 0;
+}
+template <>
+__device__ __forceinline__ uint32_t block_shift<StQ6K>(const uint8_t* row, int c) {
+  return uint32_t(reinterpret_cast<uintptr_t>(row + (c >> 2) * 210)) & 3u;
+}
+
+// ------------------------------------------------------------- bf16 kernel --
+template <class S>
+__global__ void __launch_bounds__(kMmThreads)
+    mm_bf16_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                   const uint16_t* __restrict__ xb, int m, float* __restrict__ y, int n_tiles_m, int q6s) {
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][kMmBN * kMmRowB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  int r0, t0;
+  tile_of(n_tiles_m, r0, t0);
+  const int nchunks = cols / kMmKC;
+
+  // staging task of this thread: (row, piece); the first kMmBN * kPieces
+  // threads (whole waves) stage, the rest only compute
+  constexpr int kTasks = kMmBN * S::kPieces;
+  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
+  const bool stager = tid < kTasks;
+  const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
+  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
+
+  const uint16_t* xr[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int t = min(t0 + 64 * wave + 32 * mi + l32, m - 1);
+    xr[mi] = xb + int64_t(t) * cols + 32 * half;
+  }
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+
+  auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf) {
+    uint32_t run0[8], run1[8];
+    int o0, o1;
+    Bf16Emit<S>::run(raw, c, piece, block_shift<S>(wrow, c), run0, run1, o0, o1, q6s);
+    uint8_t* dst = buf + srow * kMmRowB;
+    *reinterpret_cast<u32x4*>(dst + 2 * o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o0 + 16) = u32x4{run0[4], run0[5], run0[6], run0[7]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o1) = u32x4{run1[0], run1[1], run1[2], run1[3]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o1 + 16) = u32x4{run1[4], run1[5], run1[6], run1[7]};
+  };
+
+  typename S::Raw raw{};
+  if (stager) {
+    raw = S::load(wrow, 0, piece);
+    stage(raw, 0, wl[0]);
+  }
+  bf16x8 xc[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xc[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + 8 * s);
+  __syncthreads();
+
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    bf16x8 xn[2][4];
+    if (more) {
+      if (stager) raw = S::load(wrow, c + 1, piece);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          xn[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + int64_t(c + 1) * kMmKC + 8 * s);
+    }
+    const uint8_t* wb = wl[c & 1];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 bfr[3];
+#pragma unroll
+      for (int ni = 0; ni < 3; ++ni)
+        bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 3; ++ni)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xc[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
+    }
+    if (more) {
+      if (stager) stage(raw, c + 1, wl[(c + 1) & 1]);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xc[mi][s] = xn[mi][s];
+    }
+    __syncthreads();
+  }
+
+  // D layout of the 32x32 MFMA: lane l holds column l % 32 (a weight row)
+  // and, in register i, row 8 * (i / 4) + 4 * (l / 32) + i % 4 (a token)
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) {
+      const int r = r0 + 32 * ni + l32;
+      if (r >= n_rows) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = t0 + 64 * wave + 32 * mi + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (t < m) y[int64_t(t) * n_rows + r] = acc[mi][ni][i];
+      }
+    }
+}
+
+// --------------------------------------------------------------- q8 kernel --
+// A = weight codes (rows r), B = activation codes (tokens t), so the D
+// layout puts one token per lane and the activation block scale is a
+// per-lane scalar; the weight block scales come from LDS per row.
+// Per 32-element block j:  y += d_rj * s_tj * I - m_rj * u_tj, with I the
+// exact int32 dot of the codes and u_tj = s_tj * sum(q_x); the second term
+// is a K = 2 f32 MFMA per chunk, the first three VALU ops per output.
+template <class S>
+__global__ void __launch_bounds__(kMmThreads)
+    mm_q8_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                 const int8_t* __restrict__ xq, const float* __restrict__ xs, const float* __restrict__ xu,
+                 int m, float* __restrict__ y, int n_tiles_m) {
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][kMmBN * kMmRowQ];
+  __shared__ __attribute__((aligned(16))) float wsc[2][2][2][kMmBN];  // [buf][block][d|m][row]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  int r0, t0;
+  tile_of(n_tiles_m, r0, t0);
+  const int nchunks = cols / kMmKC;
+  const int nblk = cols / 32;
+
+  constexpr int kTasks = kMmBN * S::kPieces;
+  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
+  const bool stager = tid < kTasks;
+  const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
+  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
+
+  // this lane's tokens (one per M-subtile) and their code rows
+  int tok[2];
+  const int8_t* xr[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    tok[mi] = min(t0 + 64 * wave + 32 * mi + l32, m - 1);
+    xr[mi] = xq + int64_t(tok[mi]) * cols + 16 * half;
+  }
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+
+  auto stage = [&](const typename S::Raw& raw, int c, int buf) {
+    uint32_t run0[4], run1[4];
+    int o0, o1, jb0, jb1;
+    float dj[2], mj[2];
+    S::emit_q8(raw, c, piece, run0, run1, o0, o1, jb0, jb1, dj, mj);
+    uint8_t* dst = wl[buf] + srow * kMmRowQ;
+    *reinterpret_cast<u32x4*>(dst + o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
+    *reinterpret_cast<u32x4*>(dst + o1) = u32x4{run1[0], run1[1], run1[2], run1[3]};
+    // (two pieces of a Q4_K row write the same scales of both blocks)
+    wsc[buf][jb0][0][srow] = dj[0];
+    wsc[buf][jb0][1][srow] = mj[0];
+    wsc[buf][jb1][0][srow] = dj[1];
+    wsc[buf][jb1][1][srow] = mj[1];
+  };
+
+  typename S::Raw raw{};
+  if (stager) {
+    raw = S::load(wrow, 0, piece);
+    stage(raw, 0, 0);
+  }
+  i32x4 xc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 32 * s);
+  __syncthreads();
+
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    i32x4 xn[2][2];
+    if (more) {
+      if (stager) raw = S::load(wrow, c + 1, piece);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * kMmKC + 32 * s);
+    }
+    const int buf = c & 1;
+    const uint8_t* wb = wl[buf];
+    // min term of both blocks of the chunk on the f32 MFMA (K = 2 blocks):
+    // A[row][k] = -m of the lane's row and block k = lane half, B[k][token] = u
+    if constexpr (S::kMin) {
+      float um[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) um[mi] = xu[int64_t(tok[mi]) * nblk + 2 * c + half];
+#pragma unroll
+      for (int ni = 0; ni < 3; ++ni) {
+        const float ma = -wsc[buf][half][1][32 * ni + l32];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ma, um[mi], acc[mi][ni], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {  // one 32-element block per step
+      const int j = 2 * c + s;
+      float sx[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) sx[mi] = xs[int64_t(tok[mi]) * nblk + j];
+#pragma unroll
+      for (int ni = 0; ni < 3; ++ni) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(wb + (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half);
+        // weight rows of this lane's registers: 32 ni + 8 (i / 4) + 4 half + i % 4
+        f32x4 dw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dw[q] = *reinterpret_cast<const f32x4*>(&wsc[buf][s][0][32 * ni + 8 * q + 4 * half]);
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+          // volatile fences keep each integer MFMA next to its scaling, so
+          // at most one 16-register integer result is live at a time
+          i32x4 av = a;
+          asm volatile("" : "+v"(av));
+          const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, xc[mi][s], i32x16{}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            acc[mi][ni][i] = __builtin_fmaf(float(I[i]), dw[i >> 2][i & 3] * sx[mi], acc[mi][ni][i]);
+          asm volatile("" : "+v"(acc[mi][ni]));
+        }
+      }
+    }
+    if (more) {
+      if (stager) stage(raw, c + 1, (c + 1) & 1);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
+    }
+    __syncthreads();
+  }
+
+  // D: lane l holds column l % 32 (a token), register i the weight row
+  // 8 * (i / 4) + 4 * (l / 32) + i % 4 -> four runs of 4 consecutive rows
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int t = t0 + 64 * wave + 32 * mi + l32;
+    if (t >= m) continue;
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 32 * ni + 8 * q + 4 * half;
+        float* dst = y + int64_t(t) * n_rows + r;
+        if (r + 3 < n_rows && (n_rows & 3) == 0) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (r + e < n_rows) dst[e] = acc[mi][ni][4 * q + e];
+        }
+      }
+  }
+}
+
+// -------------------------------------------------------------------- host --
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint32_t mode) {
+  if (!device_quant(quant) || rows <= 0 || cols <= 0 || m <= 0) return false;
+  if (cols % kMmKC != 0 || cols % geometry(quant).block != 0) return false;
+  if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 30) || m > (int64_t(1) << 24)) return false;
+  if (mode == 1 && quant == kQ6_K) return false;  // 16-element Q6_K scales: bf16 mode only
+  if (mode > 1) return false;
+  const int64_t tiles = ((rows + kMmBN - 1) / kMmBN) * ((m + kMmBM - 1) / kMmBM);
+  return tiles <= (int64_t(1) << 31) - 1;
+}
+
+size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
+  if (mode == 0) return align256(size_t(m) * size_t(cols) * 2);
+  const size_t blocks = size_t(m) * size_t(cols / 32);
+  return align256(size_t(m) * size_t(cols)) + 2 * align256(blocks * sizeof(float));
+}
+
+template <class S>
+static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64_t rb, uint8_t* ws, int m,
+                      float* y, int q6s, hipStream_t s) {
+  const int ntm = (m + kMmBM - 1) / kMmBM, ntn = (rows + kMmBN - 1) / kMmBN;
+  const dim3 grid(unsigned(ntm * ntn));
+  if (mode == 0) {
+    hipLaunchKernelGGL(mm_bf16_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
+                       reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
+  } else if constexpr (S::kQ8) {
+    const size_t blocks = size_t(m) * size_t(cols / 32);
+    const int8_t* xq = reinterpret_cast<const int8_t*>(ws);
+    const float* xs = reinterpret_cast<const float*>(ws + align256(size_t(m) * size_t(cols)));
+    const float* xu = reinterpret_cast<const float*>(ws + align256(size_t(m) * size_t(cols)) +
+                                                     align256(blocks * sizeof(float)));
+    hipLaunchKernelGGL(mm_q8_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb, xq, xs, xu, m, y,
+                       ntm);
+  }
+}
+
+hipError_t launch_quantize_q8(const float* x, int64_t n, int8_t* q, float* scales, float* usum,
+                              hipStream_t s) {
+  if (n <= 0 || n % 32 != 0) return hipErrorInvalidValue;
+  const int64_t blocks = n / 32;
+  hipLaunchKernelGGL(x_q8_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, x, q, scales,
+                     usum, blocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,
+                         int64_t m, float* y, uint32_t mode, void* workspace, int q6_signed,
+                         hipStream_t s) {
+  if (!matmul_shape_ok(quant, rows, cols, m, mode)) return hipErrorInvalidValue;
+  const uint8_t* w = static_cast<const uint8_t*>(wv);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const int64_t rb = byte_size(quant, cols);
+  if (mode == 0) {
+    const int64_t n8 = m * cols / 8;
+    hipLaunchKernelGGL(x_bf16_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s, x,
+                       reinterpret_cast<uint32_t*>(ws), n8);
+  } else {
+    const size_t blocks = size_t(m) * size_t(cols / 32);
+    float* xs = reinterpret_cast<float*>(ws + align256(size_t(m) * size_t(cols)));
+    float* xu = reinterpret_cast<float*>(ws + align256(size_t(m) * size_t(cols)) +
+                                         align256(blocks * sizeof(float)));
+    hipError_t e = launch_quantize_q8(x, m * cols, reinterpret_cast<int8_t*>(ws), xs, xu, s);
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (quant) {
+    case kQ4_K: launch_mm<StQ4K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
+    case kQ8_0: launch_mm<StQ8>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
+    default: launch_mm<StQ6K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sh

@@ -52,8 +52,9 @@ EXPORTS = (
     "sh_abi_version", "sh_last_error", "sh_device_count", "sh_quant_geometry",
     "sh_create", "sh_destroy", "sh_name", "sh_resident_bytes", "sh_evict",
     "sh_gemv", "sh_gemv_batch", "sh_expert_gemv", "sh_dequantize_row",
-    "sh_moe_route", "sh_moe_ffn",
-    "sh_dequant_dev", "sh_gemv_dev", "sh_moe_workspace_bytes", "sh_moe_ffn_dev",
+    "sh_moe_route", "sh_moe_ffn", "sh_matmul",
+    "sh_moe_workspace_bytes", "sh_moe_ffn_dev", "sh_matmul_workspace_bytes", "sh_matmul_dev",
+    "sh_quantize_q8_dev", "sh_dequant_dev", "sh_gemv_dev",
 )
 
 
@@ -150,6 +151,10 @@ def load_library() -> C.CDLL:
     L.sh_moe_workspace_bytes.argtypes = [u32, u32, u64, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
     L.sh_moe_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC),
                                  u64, u64, u64, vp, u32, u32, vp, vp, vp, u64, vp]
+    L.sh_matmul.argtypes = [vp, C.POINTER(_QuantTensorC), f32p, u32, f32p, u32]
+    L.sh_matmul_workspace_bytes.argtypes = [u32, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
+    L.sh_matmul_dev.argtypes = [u32, u32, vp, u64, u64, vp, u32, vp, u32, vp, u64, vp]
+    L.sh_quantize_q8_dev.argtypes = [vp, u64, vp, vp, vp, vp]
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
     _lib = L
@@ -343,6 +348,20 @@ class HipBackend:
                                  top_k, xv.ctypes.data, out.ctypes.data))
         return out
 
+    def matmul(self, w: QuantTensor, x, mode: int = MATMUL_BF16) -> np.ndarray:
+        """Prefill matmul ``y[t] = W x[t]`` for ``x [m][cols]`` -> ``[m][rows]``:
+        m gemvs (ops.rs:14-28) with bf16 or Q8-block activations (``mode``)."""
+        xv = _f32_in(x)
+        if xv.ndim == 1:
+            xv = xv[None, :]
+        if xv.ndim != 2 or xv.shape[1] != w.cols:
+            raise ShapeError(SH_ERR_SHAPE, f"x has shape {xv.shape}, want [m][{w.cols}]")
+        m = xv.shape[0]
+        y = np.empty((m, w.rows), dtype=np.float32)
+        wc = w._c()
+        check(self._L.sh_matmul(self._ctx, C.byref(wc), xv.ctypes.data, m, y.ctypes.data, int(mode)))
+        return y
+
     def dequantize_row(self, quant: int, block, out: np.ndarray, flags: int = 0) -> None:
         """dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device."""
         b = _bytes(block)
@@ -380,3 +399,20 @@ def moe_ffn_dev(gate: tuple, up: tuple, down: tuple, n_expert: int, n_embd: int,
     check(load_library().sh_moe_ffn_dev(C.byref(g), C.byref(u), C.byref(d), n_expert, n_embd, n_ff,
                                         logits_ptr, n_tok, top_k, x_ptr, out_ptr, ws_ptr, ws_bytes,
                                         stream or None))
+
+
+def matmul_workspace_bytes(quant: int, rows: int, cols: int, m: int, mode: int = MATMUL_BF16) -> int:
+    v = C.c_uint64()
+    check(load_library().sh_matmul_workspace_bytes(int(quant), rows, cols, m, int(mode), C.byref(v)))
+    return v.value
+
+
+def matmul_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, m: int, y_ptr: int, mode: int,
+               ws_ptr: int, ws_bytes: int, stream: int = 0, flags: int = 0) -> None:
+    check(load_library().sh_matmul_dev(int(quant), flags, w_ptr, rows, cols, x_ptr, m, y_ptr, int(mode),
+                                       ws_ptr, ws_bytes, stream or None))
+
+
+def quantize_q8_dev(x_ptr: int, n: int, codes_ptr: int, scales_ptr: int, sums_ptr: int,
+                    stream: int = 0) -> None:
+    check(load_library().sh_quantize_q8_dev(x_ptr, n, codes_ptr, scales_ptr, sums_ptr, stream or None))

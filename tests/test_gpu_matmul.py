@@ -1,0 +1,159 @@
+"""Batched prefill matmul on MFMA vs the oracle.
+
+No reference op exists (crates/strata-core/src/generate.rs:116-117); the op
+is m independent ops::gemv calls (crates/strata-core/src/ops.rs:14-28).
+Metric: max|y - r| / max|r| per token row.
+
+* bf16 mode against the f32 oracle: <= 2e-2 (the MFMA tolerance), and against
+  the same gemvs on bf16-rounded operands (W dequantized exactly then rounded
+  to bf16, x rounded to bf16, f64 sums): <= 1e-3 -- this isolates the
+  kernel's indexing and accumulation from the rounding the mode defines.
+* q8 mode against the oracle gemv of x rounded through Q8 blocks
+  (scale * code): <= 1e-3 (the int8 products are exact); against the f32
+  oracle: <= 2e-2.
+* the device Q8 quantizer is bit-exact with the oracle's.
+"""
+import numpy as np
+import pytest
+
+import strata_hip as H
+from conftest import elem_rel_err, rel_err
+from strata_hip import synth as S
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 2e-2
+TOL_EXACT_OPERANDS = 1e-3
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def bf16_operand_ref(oracle, quant, rows, cols, w, x, scale_mode=0):
+    W = oracle.dequantize(quant, w, rows, cols, scale_mode)
+    Wb = oracle.bf16_round_array(W).astype(np.float64)
+    xb = oracle.bf16_round_array(x).astype(np.float64)
+    return (xb @ Wb.T).astype(np.float32)
+
+
+def check_rows(got, want, tol):
+    worst = max(rel_err(got[t], want[t]) for t in range(want.shape[0]))
+    assert worst <= tol, worst
+    return worst
+
+
+SHAPES = [(12, 96, 256, 1), (12, 200, 512, 37), (12, 100, 768, 300), (8, 96, 256, 5),
+          (8, 130, 320, 70), (14, 97, 512, 33), (14, 96, 256, 256), (12, 192, 1024, 513)]
+
+
+@pytest.mark.parametrize("quant,rows,cols,m", SHAPES)
+def test_matmul_bf16(backend, oracle, quant, rows, cols, m):
+    say("matmul bf16", quant, rows, cols, m)
+    w = S.matrix(quant, 900 + rows, rows, cols)
+    x = S.normal_f32(901 + m, m * cols).reshape(m, cols)
+    y = backend.matmul(H.QuantTensor(f"mm{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_BF16)
+    check_rows(y, bf16_operand_ref(oracle, quant, rows, cols, w, x), TOL_EXACT_OPERANDS)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
+
+
+def test_matmul_bf16_q6k_signed_scales(backend, oracle):
+    rows, cols, m = 64, 512, 9
+    say("matmul bf16 q6k signed")
+    w = S.matrix(14, 911, rows, cols)
+    x = S.normal_f32(912, m * cols).reshape(m, cols)
+    y = backend.matmul(H.QuantTensor("mm_q6s", 14, rows, cols, w, flags=H.FLAG_Q6K_SIGNED_SCALES), x,
+                       H.MATMUL_BF16)
+    check_rows(y, bf16_operand_ref(oracle, 14, rows, cols, w, x, scale_mode=1), TOL_EXACT_OPERANDS)
+
+
+@pytest.mark.parametrize("quant,rows,cols,m", [s for s in SHAPES if s[0] != 14])
+def test_matmul_q8(backend, oracle, quant, rows, cols, m):
+    say("matmul q8", quant, rows, cols, m)
+    w = S.matrix(quant, 920 + rows, rows, cols)
+    x = S.normal_f32(921 + m, m * cols).reshape(m, cols)
+    y = backend.matmul(H.QuantTensor(f"mq{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_Q8)
+    xq = oracle.dequantize_q8_activations(x)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
+
+
+@pytest.fixture(scope="module")
+def prefill_weight():
+    # W 12288 x 4096 Q4_K (the prefill configuration's weight)
+    return S.matrix(12, 0x5EED0005, 12288, 4096)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_matmul_prefill_config(backend, oracle, prefill_weight, mode):
+    rows, cols, m = 12288, 4096, 512
+    say("matmul prefill config, mode", mode)
+    w = prefill_weight
+    x = S.normal_f32(0x5EED0006, m * cols).reshape(m, cols)
+    y = backend.matmul(H.QuantTensor("prefill.w", 12, rows, cols, w), x, mode)
+    ref = oracle.matmul(12, rows, cols, w, x, threads=16)
+    worst = check_rows(y, ref, TOL_F32)
+    print(f"[case] mode {mode}: worst row rel err vs f32 oracle {worst:.3g}", flush=True)
+    if mode == 1:
+        exact = oracle.matmul(12, rows, cols, w, oracle.dequantize_q8_activations(x), threads=16)
+    else:
+        exact = bf16_operand_ref(oracle, 12, rows, cols, w, x)
+    check_rows(y, exact, TOL_EXACT_OPERANDS)
+    # per element, |y - r| / max(|r|, rms(r)), against the same-operand sums
+    assert elem_rel_err(y, exact, floor=1.0) <= TOL_EXACT_OPERANDS
+
+
+def test_quantize_q8_dev_bit_exact(backend, oracle):
+    import torch
+    say("quantize q8 dev")
+    x = S.normal_f32(930, 32 * 1000) * np.float32(5.0)
+    x[:32] = 0.0
+    x[32:40] = [127.0, 2.5, 3.5, -2.5, -127.0, 0.5, 1.5, -0.49]
+    x[64:96] = 0.0
+    x[70] = -3.0
+    dev = torch.device("cuda:0")
+    tx = torch.from_numpy(x).to(dev)
+    q = torch.empty(x.size, dtype=torch.int8, device=dev)
+    s = torch.empty(x.size // 32, dtype=torch.float32, device=dev)
+    u = torch.empty(x.size // 32, dtype=torch.float32, device=dev)
+    H.quantize_q8_dev(tx.data_ptr(), x.size, q.data_ptr(), s.data_ptr(), u.data_ptr(),
+                      torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    oq, os_, ou = oracle.quantize_q8(x)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(u.cpu().numpy().view(np.uint32), ou.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_matmul_dev_matches_host_path(backend, mode):
+    import torch
+    rows, cols, m = 192, 512, 40
+    say("matmul dev", mode)
+    w = S.matrix(12, 940, rows, cols)
+    x = S.normal_f32(941, m * cols).reshape(m, cols)
+    host = backend.matmul(H.QuantTensor("mm_dev", 12, rows, cols, w), x, mode)
+    dev = torch.device("cuda:0")
+    tw, tx = torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev)
+    ty = torch.empty((m, rows), dtype=torch.float32, device=dev)
+    nb = H.matmul_workspace_bytes(12, rows, cols, m, mode)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    H.matmul_dev(12, tw.data_ptr(), rows, cols, tx.data_ptr(), m, ty.data_ptr(), mode, ws.data_ptr(), nb,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(ty.cpu().numpy(), host)
+
+
+def test_matmul_errors(backend):
+    say("matmul errors")
+    w6 = H.QuantTensor("e6", 14, 4, 256, S.matrix(14, 1, 4, 256))
+    with pytest.raises(H.UnsupportedQuantError):
+        backend.matmul(w6, np.zeros((2, 256), np.float32), H.MATMUL_Q8)
+    w8 = H.QuantTensor("e8", 8, 4, 96, S.matrix(8, 1, 4, 96))
+    with pytest.raises(H.BackendError):
+        backend.matmul(w8, np.zeros((2, 96), np.float32), H.MATMUL_BF16)  # cols not a multiple of 64
+    w4 = H.QuantTensor("e4", 12, 4, 256, S.matrix(12, 1, 4, 256))
+    with pytest.raises(H.ShapeError):
+        backend.matmul(w4, np.zeros((2, 128), np.float32))
+    with pytest.raises(H.BackendError):
+        backend.matmul(w4, np.zeros((2, 256), np.float32), 7)

@@ -202,3 +202,57 @@ def test_silu_closed_form(oracle):
     for v in [-20.0, -1.0, 0.0, 0.5, 3.0, 40.0]:
         ref = v / (1.0 + np.exp(-v))
         assert abs(oracle.silu(v) - ref) <= 2e-7 * max(1.0, abs(ref))
+
+
+# ---- prefill matmul and Q8 activation blocks --------------------------------
+
+def test_matmul_is_stacked_gemv(oracle):
+    # no reference matmul exists (generate.rs:116-117): the op is m gemvs
+    rows, cols, m = 40, 512, 5
+    w = S.matrix(12, 71, rows, cols)
+    x = S.normal_f32(72, m * cols).reshape(m, cols)
+    y = oracle.matmul(12, rows, cols, w, x, threads=3)
+    for t in range(m):
+        assert np.array_equal(y[t], oracle.gemv(12, rows, cols, w, x[t]))
+
+
+def test_quantize_q8_known_answers(oracle):
+    # block 0: max|x| = 127 -> s = 1 exactly, so codes are x rounded to
+    # nearest even (2.5 -> 2, 3.5 -> 4, -2.5 -> -2, 0.5 -> 0, 1.5 -> 2);
+    # block 1: all zero -> s = 0, codes 0; block 2: one non-zero value
+    x = np.zeros(96, np.float32)
+    x[:8] = [127.0, 2.5, 3.5, -2.5, -127.0, 0.5, 1.5, -0.49]
+    x[64 + 7] = -3.0
+    q, s, u = oracle.quantize_q8(x)
+    assert s[0] == 1.0 and s[1] == 0.0 and s[2] == np.float32(3.0) / np.float32(127.0)
+    assert q[:8].tolist() == [127, 2, 4, -2, -127, 0, 2, 0]
+    assert not q[8:64].any()
+    assert q[64 + 7] == -127 and np.count_nonzero(q[64:]) == 1
+    assert u[0] == np.float32(sum(q[:32].astype(int)))
+    assert u[1] == 0.0 and u[2] == np.float32(s[2] * np.float32(-127))
+
+
+def test_quantize_q8_closed_form(oracle):
+    # every code is within half a step of x / s, the block max maps to +-127,
+    # and round-half-even agrees with numpy's rint
+    x = S.normal_f32(73, 32 * 500) * np.float32(3.0)
+    q, s, u = oracle.quantize_q8(x)
+    xb = x.reshape(-1, 32).astype(np.float64)
+    sb = s.astype(np.float64)[:, None]
+    assert np.all(np.abs(xb / sb - q.reshape(-1, 32)) <= 0.5 + 1e-6)
+    assert np.all(np.abs(q.reshape(-1, 32)).max(axis=1) == 127)
+    ref = np.rint((x.reshape(-1, 32) / s[:, None]).astype(np.float32)).astype(np.int8)
+    assert np.array_equal(q.reshape(-1, 32), ref)
+    assert np.array_equal(u, (s * q.reshape(-1, 32).astype(np.int64).sum(axis=1).astype(np.float32)))
+
+
+def test_bf16_round_matches_torch_and_scalar(oracle):
+    import torch
+    x = np.concatenate([S.normal_f32(74, 4096) * np.float32(100.0),
+                        np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 0.0, -0.0,
+                                  3.0e38, 1.0e-40], np.float32)])
+    got = oracle.bf16_round_array(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for v in x[-7:]:
+        assert np.float32(oracle.lib().sho_bf16_round(float(v))) == oracle.bf16_round_array(np.float32(v))
