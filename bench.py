@@ -49,7 +49,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", help="profile one shape: q4k_down|q4k_gate|q8|q6k")
+    ap.add_argument("--only", default="", choices=("", "headline"),
+                    help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
+                         "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
 
 
@@ -277,6 +281,18 @@ def main():
         sys.exit(1)
     H.load_library()
 
+    if args.calibrate_copy:
+        src = torch.ones(1 << 26, dtype=torch.float32, device="cuda:0")  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+        print("[bench] copy calibration: 3 x 256 MiB read + 256 MiB written", file=sys.stderr, flush=True)
+    if args.only == "headline":
+        args.no_extra = True
+        args.no_cpu = True
+
     rows, cols = 4096, 12288
     w = S.matrix(S.Q4_K, 0x5EED0002, rows, cols)
     wbytes = w.nbytes
@@ -305,7 +321,7 @@ def main():
                    "rows": rows, "cols": cols, "batch": 1, "weight_bytes": wbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("q4k_gemv_4096x12288_traffic.json")},
+                     "traffic": load_traffic("gemv_q4k_4096x12288_b1.traffic.json")},
     }
     print(f"[bench] {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
 
