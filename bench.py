@@ -49,8 +49,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", choices=("", "headline"),
-                    help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg)")
+    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill"),
+                    help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
+                         "'moe' / 'prefill': that extra alone (for profiling; prints its JSON)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -292,6 +293,13 @@ def main():
     if args.only == "headline":
         args.no_extra = True
         args.no_cpu = True
+    elif args.only == "moe":
+        print(json.dumps(bench_moe(torch, H, S, args.steps)), flush=True)
+        return
+    elif args.only == "prefill":
+        wp = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
+        print(json.dumps(bench_prefill(torch, H, S, wp, 12288, 4096, 512, args.steps)), flush=True)
+        return
 
     rows, cols = 4096, 12288
     w = S.matrix(S.Q4_K, 0x5EED0002, rows, cols)

@@ -18,12 +18,24 @@ namespace sh {
 // pair of Q8_0 blocks (the same units as the matvec kernels).
 struct AxQ4K {
   static constexpr int kOff = 2;
-  template <int NT>
-  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
-                                              float (*acc)[64], float (*off)[kOff], int) {
+  struct Raw {
+    u32x4 h, a, b;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int u) {
     const uint8_t* sb = row + (u >> 2) * 144;
     const int g = u & 3;
-    const u32x4 h = ld16(sb), a = ld16(sb + 16 + 32 * g), b = ld16(sb + 32 + 32 * g);
+    return {ld16u(sb), ld16u(sb + 16 + 32 * g), ld16u(sb + 32 + 32 * g)};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
+                                              float (*acc)[64], float (*off)[kOff], int q6s) {
+    apply<NT>(load(row, u), u, xi, acc, off, q6s);
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int u, const float* xi, float (*acc)[64],
+                                               float (*off)[kOff], int) {
+    const int g = u & 3;
+    const u32x4 h = r.h, a = r.a, b = r.b;
     const uint32_t sh = (g & 1) << 4;
     const uint32_t t1 = h.y >> sh, t2 = h.z >> sh, t3 = h.w >> sh;
     const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
@@ -63,12 +75,24 @@ struct AxQ4K {
 
 struct AxQ8 {
   static constexpr int kOff = 2;
+  struct Raw {
+    u32x4 a, b, c, d;
+    uint32_t e;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int u) {
+    const uint8_t* p = row + u * 68;
+    return {ld16u(p), ld16u(p + 16), ld16u(p + 32), ld16u(p + 48), ld4(p + 64)};
+  }
   template <int NT>
   __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
-                                              float (*acc)[64], float (*off)[kOff], int) {
-    const uint8_t* p = row + u * 68;
-    const u32x4 A = ld16(p), B = ld16(p + 16), C = ld16(p + 32), Dv = ld16(p + 48);
-    const uint32_t E = ld4(p + 64);
+                                              float (*acc)[64], float (*off)[kOff], int q6s) {
+    apply<NT>(load(row, u), u, xi, acc, off, q6s);
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int, const float* xi, float (*acc)[64],
+                                               float (*off)[kOff], int) {
+    const u32x4 A = r.a, B = r.b, C = r.c, Dv = r.d;
+    const uint32_t E = r.e;
     const uint32_t D[17] = {A.x, A.y, A.z, A.w, B.x, B.y, B.z, B.w, C.x,
                             C.y, C.z, C.w, Dv.x, Dv.y, Dv.z, Dv.w, E};
     const float d0 = h2f(D[0]), d1 = h2f(D[8] >> 16);
@@ -103,25 +127,48 @@ struct AxQ8 {
 
 struct AxQ6K {
   static constexpr int kOff = 4;
-  template <int NT>
-  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
-                                              float (*acc)[64], float (*off)[kOff], int q6_signed) {
+  struct Raw {
+    u32x4 l0, l1, l2, l3, h0, h1;
+    uint32_t l4, h2, s0, s1, d, s;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int u) {
     const uint8_t* blk = row + (u >> 2) * 210;
     const int j = u & 3, h = j >> 1;
     const uint32_t tp = uint32_t(j & 1);
     const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
     const uint8_t* base = blk - s;
     const uint8_t* qlp = base + 64 * h;
-    const u32x4 l0 = ld16(qlp), l1 = ld16(qlp + 16), l2 = ld16(qlp + 32), l3 = ld16(qlp + 48);
-    const uint32_t l4 = ld4(qlp + 64);
     const uint8_t* qhp = base + 128 + 32 * h;
-    const u32x4 h0 = ld16(qhp), h1 = ld16(qhp + 16);
-    const uint32_t h2 = ld4(qhp + 32);
     const uint8_t* scp = base + 192 + 8 * h + 4 * tp;
-    const uint32_t s0 = ld4(scp);
-    const uint32_t s1 = s ? ld4(scp + 4) : 0u;
-    const float d = h2f(*reinterpret_cast<const uint16_t*>(blk + 208));
-    const uint32_t scw = realign(s0, s1, s);
+    Raw r;
+    r.l0 = ld16u(qlp);
+    r.l1 = ld16u(qlp + 16);
+    r.l2 = ld16u(qlp + 32);
+    r.l3 = ld16u(qlp + 48);
+    r.l4 = ld4(qlp + 64);
+    r.h0 = ld16u(qhp);
+    r.h1 = ld16u(qhp + 16);
+    r.h2 = ld4(qhp + 32);
+    r.s0 = ld4(scp);
+    r.s1 = s ? ld4(scp + 4) : 0u;
+    r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    r.s = s;
+    return r;
+  }
+  template <int NT>
+  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
+                                              float (*acc)[64], float (*off)[kOff], int q6_signed) {
+    apply<NT>(load(row, u), u, xi, acc, off, q6_signed);
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int u, const float* xi, float (*acc)[64],
+                                               float (*off)[kOff], int q6_signed) {
+    const uint32_t tp = uint32_t(u & 1);
+    const uint32_t s = r.s;
+    const u32x4 l0 = r.l0, l1 = r.l1, l2 = r.l2, l3 = r.l3, h0 = r.h0, h1 = r.h1;
+    const uint32_t l4 = r.l4, h2 = r.h2;
+    const float d = h2f(r.d);
+    const uint32_t scw = realign(r.s0, r.s1, s);
     float sc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {

@@ -60,6 +60,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// The same 16 bytes from an address known only to be 4-byte aligned (safe
+// for LDS as well as global memory).
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ u32x4 ld16u(const uint8_t* p) {
+  const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(p);
+  return u32x4{v.x, v.y, v.z, v.w};
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
   return *reinterpret_cast<const uint32_t*>(p);
 }

@@ -37,11 +37,16 @@ constexpr int kMoeMaxTokens = 256;
 struct MoePlan {
   int n_tok, top_k, n_expert, n_embd, n_ff;
   int s_max;                     // most unique experts a call can route to
-  int nch_a, chunk_a;            // gate/up row chunks (rows = n_embd)
-  int nch_b, chunk_b;            // down row chunks (rows = n_ff)
   int64_t rb_a, rb_b;            // row bytes of gate/up and of down
-  size_t o_ids, o_wts, o_meta, o_slot_e, o_slot_off, o_slot_cnt, o_pair_tok, o_pair_w, o_tokpair;
-  size_t o_part_a, o_part_b;
+  int ca, nch_a;                 // gate/up: rows per chunk, chunks (over n_embd)
+  int cb, nch_b;                 // down: rows per chunk, chunks (over n_ff)
+  int sr_a, sr_b;                // rows per LDS sub-tile
+  int nbuf_a, nbuf_b;            // LDS sub-tile buffers (1 when one sub-tile holds the chunk)
+  size_t o_ids, o_wts, o_meta, o_slot_e, o_slot_off, o_slot_cnt, o_pair_tok, o_tokpair;
+  size_t o_part_a;               // [pair][2][nch_a][n_ff]: chunk sums of gate . x, up . x
+  size_t o_part_b;               // [pair][nch_b][n_embd]: chunk sums of down . a
+  size_t route_lds, lds_a, lds_b;  // dynamic LDS per kernel
+  bool staged;                   // row bytes allow 16-byte tile copies
   size_t bytes;
 };
 

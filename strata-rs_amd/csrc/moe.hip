@@ -14,16 +14,24 @@
 // (moe.rs:129-143) is not part of this op.
 //
 // Four launches:
-//   route    one workgroup routes every token and groups the (token, expert)
-//            pairs by expert: the unique experts in ascending id order are
-//            "slots", each with its tokens in ascending order ("pairs");
-//   gate/up  workgroup (slot, matrix, row chunk) streams that expert's rows
-//            once for all of the slot's tokens (one at a time; the repeat of
-//            a chunk hits in L2) and writes one partial sum per pair;
-//   down     workgroup (slot, row chunk) forms a = silu(h) * p for its rows
-//            and the slot's tokens in LDS, then streams the down rows;
-//   combine  out[t] = sum over t's experts in ascending id of w * d.
-// Weight bytes cross HBM once per unique expert, however many tokens chose it.
+//   route    one workgroup routes every token (a wave per token) and groups
+//            the (token, expert) pairs by expert: the unique experts in
+//            ascending id are "slots", each with its pairs;
+//   gate/up  workgroup (row chunk, matrix, slot): the chunk's rows are
+//            contiguous bytes, streamed into LDS with coalesced 16-byte loads
+//            (two sub-tiles in flight); threads decode their 64-column unit
+//            from LDS and apply each row to two of the slot's tokens per
+//            pass; row-slot sums reduce in LDS to one chunk sum per pair;
+//   down     workgroup (row chunk, slot): a = silu(h) * p for its rows from
+//            the gate/up chunk sums (fixed order), then the same streaming;
+//   combine  out[t] = sum over t's experts in ascending id of w * d, with d
+//            the sum of the down chunk sums.
+// Chunk counts scale with the experts routed: a single token still spreads
+// over the whole chip, and many tokens keep the chunk sums small. Each
+// unique expert's weight bytes cross HBM once per call, however many tokens
+// chose it.
+#include <algorithm>
+
 #include "axpy.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -31,29 +39,68 @@
 namespace sh {
 
 constexpr int kMoeThreads = 256;
-constexpr int kMoeTok = 1;  // tokens sharing one decoded weight row (a chunk re-read for the next token hits in L2)
+constexpr int kMoeMaxChunks = 32;    // row chunks per matrix (their sums are added in one load round)
+constexpr int kRouteThreads = 1024;  // one thread per expert in the grouping scan
+static_assert(kRouteThreads == kMoeMaxExperts, "the scan gives each thread one expert");
 
 // ------------------------------------------------------------------ route --
+// Wave-wide max / min through DPP (quad swaps, row mirrors, row
+// broadcasts; lane 63 ends with the result), returned to every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  const int id = __builtin_bit_cast(int, -__builtin_inff());
+#define SH_DPP_MAX(ctrl, rm) \
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), ctrl, rm, 0xF, false)))
+  SH_DPP_MAX(0xB1, 0xF);
+  SH_DPP_MAX(0x4E, 0xF);
+  SH_DPP_MAX(0x141, 0xF);
+  SH_DPP_MAX(0x140, 0xF);
+  SH_DPP_MAX(0x142, 0xA);
+  SH_DPP_MAX(0x143, 0xC);
+#undef SH_DPP_MAX
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ int wave_min_dpp(int v) {
+#define SH_DPP_MIN(ctrl, rm) v = min(v, __builtin_amdgcn_update_dpp(0x7FFFFFFF, v, ctrl, rm, 0xF, false))
+  SH_DPP_MIN(0xB1, 0xF);
+  SH_DPP_MIN(0x4E, 0xF);
+  SH_DPP_MIN(0x141, 0xF);
+  SH_DPP_MIN(0x140, 0xF);
+  SH_DPP_MIN(0x142, 0xA);
+  SH_DPP_MIN(0x143, 0xC);
+#undef SH_DPP_MIN
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
   return v;
 }
 
-__global__ void __launch_bounds__(kMoeThreads) moe_route_kernel(const float* __restrict__ logits,
-                                                                MoePlan plan, uint8_t* ws) {
+// KPER: experts per lane (KPER * 64 >= n_expert)
+template <int KPER>
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits,
+                                                                  MoePlan plan, uint8_t* ws) {
+  extern __shared__ __attribute__((aligned(16))) int rlds[];
+  constexpr int kWaves = kRouteThreads / kWave;
   __shared__ int cnt[kMoeMaxExperts];
-  __shared__ int eslot[kMoeMaxExperts];
-  __shared__ int sel_id[kMoeThreads / kWave][kMoeMaxTopK];
-  __shared__ float sel_p[kMoeThreads / kWave][kMoeMaxTopK];
-  __shared__ int wave_nz[kMoeThreads / kWave], wave_sum[kMoeThreads / kWave];
+  __shared__ int cursor[kMoeMaxExperts];
+  __shared__ int sel_id[kWaves][kMoeMaxTopK];
+  __shared__ float sel_p[kWaves][kMoeMaxTopK];
+  __shared__ int wave_nz[kWaves], wave_tot[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = plan.n_expert, K = plan.top_k;
+  const int pairs = plan.n_tok * K;
+  int* s_ids = rlds;                                     // [pairs]
+  float* s_w = reinterpret_cast<float*>(rlds + pairs);   // [pairs]
   int* ids = reinterpret_cast<int*>(ws + plan.o_ids);
   float* wts = reinterpret_cast<float*>(ws + plan.o_wts);
-  constexpr int kPer = kMoeMaxExperts / kWave;  // experts per lane
+  constexpr int kPer = KPER;
 
-  for (int t = wave; t < plan.n_tok; t += kMoeThreads / kWave) {
+  for (int e = tid; e < kMoeMaxExperts; e += kRouteThreads) cnt[e] = 0;
+
+  for (int t = wave; t < plan.n_tok; t += kWaves) {
     const float* lg = logits + int64_t(t) * E;
     float p[kPer];
     float mx = -__builtin_inff();
@@ -78,31 +125,28 @@ __global__ void __launch_bounds__(kMoeThreads) moe_route_kernel(const float* __r
     const float inv = float(1.0 / sum);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) p[j] *= inv;
-    // top-k: k rounds of (largest p, then lowest id) over what is left
+    // top-k: k rounds of (largest p, then lowest id) over what is left; a
+    // NaN probability ranks below every number, so each round picks a valid
+    // id (k <= n_expert)
     uint32_t taken = 0;
     for (int r = 0; r < K; ++r) {
-      // a NaN probability ranks below every number, so each round always
-      // picks a valid id (k <= n_expert)
+      // exact: the largest remaining probability, then the lowest id holding it
       float bp = -2.f;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int e = lane + kWave * j;
+        const float pj = p[j] == p[j] ? p[j] : -1.f;
+        if (e < E && !(taken >> j & 1u)) bp = fmaxf(bp, pj);
+      }
+      bp = wave_max_dpp(bp);
       int bi = 0x7FFFFFFF;
 #pragma unroll
       for (int j = 0; j < kPer; ++j) {
         const int e = lane + kWave * j;
         const float pj = p[j] == p[j] ? p[j] : -1.f;
-        if (e < E && !(taken >> j & 1u) && (pj > bp || (pj == bp && e < bi))) {
-          bp = pj;
-          bi = e;
-        }
+        if (e < E && !(taken >> j & 1u) && pj == bp) bi = min(bi, e);
       }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float op = __shfl_xor(bp, off, kWave);
-        const int oi = __shfl_xor(bi, off, kWave);
-        if (op > bp || (op == bp && oi < bi)) {
-          bp = op;
-          bi = oi;
-        }
-      }
+      bi = wave_min_dpp(bi);
       if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
       if (lane == 0) {
         sel_id[wave][r] = bi;
@@ -110,47 +154,43 @@ __global__ void __launch_bounds__(kMoeThreads) moe_route_kernel(const float* __r
       }
     }
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-      // ids ascending (insertion sort of k <= 32), then the f64 renormalisation
-      for (int a = 1; a < K; ++a) {
-        const int id = sel_id[wave][a];
-        const float pv = sel_p[wave][a];
-        int b = a - 1;
-        while (b >= 0 && sel_id[wave][b] > id) {
-          sel_id[wave][b + 1] = sel_id[wave][b];
-          sel_p[wave][b + 1] = sel_p[wave][b];
-          --b;
-        }
-        sel_id[wave][b + 1] = id;
-        sel_p[wave][b + 1] = pv;
-      }
-      double wsum = 0.0;
-      for (int a = 0; a < K; ++a) wsum += double(sel_p[wave][a]);
-      const double s = wsum > 6.103515625e-05 ? wsum : 6.103515625e-05;  // 2^-14
-      for (int a = 0; a < K; ++a) {
-        ids[t * K + a] = sel_id[wave][a];
-        wts[t * K + a] = float(double(sel_p[wave][a]) / s);
-      }
+    // ids ascending: lane a < K goes to its rank among the selected ids
+    int myid = 0, rank = 0;
+    float myp = 0.f;
+    if (lane < K) {
+      myid = sel_id[wave][lane];
+      myp = sel_p[wave][lane];
+      for (int b = 0; b < K; ++b) rank += sel_id[wave][b] < myid;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) {
+      sel_id[wave][rank] = myid;
+      sel_p[wave][rank] = myp;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // f64 renormalisation in ascending-id order (moe.rs:80-90)
+    double wsum = 0.0;
+    for (int a = 0; a < K; ++a) wsum += double(sel_p[wave][a]);
+    const double sden = wsum > 6.103515625e-05 ? wsum : 6.103515625e-05;  // 2^-14
+    if (lane < K) {
+      const int id = sel_id[wave][lane];
+      const float wv = float(double(sel_p[wave][lane]) / sden);
+      s_ids[t * K + lane] = id;
+      s_w[t * K + lane] = wv;
+      ids[t * K + lane] = id;
+      wts[t * K + lane] = wv;
     }
     __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
 
-  // group the pairs by expert: counts, then an exclusive scan over experts
-  for (int e = tid; e < kMoeMaxExperts; e += kMoeThreads) cnt[e] = 0;
+  // group the pairs by expert: counts, an exclusive scan over experts (one
+  // per thread), then each pair claims its position with an LDS atomic
+  for (int i = tid; i < pairs; i += kRouteThreads) atomicAdd(&cnt[s_ids[i]], 1);
   __syncthreads();
-  for (int i = tid; i < plan.n_tok * K; i += kMoeThreads) atomicAdd(&cnt[ids[i]], 1);
-  __syncthreads();
-  constexpr int kEper = kMoeMaxExperts / kMoeThreads;  // experts per thread
-  int nz = 0, tot = 0;
-#pragma unroll
-  for (int j = 0; j < kEper; ++j) {
-    const int c = cnt[tid * kEper + j];
-    nz += c > 0;
-    tot += c;
-  }
-  // inclusive scans of (nz, tot) within the wave, then across waves
-  int snz = nz, stot = tot;
+  const int c = cnt[tid];
+  const int nz = c > 0;
+  int snz = nz, stot = c;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const int a = __shfl_up(snz, off, kWave), b = __shfl_up(stot, off, kWave);
@@ -161,192 +201,336 @@ __global__ void __launch_bounds__(kMoeThreads) moe_route_kernel(const float* __r
   }
   if (lane == 63) {
     wave_nz[wave] = snz;
-    wave_sum[wave] = stot;
+    wave_tot[wave] = stot;
   }
   __syncthreads();
   int base_nz = 0, base_tot = 0;
   for (int w2 = 0; w2 < wave; ++w2) {
     base_nz += wave_nz[w2];
-    base_tot += wave_sum[w2];
+    base_tot += wave_tot[w2];
   }
-  int slot = base_nz + snz - nz, pos = base_tot + stot - tot;
-  int* slot_e = reinterpret_cast<int*>(ws + plan.o_slot_e);
-  int* slot_off = reinterpret_cast<int*>(ws + plan.o_slot_off);
-  int* slot_cnt = reinterpret_cast<int*>(ws + plan.o_slot_cnt);
-#pragma unroll
-  for (int j = 0; j < kEper; ++j) {
-    const int e = tid * kEper + j;
-    const int c = cnt[e];
-    if (c > 0) {
-      slot_e[slot] = e;
-      slot_off[slot] = pos;
-      slot_cnt[slot] = c;
-      eslot[e] = slot;
-      ++slot;
-      pos += c;
-    }
+  const int slot = base_nz + snz - nz, pos = base_tot + stot - c;
+  if (c > 0) {
+    reinterpret_cast<int*>(ws + plan.o_slot_e)[slot] = tid;
+    reinterpret_cast<int*>(ws + plan.o_slot_off)[slot] = pos;
+    reinterpret_cast<int*>(ws + plan.o_slot_cnt)[slot] = c;
   }
-  if (tid == kMoeThreads - 1) reinterpret_cast<int*>(ws + plan.o_meta)[0] = slot;
+  cursor[tid] = pos;
+  if (tid == kRouteThreads - 1) reinterpret_cast<int*>(ws + plan.o_meta)[0] = base_nz + snz;
   __syncthreads();
-  // pairs of each expert in ascending token order
+  // a pair's position within its expert's run does not affect any result:
+  // each pair's sums are computed on their own and found through tokpair
   int* pair_tok = reinterpret_cast<int*>(ws + plan.o_pair_tok);
-  float* pair_w = reinterpret_cast<float*>(ws + plan.o_pair_w);
   int* tokpair = reinterpret_cast<int*>(ws + plan.o_tokpair);
-  for (int e = tid; e < E; e += kMoeThreads) {
-    if (cnt[e] == 0) continue;
-    const int s = eslot[e];
-    int p = slot_off[s];
-    for (int t = 0; t < plan.n_tok; ++t)
-      for (int a = 0; a < K; ++a)
-        if (ids[t * K + a] == e) {
-          pair_tok[p] = t;
-          pair_w[p] = wts[t * K + a];
-          tokpair[t * K + a] = p;
-          ++p;
-        }
+  for (int i = tid; i < pairs; i += kRouteThreads) {
+    const int q = atomicAdd(&cursor[s_ids[i]], 1);
+    pair_tok[q] = i / K;
+    tokpair[i] = q;
   }
 }
 
-// Column sums of one row chunk for `nt` tokens, reduced over the workgroup's
-// row slots through LDS and written to dst[t * cols + c].
-template <class F>
-__device__ __forceinline__ void chunk_axpy(const uint8_t* w, int64_t row_bytes, int cols, int r0,
-                                           int r1, const float* const* xs, int xoff, int nt,
-                                           float* red, float* dst, int64_t dst_stride, int q6_signed) {
-  const int U = cols >> 6;
-  const int RS = kMoeThreads / U;
-  const int tid = threadIdx.x;
-  const int u = tid % U, slot = tid / U;
-  float acc[kMoeTok][64];
-  float off[kMoeTok][F::kOff];
+// ------------------------------------------------------- LDS row tiles --
+// Copies bytes [src, src + n) of a weight tensor of `total` bytes into LDS
+// at `dst` + (src & 15): whole 16-byte pieces from the 16-byte boundary at or
+// below src, each thread a piece at a time; a piece that would run past the
+// tensor's end is copied byte by byte. Returns the lead (src & 15). Loads
+// are issued into registers first (`pieces` per thread at most), then
+// stored, so they are all in flight together.
+// 16-byte pieces per thread per tile: 4 (16 KiB tiles) for one token per
+// pass, where many short tiles overlap loads with compute best; 8 (32 KiB)
+// for two, where fewer, longer tiles do
+constexpr int tile_pieces(int nt) { return nt == 1 ? 4 : 8; }
+
+template <int TP>
+struct TileLoad {
+  u32x4 v[TP];
+  int n;     // pieces in the tile
+  int lead;  // src & 15
+};
+
+template <int TP>
+__device__ __forceinline__ void tile_issue(const uint8_t* base, int64_t src, int64_t n, int64_t total,
+                                           TileLoad<TP>& t) {
+  const int64_t a0 = src & ~int64_t(15);
+  t.lead = int(src - a0);
+  t.n = int((t.lead + n + 15) >> 4);
 #pragma unroll
-  for (int t = 0; t < kMoeTok; ++t) {
+  for (int k = 0; k < TP; ++k) {
+    const int pc = int(threadIdx.x) + kMoeThreads * k;
+    const int64_t at = a0 + 16 * int64_t(pc);
+    if (pc < t.n && at + 16 <= total) {
+      t.v[k] = ld16(base + at);
+    } else if (pc < t.n) {
+      uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) {
+        const uint32_t byte = at + b < total ? uint32_t(base[at + b]) : 0u;
+        const uint32_t sh = 8 * (b & 3);
+        if (b < 4) w0 |= byte << sh;
+        else if (b < 8) w1 |= byte << sh;
+        else if (b < 12) w2 |= byte << sh;
+        else w3 |= byte << sh;
+      }
+      t.v[k] = u32x4{w0, w1, w2, w3};
+    }
+  }
+}
+
+template <int TP>
+__device__ __forceinline__ void tile_store(uint8_t* dst, const TileLoad<TP>& t) {
+#pragma unroll
+  for (int k = 0; k < TP; ++k) {
+    const int pc = int(threadIdx.x) + kMoeThreads * k;
+    if (pc < t.n) *reinterpret_cast<u32x4*>(dst + 16 * pc) = t.v[k];
+  }
+}
+
+// Column sums of one row chunk, for NT (1 or 2) input vectors at once
+// (nt <= NT of them in use). The chunk (rows [r0, r0 + nrows) of W) is
+// streamed through two LDS sub-tiles of `sr` rows; thread (unit u = tid % U,
+// slot sl = tid / U) applies rows sl, sl + RS, ... of each sub-tile to the
+// inputs, reading the next row from LDS while applying the current one. The
+// inputs' values for the chunk's rows are xs0[r], xs1[r]. The slots' sums are
+// reduced through `red` (RS * U * 36 floats) half a unit at a time, and the
+// column sums of input t go to out_t[col].
+// `pre()` runs after the first sub-tile's loads are issued and before they
+// are stored, so input staging overlaps the first weight bytes' latency.
+template <class F, int NT, class Pre>
+__device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t w_off, int64_t w_total, int cols,
+                           int nrows, int sr, const float* xs0, const float* xs1, int nt, uint8_t* tiles,
+                           int tile_cap, float* red, float* out0, float* out1, int q6s, Pre pre) {
+  const int tid = threadIdx.x;
+  const int U = cols >> 6, RS = kMoeThreads / U;
+  const int u = tid % U, sl = tid / U;
+  const bool active = sl < RS;
+  float acc[NT][64];
+  float off[NT][F::kOff];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
 #pragma unroll
     for (int e = 0; e < 64; ++e) acc[t][e] = 0.f;
 #pragma unroll
     for (int k = 0; k < F::kOff; ++k) off[t][k] = 0.f;
   }
-  if (slot < RS) {
-    for (int i = r0 + slot; i < r1; i += RS) {
-      float xi[kMoeTok];
-#pragma unroll
-      for (int t = 0; t < kMoeTok; ++t) xi[t] = t < nt ? xs[t][i - xoff] : 0.f;
-      F::template axpy<kMoeTok>(w + int64_t(i) * row_bytes, u, xi, acc, off, q6_signed);
+  const int nsub = (nrows + sr - 1) / sr;
+  TileLoad<tile_pieces(NT)> tl;
+  tile_issue(W, w_off, int64_t(min(sr, nrows)) * rb, w_total, tl);
+  pre();
+  tile_store(tiles, tl);
+  int lead = tl.lead;
+  __syncthreads();
+  for (int sb = 0; sb < nsub; ++sb) {
+    const bool more = sb + 1 < nsub;
+    int next_lead = 0;
+    if (more) {
+      const int r1 = (sb + 1) * sr;
+      tile_issue(W, w_off + int64_t(r1) * rb, int64_t(min(sr, nrows - r1)) * rb, w_total, tl);
+      next_lead = tl.lead;
     }
+    const uint8_t* tile = tiles + (sb & 1) * tile_cap + lead;
+    const int rows_here = min(sr, nrows - sb * sr);
+    if (active && sl < rows_here) {
+      typename F::Raw cur = F::load(tile + int64_t(sl) * rb, u);
+      for (int r = sl; r < rows_here; r += RS) {
+        const typename F::Raw nxt = F::load(tile + int64_t(min(r + RS, rows_here - 1)) * rb, u);
+        const int rr = sb * sr + r;
+        float xi[NT];
+        xi[0] = xs0[rr];
+        if constexpr (NT > 1) xi[1] = nt > 1 ? xs1[rr] : 0.f;
+        F::template apply<NT>(cur, u, xi, acc, off, q6s);
+        cur = nxt;
+      }
+    }
+    if (more) tile_store(tiles + ((sb + 1) & 1) * tile_cap, tl);
+    lead = next_lead;
+    __syncthreads();
   }
-  for (int t = 0; t < nt; ++t) {
-    if (slot < RS) {
-      float* d = red + slot * cols + 64 * u;
+  // red rows: half a unit (32 sums) per unit, padded to 36 floats so lanes of
+  // neighbouring units write to different banks
+  const int rstride = U * 36;
 #pragma unroll
-      for (int e = 0; e < 64; e += 4)
-        *reinterpret_cast<f32x4*>(d + e) =
-            f32x4{acc[t][e] - off[t][F::off_index(e)], acc[t][e + 1] - off[t][F::off_index(e + 1)],
-                  acc[t][e + 2] - off[t][F::off_index(e + 2)], acc[t][e + 3] - off[t][F::off_index(e + 3)]};
+  for (int t = 0; t < NT; ++t) {
+    if (t >= nt) break;  // uniform: nt is the same for the whole workgroup
+    float* o = t == 0 ? out0 : out1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (active) {
+        float* dst = red + sl * rstride + 36 * u;
+#pragma unroll
+        for (int e = 0; e < 32; e += 4) {
+          const int g = 32 * h + e;
+          *reinterpret_cast<f32x4*>(dst + e) =
+              f32x4{acc[t][g] - off[t][F::off_index(g)], acc[t][g + 1] - off[t][F::off_index(g + 1)],
+                    acc[t][g + 2] - off[t][F::off_index(g + 2)], acc[t][g + 3] - off[t][F::off_index(g + 3)]};
+        }
+      }
+      __syncthreads();
+      for (int q = tid; q < U * 32; q += kMoeThreads) {
+        const int un = q >> 5, e = q & 31;
+        const float* src = red + 36 * un + e;
+        float v = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < RS; ++k) v += src[k * rstride];
+        o[64 * un + 32 * h + e] = v;
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    for (int c = tid; c < cols; c += kMoeThreads) {
-      float s = 0.f;
-      for (int k = 0; k < RS; ++k) s += red[k * cols + c];
-      dst[int64_t(t) * dst_stride + c] = s;
-    }
-    __syncthreads();
   }
 }
 
 // -------------------------------------------------------------- gate / up --
-template <class F>
+// Workgroup (row chunk c, matrix m, slot s): chunk sums of gate_e . x_t or
+// up_e . x_t for every pair (token t, expert e) of the slot, two tokens per
+// pass over the chunk's bytes.
+template <class F, int NT>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_gateup_kernel(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, MoePlan plan,
                       const float* __restrict__ x, uint8_t* ws, int q6_gate, int q6_up) {
-  extern __shared__ __attribute__((aligned(16))) float red[];
-  const int s = blockIdx.x, m = blockIdx.y, c = blockIdx.z;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int c = blockIdx.x, m = blockIdx.y, s = blockIdx.z;
   const int n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
   if (s >= n_slots) return;
   const int e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
   const int p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
   const int cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
   const int* pair_tok = reinterpret_cast<const int*>(ws + plan.o_pair_tok);
-  const int64_t rb = plan.rb_a;
-  const uint8_t* w = (m == 0 ? gate : up) + int64_t(e) * plan.n_embd * rb;
-  const int r0 = c * plan.chunk_a, r1 = min(plan.n_embd, r0 + plan.chunk_a);
   float* part = reinterpret_cast<float*>(ws + plan.o_part_a);
-  for (int tg = 0; tg < cnt; tg += kMoeTok) {
-    const int nt = min(kMoeTok, cnt - tg);
-    const float* xs[kMoeTok];
-#pragma unroll
-    for (int t = 0; t < kMoeTok; ++t) xs[t] = x + int64_t(pair_tok[p0 + tg + (t < nt ? t : 0)]) * plan.n_embd;
-    // partial sums of pair p: part[((p * 2 + m) * nch_a + c) * n_ff + col]
-    float* dst = part + ((int64_t(p0 + tg) * 2 + m) * plan.nch_a + c) * plan.n_ff;
-    chunk_axpy<F>(w, rb, plan.n_ff, r0, r1, xs, 0, nt, red, dst, int64_t(2) * plan.nch_a * plan.n_ff,
-                  m == 0 ? q6_gate : q6_up);
+  const int r0 = c * plan.ca, nrows = min(plan.ca, plan.n_embd - r0);
+  const int tile_cap = (plan.sr_a * int(plan.rb_a) + 31) & ~15;
+  uint8_t* tiles = smem;
+  float* xs = reinterpret_cast<float*>(smem + plan.nbuf_a * tile_cap);  // [2][ca]
+  float* red = xs + 2 * plan.ca;
+  const uint8_t* W = m == 0 ? gate : up;
+  const int64_t w_total = int64_t(plan.n_expert) * plan.n_embd * plan.rb_a;
+  const int64_t w_off = (int64_t(e) * plan.n_embd + r0) * plan.rb_a;
+  for (int j = 0; j < cnt; j += NT) {
+    const int nt = min(NT, cnt - j);
+    auto stage_x = [&]() {
+      for (int i = threadIdx.x; i < nt * nrows; i += kMoeThreads) {
+        const int t = i / nrows, r = i - t * nrows;
+        xs[t * plan.ca + r] = x[int64_t(pair_tok[p0 + j + t]) * plan.n_embd + r0 + r];
+      }
+    };
+    // part[((p * 2 + m) * nch_a + c) * n_ff + col]
+    float* o0 = part + ((int64_t(p0 + j) * 2 + m) * plan.nch_a + c) * plan.n_ff;
+    float* o1 = o0 + int64_t(2) * plan.nch_a * plan.n_ff;
+    chunk_sums<F, NT>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt, tiles,
+                  tile_cap, red, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
   }
 }
 
 // ------------------------------------------------------------------- down --
-template <class F>
+// Workgroup (row chunk c over n_ff, slot s): first a = silu(h) * p for the
+// chunk's rows and the slot's tokens, h and p summed over the gate/up chunks
+// in a fixed order (ops.rs:85-87, moe.rs:119-121); then chunk sums of
+// down_e . a.
+template <class F, int NT>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_down_kernel(const uint8_t* __restrict__ down, MoePlan plan, uint8_t* ws, int q6_down) {
-  extern __shared__ __attribute__((aligned(16))) float red[];
-  const int s = blockIdx.x, c = blockIdx.y;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int c = blockIdx.x, s = blockIdx.y;
   const int n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
   if (s >= n_slots) return;
   const int e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
   const int p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
   const int cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
-  const int r0 = c * plan.chunk_b, r1 = min(plan.n_ff, r0 + plan.chunk_b);
-  const int nr = r1 - r0;
-  // a = silu(h) * p for this chunk's rows and every token of the slot
-  // (moe.rs:119-121), from the gate/up partials summed in chunk order
-  float* a = red + kMoeThreads / (plan.n_embd >> 6) * plan.n_embd;  // after the reduction area
-  const float* part = reinterpret_cast<const float*>(ws + plan.o_part_a);
-  for (int idx = threadIdx.x; idx < cnt * nr; idx += kMoeThreads) {
-    const int t = idx / nr, i = r0 + idx % nr;
-    const float* hp = part + (int64_t(p0 + t) * 2 * plan.nch_a) * plan.n_ff + i;
-    float h = 0.f, pv = 0.f;
-    for (int k = 0; k < plan.nch_a; ++k) {
-      h += hp[int64_t(k) * plan.n_ff];
-      pv += hp[int64_t(plan.nch_a + k) * plan.n_ff];
-    }
-    a[t * nr + (i - r0)] = h / (1.f + expf(-h)) * pv;  // ops.rs:85-87
-  }
-  __syncthreads();
-  const int64_t rb = plan.rb_b;
-  const uint8_t* w = down + int64_t(e) * plan.n_ff * rb;
-  float* out = reinterpret_cast<float*>(ws + plan.o_part_b);
-  for (int tg = 0; tg < cnt; tg += kMoeTok) {
-    const int nt = min(kMoeTok, cnt - tg);
-    const float* xs[kMoeTok];
+  const float* pa = reinterpret_cast<const float*>(ws + plan.o_part_a);
+  float* part = reinterpret_cast<float*>(ws + plan.o_part_b);
+  const int r0 = c * plan.cb, nrows = min(plan.cb, plan.n_ff - r0);
+  const int tile_cap = (plan.sr_b * int(plan.rb_b) + 31) & ~15;
+  uint8_t* tiles = smem;
+  float* xs = reinterpret_cast<float*>(smem + plan.nbuf_b * tile_cap);  // [2][cb]
+  float* hp = xs + 2 * plan.cb;                                 // [2][2][cb]
+  float* red = hp + 4 * plan.cb;
+  const int64_t w_total = int64_t(plan.n_expert) * plan.n_ff * plan.rb_b;
+  const int64_t w_off = (int64_t(e) * plan.n_ff + r0) * plan.rb_b;
+  const int tid = threadIdx.x, sub = tid & 3;
+  for (int j = 0; j < cnt; j += NT) {
+    const int nt = min(NT, cnt - j);
+    auto stage_a = [&]() {
+      // h, p for (token t, matrix mm, row r): 4 adjacent lanes load every 4th
+      // of the (at most 32) gate/up chunk sums at once, then a fixed shuffle
+      // tree adds the 4
+      const int n_el = nt * 2 * nrows;
+      for (int i0 = 0; i0 < n_el * 4; i0 += kMoeThreads) {
+        const int idx = i0 + tid, el = idx >> 2;
+        const bool ok = el < n_el;
+        const int elc = ok ? el : 0;
+        const int t = elc / (2 * nrows), rem = elc - t * 2 * nrows, mm = rem / nrows, r = rem - mm * nrows;
+        const float* src = pa + ((int64_t(p0 + j + t) * 2 + mm) * plan.nch_a) * plan.n_ff + r0 + r;
+        float v[kMoeMaxChunks / 4];
 #pragma unroll
-    for (int t = 0; t < kMoeTok; ++t) xs[t] = a + (tg + (t < nt ? t : 0)) * nr;
-    // partial sums of pair p: out[(p * nch_b + c) * n_embd + col]
-    float* dst = out + (int64_t(p0 + tg) * plan.nch_b + c) * plan.n_embd;
-    chunk_axpy<F>(w, rb, plan.n_embd, r0, r1, xs, r0, nt, red, dst, int64_t(plan.nch_b) * plan.n_embd,
-                  q6_down);
+        for (int q = 0; q < kMoeMaxChunks / 4; ++q) {
+          const int k = sub + 4 * q;
+          v[q] = ok && k < plan.nch_a ? src[int64_t(k) * plan.n_ff] : 0.f;
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kMoeMaxChunks / 4; ++q) sum += v[q];
+        sum += __shfl_xor(sum, 1, kWave);
+        sum += __shfl_xor(sum, 2, kWave);
+        if (ok && sub == 0) hp[el] = sum;
+      }
+      __syncthreads();
+      for (int i = tid; i < nt * nrows; i += kMoeThreads) {
+        const int t = i / nrows, r = i - t * nrows;
+        const float h = hp[(t * 2) * nrows + r], pv = hp[(t * 2 + 1) * nrows + r];
+        xs[t * plan.cb + r] = h / (1.f + expf(-h)) * pv;
+      }
+    };
+    // part[(p * nch_b + c) * n_embd + col]
+    float* o0 = part + (int64_t(p0 + j) * plan.nch_b + c) * plan.n_embd;
+    float* o1 = o0 + int64_t(plan.nch_b) * plan.n_embd;
+    chunk_sums<F, NT>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
+                  tiles, tile_cap, red, o0, o1, q6_down, stage_a);
   }
 }
 
 // ---------------------------------------------------------------- combine --
-__global__ void moe_combine_kernel(MoePlan plan, const uint8_t* ws, float* __restrict__ out) {
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= int64_t(plan.n_tok) * plan.n_embd) return;
-  const int t = int(i / plan.n_embd), col = int(i - int64_t(t) * plan.n_embd);
-  const int* tokpair = reinterpret_cast<const int*>(ws + plan.o_tokpair);
-  const float* wts = reinterpret_cast<const float*>(ws + plan.o_wts);
+// Block: 32 columns of one token x 8 expert lanes. Lane (col, a) sums the
+// down chunk sums of the token's a-th expert; then the token's experts are
+// added in ascending id order: out += w * d, skipping w == 0 (moe.rs:112-126).
+__global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const uint8_t* ws,
+                                                          float* __restrict__ out) {
+  __shared__ float dsum[kMoeMaxTopK][32];
+  const int blocks_per_tok = plan.n_embd / 32;
+  const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
+  const int cl = threadIdx.x & 31, al = threadIdx.x >> 5;
+  const int* tokpair = reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k;
+  const float* wts = reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k;
   const float* part = reinterpret_cast<const float*>(ws + plan.o_part_b);
-  float acc = 0.f;
-  for (int a = 0; a < plan.top_k; ++a) {
-    const float wv = wts[t * plan.top_k + a];
-    if (wv == 0.f) continue;  // moe.rs:112-114
-    const int p = tokpair[t * plan.top_k + a];
-    float d = 0.f;
-    for (int k = 0; k < plan.nch_b; ++k) d += part[(int64_t(p) * plan.nch_b + k) * plan.n_embd + col];
-    acc = __fadd_rn(acc, __fmul_rn(wv, d));  // out += w * d, product then sum
+  for (int a = al; a < plan.top_k; a += 8) {
+    const float* src = part + int64_t(tokpair[a]) * plan.nch_b * plan.n_embd + col0 + cl;
+    float v[kMoeMaxChunks];
+#pragma unroll
+    for (int k = 0; k < kMoeMaxChunks; ++k) v[k] = k < plan.nch_b ? src[int64_t(k) * plan.n_embd] : 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMoeMaxChunks; ++k) sum += v[k];
+    dsum[a][cl] = sum;
   }
-  out[i] = acc;
+  __syncthreads();
+  if (al == 0) {
+    float acc = 0.f;
+    for (int a = 0; a < plan.top_k; ++a) {
+      const float wv = wts[a];
+      if (wv != 0.f) acc = __fadd_rn(acc, __fmul_rn(wv, dsum[a][cl]));
+    }
+    out[int64_t(t) * plan.n_embd + col0 + cl] = acc;
+  }
 }
 
 // ------------------------------------------------------------------- host --
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static int sub_rows(int64_t rb, int cols, int chunk, int tp) {
+  const int rs = kMoeThreads / (cols >> 6);
+  // rows that fit one tile with room for the 16-byte lead
+  const int fit = int((int64_t(tp) * 16 * kMoeThreads - 16) / rb);
+  if (chunk <= fit) return chunk;  // the whole chunk in one tile
+  int sr = fit >= rs ? fit / rs * rs : fit;
+  return sr < 1 ? 1 : sr;
+}
 
 bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t qa, uint32_t qb,
               MoePlan* plan) {
@@ -354,7 +538,7 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
       n_expert > kMoeMaxExperts || n_embd <= 0 || n_ff <= 0)
     return false;
   if (!expert_shape_ok(qa, n_embd, n_ff) || !expert_shape_ok(qb, n_ff, n_embd)) return false;
-  if (n_tok > kMoeMaxTokens) return false;
+  if (n_tok > kMoeMaxTokens || n_embd % 32 != 0) return false;
   MoePlan p{};
   p.n_tok = n_tok;
   p.top_k = top_k;
@@ -365,18 +549,30 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.rb_b = byte_size(qb, n_embd);
   const int pairs = n_tok * top_k;
   p.s_max = pairs < n_expert ? pairs : n_expert;
-  // row chunks: about 128 rows per gate/up chunk and 48 per down chunk,
-  // enough workgroups to cover the chip even for a single token
-  p.nch_a = (n_embd + 127) / 128;
-  if (p.nch_a > 32) p.nch_a = 32;
-  p.chunk_a = (n_embd + p.nch_a - 1) / p.nch_a;
-  p.nch_b = (n_ff + 47) / 48;
-  if (p.nch_b > 32) p.nch_b = 32;
-  p.chunk_b = (n_ff + p.nch_b - 1) / p.nch_b;
-  // the down kernel keeps its reduction rows and a = silu(h) * p for every
-  // token of a slot in LDS
-  const size_t lds_b = (size_t(kMoeThreads / (n_embd >> 6)) * n_embd + size_t(n_tok) * p.chunk_b) * 4;
-  if (lds_b > 160 * 1024) return false;
+  // enough workgroups to cover the chip when few experts are routed, few
+  // enough chunks that the partial sums stay small when many are
+  const int rs_a = kMoeThreads / (n_ff >> 6), rs_b = kMoeThreads / (n_embd >> 6);
+  p.nch_a = std::max(1, std::min({(2048 + 2 * p.s_max - 1) / (2 * p.s_max), (n_embd + rs_a - 1) / rs_a,
+                                   kMoeMaxChunks}));
+  p.ca = (n_embd + p.nch_a - 1) / p.nch_a;
+  p.nch_a = (n_embd + p.ca - 1) / p.ca;
+  p.nch_b = std::max(1, std::min({(1024 + p.s_max - 1) / p.s_max, (n_ff + rs_b - 1) / rs_b, kMoeMaxChunks}));
+  p.cb = (n_ff + p.nch_b - 1) / p.nch_b;
+  p.nch_b = (n_ff + p.cb - 1) / p.cb;
+  const int tp = tile_pieces(n_tok == 1 ? 1 : 2);  // the kernels' tokens per pass
+  p.sr_a = sub_rows(p.rb_a, n_ff, p.ca, tp);
+  p.sr_b = sub_rows(p.rb_b, n_embd, p.cb, tp);
+  const size_t cap_a = (size_t(p.sr_a) * p.rb_a + 31) & ~size_t(15);
+  const size_t cap_b = (size_t(p.sr_b) * p.rb_b + 31) & ~size_t(15);
+  // a chunk that fits one sub-tile needs one buffer
+  const size_t nbuf_a = p.sr_a < p.ca ? 2 : 1, nbuf_b = p.sr_b < p.cb ? 2 : 1;
+  p.lds_a = nbuf_a * cap_a + sizeof(float) * (2 * size_t(p.ca) + size_t(rs_a) * (n_ff / 64) * 36);
+  p.lds_b = nbuf_b * cap_b + sizeof(float) * (6 * size_t(p.cb) + size_t(rs_b) * (n_embd / 64) * 36);
+  p.nbuf_a = int(nbuf_a);
+  p.nbuf_b = int(nbuf_b);
+  if (p.lds_a > 160 * 1024 || p.lds_b > 160 * 1024) return false;
+  if (cap_a > size_t(tp) * 16 * kMoeThreads || cap_b > size_t(tp) * 16 * kMoeThreads) return false;
+  p.route_lds = size_t(pairs) * 8;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -390,7 +586,6 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.o_slot_off = take(sizeof(int) * p.s_max);
   p.o_slot_cnt = take(sizeof(int) * p.s_max);
   p.o_pair_tok = take(sizeof(int) * pairs);
-  p.o_pair_w = take(sizeof(float) * pairs);
   p.o_tokpair = take(sizeof(int) * pairs);
   p.o_part_a = take(sizeof(float) * size_t(pairs) * 2 * p.nch_a * n_ff);
   p.o_part_b = take(sizeof(float) * size_t(pairs) * p.nch_b * n_embd);
@@ -399,22 +594,22 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   return true;
 }
 
+// one token per pass when every expert has one token (decode), two otherwise
 template <class FA>
 static void launch_gateup(const MoePlan& p, const void* gate, const void* up, const float* x,
                           uint8_t* ws, int q6g, int q6u, hipStream_t s) {
-  const size_t lds = size_t(kMoeThreads / (p.n_ff >> 6)) * p.n_ff * sizeof(float);
-  hipLaunchKernelGGL(moe_gateup_kernel<FA>, dim3(p.s_max, 2, p.nch_a), dim3(kMoeThreads), lds, s,
-                     static_cast<const uint8_t*>(gate), static_cast<const uint8_t*>(up), p, x, ws, q6g,
-                     q6u);
+  const dim3 g(p.nch_a, 2, p.s_max), b(kMoeThreads);
+  const uint8_t *gp = static_cast<const uint8_t*>(gate), *upp = static_cast<const uint8_t*>(up);
+  if (p.n_tok == 1) hipLaunchKernelGGL((moe_gateup_kernel<FA, 1>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+  else hipLaunchKernelGGL((moe_gateup_kernel<FA, 2>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
 }
 
 template <class FB>
 static void launch_down(const MoePlan& p, const void* down, uint8_t* ws, int q6d, hipStream_t s) {
-  const size_t lds = (size_t(kMoeThreads / (p.n_embd >> 6)) * p.n_embd +
-                      size_t(p.n_tok) * p.chunk_b) *
-                     sizeof(float);
-  hipLaunchKernelGGL(moe_down_kernel<FB>, dim3(p.s_max, p.nch_b), dim3(kMoeThreads), lds, s,
-                     static_cast<const uint8_t*>(down), p, ws, q6d);
+  const dim3 g(p.nch_b, p.s_max), b(kMoeThreads);
+  const uint8_t* dp = static_cast<const uint8_t*>(down);
+  if (p.n_tok == 1) hipLaunchKernelGGL((moe_down_kernel<FB, 1>), g, b, p.lds_b, s, dp, p, ws, q6d);
+  else hipLaunchKernelGGL((moe_down_kernel<FB, 2>), g, b, p.lds_b, s, dp, p, ws, q6d);
 }
 
 hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, const void* gate,
@@ -423,7 +618,8 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       hipStream_t s) {
   if (qg != qu) return hipErrorInvalidValue;  // gate and up share one kernel
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kMoeThreads), 0, s, logits, p, ws);
+  hipError_t e = launch_moe_route(p, logits, workspace, s);
+  if (e != hipSuccess) return e;
   switch (qg) {
     case kQ4_K: launch_gateup<AxQ4K>(p, gate, up, x, ws, q6g, q6u, s); break;
     case kQ8_0: launch_gateup<AxQ8>(p, gate, up, x, ws, q6g, q6u, s); break;
@@ -434,15 +630,20 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
     case kQ8_0: launch_down<AxQ8>(p, down, ws, q6d, s); break;
     default: launch_down<AxQ6K>(p, down, ws, q6d, s);
   }
-  const int64_t n = int64_t(p.n_tok) * p.n_embd;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, p, ws, out);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned(p.n_tok * (p.n_embd / 32))), dim3(256), 0, s, p,
+                     ws, out);
   return hipGetLastError();
 }
 
 // Routing alone (for the host-slice sh_moe_route): ids and weights per token.
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s) {
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kMoeThreads), 0, s, logits, p,
-                     static_cast<uint8_t*>(workspace));
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const dim3 g(1), b(kRouteThreads);
+  if (p.n_expert <= 64) hipLaunchKernelGGL(moe_route_kernel<1>, g, b, p.route_lds, s, logits, p, ws);
+  else if (p.n_expert <= 128) hipLaunchKernelGGL(moe_route_kernel<2>, g, b, p.route_lds, s, logits, p, ws);
+  else if (p.n_expert <= 256) hipLaunchKernelGGL(moe_route_kernel<4>, g, b, p.route_lds, s, logits, p, ws);
+  else if (p.n_expert <= 512) hipLaunchKernelGGL(moe_route_kernel<8>, g, b, p.route_lds, s, logits, p, ws);
+  else hipLaunchKernelGGL(moe_route_kernel<16>, g, b, p.route_lds, s, logits, p, ws);
   return hipGetLastError();
 }
 
