@@ -44,6 +44,7 @@ constexpr int kMmKC = 64;                   // K elements per chunk
 constexpr int kMmThreads = 256;
 constexpr int kMmRowB = kMmKC * 2 + 16;     // bytes per bf16 LDS row (padded)
 constexpr int kMmRowQ = kMmKC + 16;         // bytes per int8 LDS row (padded)
+constexpr int kDepth = 4;                   // weight chunks in flight ahead of staging
 
 // Two floats -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -387,10 +388,15 @@ __global__ void __launch_bounds__(kMmThreads)
     *reinterpret_cast<u32x4*>(dst + 2 * o1 + 16) = u32x4{run1[4], run1[5], run1[6], run1[7]};
   };
 
-  typename S::Raw raw{};
+  // weight chunks are requested kDepth chunks ahead of their staging: the
+  // ring slot of chunk c is c % kDepth, and the loop is unrolled by kDepth so
+  // every slot index is a constant
+  typename S::Raw raw[kDepth];
   if (stager) {
-    raw = S::load(wrow, 0, piece);
-    stage(raw, 0, wl[0]);
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    stage(raw[0], 0, wl[0]);
+    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
   }
   bf16x8 xc[2][4];
 #pragma unroll
@@ -399,38 +405,47 @@ __global__ void __launch_bounds__(kMmThreads)
     for (int s = 0; s < 4; ++s) xc[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + 8 * s);
   __syncthreads();
 
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    bf16x8 xn[2][4];
-    if (more) {
-      if (stager) raw = S::load(wrow, c + 1, piece);
+  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+    for (int j = 0; j < kDepth; ++j) {
+      const int c = c0 + j;
+      if (c < nchunks) {  // uniform
+        const bool more = c + 1 < nchunks;
+        bf16x8 xn[2][4];
+        if (more) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          xn[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + int64_t(c + 1) * kMmKC + 8 * s);
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              xn[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + int64_t(c + 1) * kMmKC + 8 * s);
+        }
+        const uint8_t* wb = wl[c & 1];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          bf16x8 bfr[3];
+#pragma unroll
+          for (int ni = 0; ni < 3; ++ni)
+            bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 3; ++ni)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xc[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
+        }
+        if (more) {
+          const int slot = (j + 1) % kDepth;  // chunk c + 1 (a constant once unrolled)
+          if (stager) {
+            stage(raw[slot], c + 1, wl[(c + 1) & 1]);
+            raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+          }
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) xc[mi][s] = xn[mi][s];
+        }
+        __syncthreads();
+      }
     }
-    const uint8_t* wb = wl[c & 1];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 bfr[3];
-#pragma unroll
-      for (int ni = 0; ni < 3; ++ni)
-        bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 3; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xc[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
-    }
-    if (more) {
-      if (stager) stage(raw, c + 1, wl[(c + 1) & 1]);
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) xc[mi][s] = xn[mi][s];
-    }
-    __syncthreads();
   }
 
   // D layout of the 32x32 MFMA: lane l holds column l % 32 (a weight row)
@@ -506,10 +521,12 @@ __global__ void __launch_bounds__(kMmThreads)
     wsc[buf][jb1][1][srow] = mj[1];
   };
 
-  typename S::Raw raw{};
+  typename S::Raw raw[kDepth];
   if (stager) {
-    raw = S::load(wrow, 0, piece);
-    stage(raw, 0, 0);
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    stage(raw[0], 0, 0);
+    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
   }
   i32x4 xc[2][2];
 #pragma unroll
@@ -518,69 +535,78 @@ __global__ void __launch_bounds__(kMmThreads)
     for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 32 * s);
   __syncthreads();
 
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    i32x4 xn[2][2];
-    if (more) {
-      if (stager) raw = S::load(wrow, c + 1, piece);
+  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+    for (int jj = 0; jj < kDepth; ++jj) {
+      const int c = c0 + jj;
+      if (c < nchunks) {  // uniform
+        const bool more = c + 1 < nchunks;
+        i32x4 xn[2][2];
+        if (more) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-          xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * kMmKC + 32 * s);
-    }
-    const int buf = c & 1;
-    const uint8_t* wb = wl[buf];
-    // min term of both blocks of the chunk on the f32 MFMA (K = 2 blocks):
-    // A[row][k] = -m of the lane's row and block k = lane half, B[k][token] = u
-    if constexpr (S::kMin) {
-      float um[2];
+          for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi) um[mi] = xu[int64_t(tok[mi]) * nblk + 2 * c + half];
-#pragma unroll
-      for (int ni = 0; ni < 3; ++ni) {
-        const float ma = -wsc[buf][half][1][32 * ni + l32];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ma, um[mi], acc[mi][ni], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {  // one 32-element block per step
-      const int j = 2 * c + s;
-      float sx[2];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) sx[mi] = xs[int64_t(tok[mi]) * nblk + j];
-#pragma unroll
-      for (int ni = 0; ni < 3; ++ni) {
-        const i32x4 a = *reinterpret_cast<const i32x4*>(wb + (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half);
-        // weight rows of this lane's registers: 32 ni + 8 (i / 4) + 4 half + i % 4
-        f32x4 dw[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dw[q] = *reinterpret_cast<const f32x4*>(&wsc[buf][s][0][32 * ni + 8 * q + 4 * half]);
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-          // volatile fences keep each integer MFMA next to its scaling, so
-          // at most one 16-register integer result is live at a time
-          i32x4 av = a;
-          asm volatile("" : "+v"(av));
-          const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, xc[mi][s], i32x16{}, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            acc[mi][ni][i] = __builtin_fmaf(float(I[i]), dw[i >> 2][i & 3] * sx[mi], acc[mi][ni][i]);
-          asm volatile("" : "+v"(acc[mi][ni]));
+            for (int s = 0; s < 2; ++s)
+              xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * kMmKC + 32 * s);
         }
+        const int buf = c & 1;
+        const uint8_t* wb = wl[buf];
+        // min term of both blocks of the chunk on the f32 MFMA (K = 2 blocks):
+        // A[row][k] = -m of the lane's row and block k = lane half, B[k][token] = u
+        if constexpr (S::kMin) {
+          float um[2];
+    #pragma unroll
+          for (int mi = 0; mi < 2; ++mi) um[mi] = xu[int64_t(tok[mi]) * nblk + 2 * c + half];
+    #pragma unroll
+          for (int ni = 0; ni < 3; ++ni) {
+            const float ma = -wsc[buf][half][1][32 * ni + l32];
+    #pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ma, um[mi], acc[mi][ni], 0, 0, 0);
+          }
+        }
+    #pragma unroll
+        for (int s = 0; s < 2; ++s) {  // one 32-element block per step
+          const int j = 2 * c + s;
+          float sx[2];
+    #pragma unroll
+          for (int mi = 0; mi < 2; ++mi) sx[mi] = xs[int64_t(tok[mi]) * nblk + j];
+    #pragma unroll
+          for (int ni = 0; ni < 3; ++ni) {
+            const i32x4 a = *reinterpret_cast<const i32x4*>(wb + (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half);
+            // weight rows of this lane's registers: 32 ni + 8 (i / 4) + 4 half + i % 4
+            f32x4 dw[4];
+    #pragma unroll
+            for (int q = 0; q < 4; ++q)
+              dw[q] = *reinterpret_cast<const f32x4*>(&wsc[buf][s][0][32 * ni + 8 * q + 4 * half]);
+    #pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+              // volatile fences keep each integer MFMA next to its scaling, so
+              // at most one 16-register integer result is live at a time
+              i32x4 av = a;
+              asm volatile("" : "+v"(av));
+              const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, xc[mi][s], i32x16{}, 0, 0, 0);
+    #pragma unroll
+              for (int i = 0; i < 16; ++i)
+                acc[mi][ni][i] = __builtin_fmaf(float(I[i]), dw[i >> 2][i & 3] * sx[mi], acc[mi][ni][i]);
+              asm volatile("" : "+v"(acc[mi][ni]));
+            }
+          }
+        }
+        if (more) {
+          const int slot = (jj + 1) % kDepth;  // chunk c + 1 (a constant once unrolled)
+          if (stager) {
+            stage(raw[slot], c + 1, (c + 1) & 1);
+            raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+          }
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
+        }
+        __syncthreads();
       }
     }
-    if (more) {
-      if (stager) stage(raw, c + 1, (c + 1) & 1);
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
-    }
-    __syncthreads();
   }
 
   // D: lane l holds column l % 32 (a token), register i the weight row
