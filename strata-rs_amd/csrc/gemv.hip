@@ -998,6 +998,11 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   if (quant == kQ8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(x) & 15u))
     return hipErrorInvalidValue;
+  // batch 1: 16 waves per CU for tall matrices whose rows are a single
+  // 4096-column window (more waves hide more latency, and each still has
+  // rows to stream); 8 otherwise (fewer workgroups stage x, and multi-window
+  // rows keep the x limbs of every window they visit)
+  const int wpc = (cols <= 4096 && rows >= 8192) ? 16 : 8;
   // x for all of the batch must fit in LDS; a larger batch runs in slices
   int per = int(kMaxLds / lds_bytes(int(cols), 1));
   if (per > 8) per = 8;
@@ -1008,15 +1013,15 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
     hipError_t e;
     switch (quant) {
       case kQ4_K:
-        e = nb == 1 ? launch_limb<LimbQ4K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8)
+        e = nb == 1 ? launch_limb<LimbQ4K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
                     : launch_nb<FmtQ4K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       case kQ8_0:
-        e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8)
+        e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
                     : launch_nb<FmtQ8>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       default:
-        e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, 8,
+        e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,
                                                   q6_signed)
                     : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
     }
