@@ -1,0 +1,238 @@
+// Batched (2..8 vectors) Q4_K matvec on int8 MFMA with exact integer
+// activations.
+//
+// Semantics: y[b][r] = sum_c W[r][c] * x[b][c] for every vector b, as
+// `batch` calls of ops::gemv (crates/strata-core/src/ops.rs:14-28) with the
+// Q4_K dequantization of crates/strata-gguf/src/dequant.rs:237-270.
+//
+// Per 32-element block j of vector b a power-of-two scale 2^-k is chosen so
+// that the block's largest |x| * 2^k < 2^22, and every element becomes the
+// integer v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c with balanced signed
+// bytes a, b, c (so all three are int8). Q4_K codes q are 0..15, so for a
+// sub-block with weights d1 * q - m1:
+//   sum_e w_e x_e = d1 * 2^-k * (2^16 sum q a + 2^8 sum q b + sum q c)
+//                   - m1 * sum_e x_e
+// and each of the three integer sums is one exact v_mfma_i32_16x16x32_i8
+// (K = 32 = one sub-block). x is represented to 2^-23 of its block's
+// maximum; only the per-block epilogue is f32.
+//
+// Mapping: a wave owns a tile of 16 weight rows (the MFMA's B columns; the
+// vectors are its A rows, padded to 16) and a share of the super-blocks;
+// a workgroup is T row tiles x S super-block shares (T * S waves), with the
+// activations' limbs for every block and vector in LDS. The S shares of a
+// row tile are added through LDS at the end. Lane l of a wave holds, in D,
+// weight row l % 16 for vectors 4 * (l / 16) + i, i < 4.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace sh {
+
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kMbMaxVec = 8;            // vectors per call
+constexpr int kMbTokStride = 40;        // LDS bytes per (limb, block, vector): 32 codes + 8 pad
+constexpr int kMbMaxCols = 4096;        // columns whose limbs fit LDS with the rest
+
+__host__ __device__ inline int mb_limb_bytes(int nblk) { return 3 * nblk * kMbMaxVec * kMbTokStride; }
+
+// Balanced signed-byte digits of an integer |v| < 2^22.
+__device__ __forceinline__ void balanced_digits(int v, int& a, int& b, int& c) {
+  c = ((v + 128) & 255) - 128;
+  const int v1 = (v - c) >> 8;
+  b = ((v1 + 128) & 255) - 128;
+  a = (v1 - b) >> 8;
+}
+
+template <int PER>
+__global__ void __launch_bounds__(512)
+    gemv_mfma_q4k_kernel(const uint8_t* __restrict__ w, int rows, int cols, int64_t row_bytes,
+                         const float* __restrict__ x, float* __restrict__ y, int nb, int T, int S) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nthreads = blockDim.x;
+  const int nblk = cols >> 5, nsb = cols >> 8;
+  uint8_t* limbs = lds;                                                  // [3][nblk][8][40]
+  float* pk = reinterpret_cast<float*>(lds + mb_limb_bytes(nblk));      // [nblk][8]: 2^-k
+  float* sx = pk + nblk * kMbMaxVec;                                     // [nblk][8]: sum of x
+  float* red = sx + nblk * kMbMaxVec;                                    // [T][S][64][4]
+
+  // ---- activations -> limbs: one (vector, block) pair per thread per round
+  for (int p = tid; p < nb * nblk; p += nthreads) {
+    const int b = p / nblk, j = p - b * nblk;
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + int64_t(b) * cols + 32 * j);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const f32x4 t = src[k];
+      v[4 * k] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+    float m = 0.f, s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      m = fmaxf(m, fabsf(v[k]));
+      s += v[k];
+    }
+    int e = 0;
+    (void)frexpf(m, &e);
+    const int kk = m > 0.f ? min(22 - e, 126) : 0;
+    const float up = ldexpf(1.f, kk);
+    pk[j * kMbMaxVec + b] = (m - m == 0.f) ? ldexpf(1.f, -kk) : __builtin_nanf("");
+    sx[j * kMbMaxVec + b] = s;
+    uint32_t wa[8], wb[8], wc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t pa = 0, pb = 0, pc = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
+        const float t = __builtin_fmaf(v[4 * k + q], up, 12582912.0f);
+        const int iv = int(__builtin_bit_cast(uint32_t, t) - 0x4B400000u);
+        int da, db, dc;
+        balanced_digits(iv, da, db, dc);
+        pa |= (uint32_t(da) & 0xFFu) << (8 * q);
+        pb |= (uint32_t(db) & 0xFFu) << (8 * q);
+        pc |= (uint32_t(dc) & 0xFFu) << (8 * q);
+      }
+      wa[k] = pa;
+      wb[k] = pb;
+      wc[k] = pc;
+    }
+    uint8_t* da = limbs + (0 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+    uint8_t* db = limbs + (1 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+    uint8_t* dc = limbs + (2 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      *reinterpret_cast<uint64_t*>(da + 4 * k) = uint64_t(wa[k]) | (uint64_t(wa[k + 1]) << 32);
+      *reinterpret_cast<uint64_t*>(db + 4 * k) = uint64_t(wb[k]) | (uint64_t(wb[k + 1]) << 32);
+      *reinterpret_cast<uint64_t*>(dc + 4 * k) = uint64_t(wc[k]) | (uint64_t(wc[k + 1]) << 32);
+    }
+  }
+  __syncthreads();
+
+  // ---- this wave's row tile and super-block share
+  const int rt = wave % T, sh_ = wave / T;
+  const int sb0 = sh_ * PER, sb1 = min(nsb, sb0 + PER);
+  const int r16 = lane & 15, kg = lane >> 4;  // B column (weight row) and k group
+  const int row = min(blockIdx.x * (16 * T) + 16 * rt + r16, rows - 1);
+  const uint8_t* wr = w + int64_t(row) * row_bytes;
+  const int tok_a = r16;            // the vector this lane feeds as an A row
+  const bool a_real = tok_a < nb;
+  const int tok_d = 4 * kg;         // first vector of this lane's D values
+  const bool d_real = tok_d < nb;   // (kg 2, 3 hold padding vectors)
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  u32x4 h_cur, h_nxt;
+  uint64_t q_cur[4], q_nxt[4];
+  auto load_sb = [&](int sb, u32x4& h, uint64_t* q) {
+    const uint8_t* p = wr + int64_t(min(sb, nsb - 1)) * 144;
+    h = ld16(p);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const uint64_t*>(p + 16 + 32 * g + 8 * kg);
+  };
+  if (sb0 < sb1) load_sb(sb0, h_cur, q_cur);
+  for (int sb = sb0; sb < sb1; ++sb) {
+    load_sb(sb + 1, h_nxt, q_nxt);  // the next super-block in flight (past the share: valid, unused)
+    const float d = h2f(h_cur.x), dm = h2f(h_cur.x >> 16);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // scales and mins of sub-blocks 2g, 2g + 1 (get_scale_min_k4)
+      const uint32_t shv = (g & 1) << 4;
+      const uint32_t t1 = h_cur.y >> shv, t2 = h_cur.z >> shv, t3 = h_cur.w >> shv;
+      const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+      const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int jb = 8 * sb + 2 * g + hh;  // 32-element block of this sub-block
+        const uint64_t codes = hh ? ((q_cur[g] >> 4) & 0x0F0F0F0F0F0F0F0Full) : (q_cur[g] & 0x0F0F0F0F0F0F0F0Full);
+        long A[3];
+#pragma unroll
+        for (int l = 0; l < 3; ++l) {
+          const uint8_t* src = limbs + (l * nblk + jb) * (kMbMaxVec * kMbTokStride) + tok_a * kMbTokStride + 8 * kg;
+          A[l] = a_real ? *reinterpret_cast<const long*>(src) : 0l;
+        }
+        const i32x4v Ia = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[0], long(codes), i32x4v{}, 0, 0, 0);
+        const i32x4v Ib = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[1], long(codes), i32x4v{}, 0, 0, 0);
+        const i32x4v Ic = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[2], long(codes), i32x4v{}, 0, 0, 0);
+        const float dsc = d * ubyte<0>(hh ? (scp >> 8) : scp), dmm = dm * ubyte<0>(hh ? (mp >> 8) : mp);
+        f32x4 pk4 = {0.f, 0.f, 0.f, 0.f}, sx4 = {0.f, 0.f, 0.f, 0.f};
+        if (d_real) {
+          pk4 = *reinterpret_cast<const f32x4*>(pk + jb * kMbMaxVec + tok_d);
+          sx4 = *reinterpret_cast<const f32x4*>(sx + jb * kMbMaxVec + tok_d);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float f = __builtin_fmaf(float(Ia[k]), 65536.f, float(Ib[k] * 256 + Ic[k]));
+          acc[k] = __builtin_fmaf(f, dsc * pk4[k], acc[k]);
+          acc[k] = __builtin_fmaf(-dmm, sx4[k], acc[k]);
+        }
+      }
+    }
+    h_cur = h_nxt;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q_cur[g] = q_nxt[g];
+  }
+
+  // ---- add the S shares of each row tile, in share order
+  float* mine = red + ((rt * S + sh_) * 64 + lane) * 4;
+  *reinterpret_cast<f32x4*>(mine) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  __syncthreads();
+  if (sh_ == 0) {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    for (int s2 = 0; s2 < S; ++s2) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(red + ((rt * S + s2) * 64 + lane) * 4);
+      t = f32x4{t.x + v.x, t.y + v.y, t.z + v.z, t.w + v.w};
+    }
+    const int r = blockIdx.x * (16 * T) + 16 * rt + r16;
+    if (r < rows) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok_d + i < nb) y[int64_t(tok_d + i) * rows + r] = t[i];
+    }
+  }
+}
+
+bool gemv_mfma_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
+  return quant == kQ4_K && batch >= 2 && batch <= kMbMaxVec && cols % 256 == 0 && cols <= kMbMaxCols &&
+         rows > 0 && rows <= (int64_t(1) << 31) - 1;
+}
+
+template <int PER>
+static void launch_mb(const void* wv, int64_t rows, int64_t cols, const float* x, float* y, int batch, int T,
+                      int S, size_t lds, hipStream_t s) {
+  const unsigned blocks = unsigned((rows + 16 * T - 1) / (16 * T));
+  hipLaunchKernelGGL(gemv_mfma_q4k_kernel<PER>, dim3(blocks), dim3(64 * T * S), lds, s,
+                     static_cast<const uint8_t*>(wv), int(rows), int(cols), byte_size(kQ4_K, cols), x, y, batch,
+                     T, S);
+}
+
+hipError_t launch_gemv_mfma(const void* wv, int64_t rows, int64_t cols, const float* x, float* y, int batch,
+                            int cu, hipStream_t s) {
+  if (!gemv_mfma_ok(kQ4_K, rows, cols, batch)) return hipErrorInvalidValue;
+  // T row tiles per workgroup so the tiles cover the CUs about once; the
+  // rest of 8 waves split the super-blocks into shares of PER <= 8
+  int T = int((rows + 16LL * cu - 1) / (16LL * cu));
+  if (T < 1) T = 1;
+  if (T > 4) T = 4;
+  const int S = T >= 3 ? 2 : 8 / T;  // T * S <= 8 waves
+  const int nsb = int(cols / 256);
+  const int per = (nsb + S - 1) / S;  // <= 8: cols <= 4096 and S >= 2
+  const int nblk = int(cols / 32);
+  const size_t lds = size_t(mb_limb_bytes(nblk)) + 2 * sizeof(float) * nblk * kMbMaxVec +
+                     sizeof(float) * T * S * 64 * 4;
+  switch (per) {
+    case 1: launch_mb<1>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 2: launch_mb<2>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 3: launch_mb<3>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 4: launch_mb<4>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 5: launch_mb<5>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 6: launch_mb<6>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    case 7: launch_mb<7>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+    default: launch_mb<8>(wv, rows, cols, x, y, batch, T, S, lds, s); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sh
