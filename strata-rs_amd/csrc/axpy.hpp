@@ -215,4 +215,180 @@ struct AxQ6K {
   __device__ static __forceinline__ int off_index(int e) { return e >> 4; }
 };
 
+// ------------------------------------------------------- half units --
+// The same axpy for 32-column half units (one Q4_K sub-block, one Q8_0
+// block, half a Q6_K quarter), with the codes decoded four at a time next to
+// the FMAs that use them: 32 column sums per token instead of 64, and no
+// decoded row held in registers, so that several waves fit per SIMD.
+// Half unit hu covers columns [32 hu, 32 hu + 32).
+struct HxQ4K {
+  static constexpr int kOff = 1;
+  struct Raw {
+    u32x4 h, a, b;  // header, the group's 32 code bytes
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int hu) {
+    const int u = hu >> 1;
+    const uint8_t* sb = row + (u >> 2) * 144;
+    const int g = u & 3;
+    return {ld16u(sb), ld16u(sb + 16 + 32 * g), ld16u(sb + 32 + 32 * g)};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int hu, const float* xi, float (*acc)[32],
+                                               float (*off)[kOff], int) {
+    const int u = hu >> 1, g = u & 3;
+    const uint32_t hi = uint32_t(hu & 1);  // high nibbles: sub-block 2g + 1
+    const u32x4 h = r.h;
+    const uint32_t sh = (g & 1) << 4;
+    const uint32_t t1 = h.y >> sh, t2 = h.z >> sh, t3 = h.w >> sh;
+    // get_scale_min_k4 for sub-blocks 2g (byte 0) and 2g + 1 (byte 1)
+    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+    const float d = h2f(h.x), dm = h2f(h.x >> 16);
+    const float scf = float((scp >> (8 * hi)) & 0xFFu), mf = float((mp >> (8 * hi)) & 0xFFu);
+    // high nibbles are read in place as 16 * q, so their scale carries 1/16 (exact)
+    const float dsc = d * scf * (hi ? 0.0625f : 1.f), dmm = dm * mf;
+    const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    float c[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      // a zero input contributes nothing, whatever the scales hold (ops.rs:182-184)
+      c[t] = xi[t] == 0.f ? 0.f : xi[t] * dsc;
+      off[t][0] += xi[t] == 0.f ? 0.f : xi[t] * dmm;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t v = q[k] & mask;
+      const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][4 * k + 0] = __builtin_fmaf(c[t], w0, acc[t][4 * k + 0]);
+        acc[t][4 * k + 1] = __builtin_fmaf(c[t], w1, acc[t][4 * k + 1]);
+        acc[t][4 * k + 2] = __builtin_fmaf(c[t], w2, acc[t][4 * k + 2]);
+        acc[t][4 * k + 3] = __builtin_fmaf(c[t], w3, acc[t][4 * k + 3]);
+      }
+    }
+  }
+  __device__ static __forceinline__ int off_index(int) { return 0; }
+};
+
+// Q8_0: half unit hu is block hu (34 bytes from a 2-byte boundary), read as
+// nine dwords from the dword boundary at or below it. The codes are biased to
+// q + 128 for the unsigned conversion; 128 * coefficient goes to the offset.
+struct HxQ8 {
+  static constexpr int kOff = 1;
+  struct Raw {
+    u32x4 a, b;
+    uint32_t c, s;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int hu) {
+    const uint8_t* blk = row + hu * 34;
+    const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    const uint8_t* base = blk - s;
+    return {ld16u(base), ld16u(base + 16), ld4(base + 32), s};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int, const float* xi, float (*acc)[32],
+                                               float (*off)[kOff], int) {
+    const uint32_t D[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+    const bool s2 = r.s != 0;  // the block starts at byte 2 of D[0]
+    const float d = h2f(s2 ? (D[0] >> 16) : D[0]);
+    float c[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      c[t] = xi[t] == 0.f ? 0.f : xi[t] * d;  // ops.rs:182-184
+      off[t][0] += 128.f * c[t];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // codes are bytes 2..33 of the block
+      const uint32_t v = (s2 ? D[k + 1] : realign(D[k], D[k + 1], 2)) ^ 0x80808080u;
+      const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][4 * k + 0] = __builtin_fmaf(c[t], w0, acc[t][4 * k + 0]);
+        acc[t][4 * k + 1] = __builtin_fmaf(c[t], w1, acc[t][4 * k + 1]);
+        acc[t][4 * k + 2] = __builtin_fmaf(c[t], w2, acc[t][4 * k + 2]);
+        acc[t][4 * k + 3] = __builtin_fmaf(c[t], w3, acc[t][4 * k + 3]);
+      }
+    }
+  }
+  __device__ static __forceinline__ int off_index(int) { return 0; }
+};
+
+// Q6_K: half unit hu is half p = hu & 1 of quarter j = (hu >> 1) & 3 of
+// super-block hu >> 3 (the quarters as in AxQ6K: half hh = j >> 1, nibble
+// tp = j & 1). Its 32 columns take code bytes ql[64 hh + 32 p + l] (nibble
+// tp) and qh[32 hh + l] bits 4 tp + 2 p (l < 32), and the two 16-column
+// scales sc[8 hh + 4 tp + 2 p + {0, 1}].
+struct HxQ6K {
+  static constexpr int kOff = 2;
+  struct Raw {
+    u32x4 l0, l1, h0, h1;
+    uint32_t l2, h2, sc, d, s;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int hu) {
+    const int u = hu >> 1, p = hu & 1;
+    const uint8_t* blk = row + (u >> 2) * 210;
+    const int j = u & 3, hh = j >> 1, tp = j & 1;
+    const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    const uint8_t* base = blk - s;
+    const uint8_t* qlp = base + 64 * hh + 32 * p;
+    const uint8_t* qhp = base + 128 + 32 * hh;
+    Raw r;
+    r.l0 = ld16u(qlp);
+    r.l1 = ld16u(qlp + 16);
+    r.l2 = ld4(qlp + 32);  // ends at most at byte 131 of the block
+    r.h0 = ld16u(qhp);
+    r.h1 = ld16u(qhp + 16);
+    r.h2 = ld4(qhp + 32);  // ends at most at byte 195
+    // sc[8 hh + 4 tp + 2 p] and the next byte: bytes [s + 192 + off, +2) of base
+    const int so = int(s) + 192 + 8 * hh + 4 * tp + 2 * p;  // even, <= 208
+    const uint32_t sw = ld4(base + (so & ~3));
+    r.sc = (so & 2) ? (sw >> 16) : (sw & 0xFFFFu);
+    r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    r.s = s;
+    return r;
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int hu, const float* xi, float (*acc)[32],
+                                               float (*off)[kOff], int q6_signed) {
+    const int u = hu >> 1, p = hu & 1, tp = u & 1;
+    const uint32_t s = r.s;
+    const float d = h2f(r.d);
+    const uint32_t b0 = r.sc & 0xFFu, b1 = (r.sc >> 8) & 0xFFu;
+    const float sc0 = q6_signed ? float(int8_t(b0)) : float(b0);
+    const float sc1 = q6_signed ? float(int8_t(b1)) : float(b1);
+    const float ds0 = d * sc0, ds1 = d * sc1;
+    const uint32_t qlr[9] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l1.x, r.l1.y, r.l1.z, r.l1.w, r.l2};
+    const uint32_t qhr[9] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w, r.h2};
+    const uint32_t nib = 4u * uint32_t(tp);
+    const uint32_t hsh = uint32_t(4 * tp + 2 * p);  // qh bits of this half
+    float c0[NT], c1[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      c0[t] = xi[t] == 0.f ? 0.f : xi[t] * ds0;  // ops.rs:182-184
+      c1[t] = xi[t] == 0.f ? 0.f : xi[t] * ds1;
+      off[t][0] += 32.f * c0[t];
+      off[t][1] += 32.f * c1[t];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t ql = realign(qlr[k], qlr[k + 1], s);
+      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
+      const uint32_t v = ((ql >> nib) & 0x0F0F0F0Fu) | (((qh >> hsh) & 0x03030303u) << 4);
+      const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float cc = k < 4 ? c0[t] : c1[t];  // columns 0-15: sc0, 16-31: sc1
+        acc[t][4 * k + 0] = __builtin_fmaf(cc, w0, acc[t][4 * k + 0]);
+        acc[t][4 * k + 1] = __builtin_fmaf(cc, w1, acc[t][4 * k + 1]);
+        acc[t][4 * k + 2] = __builtin_fmaf(cc, w2, acc[t][4 * k + 2]);
+        acc[t][4 * k + 3] = __builtin_fmaf(cc, w3, acc[t][4 * k + 3]);
+      }
+    }
+  }
+  __device__ static __forceinline__ int off_index(int e) { return e >> 4; }
+};
+
 }  // namespace sh

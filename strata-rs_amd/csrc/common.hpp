@@ -80,6 +80,45 @@ __device__ __forceinline__ uint32_t ld4_stream(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
 
+// s_waitcnt vmcnt(N) (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at
+// their maxima), with the scheduler kept from moving memory operations across.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// vmcnt(n) for a wave-uniform n: at most n of this wave's vector memory
+// operations (loads, and global_load_lds copies, which complete in order)
+// remain outstanding. n above 15 waits for 15 (stricter).
+__device__ __forceinline__ void wait_vmem(int n) {
+  switch (n) {
+    case 0: wait_vmem<0>(); break;
+    case 1: wait_vmem<1>(); break;
+    case 2: wait_vmem<2>(); break;
+    case 3: wait_vmem<3>(); break;
+    case 4: wait_vmem<4>(); break;
+    case 5: wait_vmem<5>(); break;
+    case 6: wait_vmem<6>(); break;
+    case 7: wait_vmem<7>(); break;
+    case 8: wait_vmem<8>(); break;
+    case 9: wait_vmem<9>(); break;
+    case 10: wait_vmem<10>(); break;
+    case 11: wait_vmem<11>(); break;
+    case 12: wait_vmem<12>(); break;
+    case 13: wait_vmem<13>(); break;
+    case 14: wait_vmem<14>(); break;
+    default: wait_vmem<15>();
+  }
+}
+
+// 16 bytes a lane from global `src` (per lane) to LDS at `dst` + 16 * lane,
+// `dst` wave-uniform, without passing through registers (global_load_lds).
+__device__ __forceinline__ void copy16_to_lds(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
 // bytes [shift, shift + 4) of the 8-byte little-endian pair (lo, hi).
 __device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
   return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);

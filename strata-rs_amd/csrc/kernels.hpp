@@ -48,6 +48,7 @@ struct MoePlan {
   int cb, nch_b;                 // down: rows per chunk, chunks (over n_ff)
   int sr_a, sr_b;                // rows per LDS sub-tile
   int nbuf_a, nbuf_b;            // LDS sub-tile buffers (1 when one sub-tile holds the chunk)
+  int reg_a, reg_b;              // LDS bytes of the sub-tiles, reused for the row-slot reduction
   size_t o_ids, o_wts, o_meta, o_slot_e, o_slot_off, o_slot_cnt, o_pair_tok, o_tokpair;
   size_t o_part_a;               // [pair][2][nch_a][n_ff]: chunk sums of gate . x, up . x
   size_t o_part_b;               // [pair][nch_b][n_embd]: chunk sums of down . a

@@ -236,10 +236,9 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
 // tensor's end is copied byte by byte. Returns the lead (src & 15). Loads
 // are issued into registers first (`pieces` per thread at most), then
 // stored, so they are all in flight together.
-// 16-byte pieces per thread per tile: 4 (16 KiB tiles) for one token per
-// pass, where many short tiles overlap loads with compute best; 8 (32 KiB)
-// for two, where fewer, longer tiles do
-constexpr int tile_pieces(int nt) { return nt == 1 ? 4 : 8; }
+// 16-byte pieces per thread per tile (16 KiB tiles): small enough that
+// four workgroups share a CU's LDS
+constexpr int kTilePieces = 4;
 
 template <int TP>
 struct TileLoad {
@@ -287,33 +286,35 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const TileLoad<TP>& t) 
 
 // Column sums of one row chunk, for NT (1 or 2) input vectors at once
 // (nt <= NT of them in use). The chunk (rows [r0, r0 + nrows) of W) is
-// streamed through two LDS sub-tiles of `sr` rows; thread (unit u = tid % U,
-// slot sl = tid / U) applies rows sl, sl + RS, ... of each sub-tile to the
-// inputs, reading the next row from LDS while applying the current one. The
-// inputs' values for the chunk's rows are xs0[r], xs1[r]. The slots' sums are
-// reduced through `red` (RS * U * 36 floats) half a unit at a time, and the
+// streamed through two LDS sub-tiles of `sr` rows; thread (half unit
+// u = tid % U of 32 columns, slot sl = tid / U) applies rows sl, sl + RS, ...
+// of each sub-tile to the inputs. The inputs' values for the chunk's rows are
+// xs0[r], xs1[r]. The slots' sums are then reduced through the sub-tiles'
+// LDS (`tiles`, at least RS * U * 20 floats), 16 columns a round, and the
 // column sums of input t go to out_t[col].
 // `pre()` runs after the first sub-tile's loads are issued and before they
 // are stored, so input staging overlaps the first weight bytes' latency.
+constexpr int kRedStride = 20;  // floats per (slot, half unit) in a round: 16 sums + 4 pad
+
 template <class F, int NT, class Pre>
 __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t w_off, int64_t w_total, int cols,
                            int nrows, int sr, const float* xs0, const float* xs1, int nt, uint8_t* tiles,
-                           int tile_cap, float* red, float* out0, float* out1, int q6s, Pre pre) {
+                           int tile_cap, float* out0, float* out1, int q6s, Pre pre) {
   const int tid = threadIdx.x;
-  const int U = cols >> 6, RS = kMoeThreads / U;
+  const int U = cols >> 5, RS = kMoeThreads / U;
   const int u = tid % U, sl = tid / U;
   const bool active = sl < RS;
-  float acc[NT][64];
+  float acc[NT][32];
   float off[NT][F::kOff];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int e = 0; e < 64; ++e) acc[t][e] = 0.f;
+    for (int e = 0; e < 32; ++e) acc[t][e] = 0.f;
 #pragma unroll
     for (int k = 0; k < F::kOff; ++k) off[t][k] = 0.f;
   }
   const int nsub = (nrows + sr - 1) / sr;
-  TileLoad<tile_pieces(NT)> tl;
+  TileLoad<kTilePieces> tl;
   tile_issue(W, w_off, int64_t(min(sr, nrows)) * rb, w_total, tl);
   pre();
   tile_store(tiles, tl);
@@ -329,25 +330,24 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
     }
     const uint8_t* tile = tiles + (sb & 1) * tile_cap + lead;
     const int rows_here = min(sr, nrows - sb * sr);
-    if (active && sl < rows_here) {
-      typename F::Raw cur = F::load(tile + int64_t(sl) * rb, u);
+    if (active) {
       for (int r = sl; r < rows_here; r += RS) {
-        const typename F::Raw nxt = F::load(tile + int64_t(min(r + RS, rows_here - 1)) * rb, u);
         const int rr = sb * sr + r;
         float xi[NT];
         xi[0] = xs0[rr];
         if constexpr (NT > 1) xi[1] = nt > 1 ? xs1[rr] : 0.f;
-        F::template apply<NT>(cur, u, xi, acc, off, q6s);
-        cur = nxt;
+        if (xi[0] == 0.f && (NT == 1 || xi[NT - 1] == 0.f)) continue;  // ops.rs:182-184
+        F::template apply<NT>(F::load(tile + int64_t(r) * rb, u), u, xi, acc, off, q6s);
       }
     }
     if (more) tile_store(tiles + ((sb + 1) & 1) * tile_cap, tl);
     lead = next_lead;
     __syncthreads();
   }
-  // red rows: half a unit (32 sums) per unit, padded to 36 floats so lanes of
-  // neighbouring units write to different banks
-  const int rstride = U * 36;
+  // the sub-tiles are free now: slot sums of 16 columns a round go through
+  // them, (slot, half unit) rows 20 floats apart so neighbouring threads'
+  // 16-byte writes fall in different banks
+  float* red = reinterpret_cast<float*>(tiles);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t >= nt) break;  // uniform: nt is the same for the whole workgroup
@@ -355,23 +355,23 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       if (active) {
-        float* dst = red + sl * rstride + 36 * u;
+        float* dst = red + (sl * U + u) * kRedStride;
 #pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-          const int g = 32 * h + e;
+        for (int e = 0; e < 16; e += 4) {
+          const int g = 16 * h + e;
           *reinterpret_cast<f32x4*>(dst + e) =
               f32x4{acc[t][g] - off[t][F::off_index(g)], acc[t][g + 1] - off[t][F::off_index(g + 1)],
                     acc[t][g + 2] - off[t][F::off_index(g + 2)], acc[t][g + 3] - off[t][F::off_index(g + 3)]};
         }
       }
       __syncthreads();
-      for (int q = tid; q < U * 32; q += kMoeThreads) {
-        const int un = q >> 5, e = q & 31;
-        const float* src = red + 36 * un + e;
+      for (int q = tid; q < U * 16; q += kMoeThreads) {
+        const int un = q >> 4, e = q & 15;
+        const float* src = red + un * kRedStride + e;
         float v = 0.f;
 #pragma unroll 8
-        for (int k = 0; k < RS; ++k) v += src[k * rstride];
-        o[64 * un + 32 * h + e] = v;
+        for (int k = 0; k < RS; ++k) v += src[k * U * kRedStride];
+        o[32 * un + 16 * h + e] = v;
       }
       __syncthreads();
     }
@@ -398,8 +398,7 @@ __global__ void __launch_bounds__(kMoeThreads)
   const int r0 = c * plan.ca, nrows = min(plan.ca, plan.n_embd - r0);
   const int tile_cap = (plan.sr_a * int(plan.rb_a) + 31) & ~15;
   uint8_t* tiles = smem;
-  float* xs = reinterpret_cast<float*>(smem + plan.nbuf_a * tile_cap);  // [2][ca]
-  float* red = xs + 2 * plan.ca;
+  float* xs = reinterpret_cast<float*>(smem + plan.reg_a);  // [2][ca]
   const uint8_t* W = m == 0 ? gate : up;
   const int64_t w_total = int64_t(plan.n_expert) * plan.n_embd * plan.rb_a;
   const int64_t w_off = (int64_t(e) * plan.n_embd + r0) * plan.rb_a;
@@ -415,7 +414,7 @@ __global__ void __launch_bounds__(kMoeThreads)
     float* o0 = part + ((int64_t(p0 + j) * 2 + m) * plan.nch_a + c) * plan.n_ff;
     float* o1 = o0 + int64_t(2) * plan.nch_a * plan.n_ff;
     chunk_sums<F, NT>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt, tiles,
-                  tile_cap, red, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
+                      tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
   }
 }
 
@@ -439,9 +438,8 @@ __global__ void __launch_bounds__(kMoeThreads)
   const int r0 = c * plan.cb, nrows = min(plan.cb, plan.n_ff - r0);
   const int tile_cap = (plan.sr_b * int(plan.rb_b) + 31) & ~15;
   uint8_t* tiles = smem;
-  float* xs = reinterpret_cast<float*>(smem + plan.nbuf_b * tile_cap);  // [2][cb]
+  float* xs = reinterpret_cast<float*>(smem + plan.reg_b);  // [2][cb]
   float* hp = xs + 2 * plan.cb;                                 // [2][2][cb]
-  float* red = hp + 4 * plan.cb;
   const int64_t w_total = int64_t(plan.n_expert) * plan.n_ff * plan.rb_b;
   const int64_t w_off = (int64_t(e) * plan.n_ff + r0) * plan.rb_b;
   const int tid = threadIdx.x, sub = tid & 3;
@@ -482,7 +480,7 @@ __global__ void __launch_bounds__(kMoeThreads)
     float* o0 = part + (int64_t(p0 + j) * plan.nch_b + c) * plan.n_embd;
     float* o1 = o0 + int64_t(plan.nch_b) * plan.n_embd;
     chunk_sums<F, NT>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
-                  tiles, tile_cap, red, o0, o1, q6_down, stage_a);
+                      tiles, tile_cap, o0, o1, q6_down, stage_a);
   }
 }
 
@@ -524,7 +522,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const ui
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 static int sub_rows(int64_t rb, int cols, int chunk, int tp) {
-  const int rs = kMoeThreads / (cols >> 6);
+  const int rs = kMoeThreads / (cols >> 5);
   // rows that fit one tile with room for the 16-byte lead
   const int fit = int((int64_t(tp) * 16 * kMoeThreads - 16) / rb);
   if (chunk <= fit) return chunk;  // the whole chunk in one tile
@@ -539,6 +537,8 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
     return false;
   if (!expert_shape_ok(qa, n_embd, n_ff) || !expert_shape_ok(qb, n_ff, n_embd)) return false;
   if (n_tok > kMoeMaxTokens || n_embd % 32 != 0) return false;
+  // one thread per 32-column half unit of a row at least
+  if (n_ff > 32 * kMoeThreads || n_embd > 32 * kMoeThreads) return false;
   MoePlan p{};
   p.n_tok = n_tok;
   p.top_k = top_k;
@@ -551,7 +551,7 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.s_max = pairs < n_expert ? pairs : n_expert;
   // enough workgroups to cover the chip when few experts are routed, few
   // enough chunks that the partial sums stay small when many are
-  const int rs_a = kMoeThreads / (n_ff >> 6), rs_b = kMoeThreads / (n_embd >> 6);
+  const int rs_a = kMoeThreads / (n_ff >> 5), rs_b = kMoeThreads / (n_embd >> 5);
   p.nch_a = std::max(1, std::min({(2048 + 2 * p.s_max - 1) / (2 * p.s_max), (n_embd + rs_a - 1) / rs_a,
                                    kMoeMaxChunks}));
   p.ca = (n_embd + p.nch_a - 1) / p.nch_a;
@@ -559,15 +559,21 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.nch_b = std::max(1, std::min({(1024 + p.s_max - 1) / p.s_max, (n_ff + rs_b - 1) / rs_b, kMoeMaxChunks}));
   p.cb = (n_ff + p.nch_b - 1) / p.nch_b;
   p.nch_b = (n_ff + p.cb - 1) / p.cb;
-  const int tp = tile_pieces(n_tok == 1 ? 1 : 2);  // the kernels' tokens per pass
+  const int tp = kTilePieces;
   p.sr_a = sub_rows(p.rb_a, n_ff, p.ca, tp);
   p.sr_b = sub_rows(p.rb_b, n_embd, p.cb, tp);
   const size_t cap_a = (size_t(p.sr_a) * p.rb_a + 31) & ~size_t(15);
   const size_t cap_b = (size_t(p.sr_b) * p.rb_b + 31) & ~size_t(15);
   // a chunk that fits one sub-tile needs one buffer
   const size_t nbuf_a = p.sr_a < p.ca ? 2 : 1, nbuf_b = p.sr_b < p.cb ? 2 : 1;
-  p.lds_a = nbuf_a * cap_a + sizeof(float) * (2 * size_t(p.ca) + size_t(rs_a) * (n_ff / 64) * 36);
-  p.lds_b = nbuf_b * cap_b + sizeof(float) * (6 * size_t(p.cb) + size_t(rs_b) * (n_embd / 64) * 36);
+  // the sub-tiles' LDS is reused for the row-slot reduction (16 columns a round)
+  const size_t red_a = sizeof(float) * size_t(rs_a) * (n_ff / 32) * kRedStride;
+  const size_t red_b = sizeof(float) * size_t(rs_b) * (n_embd / 32) * kRedStride;
+  const size_t reg_a = std::max(nbuf_a * cap_a, red_a), reg_b = std::max(nbuf_b * cap_b, red_b);
+  p.reg_a = int(reg_a);
+  p.reg_b = int(reg_b);
+  p.lds_a = reg_a + sizeof(float) * 2 * size_t(p.ca);
+  p.lds_b = reg_b + sizeof(float) * 6 * size_t(p.cb);
   p.nbuf_a = int(nbuf_a);
   p.nbuf_b = int(nbuf_b);
   if (p.lds_a > 160 * 1024 || p.lds_b > 160 * 1024) return false;
@@ -621,14 +627,14 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
   hipError_t e = launch_moe_route(p, logits, workspace, s);
   if (e != hipSuccess) return e;
   switch (qg) {
-    case kQ4_K: launch_gateup<AxQ4K>(p, gate, up, x, ws, q6g, q6u, s); break;
-    case kQ8_0: launch_gateup<AxQ8>(p, gate, up, x, ws, q6g, q6u, s); break;
-    default: launch_gateup<AxQ6K>(p, gate, up, x, ws, q6g, q6u, s);
+    case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, s); break;
+    case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, s); break;
+    default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, s);
   }
   switch (qd) {
-    case kQ4_K: launch_down<AxQ4K>(p, down, ws, q6d, s); break;
-    case kQ8_0: launch_down<AxQ8>(p, down, ws, q6d, s); break;
-    default: launch_down<AxQ6K>(p, down, ws, q6d, s);
+    case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
+    case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
+    default: launch_down<HxQ6K>(p, down, ws, q6d, s);
   }
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned(p.n_tok * (p.n_embd / 32))), dim3(256), 0, s, p,
                      ws, out);
