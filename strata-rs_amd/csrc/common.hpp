@@ -112,6 +112,17 @@ __device__ __forceinline__ void wait_vmem(int n) {
   }
 }
 
+// Workgroup barrier after this wave's LDS writes have completed, without
+// waiting for outstanding global loads or global_load_lds copies (which
+// __syncthreads() drains): for pipelines that keep copies in flight across
+// barriers and wait for them with wait_vmem().
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt((15 << 0) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // 16 bytes a lane from global `src` (per lane) to LDS at `dst` + 16 * lane,
 // `dst` wave-uniform, without passing through registers (global_load_lds).
 __device__ __forceinline__ void copy16_to_lds(const uint8_t* src, uint8_t* dst) {

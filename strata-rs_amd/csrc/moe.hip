@@ -239,6 +239,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
 // 16-byte pieces per thread per tile (16 KiB tiles): small enough that
 // four workgroups share a CU's LDS
 constexpr int kTilePieces = 4;
+constexpr int kRing = 3;  // sub-tile slots of the copy ring
 
 template <int TP>
 struct TileLoad {
@@ -296,7 +297,7 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const TileLoad<TP>& t) 
 // are stored, so input staging overlaps the first weight bytes' latency.
 constexpr int kRedStride = 20;  // floats per (slot, half unit) in a round: 16 sums + 4 pad
 
-template <class F, int NT, class Pre>
+template <class F, int NT, bool DMA, class Pre>
 __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t w_off, int64_t w_total, int cols,
                            int nrows, int sr, const float* xs0, const float* xs1, int nt, uint8_t* tiles,
                            int tile_cap, float* out0, float* out1, int q6s, Pre pre) {
@@ -314,35 +315,77 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
     for (int k = 0; k < F::kOff; ++k) off[t][k] = 0.f;
   }
   const int nsub = (nrows + sr - 1) / sr;
-  TileLoad<kTilePieces> tl;
-  tile_issue(W, w_off, int64_t(min(sr, nrows)) * rb, w_total, tl);
-  pre();
-  tile_store(tiles, tl);
-  int lead = tl.lead;
-  __syncthreads();
-  for (int sb = 0; sb < nsub; ++sb) {
-    const bool more = sb + 1 < nsub;
-    int next_lead = 0;
-    if (more) {
-      const int r1 = (sb + 1) * sr;
-      tile_issue(W, w_off + int64_t(r1) * rb, int64_t(min(sr, nrows - r1)) * rb, w_total, tl);
-      next_lead = tl.lead;
-    }
-    const uint8_t* tile = tiles + (sb & 1) * tile_cap + lead;
+  // rows of sub-tile sb, applied by this thread
+  auto apply_tile = [&](const uint8_t* tile, int sb) {
     const int rows_here = min(sr, nrows - sb * sr);
-    if (active) {
-      for (int r = sl; r < rows_here; r += RS) {
-        const int rr = sb * sr + r;
-        float xi[NT];
-        xi[0] = xs0[rr];
-        if constexpr (NT > 1) xi[1] = nt > 1 ? xs1[rr] : 0.f;
-        if (xi[0] == 0.f && (NT == 1 || xi[NT - 1] == 0.f)) continue;  // ops.rs:182-184
-        F::template apply<NT>(F::load(tile + int64_t(r) * rb, u), u, xi, acc, off, q6s);
-      }
+    if (!active) return;
+    for (int r = sl; r < rows_here; r += RS) {
+      const int rr = sb * sr + r;
+      float xi[NT];
+      xi[0] = xs0[rr];
+      if constexpr (NT > 1) xi[1] = nt > 1 ? xs1[rr] : 0.f;
+      if (xi[0] == 0.f && (NT == 1 || xi[NT - 1] == 0.f)) continue;  // ops.rs:182-184
+      F::template apply<NT>(F::load(tile + int64_t(r) * rb, u), u, xi, acc, off, q6s);
     }
-    if (more) tile_store(tiles + ((sb + 1) & 1) * tile_cap, tl);
-    lead = next_lead;
+  };
+  if constexpr (DMA) {
+    // A ring of kRing sub-tile slots filled by global_load_lds copies (no
+    // registers hold bytes in flight): kRing - 1 sub-tiles travel while one
+    // is applied. Sub-tile k is the 16-byte pieces from the boundary at or
+    // below its first byte; piece p of it is copied by wave p / 64 % 4.
+    const int wave = tid >> 6, lane = tid & 63;
+    auto first = [&](int k) { return w_off + int64_t(k) * sr * rb; };
+    auto pieces = [&](int k) {
+      return int(((first(k) & 15) + int64_t(min(sr, nrows - k * sr)) * rb + 15) >> 4);
+    };
+    auto wave_copies = [&](int k) {  // this wave's copies of sub-tile k
+      const int np = pieces(k), f = 64 * wave;
+      return np > f ? (np - f + kMoeThreads - 1) / kMoeThreads : 0;
+    };
+    auto issue = [&](int k) {
+      const int64_t a0 = first(k) & ~int64_t(15);
+      const int np = pieces(k);
+      uint8_t* dst = tiles + (k % kRing) * tile_cap;
+      for (int p0 = 64 * wave; p0 < np; p0 += kMoeThreads)
+        if (p0 + lane < np) copy16_to_lds(W + a0 + 16 * int64_t(p0 + lane), dst + 16 * p0);
+    };
+    int issued = 0;
+    for (; issued < min(kRing - 1, nsub); ++issued) issue(issued);
+    pre();
+    for (int sb = 0; sb < nsub; ++sb) {
+      // sub-tile sb has landed once only this wave's later copies remain;
+      // the barrier then covers every wave's (and, on the first pass, the
+      // inputs pre() staged)
+      int later = 0;
+      for (int k = sb + 1; k < issued; ++k) later += wave_copies(k);
+      wait_vmem(later);
+      lds_barrier();
+      // the slot of sub-tile sb - 1: every wave is past it
+      if (issued < nsub) issue(issued++);
+      apply_tile(tiles + (sb % kRing) * tile_cap + int(first(sb) & 15), sb);
+    }
+    lds_barrier();
+  } else {
+    (void)w_total;
+    TileLoad<kTilePieces> tl;
+    tile_issue(W, w_off, int64_t(min(sr, nrows)) * rb, w_total, tl);
+    pre();
+    tile_store(tiles, tl);
+    int lead = tl.lead;
     __syncthreads();
+    for (int sb = 0; sb < nsub; ++sb) {
+      const bool more = sb + 1 < nsub;
+      int next_lead = 0;
+      if (more) {
+        const int r1 = (sb + 1) * sr;
+        tile_issue(W, w_off + int64_t(r1) * rb, int64_t(min(sr, nrows - r1)) * rb, w_total, tl);
+        next_lead = tl.lead;
+      }
+      apply_tile(tiles + (sb & 1) * tile_cap + lead, sb);
+      if (more) tile_store(tiles + ((sb + 1) & 1) * tile_cap, tl);
+      lead = next_lead;
+      __syncthreads();
+    }
   }
   // the sub-tiles are free now: slot sums of 16 columns a round go through
   // them, (slot, half unit) rows 20 floats apart so neighbouring threads'
@@ -382,7 +425,7 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
 // Workgroup (row chunk c, matrix m, slot s): chunk sums of gate_e . x_t or
 // up_e . x_t for every pair (token t, expert e) of the slot, two tokens per
 // pass over the chunk's bytes.
-template <class F, int NT>
+template <class F, int NT, bool DMA>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_gateup_kernel(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, MoePlan plan,
                       const float* __restrict__ x, uint8_t* ws, int q6_gate, int q6_up) {
@@ -413,7 +456,7 @@ __global__ void __launch_bounds__(kMoeThreads)
     // part[((p * 2 + m) * nch_a + c) * n_ff + col]
     float* o0 = part + ((int64_t(p0 + j) * 2 + m) * plan.nch_a + c) * plan.n_ff;
     float* o1 = o0 + int64_t(2) * plan.nch_a * plan.n_ff;
-    chunk_sums<F, NT>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt, tiles,
+    chunk_sums<F, NT, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt, tiles,
                       tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
   }
 }
@@ -423,7 +466,7 @@ __global__ void __launch_bounds__(kMoeThreads)
 // chunk's rows and the slot's tokens, h and p summed over the gate/up chunks
 // in a fixed order (ops.rs:85-87, moe.rs:119-121); then chunk sums of
 // down_e . a.
-template <class F, int NT>
+template <class F, int NT, bool DMA>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_down_kernel(const uint8_t* __restrict__ down, MoePlan plan, uint8_t* ws, int q6_down) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -479,7 +522,7 @@ __global__ void __launch_bounds__(kMoeThreads)
     // part[(p * nch_b + c) * n_embd + col]
     float* o0 = part + (int64_t(p0 + j) * plan.nch_b + c) * plan.n_embd;
     float* o1 = o0 + int64_t(plan.nch_b) * plan.n_embd;
-    chunk_sums<F, NT>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
+    chunk_sums<F, NT, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
                       tiles, tile_cap, o0, o1, q6_down, stage_a);
   }
 }
@@ -564,8 +607,13 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.sr_b = sub_rows(p.rb_b, n_embd, p.cb, tp);
   const size_t cap_a = (size_t(p.sr_a) * p.rb_a + 31) & ~size_t(15);
   const size_t cap_b = (size_t(p.sr_b) * p.rb_b + 31) & ~size_t(15);
-  // a chunk that fits one sub-tile needs one buffer
-  const size_t nbuf_a = p.sr_a < p.ca ? 2 : 1, nbuf_b = p.sr_b < p.cb ? 2 : 1;
+  // sub-tiles stream through a ring of copies when every 16-byte piece of a
+  // tensor lies inside it (its size is a multiple of 16), else through
+  // registers and two buffers; a chunk that fits one sub-tile needs one slot
+  const int64_t total_a = int64_t(n_expert) * n_embd * p.rb_a, total_b = int64_t(n_expert) * n_ff * p.rb_b;
+  p.staged = total_a % 16 == 0 && total_b % 16 == 0;
+  const int nsub_a = (p.ca + p.sr_a - 1) / p.sr_a, nsub_b = (p.cb + p.sr_b - 1) / p.sr_b;
+  const size_t nbuf_a = std::min(p.staged ? kRing : 2, nsub_a), nbuf_b = std::min(p.staged ? kRing : 2, nsub_b);
   // the sub-tiles' LDS is reused for the row-slot reduction (16 columns a round)
   const size_t red_a = sizeof(float) * size_t(rs_a) * (n_ff / 32) * kRedStride;
   const size_t red_b = sizeof(float) * size_t(rs_b) * (n_embd / 32) * kRedStride;
@@ -600,22 +648,35 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   return true;
 }
 
-// one token per pass when every expert has one token (decode), two otherwise
+static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// one token per pass when every expert has one token (decode), two otherwise;
+// the copy ring when the plan allows it and the tensors start on 16 bytes
 template <class FA>
 static void launch_gateup(const MoePlan& p, const void* gate, const void* up, const float* x,
                           uint8_t* ws, int q6g, int q6u, hipStream_t s) {
   const dim3 g(p.nch_a, 2, p.s_max), b(kMoeThreads);
   const uint8_t *gp = static_cast<const uint8_t*>(gate), *upp = static_cast<const uint8_t*>(up);
-  if (p.n_tok == 1) hipLaunchKernelGGL((moe_gateup_kernel<FA, 1>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
-  else hipLaunchKernelGGL((moe_gateup_kernel<FA, 2>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+  const bool dma = p.staged && aligned16(gate) && aligned16(up);
+  if (dma && p.n_tok == 1)
+    hipLaunchKernelGGL((moe_gateup_kernel<FA, 1, true>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+  else if (dma)
+    hipLaunchKernelGGL((moe_gateup_kernel<FA, 2, true>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+  else if (p.n_tok == 1)
+    hipLaunchKernelGGL((moe_gateup_kernel<FA, 1, false>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+  else
+    hipLaunchKernelGGL((moe_gateup_kernel<FA, 2, false>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
 }
 
 template <class FB>
 static void launch_down(const MoePlan& p, const void* down, uint8_t* ws, int q6d, hipStream_t s) {
   const dim3 g(p.nch_b, p.s_max), b(kMoeThreads);
   const uint8_t* dp = static_cast<const uint8_t*>(down);
-  if (p.n_tok == 1) hipLaunchKernelGGL((moe_down_kernel<FB, 1>), g, b, p.lds_b, s, dp, p, ws, q6d);
-  else hipLaunchKernelGGL((moe_down_kernel<FB, 2>), g, b, p.lds_b, s, dp, p, ws, q6d);
+  const bool dma = p.staged && aligned16(down);
+  if (dma && p.n_tok == 1) hipLaunchKernelGGL((moe_down_kernel<FB, 1, true>), g, b, p.lds_b, s, dp, p, ws, q6d);
+  else if (dma) hipLaunchKernelGGL((moe_down_kernel<FB, 2, true>), g, b, p.lds_b, s, dp, p, ws, q6d);
+  else if (p.n_tok == 1) hipLaunchKernelGGL((moe_down_kernel<FB, 1, false>), g, b, p.lds_b, s, dp, p, ws, q6d);
+  else hipLaunchKernelGGL((moe_down_kernel<FB, 2, false>), g, b, p.lds_b, s, dp, p, ws, q6d);
 }
 
 hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, const void* gate,
