@@ -18,10 +18,11 @@
 //            the (token, expert) pairs by expert: the unique experts in
 //            ascending id are "slots", each with its pairs;
 //   gate/up  workgroup (row chunk, matrix, slot): the chunk's rows are
-//            contiguous bytes, streamed into LDS with coalesced 16-byte loads
-//            (two sub-tiles in flight); threads decode their 64-column unit
-//            from LDS and apply each row to two of the slot's tokens per
-//            pass; row-slot sums reduce in LDS to one chunk sum per pair;
+//            contiguous bytes, copied into an LDS ring of sub-tiles with
+//            global_load_lds (two sub-tiles in flight); threads decode their
+//            32-column half unit from LDS and apply each row to two of the
+//            slot's tokens per pass (one for a slot's odd last token);
+//            row-slot sums reduce in LDS to one chunk sum per pair;
 //   down     workgroup (row chunk, slot): a = silu(h) * p for its rows from
 //            the gate/up chunk sums (fixed order), then the same streaming;
 //   combine  out[t] = sum over t's experts in ascending id of w * d, with d
@@ -456,8 +457,13 @@ __global__ void __launch_bounds__(kMoeThreads)
     // part[((p * 2 + m) * nch_a + c) * n_ff + col]
     float* o0 = part + ((int64_t(p0 + j) * 2 + m) * plan.nch_a + c) * plan.n_ff;
     float* o1 = o0 + int64_t(2) * plan.nch_a * plan.n_ff;
-    chunk_sums<F, NT, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt, tiles,
-                      tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
+    // a slot's last token alone takes the one-token pass (no FMAs for an absent second token)
+    if (NT > 1 && nt == 1)
+      chunk_sums<F, 1, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt,
+                            tiles, tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
+    else
+      chunk_sums<F, NT, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt,
+                             tiles, tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
   }
 }
 
@@ -522,8 +528,12 @@ __global__ void __launch_bounds__(kMoeThreads)
     // part[(p * nch_b + c) * n_embd + col]
     float* o0 = part + (int64_t(p0 + j) * plan.nch_b + c) * plan.n_embd;
     float* o1 = o0 + int64_t(plan.nch_b) * plan.n_embd;
-    chunk_sums<F, NT, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
-                      tiles, tile_cap, o0, o1, q6_down, stage_a);
+    if (NT > 1 && nt == 1)
+      chunk_sums<F, 1, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
+                            tiles, tile_cap, o0, o1, q6_down, stage_a);
+    else
+      chunk_sums<F, NT, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
+                             tiles, tile_cap, o0, o1, q6_down, stage_a);
   }
 }
 
@@ -595,11 +605,11 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   // enough workgroups to cover the chip when few experts are routed, few
   // enough chunks that the partial sums stay small when many are
   const int rs_a = kMoeThreads / (n_ff >> 5), rs_b = kMoeThreads / (n_embd >> 5);
-  p.nch_a = std::max(1, std::min({(2048 + 2 * p.s_max - 1) / (2 * p.s_max), (n_embd + rs_a - 1) / rs_a,
+  p.nch_a = std::max(1, std::min({(4096 + 2 * p.s_max - 1) / (2 * p.s_max), (n_embd + rs_a - 1) / rs_a,
                                    kMoeMaxChunks}));
   p.ca = (n_embd + p.nch_a - 1) / p.nch_a;
   p.nch_a = (n_embd + p.ca - 1) / p.ca;
-  p.nch_b = std::max(1, std::min({(1024 + p.s_max - 1) / p.s_max, (n_ff + rs_b - 1) / rs_b, kMoeMaxChunks}));
+  p.nch_b = std::max(1, std::min({(2048 + p.s_max - 1) / p.s_max, (n_ff + rs_b - 1) / rs_b, kMoeMaxChunks}));
   p.cb = (n_ff + p.nch_b - 1) / p.nch_b;
   p.nch_b = (n_ff + p.cb - 1) / p.cb;
   const int tp = kTilePieces;
