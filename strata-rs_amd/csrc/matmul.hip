@@ -17,10 +17,12 @@
 //
 // Workgroup tile: 256 tokens x 96 weight rows, 4 waves stacked along the
 // tokens (wave w owns tokens [64w, 64w + 64) and all 96 rows: 2 x 3 MFMA
-// tiles of 32 x 32). Activations are private to a wave, so each wave loads
-// its A fragments straight from global memory (L2-resident) into registers;
-// only the weight tile, shared by the 4 waves, goes through LDS (double
-// buffered, one barrier per 64-element chunk of K). The MFMA's k order is
+// tiles of 32 x 32). The weight tile, shared by the 4 waves, goes through
+// LDS (double buffered, one barrier per 64-element chunk of K). In bf16 mode
+// the activation tile does too (mm_bf16_lds_kernel: global_load_lds copies
+// into a three-slot ring); the q8 kernel, and bf16 calls whose activations
+// exceed 32-bit byte offsets, load each wave's A fragments straight from
+// global memory (L2-resident) into registers. The MFMA's k order is
 // free as long as A and B agree, so lane half h of k-step s holds chunk
 // elements [32h + 8s, +8) (bf16) or [32s + 16h, +16) (int8) of both operands,
 // which keeps every fragment one 16-byte load. Tiles are numbered so that the
@@ -80,8 +82,11 @@ struct StQ4K {
                                                 float& m1) {
     const uint32_t s = (g & 1) << 4;
     const uint32_t t1 = h.y >> s, t2 = h.z >> s, t3 = h.w >> s;
-    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
-    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+    // both readings, then a mask select: no branch on the wave-uniform g, so
+    // staging stays in the MFMAs' basic block
+    const uint32_t hi_sel = 0u - uint32_t(g >> 1);  // all ones for g >= 2
+    const uint32_t scp = ((t1 & 0x3F3Fu) & ~hi_sel) | (((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u)) & hi_sel);
+    const uint32_t mp = ((t2 & 0x3F3Fu) & ~hi_sel) | ((((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u)) & hi_sel);
     const float d = h2f(h.x), dm = h2f(h.x >> 16);
     d0 = d * ubyte<0>(scp);
     d1 = d * ubyte<1>(scp);
@@ -95,7 +100,10 @@ struct StQ4K {
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+      uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+      // keep the masked words whole, so each byte converts with one
+      // v_cvt_f32_ubyteN instead of an extract and a convert
+      asm volatile("" : "+v"(lo), "+v"(hi));
       run0[2 * k] = pack_bf16(__builtin_fmaf(d0, ubyte<0>(lo), -m0), __builtin_fmaf(d0, ubyte<1>(lo), -m0));
       run0[2 * k + 1] =
           pack_bf16(__builtin_fmaf(d0, ubyte<2>(lo), -m0), __builtin_fmaf(d0, ubyte<3>(lo), -m0));
@@ -464,6 +472,148 @@ __global__ void __launch_bounds__(kMmThreads)
     }
 }
 
+// ------------------------------------------------ bf16 kernel, LDS operands --
+// The same tile and MFMA as mm_bf16_kernel with the activations staged too:
+// chunk c's 256 tokens x 64 bf16 (32 KiB) are copied with global_load_lds
+// (no registers hold them in flight; each wave load covers 8 token rows of
+// 128 contiguous bytes) into a ring of three slots, two chunks ahead. Lane p
+// fetches the logical 16-byte chunk that belongs in physical slot p: row r
+// keeps logical chunk cc at physical cc ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1),
+// so fragment reads of 8 or 16 consecutive rows hit distinct bank groups.
+// Every thread stages weights (threads past the 96 * kPieces tasks repeat one
+// and write the same bytes), as straight-line code in the MFMAs' basic block.
+constexpr int kMmRing = 3;
+constexpr int kMmATile = kMmBM * kMmKC * 2;
+constexpr size_t kMmLdsBf16 = size_t(kMmRing) * kMmATile + 2 * kMmBN * kMmRowB;
+
+__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <class S>
+__global__ void __launch_bounds__(kMmThreads)
+    mm_bf16_lds_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                       const uint16_t* __restrict__ xb, int m, float* __restrict__ y, int n_tiles_m, int q6s) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint8_t* at = lds;                              // [kMmRing][kMmBM][128]
+  uint8_t* wlb = lds + kMmRing * kMmATile;        // [2][kMmBN * kMmRowB]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  int r0, t0;
+  tile_of(n_tiles_m, r0, t0);
+  const int nchunks = cols / kMmKC;
+
+  constexpr int kTasks = kMmBN * S::kPieces;
+  static_assert(kTasks <= kMmThreads, "staging tasks fit the workgroup");
+  const int task = tid % kTasks;
+  const int srow = task / S::kPieces, piece = task % S::kPieces;
+  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
+
+  // this wave's 8 wave loads of a chunk: tile rows 64 wave + 8 i + lane / 8,
+  // as byte offsets from the chunk's first column (m * cols * 2 < 2^32 is
+  // checked on the host), added to a wave-uniform base
+  uint32_t aoffs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 64 * wave + 8 * i + (lane >> 3);
+    const int cc = (lane & 7) ^ a_swz(r);
+    aoffs[i] = uint32_t(min(t0 + r, m - 1)) * uint32_t(cols) * 2u + 16u * uint32_t(cc);
+  }
+  const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(xb);
+  auto issue_a = [&](int c) {
+    uint8_t* slot = at + (c % kMmRing) * kMmATile + 8 * wave * 1024;
+    const uint8_t* base = xbytes + int64_t(c) * kMmKC * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) copy16_to_lds(base + aoffs[i], slot + 1024 * i);
+  };
+  // fragment offsets in a slot: row 64 wave + 32 mi + l32, logical chunk 4 half + s
+  int aoff[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int r = 64 * wave + 32 * mi + l32;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) aoff[mi][s] = r * 128 + 16 * ((4 * half + s) ^ a_swz(r));
+  }
+
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+
+  auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf) {
+    uint32_t run0[8], run1[8];
+    int o0, o1;
+    Bf16Emit<S>::run(raw, c, piece, block_shift<S>(wrow, c), run0, run1, o0, o1, q6s);
+    uint8_t* dst = buf + srow * kMmRowB;
+    *reinterpret_cast<u32x4*>(dst + 2 * o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o0 + 16) = u32x4{run0[4], run0[5], run0[6], run0[7]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o1) = u32x4{run1[0], run1[1], run1[2], run1[3]};
+    *reinterpret_cast<u32x4*>(dst + 2 * o1 + 16) = u32x4{run1[4], run1[5], run1[6], run1[7]};
+  };
+
+  issue_a(0);
+  if (nchunks > 1) issue_a(1);
+  // weight chunks requested kDepth ahead of their staging (ring slot of
+  // chunk c: c % kDepth; the loop is unrolled by kDepth so it is a constant)
+  typename S::Raw raw[kDepth];
+#pragma unroll
+  for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+  stage(raw[0], 0, wlb);
+  raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
+
+  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
+      const int c = c0 + j;
+      if (c < nchunks) {  // uniform
+        // A(c) has landed once at most 8 later vector memory operations (the
+        // copies of A(c + 1), or weight loads issued after them) remain; the
+        // barrier then covers every wave's copies and the staged B(c)
+        if (c + 1 < nchunks) wait_vmem<8>();
+        else wait_vmem<0>();
+        lds_barrier();
+        if (c + 2 < nchunks) issue_a(c + 2);  // into the slot of chunk c - 1: every wave is past it
+        const uint8_t* as = at + (c % kMmRing) * kMmATile;
+        const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          bf16x8 afr[2], bfr[3];
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) afr[mi] = *reinterpret_cast<const bf16x8*>(as + aoff[mi][s]);
+#pragma unroll
+          for (int ni = 0; ni < 3; ++ni)
+            bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 3; ++ni)
+              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+        }
+        // the next weight chunk into the buffer of chunk c - 1 (every wave is
+        // past it); past the last chunk this re-stages the last one into the
+        // buffer nobody reads
+        const int slot = (j + 1) % kDepth;
+        stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
+        raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+      }
+    }
+  }
+
+  // D layout of the 32x32 MFMA: lane l holds column l % 32 (a weight row)
+  // and, in register i, row 8 * (i / 4) + 4 * (l / 32) + i % 4 (a token)
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) {
+      const int r = r0 + 32 * ni + l32;
+      if (r >= n_rows) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = t0 + 64 * wave + 32 * mi + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (t < m) y[int64_t(t) * n_rows + r] = acc[mi][ni][i];
+      }
+    }
+}
+
 // --------------------------------------------------------------- q8 kernel --
 // A = weight codes (rows r), B = activation codes (tokens t), so the D
 // layout puts one token per lane and the activation block scale is a
@@ -658,8 +808,13 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
   const int ntm = (m + kMmBM - 1) / kMmBM, ntn = (rows + kMmBN - 1) / kMmBN;
   const dim3 grid(unsigned(ntm * ntn));
   if (mode == 0) {
-    hipLaunchKernelGGL(mm_bf16_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
-                       reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
+    // activations staged through LDS when their byte offsets fit 32 bits
+    if (uint64_t(m) * uint64_t(cols) * 2u < (uint64_t(1) << 32))
+      hipLaunchKernelGGL(mm_bf16_lds_kernel<S>, grid, dim3(kMmThreads), kMmLdsBf16, s, w, rows, cols, rb,
+                         reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
+    else
+      hipLaunchKernelGGL(mm_bf16_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
+                         reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
   } else if constexpr (S::kQ8) {
     const size_t blocks = size_t(m) * size_t(cols / 32);
     const int8_t* xq = reinterpret_cast<const int8_t*>(ws);
