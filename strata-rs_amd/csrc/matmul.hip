@@ -683,6 +683,14 @@ __global__ void __launch_bounds__(kMmThreads)
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 32 * s);
+  // the lane's tokens' block scales and min sums, a chunk ahead with the codes
+  float sxc[2][2], umc[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) sxc[mi][s] = xs[int64_t(tok[mi]) * nblk + s];
+    umc[mi] = S::kMin ? xu[int64_t(tok[mi]) * nblk + half] : 0.f;
+  }
   __syncthreads();
 
   for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
@@ -692,12 +700,19 @@ __global__ void __launch_bounds__(kMmThreads)
       if (c < nchunks) {  // uniform
         const bool more = c + 1 < nchunks;
         i32x4 xn[2][2];
+        float sxn[2][2], umn[2];
         if (more) {
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
             for (int s = 0; s < 2; ++s)
               xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * kMmKC + 32 * s);
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) sxn[mi][s] = xs[int64_t(tok[mi]) * nblk + 2 * (c + 1) + s];
+            umn[mi] = S::kMin ? xu[int64_t(tok[mi]) * nblk + 2 * (c + 1) + half] : 0.f;
+          }
         }
         const int buf = c & 1;
         const uint8_t* wb = wl[buf];
@@ -706,7 +721,7 @@ __global__ void __launch_bounds__(kMmThreads)
         if constexpr (S::kMin) {
           float um[2];
     #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) um[mi] = xu[int64_t(tok[mi]) * nblk + 2 * c + half];
+          for (int mi = 0; mi < 2; ++mi) um[mi] = umc[mi];
     #pragma unroll
           for (int ni = 0; ni < 3; ++ni) {
             const float ma = -wsc[buf][half][1][32 * ni + l32];
@@ -717,10 +732,9 @@ __global__ void __launch_bounds__(kMmThreads)
         }
     #pragma unroll
         for (int s = 0; s < 2; ++s) {  // one 32-element block per step
-          const int j = 2 * c + s;
           float sx[2];
     #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) sx[mi] = xs[int64_t(tok[mi]) * nblk + j];
+          for (int mi = 0; mi < 2; ++mi) sx[mi] = sxc[mi][s];
     #pragma unroll
           for (int ni = 0; ni < 3; ++ni) {
             const i32x4 a = *reinterpret_cast<const i32x4*>(wb + (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half);
@@ -750,9 +764,14 @@ __global__ void __launch_bounds__(kMmThreads)
             raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
           }
 #pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
+          for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
+            for (int s = 0; s < 2; ++s) {
+              xc[mi][s] = xn[mi][s];
+              sxc[mi][s] = sxn[mi][s];
+            }
+            umc[mi] = umn[mi];
+          }
         }
         __syncthreads();
       }
