@@ -13,7 +13,8 @@
 // (crates/strata-core/src/weights.rs:14-34). The shared expert
 // (moe.rs:129-143) is not part of this op.
 //
-// Four launches:
+// Four launches (three for one token, whose gate/up workgroups route it
+// themselves):
 //   route    one workgroup routes every token (a wave per token) and groups
 //            the (token, expert) pairs by expert: the unique experts in
 //            ascending id are "slots", each with its pairs;
@@ -79,6 +80,96 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
+// Routes one token with one wave (moe.rs:58-90): max-shifted softmax (f32 exp,
+// f64 sum, inv = f32(1 / sum)), k rounds of (largest probability, then lowest
+// id), ids sorted ascending, weights f32(f64(p) / max(sum_f64(p), 2^-14)).
+// sel_id / sel_p are the wave's LDS scratch (kMoeMaxTopK entries); on return
+// they hold the ids ascending and their probabilities, and lane a < K holds
+// id sel_id[a] and its weight in id_out, w_out. KPER experts per lane, with
+// KPER * 64 >= E (a larger KPER gives the same result: experts past E are
+// skipped everywhere).
+template <int KPER>
+__device__ __forceinline__ void route_token(const float* __restrict__ lg, int E, int K, int lane, int* sel_id,
+                                            float* sel_p, int& id_out, float& w_out) {
+  constexpr int kPer = KPER;
+  float p[KPER];
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane + kWave * j;
+    p[j] = e < E ? lg[e] : -__builtin_inff();
+    mx = fmaxf(mx, p[j]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+  double sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane + kWave * j;
+    if (e < E) {
+      p[j] = expf(p[j] - mx);
+      sum += double(p[j]);
+    }
+  }
+  sum = wave_sum_f64(sum);
+  const float inv = float(1.0 / sum);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) p[j] *= inv;
+  // top-k: k rounds of (largest p, then lowest id) over what is left; a
+  // NaN probability ranks below every number, so each round picks a valid
+  // id (k <= n_expert)
+  uint32_t taken = 0;
+  for (int r = 0; r < K; ++r) {
+    // exact: the largest remaining probability, then the lowest id holding it
+    float bp = -2.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane + kWave * j;
+      const float pj = p[j] == p[j] ? p[j] : -1.f;
+      if (e < E && !(taken >> j & 1u)) bp = fmaxf(bp, pj);
+    }
+    bp = wave_max_dpp(bp);
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane + kWave * j;
+      const float pj = p[j] == p[j] ? p[j] : -1.f;
+      if (e < E && !(taken >> j & 1u) && pj == bp) bi = min(bi, e);
+    }
+    bi = wave_min_dpp(bi);
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if (lane == 0) {
+      sel_id[r] = bi;
+      sel_p[r] = bp;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // ids ascending: lane a < K goes to its rank among the selected ids
+  int myid = 0, rank = 0;
+  float myp = 0.f;
+  if (lane < K) {
+    myid = sel_id[lane];
+    myp = sel_p[lane];
+    for (int b = 0; b < K; ++b) rank += sel_id[b] < myid;
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < K) {
+    sel_id[rank] = myid;
+    sel_p[rank] = myp;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // f64 renormalisation in ascending-id order (moe.rs:80-90)
+  double wsum = 0.0;
+  for (int a = 0; a < K; ++a) wsum += double(sel_p[a]);
+  const double sden = wsum > 6.103515625e-05 ? wsum : 6.103515625e-05;  // 2^-14
+  id_out = 0;
+  w_out = 0.f;
+  if (lane < K) {
+    id_out = sel_id[lane];
+    w_out = float(double(sel_p[lane]) / sden);
+  }
+}
+
 // KPER: experts per lane (KPER * 64 >= n_expert)
 template <int KPER>
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits,
@@ -97,85 +188,13 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   float* s_w = reinterpret_cast<float*>(rlds + pairs);   // [pairs]
   int* ids = reinterpret_cast<int*>(ws + plan.o_ids);
   float* wts = reinterpret_cast<float*>(ws + plan.o_wts);
-  constexpr int kPer = KPER;
-
   for (int e = tid; e < kMoeMaxExperts; e += kRouteThreads) cnt[e] = 0;
 
   for (int t = wave; t < plan.n_tok; t += kWaves) {
-    const float* lg = logits + int64_t(t) * E;
-    float p[kPer];
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      p[j] = e < E ? lg[e] : -__builtin_inff();
-      mx = fmaxf(mx, p[j]);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-    double sum = 0.0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      if (e < E) {
-        p[j] = expf(p[j] - mx);
-        sum += double(p[j]);
-      }
-    }
-    sum = wave_sum_f64(sum);
-    const float inv = float(1.0 / sum);
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) p[j] *= inv;
-    // top-k: k rounds of (largest p, then lowest id) over what is left; a
-    // NaN probability ranks below every number, so each round picks a valid
-    // id (k <= n_expert)
-    uint32_t taken = 0;
-    for (int r = 0; r < K; ++r) {
-      // exact: the largest remaining probability, then the lowest id holding it
-      float bp = -2.f;
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int e = lane + kWave * j;
-        const float pj = p[j] == p[j] ? p[j] : -1.f;
-        if (e < E && !(taken >> j & 1u)) bp = fmaxf(bp, pj);
-      }
-      bp = wave_max_dpp(bp);
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int e = lane + kWave * j;
-        const float pj = p[j] == p[j] ? p[j] : -1.f;
-        if (e < E && !(taken >> j & 1u) && pj == bp) bi = min(bi, e);
-      }
-      bi = wave_min_dpp(bi);
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-      if (lane == 0) {
-        sel_id[wave][r] = bi;
-        sel_p[wave][r] = bp;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    // ids ascending: lane a < K goes to its rank among the selected ids
-    int myid = 0, rank = 0;
-    float myp = 0.f;
+    int id;
+    float wv;
+    route_token<KPER>(logits + int64_t(t) * E, E, K, lane, sel_id[wave], sel_p[wave], id, wv);
     if (lane < K) {
-      myid = sel_id[wave][lane];
-      myp = sel_p[wave][lane];
-      for (int b = 0; b < K; ++b) rank += sel_id[wave][b] < myid;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) {
-      sel_id[wave][rank] = myid;
-      sel_p[wave][rank] = myp;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // f64 renormalisation in ascending-id order (moe.rs:80-90)
-    double wsum = 0.0;
-    for (int a = 0; a < K; ++a) wsum += double(sel_p[wave][a]);
-    const double sden = wsum > 6.103515625e-05 ? wsum : 6.103515625e-05;  // 2^-14
-    if (lane < K) {
-      const int id = sel_id[wave][lane];
-      const float wv = float(double(sel_p[wave][lane]) / sden);
       s_ids[t * K + lane] = id;
       s_w[t * K + lane] = wv;
       ids[t * K + lane] = id;
@@ -426,17 +445,52 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
 // Workgroup (row chunk c, matrix m, slot s): chunk sums of gate_e . x_t or
 // up_e . x_t for every pair (token t, expert e) of the slot, two tokens per
 // pass over the chunk's bytes.
-template <class F, int NT, bool DMA>
+// ROUTE (one token, at most 256 experts): the workgroup routes the token
+// itself (route_token, the route kernel's own steps, so ids and weights are
+// the same), its slots being the token's k experts in ascending id; workgroup
+// (0, 0, 0) writes the ids, weights and slot tables that down and combine
+// read, and no workgroup reads them here.
+template <class F, int NT, bool DMA, bool ROUTE>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_gateup_kernel(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, MoePlan plan,
-                      const float* __restrict__ x, uint8_t* ws, int q6_gate, int q6_up) {
+                      const float* __restrict__ x, uint8_t* ws, int q6_gate, int q6_up,
+                      const float* __restrict__ logits) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x, m = blockIdx.y, s = blockIdx.z;
-  const int n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
-  if (s >= n_slots) return;
-  const int e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
-  const int p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
-  const int cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
+  int n_slots, e, p0, cnt;
+  if constexpr (ROUTE) {
+    __shared__ int r_id[kMoeMaxTopK];
+    __shared__ float r_p[kMoeMaxTopK];
+    const int K = plan.top_k;
+    if (threadIdx.x < kWave) {
+      const int a = threadIdx.x;
+      int id;
+      float wv;
+      route_token<4>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
+      if (c == 0 && m == 0 && s == 0 && a < K) {
+        reinterpret_cast<int*>(ws + plan.o_ids)[a] = id;
+        reinterpret_cast<float*>(ws + plan.o_wts)[a] = wv;
+        reinterpret_cast<int*>(ws + plan.o_slot_e)[a] = id;
+        reinterpret_cast<int*>(ws + plan.o_slot_off)[a] = a;
+        reinterpret_cast<int*>(ws + plan.o_slot_cnt)[a] = 1;
+        reinterpret_cast<int*>(ws + plan.o_pair_tok)[a] = 0;
+        reinterpret_cast<int*>(ws + plan.o_tokpair)[a] = a;
+        if (a == 0) reinterpret_cast<int*>(ws + plan.o_meta)[0] = K;
+      }
+    }
+    __syncthreads();
+    n_slots = K;
+    if (s >= n_slots) return;
+    e = r_id[s];
+    p0 = s;
+    cnt = 1;
+  } else {
+    n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
+    if (s >= n_slots) return;
+    e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
+    p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
+    cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
+  }
   const int* pair_tok = reinterpret_cast<const int*>(ws + plan.o_pair_tok);
   float* part = reinterpret_cast<float*>(ws + plan.o_part_a);
   const int r0 = c * plan.ca, nrows = min(plan.ca, plan.n_embd - r0);
@@ -451,7 +505,8 @@ __global__ void __launch_bounds__(kMoeThreads)
     auto stage_x = [&]() {
       for (int i = threadIdx.x; i < nt * nrows; i += kMoeThreads) {
         const int t = i / nrows, r = i - t * nrows;
-        xs[t * plan.ca + r] = x[int64_t(pair_tok[p0 + j + t]) * plan.n_embd + r0 + r];
+        const int tok = ROUTE ? 0 : pair_tok[p0 + j + t];
+        xs[t * plan.ca + r] = x[int64_t(tok) * plan.n_embd + r0 + r];
       }
     };
     // part[((p * 2 + m) * nch_a + c) * n_ff + col]
@@ -662,20 +717,22 @@ static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 
 // one token per pass when every expert has one token (decode), two otherwise;
 // the copy ring when the plan allows it and the tensors start on 16 bytes
+// `route`: one token routed inside gate/up (no route launch)
 template <class FA>
 static void launch_gateup(const MoePlan& p, const void* gate, const void* up, const float* x,
-                          uint8_t* ws, int q6g, int q6u, hipStream_t s) {
+                          uint8_t* ws, int q6g, int q6u, const float* logits, bool route, hipStream_t s) {
   const dim3 g(p.nch_a, 2, p.s_max), b(kMoeThreads);
   const uint8_t *gp = static_cast<const uint8_t*>(gate), *upp = static_cast<const uint8_t*>(up);
   const bool dma = p.staged && aligned16(gate) && aligned16(up);
-  if (dma && p.n_tok == 1)
-    hipLaunchKernelGGL((moe_gateup_kernel<FA, 1, true>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
-  else if (dma)
-    hipLaunchKernelGGL((moe_gateup_kernel<FA, 2, true>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
-  else if (p.n_tok == 1)
-    hipLaunchKernelGGL((moe_gateup_kernel<FA, 1, false>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
-  else
-    hipLaunchKernelGGL((moe_gateup_kernel<FA, 2, false>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u);
+#define SH_GATEUP(NT, DMA, ROUTE) \
+  hipLaunchKernelGGL((moe_gateup_kernel<FA, NT, DMA, ROUTE>), g, b, p.lds_a, s, gp, upp, p, x, ws, q6g, q6u, logits)
+  if (route && dma) SH_GATEUP(1, true, true);
+  else if (route) SH_GATEUP(1, false, true);
+  else if (dma && p.n_tok == 1) SH_GATEUP(1, true, false);
+  else if (dma) SH_GATEUP(2, true, false);
+  else if (p.n_tok == 1) SH_GATEUP(1, false, false);
+  else SH_GATEUP(2, false, false);
+#undef SH_GATEUP
 }
 
 template <class FB>
@@ -695,12 +752,17 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       hipStream_t s) {
   if (qg != qu) return hipErrorInvalidValue;  // gate and up share one kernel
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  hipError_t e = launch_moe_route(p, logits, workspace, s);
-  if (e != hipSuccess) return e;
+  // one token (decode): gate/up routes it itself; otherwise the route kernel
+  // groups every token's pairs by expert first
+  const bool fused_route = p.n_tok == 1 && p.n_expert <= 4 * kWave;
+  if (!fused_route) {
+    hipError_t e = launch_moe_route(p, logits, workspace, s);
+    if (e != hipSuccess) return e;
+  }
   switch (qg) {
-    case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, s); break;
-    case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, s); break;
-    default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, s);
+    case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+    case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+    default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
   }
   switch (qd) {
     case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
