@@ -118,6 +118,55 @@ def test_moe_ffn_dev_matches_host_path(backend):
     assert np.array_equal(out.cpu().numpy(), host)
 
 
+def test_moe_ffn_one_token_many_experts(backend, oracle):
+    """One token over more than 256 experts: routed by the route kernel rather
+    than inside gate/up (which takes up to 256)."""
+    n_expert, n_embd, n_ff, top_k, n_tok = 320, 256, 256, 6, 1
+    say("moe ffn one token", n_expert, "experts")
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 6600)
+    logits = S.router_logits(6700, n_tok, n_expert)
+    x = S.normal_f32(6800, n_tok * n_embd).reshape(n_tok, n_embd)
+    out = backend.moe_ffn(H.ExpertView("gm", 12, n_expert, n_embd, n_ff, gate),
+                          H.ExpertView("um", 12, n_expert, n_embd, n_ff, up),
+                          H.ExpertView("dm", 14, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    assert rel_err(out, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_moe_ffn_dev_unaligned_tensors_match(backend, n_tok):
+    """Expert tensors 2 bytes off a 16-byte boundary (allowed for Q4_K/Q6_K)
+    take the register-staged row stream instead of the global_load_lds ring;
+    both apply the rows in the same order, so the outputs are identical."""
+    import torch
+    n_expert, n_embd, n_ff, top_k = 32, 512, 256, 8
+    say("moe ffn dev unaligned", n_tok)
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 6300)
+    logits = S.router_logits(6400 + n_tok, n_tok, n_expert)
+    x = S.normal_f32(6500 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    dev = torch.device("cuda:0")
+    tl, tx = torch.from_numpy(logits).to(dev), torch.from_numpy(x).to(dev)
+    nb = H.moe_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, 12, 14)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    outs = []
+    for shift in (0, 2):
+        bufs = []
+        for a in (gate, up, down):
+            t = torch.zeros(a.nbytes + 16, dtype=torch.uint8, device=dev)
+            t[shift:shift + a.nbytes] = torch.from_numpy(a.view(np.uint8).reshape(-1)).to(dev)
+            bufs.append(t)
+        assert (bufs[0].data_ptr() + shift) % 16 == shift
+        out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+        H.moe_ffn_dev((12, 0, bufs[0].data_ptr() + shift), (12, 0, bufs[1].data_ptr() + shift),
+                      (14, 0, bufs[2].data_ptr() + shift), n_expert, n_embd, n_ff, tl.data_ptr(), n_tok,
+                      top_k, tx.data_ptr(), out.data_ptr(), ws.data_ptr(), nb,
+                      torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    assert np.all(np.isfinite(outs[0]))
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_moe_errors(backend):
     say("moe errors")
     g = H.ExpertView("eg", 12, 4, 256, 256, S.matrix(12, 1, 4 * 256, 256))
