@@ -33,6 +33,7 @@
 // unique expert's weight bytes cross HBM once per call, however many tokens
 // chose it.
 #include <algorithm>
+#include <type_traits>
 
 #include "axpy.hpp"
 #include "common.hpp"
@@ -311,16 +312,17 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const TileLoad<TP>& t) 
 // u = tid % U of 32 columns, slot sl = tid / U) applies rows sl, sl + RS, ...
 // of each sub-tile to the inputs. The inputs' values for the chunk's rows are
 // xs0[r], xs1[r]. The slots' sums are then reduced through the sub-tiles'
-// LDS (`tiles`, at least RS * U * 20 floats), 16 columns a round, and the
+// LDS (`tiles`, `reg_bytes` of it, at least RS * U * 20 floats): all 32
+// columns in one round when RS * U * 36 floats fit, else 16 a round; the
 // column sums of input t go to out_t[col].
 // `pre()` runs after the first sub-tile's loads are issued and before they
 // are stored, so input staging overlaps the first weight bytes' latency.
-constexpr int kRedStride = 20;  // floats per (slot, half unit) in a round: 16 sums + 4 pad
+constexpr int kRedStride = 20;  // floats per (slot, half unit) in a 16-column round: 16 sums + 4 pad
 
 template <class F, int NT, bool DMA, class Pre>
 __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t w_off, int64_t w_total, int cols,
                            int nrows, int sr, const float* xs0, const float* xs1, int nt, uint8_t* tiles,
-                           int tile_cap, float* out0, float* out1, int q6s, Pre pre) {
+                           int tile_cap, int64_t reg_bytes, float* out0, float* out1, int q6s, Pre pre) {
   const int tid = threadIdx.x;
   const int U = cols >> 5, RS = kMoeThreads / U;
   const int u = tid % U, sl = tid / U;
@@ -351,7 +353,7 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
   if constexpr (DMA) {
     // A ring of kRing sub-tile slots filled by global_load_lds copies (no
     // registers hold bytes in flight): kRing - 1 sub-tiles travel while one
-    // is applied. Sub-tile k is the 16-byte pieces from the boundary at or
+    // is applied (all of them when the chunk has at most kRing). Sub-tile k is the 16-byte pieces from the boundary at or
     // below its first byte; piece p of it is copied by wave p / 64 % 4.
     const int wave = tid >> 6, lane = tid & 63;
     auto first = [&](int k) { return w_off + int64_t(k) * sr * rb; };
@@ -369,8 +371,9 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
       for (int p0 = 64 * wave; p0 < np; p0 += kMoeThreads)
         if (p0 + lane < np) copy16_to_lds(W + a0 + 16 * int64_t(p0 + lane), dst + 16 * p0);
     };
+    // a chunk of at most kRing sub-tiles is requested whole up front
     int issued = 0;
-    for (; issued < min(kRing - 1, nsub); ++issued) issue(issued);
+    for (; issued < (nsub <= kRing ? nsub : kRing - 1); ++issued) issue(issued);
     pre();
     for (int sb = 0; sb < nsub; ++sb) {
       // sub-tile sb has landed once only this wave's later copies remain;
@@ -407,38 +410,47 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
       __syncthreads();
     }
   }
-  // the sub-tiles are free now: slot sums of 16 columns a round go through
-  // them, (slot, half unit) rows 20 floats apart so neighbouring threads'
-  // 16-byte writes fall in different banks
+  // the sub-tiles are free now: slot sums go through them, all 32 columns in
+  // one round when `reg_bytes` holds them, else 16 a round; (slot, half
+  // unit) rows are C + 4 floats apart so neighbouring threads' 16-byte
+  // writes fall in different banks. Each column adds its slots in order, so
+  // the result is the same either way.
   float* red = reinterpret_cast<float*>(tiles);
+  auto reduce = [&](auto cols_c) {
+    constexpr int C = decltype(cols_c)::value, stride = C + 4;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (t >= nt) break;  // uniform: nt is the same for the whole workgroup
-    float* o = t == 0 ? out0 : out1;
+    for (int t = 0; t < NT; ++t) {
+      if (t >= nt) break;  // uniform: nt is the same for the whole workgroup
+      float* o = t == 0 ? out0 : out1;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (active) {
-        float* dst = red + (sl * U + u) * kRedStride;
+      for (int h = 0; h < 32 / C; ++h) {
+        if (active) {
+          float* dst = red + (sl * U + u) * stride;
 #pragma unroll
-        for (int e = 0; e < 16; e += 4) {
-          const int g = 16 * h + e;
-          *reinterpret_cast<f32x4*>(dst + e) =
-              f32x4{acc[t][g] - off[t][F::off_index(g)], acc[t][g + 1] - off[t][F::off_index(g + 1)],
-                    acc[t][g + 2] - off[t][F::off_index(g + 2)], acc[t][g + 3] - off[t][F::off_index(g + 3)]};
+          for (int e = 0; e < C; e += 4) {
+            const int g = C * h + e;
+            *reinterpret_cast<f32x4*>(dst + e) =
+                f32x4{acc[t][g] - off[t][F::off_index(g)], acc[t][g + 1] - off[t][F::off_index(g + 1)],
+                      acc[t][g + 2] - off[t][F::off_index(g + 2)], acc[t][g + 3] - off[t][F::off_index(g + 3)]};
+          }
         }
-      }
-      __syncthreads();
-      for (int q = tid; q < U * 16; q += kMoeThreads) {
-        const int un = q >> 4, e = q & 15;
-        const float* src = red + un * kRedStride + e;
-        float v = 0.f;
+        __syncthreads();
+        for (int q = tid; q < U * C; q += kMoeThreads) {
+          const int un = q / C, e = q - un * C;
+          const float* src = red + un * stride + e;
+          float v = 0.f;
 #pragma unroll 8
-        for (int k = 0; k < RS; ++k) v += src[k * U * kRedStride];
-        o[32 * un + 16 * h + e] = v;
+          for (int k = 0; k < RS; ++k) v += src[k * U * stride];
+          o[32 * un + C * h + e] = v;
+        }
+        __syncthreads();
       }
-      __syncthreads();
     }
-  }
+  };
+  if (int64_t(RS) * U * (32 + 4) * int64_t(sizeof(float)) <= reg_bytes)
+    reduce(std::integral_constant<int, 32>{});
+  else
+    reduce(std::integral_constant<int, 16>{});
 }
 
 // -------------------------------------------------------------- gate / up --
@@ -515,14 +527,50 @@ __global__ void __launch_bounds__(kMoeThreads)
     // a slot's last token alone takes the one-token pass (no FMAs for an absent second token)
     if (NT > 1 && nt == 1)
       chunk_sums<F, 1, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt,
-                            tiles, tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
+                            tiles, tile_cap, plan.reg_a, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
     else
       chunk_sums<F, NT, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt,
-                             tiles, tile_cap, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
+                             tiles, tile_cap, plan.reg_a, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
   }
 }
 
 // ------------------------------------------------------------------- down --
+// a = silu(h) * p for rows [r0, r0 + nrows) of the down chunk and tokens
+// (pairs) q0 .. q0 + nt - 1, h and p summed over the gate/up chunk sums in a
+// fixed order (ops.rs:85-87, moe.rs:119-121): 4 adjacent lanes load every 4th
+// of the (at most 32) chunk sums, then a fixed shuffle tree adds the 4.
+// Writes xs[t * cb + r]; hp ([2][2][cb] floats) is scratch.
+__device__ __forceinline__ void stage_silu(const MoePlan& plan, const float* __restrict__ pa, int q0, int nt,
+                                           int r0, int nrows, float* xs, float* hp) {
+  const int tid = threadIdx.x, sub = tid & 3;
+  const int n_el = nt * 2 * nrows;
+  for (int i0 = 0; i0 < n_el * 4; i0 += kMoeThreads) {
+    const int idx = i0 + tid, el = idx >> 2;
+    const bool ok = el < n_el;
+    const int elc = ok ? el : 0;
+    const int t = elc / (2 * nrows), rem = elc - t * 2 * nrows, mm = rem / nrows, r = rem - mm * nrows;
+    const float* src = pa + ((int64_t(q0 + t) * 2 + mm) * plan.nch_a) * plan.n_ff + r0 + r;
+    float v[kMoeMaxChunks / 4];
+#pragma unroll
+    for (int q = 0; q < kMoeMaxChunks / 4; ++q) {
+      const int k = sub + 4 * q;
+      v[q] = ok && k < plan.nch_a ? src[int64_t(k) * plan.n_ff] : 0.f;
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < kMoeMaxChunks / 4; ++q) sum += v[q];
+    sum += __shfl_xor(sum, 1, kWave);
+    sum += __shfl_xor(sum, 2, kWave);
+    if (ok && sub == 0) hp[el] = sum;
+  }
+  __syncthreads();
+  for (int i = tid; i < nt * nrows; i += kMoeThreads) {
+    const int t = i / nrows, r = i - t * nrows;
+    const float h = hp[(t * 2) * nrows + r], pv = hp[(t * 2 + 1) * nrows + r];
+    xs[t * plan.cb + r] = h / (1.f + expf(-h)) * pv;
+  }
+}
+
 // Workgroup (row chunk c over n_ff, slot s): first a = silu(h) * p for the
 // chunk's rows and the slot's tokens, h and p summed over the gate/up chunks
 // in a fixed order (ops.rs:85-87, moe.rs:119-121); then chunk sums of
@@ -546,67 +594,32 @@ __global__ void __launch_bounds__(kMoeThreads)
   float* hp = xs + 2 * plan.cb;                                 // [2][2][cb]
   const int64_t w_total = int64_t(plan.n_expert) * plan.n_ff * plan.rb_b;
   const int64_t w_off = (int64_t(e) * plan.n_ff + r0) * plan.rb_b;
-  const int tid = threadIdx.x, sub = tid & 3;
   for (int j = 0; j < cnt; j += NT) {
     const int nt = min(NT, cnt - j);
-    auto stage_a = [&]() {
-      // h, p for (token t, matrix mm, row r): 4 adjacent lanes load every 4th
-      // of the (at most 32) gate/up chunk sums at once, then a fixed shuffle
-      // tree adds the 4
-      const int n_el = nt * 2 * nrows;
-      for (int i0 = 0; i0 < n_el * 4; i0 += kMoeThreads) {
-        const int idx = i0 + tid, el = idx >> 2;
-        const bool ok = el < n_el;
-        const int elc = ok ? el : 0;
-        const int t = elc / (2 * nrows), rem = elc - t * 2 * nrows, mm = rem / nrows, r = rem - mm * nrows;
-        const float* src = pa + ((int64_t(p0 + j + t) * 2 + mm) * plan.nch_a) * plan.n_ff + r0 + r;
-        float v[kMoeMaxChunks / 4];
-#pragma unroll
-        for (int q = 0; q < kMoeMaxChunks / 4; ++q) {
-          const int k = sub + 4 * q;
-          v[q] = ok && k < plan.nch_a ? src[int64_t(k) * plan.n_ff] : 0.f;
-        }
-        float sum = 0.f;
-#pragma unroll
-        for (int q = 0; q < kMoeMaxChunks / 4; ++q) sum += v[q];
-        sum += __shfl_xor(sum, 1, kWave);
-        sum += __shfl_xor(sum, 2, kWave);
-        if (ok && sub == 0) hp[el] = sum;
-      }
-      __syncthreads();
-      for (int i = tid; i < nt * nrows; i += kMoeThreads) {
-        const int t = i / nrows, r = i - t * nrows;
-        const float h = hp[(t * 2) * nrows + r], pv = hp[(t * 2 + 1) * nrows + r];
-        xs[t * plan.cb + r] = h / (1.f + expf(-h)) * pv;
-      }
-    };
+    auto stage_a = [&]() { stage_silu(plan, pa, p0 + j, nt, r0, nrows, xs, hp); };
     // part[(p * nch_b + c) * n_embd + col]
     float* o0 = part + (int64_t(p0 + j) * plan.nch_b + c) * plan.n_embd;
     float* o1 = o0 + int64_t(plan.nch_b) * plan.n_embd;
     if (NT > 1 && nt == 1)
       chunk_sums<F, 1, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
-                            tiles, tile_cap, o0, o1, q6_down, stage_a);
+                            tiles, tile_cap, plan.reg_b, o0, o1, q6_down, stage_a);
     else
       chunk_sums<F, NT, DMA>(down, plan.rb_b, w_off, w_total, plan.n_embd, nrows, plan.sr_b, xs, xs + plan.cb, nt,
-                             tiles, tile_cap, o0, o1, q6_down, stage_a);
+                             tiles, tile_cap, plan.reg_b, o0, o1, q6_down, stage_a);
   }
 }
 
 // ---------------------------------------------------------------- combine --
-// Block: 32 columns of one token x 8 expert lanes. Lane (col, a) sums the
-// down chunk sums of the token's a-th expert; then the token's experts are
-// added in ascending id order: out += w * d, skipping w == 0 (moe.rs:112-126).
-__global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const uint8_t* ws,
-                                                          float* __restrict__ out) {
-  __shared__ float dsum[kMoeMaxTopK][32];
-  const int blocks_per_tok = plan.n_embd / 32;
-  const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
+// 32 columns of token t, by 256 threads as 32 columns x 8 expert lanes. Lane
+// (col, a) sums the down chunk sums of the token's a-th expert (pair qa[a]);
+// then the token's experts are added in ascending id order: out += w * d,
+// skipping w == 0 (moe.rs:112-126).
+__device__ __forceinline__ void combine_cols(const MoePlan& plan, const float* __restrict__ part,
+                                             const int* qa, const float* wa, int t, int col0,
+                                             float* __restrict__ out, float (*dsum)[32]) {
   const int cl = threadIdx.x & 31, al = threadIdx.x >> 5;
-  const int* tokpair = reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k;
-  const float* wts = reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k;
-  const float* part = reinterpret_cast<const float*>(ws + plan.o_part_b);
   for (int a = al; a < plan.top_k; a += 8) {
-    const float* src = part + int64_t(tokpair[a]) * plan.nch_b * plan.n_embd + col0 + cl;
+    const float* src = part + int64_t(qa[a]) * plan.nch_b * plan.n_embd + col0 + cl;
     float v[kMoeMaxChunks];
 #pragma unroll
     for (int k = 0; k < kMoeMaxChunks; ++k) v[k] = k < plan.nch_b ? src[int64_t(k) * plan.n_embd] : 0.f;
@@ -619,11 +632,22 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const ui
   if (al == 0) {
     float acc = 0.f;
     for (int a = 0; a < plan.top_k; ++a) {
-      const float wv = wts[a];
+      const float wv = wa[a];
       if (wv != 0.f) acc = __fadd_rn(acc, __fmul_rn(wv, dsum[a][cl]));
     }
     out[int64_t(t) * plan.n_embd + col0 + cl] = acc;
   }
+}
+
+// Block: 32 columns of one token.
+__global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const uint8_t* ws,
+                                                          float* __restrict__ out) {
+  __shared__ float dsum[kMoeMaxTopK][32];
+  const int blocks_per_tok = plan.n_embd / 32;
+  const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
+  combine_cols(plan, reinterpret_cast<const float*>(ws + plan.o_part_b),
+               reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k,
+               reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum);
 }
 
 // ------------------------------------------------------------------- host --
@@ -679,7 +703,8 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.staged = total_a % 16 == 0 && total_b % 16 == 0;
   const int nsub_a = (p.ca + p.sr_a - 1) / p.sr_a, nsub_b = (p.cb + p.sr_b - 1) / p.sr_b;
   const size_t nbuf_a = std::min(p.staged ? kRing : 2, nsub_a), nbuf_b = std::min(p.staged ? kRing : 2, nsub_b);
-  // the sub-tiles' LDS is reused for the row-slot reduction (16 columns a round)
+  // the sub-tiles' LDS is reused for the row-slot reduction (16 columns a
+  // round at least; all 32 when the sub-tiles' bytes hold them)
   const size_t red_a = sizeof(float) * size_t(rs_a) * (n_ff / 32) * kRedStride;
   const size_t red_b = sizeof(float) * size_t(rs_b) * (n_embd / 32) * kRedStride;
   const size_t reg_a = std::max(nbuf_a * cap_a, red_a), reg_b = std::max(nbuf_b * cap_b, red_b);

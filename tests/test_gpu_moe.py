@@ -167,6 +167,74 @@ def test_moe_ffn_dev_unaligned_tensors_match(backend, n_tok):
     assert np.array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("qg,qd", [(12, 14), (8, 8), (14, 12), (12, 8), (8, 14)])
+def test_moe_ffn_one_token_formats(backend, oracle, qg, qd):
+    """One token (routed inside the gate/up launch) over aligned tensors whose
+    sizes are multiples of 16 bytes (the global_load_lds copy ring), for each
+    gate/up x down type pair."""
+    n_expert, n_embd, n_ff, top_k = 24, 512, 256, 6
+    say("moe ffn one token", qg, qd)
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, qg, qd, 7000 + 10 * qg + qd)
+    assert all(a.nbytes % 16 == 0 for a in (gate, up, down))
+    logits = S.router_logits(7100 + qg, 1, n_expert)
+    x = S.normal_f32(7200 + qd, n_embd).reshape(1, n_embd)
+    out = backend.moe_ffn(H.ExpertView(f"gf{qg}{qd}", qg, n_expert, n_embd, n_ff, gate),
+                          H.ExpertView(f"uf{qg}{qd}", qg, n_expert, n_embd, n_ff, up),
+                          H.ExpertView(f"df{qg}{qd}", qd, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    ref = oracle_moe(oracle, qg, qd, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    assert rel_err(out, ref) <= 1e-3, rel_err(out, ref)
+    assert elem_rel_err(out[0], ref[0], floor=1.0) <= 1e-3
+
+
+def test_moe_ffn_one_token_repeat_and_graph(backend):
+    """Back-to-back one-token calls on one workspace (which starts out
+    filled with garbage), with new logits each time, and replays of a
+    captured HIP graph (eager work between replays) all equal the eager
+    result of the same inputs: nothing carries over between calls."""
+    import torch
+    n_expert, n_embd, n_ff, top_k = 64, 1024, 512, 8
+    say("moe ffn one token repeat + graph")
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 7300)
+    dev = torch.device("cuda:0")
+    tg, tu, td = (torch.from_numpy(a).to(dev) for a in (gate, up, down))
+    x = torch.from_numpy(S.normal_f32(7400, n_embd)).to(dev)
+    lgs = [torch.from_numpy(S.router_logits(7500 + i, 1, n_expert)).to(dev) for i in range(3)]
+    nb = H.moe_workspace_bytes(1, top_k, n_expert, n_embd, n_ff, 12, 14)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    ws.fill_(0xA5)
+    out = torch.empty(n_embd, dtype=torch.float32, device=dev)
+
+    def call(lg, stream):
+        H.moe_ffn_dev((12, 0, tg.data_ptr()), (12, 0, tu.data_ptr()), (14, 0, td.data_ptr()), n_expert, n_embd,
+                      n_ff, lg.data_ptr(), 1, top_k, x.data_ptr(), out.data_ptr(), ws.data_ptr(), nb, stream)
+
+    eager = []
+    for lg in lgs + lgs:
+        call(lg, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        eager.append(out.cpu().numpy().copy())
+    for i in range(3):
+        assert np.all(np.isfinite(eager[i]))
+        assert np.array_equal(eager[i], eager[i + 3])
+    assert not np.array_equal(eager[0], eager[1])
+    s = torch.cuda.Stream(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        call(lgs[2], s.cuda_stream)  # warm-up outside capture
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        call(lgs[2], torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[2]), rep
+        call(lgs[0], torch.cuda.current_stream().cuda_stream)  # eager work between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[0]), rep
+
+
 def test_moe_errors(backend):
     say("moe errors")
     g = H.ExpertView("eg", 12, 4, 256, 256, S.matrix(12, 1, 4 * 256, 256))
