@@ -43,13 +43,16 @@ constexpr int kMoeMaxTokens = 256;
 struct MoePlan {
   int n_tok, top_k, n_expert, n_embd, n_ff;
   int s_max;                     // most unique experts a call can route to
+  int z_max;                     // most work items: (expert, one or two of its pairs)
   int64_t rb_a, rb_b;            // row bytes of gate/up and of down
   int ca, nch_a;                 // gate/up: rows per chunk, chunks (over n_embd)
   int cb, nch_b;                 // down: rows per chunk, chunks (over n_ff)
   int sr_a, sr_b;                // rows per LDS sub-tile
   int nbuf_a, nbuf_b;            // LDS sub-tile buffers (1 when one sub-tile holds the chunk)
   int reg_a, reg_b;              // LDS bytes of the sub-tiles, reused for the row-slot reduction
-  size_t o_ids, o_wts, o_meta, o_slot_e, o_slot_off, o_slot_cnt, o_pair_tok, o_tokpair;
+  size_t o_ids, o_wts, o_meta, o_tokpair;
+  size_t o_item_e, o_item_off, o_item_cnt;  // per work item: expert, first pair, pairs (1 or 2)
+  size_t o_item_tok;             // per work item: the tokens of its pairs
   size_t o_part_a;               // [pair][2][nch_a][n_ff]: chunk sums of gate . x, up . x
   size_t o_part_b;               // [pair][nch_b][n_embd]: chunk sums of down . a
   size_t route_lds, lds_a, lds_b;  // dynamic LDS per kernel

@@ -16,15 +16,17 @@
 // Four launches (three for one token, whose gate/up workgroups route it
 // themselves):
 //   route    one workgroup routes every token (a wave per token) and groups
-//            the (token, expert) pairs by expert: the unique experts in
-//            ascending id are "slots", each with its pairs;
-//   gate/up  workgroup (row chunk, matrix, slot): the chunk's rows are
+//            the (token, expert) pairs by expert, in ascending expert id;
+//            each expert's pairs, two at a time, are "work items" (so every
+//            workgroup below streams its rows once, and none runs twice as
+//            long as the rest);
+//   gate/up  workgroup (row chunk, matrix, item): the chunk's rows are
 //            contiguous bytes, copied into an LDS ring of sub-tiles with
-//            global_load_lds (two sub-tiles in flight); threads decode their
-//            32-column half unit from LDS and apply each row to two of the
-//            slot's tokens per pass (one for a slot's odd last token);
-//            row-slot sums reduce in LDS to one chunk sum per pair;
-//   down     workgroup (row chunk, slot): a = silu(h) * p for its rows from
+//            global_load_lds (the whole chunk, or two sub-tiles, in flight);
+//            threads decode their 32-column half unit from LDS and apply each
+//            row to the item's one or two tokens; row-slot sums reduce in
+//            LDS to one chunk sum per pair;
+//   down     workgroup (row chunk, item): a = silu(h) * p for its rows from
 //            the gate/up chunk sums (fixed order), then the same streaming;
 //   combine  out[t] = sum over t's experts in ascending id of w * d, with d
 //            the sum of the down chunk sums.
@@ -187,6 +189,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   const int pairs = plan.n_tok * K;
   int* s_ids = rlds;                                     // [pairs]
   float* s_w = reinterpret_cast<float*>(rlds + pairs);   // [pairs]
+  int* s_pt = rlds + 2 * pairs;                          // [pairs]: token of each grouped pair
   int* ids = reinterpret_cast<int*>(ws + plan.o_ids);
   float* wts = reinterpret_cast<float*>(ws + plan.o_wts);
   for (int e = tid; e < kMoeMaxExperts; e += kRouteThreads) cnt[e] = 0;
@@ -210,7 +213,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   for (int i = tid; i < pairs; i += kRouteThreads) atomicAdd(&cnt[s_ids[i]], 1);
   __syncthreads();
   const int c = cnt[tid];
-  const int nz = c > 0;
+  const int nz = (c + 1) >> 1;  // this expert's work items: its pairs two at a time
   int snz = nz, stot = c;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -230,23 +233,29 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
     base_nz += wave_nz[w2];
     base_tot += wave_tot[w2];
   }
-  const int slot = base_nz + snz - nz, pos = base_tot + stot - c;
-  if (c > 0) {
-    reinterpret_cast<int*>(ws + plan.o_slot_e)[slot] = tid;
-    reinterpret_cast<int*>(ws + plan.o_slot_off)[slot] = pos;
-    reinterpret_cast<int*>(ws + plan.o_slot_cnt)[slot] = c;
+  const int item = base_nz + snz - nz, pos = base_tot + stot - c;
+  for (int i = 0; i < nz; ++i) {
+    reinterpret_cast<int*>(ws + plan.o_item_e)[item + i] = tid;
+    reinterpret_cast<int*>(ws + plan.o_item_off)[item + i] = pos + 2 * i;
+    reinterpret_cast<int*>(ws + plan.o_item_cnt)[item + i] = min(2, c - 2 * i);
   }
   cursor[tid] = pos;
   if (tid == kRouteThreads - 1) reinterpret_cast<int*>(ws + plan.o_meta)[0] = base_nz + snz;
   __syncthreads();
   // a pair's position within its expert's run does not affect any result:
   // each pair's sums are computed on their own and found through tokpair
-  int* pair_tok = reinterpret_cast<int*>(ws + plan.o_pair_tok);
   int* tokpair = reinterpret_cast<int*>(ws + plan.o_tokpair);
   for (int i = tid; i < pairs; i += kRouteThreads) {
     const int q = atomicAdd(&cursor[s_ids[i]], 1);
-    pair_tok[q] = i / K;
+    s_pt[q] = i / K;
     tokpair[i] = q;
+  }
+  __syncthreads();
+  // each item's tokens, next to its other fields
+  int* item_tok = reinterpret_cast<int*>(ws + plan.o_item_tok);
+  for (int i = 0; i < nz; ++i) {
+    item_tok[2 * (item + i)] = s_pt[pos + 2 * i];
+    item_tok[2 * (item + i) + 1] = c - 2 * i > 1 ? s_pt[pos + 2 * i + 1] : 0;
   }
 }
 
@@ -454,14 +463,14 @@ __device__ __forceinline__ void chunk_sums(const uint8_t* W, int64_t rb, int64_t
 }
 
 // -------------------------------------------------------------- gate / up --
-// Workgroup (row chunk c, matrix m, slot s): chunk sums of gate_e . x_t or
-// up_e . x_t for every pair (token t, expert e) of the slot, two tokens per
+// Workgroup (row chunk c, matrix m, work item s): chunk sums of gate_e . x_t
+// or up_e . x_t for the item's pairs (token t, expert e), both tokens in one
 // pass over the chunk's bytes.
 // ROUTE (one token, at most 256 experts): the workgroup routes the token
 // itself (route_token, the route kernel's own steps, so ids and weights are
-// the same), its slots being the token's k experts in ascending id; workgroup
-// (0, 0, 0) writes the ids, weights and slot tables that down and combine
-// read, and no workgroup reads them here.
+// the same), its items being the token's k experts in ascending id;
+// workgroup (0, 0, 0) writes the ids, weights and item tables that down and
+// combine read, and no workgroup reads them here.
 template <class F, int NT, bool DMA, bool ROUTE>
 __global__ void __launch_bounds__(kMoeThreads)
     moe_gateup_kernel(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, MoePlan plan,
@@ -469,7 +478,7 @@ __global__ void __launch_bounds__(kMoeThreads)
                       const float* __restrict__ logits) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x, m = blockIdx.y, s = blockIdx.z;
-  int n_slots, e, p0, cnt;
+  int n_items, e, p0, cnt, tok0 = 0, tok1 = 0;
   if constexpr (ROUTE) {
     __shared__ int r_id[kMoeMaxTopK];
     __shared__ float r_p[kMoeMaxTopK];
@@ -482,28 +491,32 @@ __global__ void __launch_bounds__(kMoeThreads)
       if (c == 0 && m == 0 && s == 0 && a < K) {
         reinterpret_cast<int*>(ws + plan.o_ids)[a] = id;
         reinterpret_cast<float*>(ws + plan.o_wts)[a] = wv;
-        reinterpret_cast<int*>(ws + plan.o_slot_e)[a] = id;
-        reinterpret_cast<int*>(ws + plan.o_slot_off)[a] = a;
-        reinterpret_cast<int*>(ws + plan.o_slot_cnt)[a] = 1;
-        reinterpret_cast<int*>(ws + plan.o_pair_tok)[a] = 0;
+        reinterpret_cast<int*>(ws + plan.o_item_e)[a] = id;
+        reinterpret_cast<int*>(ws + plan.o_item_off)[a] = a;
+        reinterpret_cast<int*>(ws + plan.o_item_cnt)[a] = 1;
+        reinterpret_cast<int*>(ws + plan.o_item_tok)[2 * a] = 0;
+        reinterpret_cast<int*>(ws + plan.o_item_tok)[2 * a + 1] = 0;
         reinterpret_cast<int*>(ws + plan.o_tokpair)[a] = a;
         if (a == 0) reinterpret_cast<int*>(ws + plan.o_meta)[0] = K;
       }
     }
     __syncthreads();
-    n_slots = K;
-    if (s >= n_slots) return;
+    n_items = K;
+    if (s >= n_items) return;
     e = r_id[s];
     p0 = s;
     cnt = 1;
   } else {
-    n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
-    if (s >= n_slots) return;
-    e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
-    p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
-    cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
+    // all of the item's fields at once (the tables hold z_max entries, so
+    // an item past the count reads allocated memory before returning)
+    n_items = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
+    e = reinterpret_cast<const int*>(ws + plan.o_item_e)[s];
+    p0 = reinterpret_cast<const int*>(ws + plan.o_item_off)[s];
+    cnt = reinterpret_cast<const int*>(ws + plan.o_item_cnt)[s];
+    tok0 = reinterpret_cast<const int*>(ws + plan.o_item_tok)[2 * s];
+    tok1 = reinterpret_cast<const int*>(ws + plan.o_item_tok)[2 * s + 1];
+    if (s >= n_items) return;
   }
-  const int* pair_tok = reinterpret_cast<const int*>(ws + plan.o_pair_tok);
   float* part = reinterpret_cast<float*>(ws + plan.o_part_a);
   const int r0 = c * plan.ca, nrows = min(plan.ca, plan.n_embd - r0);
   const int tile_cap = (plan.sr_a * int(plan.rb_a) + 31) & ~15;
@@ -517,14 +530,14 @@ __global__ void __launch_bounds__(kMoeThreads)
     auto stage_x = [&]() {
       for (int i = threadIdx.x; i < nt * nrows; i += kMoeThreads) {
         const int t = i / nrows, r = i - t * nrows;
-        const int tok = ROUTE ? 0 : pair_tok[p0 + j + t];
+        const int tok = t == 0 ? tok0 : tok1;
         xs[t * plan.ca + r] = x[int64_t(tok) * plan.n_embd + r0 + r];
       }
     };
     // part[((p * 2 + m) * nch_a + c) * n_ff + col]
     float* o0 = part + ((int64_t(p0 + j) * 2 + m) * plan.nch_a + c) * plan.n_ff;
     float* o1 = o0 + int64_t(2) * plan.nch_a * plan.n_ff;
-    // a slot's last token alone takes the one-token pass (no FMAs for an absent second token)
+    // an item with one token takes the one-token pass (no FMAs for an absent second token)
     if (NT > 1 && nt == 1)
       chunk_sums<F, 1, DMA>(W, plan.rb_a, w_off, w_total, plan.n_ff, nrows, plan.sr_a, xs, xs + plan.ca, nt,
                             tiles, tile_cap, plan.reg_a, o0, o1, m == 0 ? q6_gate : q6_up, stage_x);
@@ -571,8 +584,8 @@ __device__ __forceinline__ void stage_silu(const MoePlan& plan, const float* __r
   }
 }
 
-// Workgroup (row chunk c over n_ff, slot s): first a = silu(h) * p for the
-// chunk's rows and the slot's tokens, h and p summed over the gate/up chunks
+// Workgroup (row chunk c over n_ff, work item s): first a = silu(h) * p for
+// the chunk's rows and the item's tokens, h and p summed over the gate/up chunks
 // in a fixed order (ops.rs:85-87, moe.rs:119-121); then chunk sums of
 // down_e . a.
 template <class F, int NT, bool DMA>
@@ -580,11 +593,11 @@ __global__ void __launch_bounds__(kMoeThreads)
     moe_down_kernel(const uint8_t* __restrict__ down, MoePlan plan, uint8_t* ws, int q6_down) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x, s = blockIdx.y;
-  const int n_slots = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
-  if (s >= n_slots) return;
-  const int e = reinterpret_cast<const int*>(ws + plan.o_slot_e)[s];
-  const int p0 = reinterpret_cast<const int*>(ws + plan.o_slot_off)[s];
-  const int cnt = reinterpret_cast<const int*>(ws + plan.o_slot_cnt)[s];
+  const int n_items = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
+  const int e = reinterpret_cast<const int*>(ws + plan.o_item_e)[s];
+  const int p0 = reinterpret_cast<const int*>(ws + plan.o_item_off)[s];
+  const int cnt = reinterpret_cast<const int*>(ws + plan.o_item_cnt)[s];
+  if (s >= n_items) return;
   const float* pa = reinterpret_cast<const float*>(ws + plan.o_part_a);
   float* part = reinterpret_cast<float*>(ws + plan.o_part_b);
   const int r0 = c * plan.cb, nrows = min(plan.cb, plan.n_ff - r0);
@@ -681,6 +694,9 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.rb_b = byte_size(qb, n_embd);
   const int pairs = n_tok * top_k;
   p.s_max = pairs < n_expert ? pairs : n_expert;
+  // work items (an expert's pairs two at a time): sum of ceil(cnt / 2) over
+  // the experts routed to, at most (pairs + s_max) / 2
+  p.z_max = (pairs + p.s_max + 1) / 2;
   // enough workgroups to cover the chip when few experts are routed, few
   // enough chunks that the partial sums stay small when many are
   const int rs_a = kMoeThreads / (n_ff >> 5), rs_b = kMoeThreads / (n_embd >> 5);
@@ -716,7 +732,7 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.nbuf_b = int(nbuf_b);
   if (p.lds_a > 160 * 1024 || p.lds_b > 160 * 1024) return false;
   if (cap_a > size_t(tp) * 16 * kMoeThreads || cap_b > size_t(tp) * 16 * kMoeThreads) return false;
-  p.route_lds = size_t(pairs) * 8;
+  p.route_lds = size_t(pairs) * 12;
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -726,10 +742,10 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.o_ids = take(sizeof(int) * pairs);
   p.o_wts = take(sizeof(float) * pairs);
   p.o_meta = take(sizeof(int) * 4);
-  p.o_slot_e = take(sizeof(int) * p.s_max);
-  p.o_slot_off = take(sizeof(int) * p.s_max);
-  p.o_slot_cnt = take(sizeof(int) * p.s_max);
-  p.o_pair_tok = take(sizeof(int) * pairs);
+  p.o_item_e = take(sizeof(int) * p.z_max);
+  p.o_item_off = take(sizeof(int) * p.z_max);
+  p.o_item_cnt = take(sizeof(int) * p.z_max);
+  p.o_item_tok = take(sizeof(int) * 2 * p.z_max);
   p.o_tokpair = take(sizeof(int) * pairs);
   p.o_part_a = take(sizeof(float) * size_t(pairs) * 2 * p.nch_a * n_ff);
   p.o_part_b = take(sizeof(float) * size_t(pairs) * p.nch_b * n_embd);
@@ -746,7 +762,7 @@ static bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 template <class FA>
 static void launch_gateup(const MoePlan& p, const void* gate, const void* up, const float* x,
                           uint8_t* ws, int q6g, int q6u, const float* logits, bool route, hipStream_t s) {
-  const dim3 g(p.nch_a, 2, p.s_max), b(kMoeThreads);
+  const dim3 g(p.nch_a, 2, p.z_max), b(kMoeThreads);
   const uint8_t *gp = static_cast<const uint8_t*>(gate), *upp = static_cast<const uint8_t*>(up);
   const bool dma = p.staged && aligned16(gate) && aligned16(up);
 #define SH_GATEUP(NT, DMA, ROUTE) \
@@ -762,7 +778,7 @@ static void launch_gateup(const MoePlan& p, const void* gate, const void* up, co
 
 template <class FB>
 static void launch_down(const MoePlan& p, const void* down, uint8_t* ws, int q6d, hipStream_t s) {
-  const dim3 g(p.nch_b, p.s_max), b(kMoeThreads);
+  const dim3 g(p.nch_b, p.z_max), b(kMoeThreads);
   const uint8_t* dp = static_cast<const uint8_t*>(down);
   const bool dma = p.staged && aligned16(down);
   if (dma && p.n_tok == 1) hipLaunchKernelGGL((moe_down_kernel<FB, 1, true>), g, b, p.lds_b, s, dp, p, ws, q6d);
