@@ -130,6 +130,19 @@ __device__ __forceinline__ void copy16_to_lds(const uint8_t* src, uint8_t* dst) 
                                    (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
 
+// 4 int32 values -> bytes 0, 1 and 2 of each, packed v0..v3 low to high
+// (p0 the byte-0s, p1 the byte-1s, p2 the byte-2s; one v_perm each)
+__device__ __forceinline__ void transpose_bytes(uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
+                                                uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u);  // v0b0 v1b0 v0b1 v1b1
+  const uint32_t t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
+  const uint32_t u01 = __builtin_amdgcn_perm(v1, v0, 0x07030602u);  // v0b2 v1b2 v0b3 v1b3
+  const uint32_t u23 = __builtin_amdgcn_perm(v3, v2, 0x07030602u);
+  p0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u);  // byte 0 of v0..v3
+  p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u);  // byte 1
+  p2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);  // byte 2
+}
+
 // bytes [shift, shift + 4) of the 8-byte little-endian pair (lo, hi).
 __device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
   return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);

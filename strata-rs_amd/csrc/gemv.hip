@@ -517,18 +517,6 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 __host__ __device__ inline int plane_stride(int cols) { return cols + cols / 4; }
 __host__ __device__ inline int limb_lds_bytes(int cols) { return 3 * plane_stride(cols) + (cols / 32) * 16; }
 
-// 4 int32 values -> their bytes `b` packed low to high (one v_perm each pair)
-__device__ __forceinline__ void transpose_bytes(uint32_t v0, uint32_t v1, uint32_t v2, uint32_t v3,
-                                                uint32_t& p0, uint32_t& p1, uint32_t& p2) {
-  const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u);  // v0b0 v1b0 v0b1 v1b1
-  const uint32_t t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
-  const uint32_t u01 = __builtin_amdgcn_perm(v1, v0, 0x07030602u);  // v0b2 v1b2 v0b3 v1b3
-  const uint32_t u23 = __builtin_amdgcn_perm(v3, v2, 0x07030602u);
-  p0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u);  // byte 0 of v0..v3
-  p1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u);  // byte 1
-  p2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);  // byte 2
-}
-
 // Converts one 16-column group held in registers and writes it to LDS. The
 // thread handling group g ^ 1 (the other half of the 32-column block) is the
 // neighbouring lane, which shares the block maximum and sum.

@@ -5,16 +5,18 @@
 // `batch` calls of ops::gemv (crates/strata-core/src/ops.rs:14-28) with the
 // Q4_K dequantization of crates/strata-gguf/src/dequant.rs:237-270.
 //
-// Per 32-element block j of vector b a power-of-two scale 2^-k is chosen so
-// that the block's largest |x| * 2^k < 2^22, and every element becomes the
+// Per 256-element super-block of vector b a power-of-two scale 2^-k is
+// chosen so that its largest |x| * 2^k < 2^22, and every element becomes the
 // integer v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c with balanced signed
-// bytes a, b, c (so all three are int8). Q4_K codes q are 0..15, so for a
-// sub-block with weights d1 * q - m1:
-//   sum_e w_e x_e = d1 * 2^-k * (2^16 sum q a + 2^8 sum q b + sum q c)
-//                   - m1 * sum_e x_e
-// and each of the three integer sums is one exact v_mfma_i32_16x16x32_i8
-// (K = 32 = one sub-block). x is represented to 2^-23 of its block's
-// maximum; only the per-block epilogue is f32.
+// bytes a, b, c (so all three are int8; they are the bytes of
+// v + 0x808080, each less 128). Q4_K codes q are 0..15, so for a super-block
+// with weights d * sc_j * q - dmin * m_j in sub-block j:
+//   sum_e w_e x_e = d * 2^-k * (2^16 A + 2^8 B + C) - dmin * sum_j m_j * sx_j,
+//   A = sum_j sc_j * sum_{e in j} q_e a_e   (B, C likewise)
+// where each sub-block's integer sum is one exact v_mfma_i32_16x16x32_i8
+// (K = 32) and the 6-bit scales sc_j are applied in integers (v_mad_i32_i24),
+// so the f32 work is once per super-block; sx_j is the f32 sum of x over
+// sub-block j. x is represented to 2^-23 of its super-block's maximum.
 //
 // Mapping: a wave owns a tile of 16 weight rows (the MFMA's B columns; the
 // vectors are its A rows, padded to 16) and a share of the super-blocks;
@@ -35,16 +37,10 @@ constexpr int kMbMaxCols = 4096;        // columns whose limbs fit LDS with the 
 
 __host__ __device__ inline int mb_limb_bytes(int nblk) { return 3 * nblk * kMbMaxVec * kMbTokStride; }
 
-// Balanced signed-byte digits of an integer |v| < 2^22.
-__device__ __forceinline__ void balanced_digits(int v, int& a, int& b, int& c) {
-  c = ((v + 128) & 255) - 128;
-  const int v1 = (v - c) >> 8;
-  b = ((v1 + 128) & 255) - 128;
-  a = (v1 - b) >> 8;
-}
+constexpr int kMbMaxWaves = 12;  // waves per workgroup (T * S)
 
 template <int PER>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(64 * kMbMaxWaves)
     gemv_mfma_q4k_kernel(const uint8_t* __restrict__ w, int rows, int cols, int64_t row_bytes,
                          const float* __restrict__ x, float* __restrict__ y, int nb, int T, int S) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -52,11 +48,14 @@ __global__ void __launch_bounds__(512)
   const int nthreads = blockDim.x;
   const int nblk = cols >> 5, nsb = cols >> 8;
   uint8_t* limbs = lds;                                                  // [3][nblk][8][40]
-  float* pk = reinterpret_cast<float*>(lds + mb_limb_bytes(nblk));      // [nblk][8]: 2^-k
+  float* pk = reinterpret_cast<float*>(lds + mb_limb_bytes(nblk));      // [nblk][8] (2^-k uses [nsb][8])
   float* sx = pk + nblk * kMbMaxVec;                                     // [nblk][8]: sum of x
   float* red = sx + nblk * kMbMaxVec;                                    // [T][S][64][4]
 
-  // ---- activations -> limbs: one (vector, block) pair per thread per round
+  // ---- activations -> limbs: one (vector, block) pair per thread per round;
+  // the 8 blocks of a super-block are 8 adjacent lanes (nblk and the
+  // workgroup size are multiples of 8), which share its maximum
+  float* pk8 = pk;  // [nsb][8]: 2^-k of (super-block, vector)
   for (int p = tid; p < nb * nblk; p += nthreads) {
     const int b = p / nblk, j = p - b * nblk;
     const f32x4* src = reinterpret_cast<const f32x4*>(x + int64_t(b) * cols + 32 * j);
@@ -75,30 +74,30 @@ __global__ void __launch_bounds__(512)
       m = fmaxf(m, fabsf(v[k]));
       s += v[k];
     }
+    m = fmaxf(m, __shfl_xor(m, 1, kWave));
+    m = fmaxf(m, __shfl_xor(m, 2, kWave));
+    m = fmaxf(m, __shfl_xor(m, 4, kWave));
     int e = 0;
     (void)frexpf(m, &e);
     const int kk = m > 0.f ? min(22 - e, 126) : 0;
     const float up = ldexpf(1.f, kk);
-    pk[j * kMbMaxVec + b] = (m - m == 0.f) ? ldexpf(1.f, -kk) : __builtin_nanf("");
+    if ((j & 7) == 0) pk8[(j >> 3) * kMbMaxVec + b] = (m - m == 0.f) ? ldexpf(1.f, -kk) : __builtin_nanf("");
     sx[j * kMbMaxVec + b] = s;
     uint32_t wa[8], wb[8], wc[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      uint32_t pa = 0, pb = 0, pc = 0;
+      // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22),
+      // less 0x4B400000 plus 0x808080: u = v + 0x808080, whose bytes less 128
+      // are the balanced digits c, b, a
+      uint32_t u[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
-        const float t = __builtin_fmaf(v[4 * k + q], up, 12582912.0f);
-        const int iv = int(__builtin_bit_cast(uint32_t, t) - 0x4B400000u);
-        int da, db, dc;
-        balanced_digits(iv, da, db, dc);
-        pa |= (uint32_t(da) & 0xFFu) << (8 * q);
-        pb |= (uint32_t(db) & 0xFFu) << (8 * q);
-        pc |= (uint32_t(dc) & 0xFFu) << (8 * q);
-      }
-      wa[k] = pa;
-      wb[k] = pb;
-      wc[k] = pc;
+      for (int q = 0; q < 4; ++q)
+        u[q] = __builtin_bit_cast(uint32_t, __builtin_fmaf(v[4 * k + q], up, 12582912.0f)) - 0x4ABF7F80u;
+      uint32_t pc, pb, pa;
+      transpose_bytes(u[0], u[1], u[2], u[3], pc, pb, pa);
+      wa[k] = pa ^ 0x80808080u;
+      wb[k] = pb ^ 0x80808080u;
+      wc[k] = pc ^ 0x80808080u;
     }
     uint8_t* da = limbs + (0 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
     uint8_t* db = limbs + (1 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
@@ -120,8 +119,7 @@ __global__ void __launch_bounds__(512)
   const uint8_t* wr = w + int64_t(row) * row_bytes;
   const int tok_a = r16;            // the vector this lane feeds as an A row
   const bool a_real = tok_a < nb;
-  const int tok_d = 4 * kg;         // first vector of this lane's D values
-  const bool d_real = tok_d < nb;   // (kg 2, 3 hold padding vectors)
+  const int tok_d = 4 * kg;         // first vector of this lane's D values (kg 2, 3: padding)
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   u32x4 h_cur, h_nxt;
@@ -135,7 +133,10 @@ __global__ void __launch_bounds__(512)
   if (sb0 < sb1) load_sb(sb0, h_cur, q_cur);
   for (int sb = sb0; sb < sb1; ++sb) {
     load_sb(sb + 1, h_nxt, q_nxt);  // the next super-block in flight (past the share: valid, unused)
-    const float d = h2f(h_cur.x), dm = h2f(h_cur.x >> 16);
+    // per limb: sum over the sub-blocks of sc_j * (integer dot); and the
+    // f32 min term sum_j m_j * sx_j
+    int ia[4] = {0, 0, 0, 0}, ib[4] = {0, 0, 0, 0}, ic[4] = {0, 0, 0, 0};
+    float mn[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       // scales and mins of sub-blocks 2g, 2g + 1 (get_scale_min_k4)
@@ -147,28 +148,42 @@ __global__ void __launch_bounds__(512)
       for (int hh = 0; hh < 2; ++hh) {
         const int jb = 8 * sb + 2 * g + hh;  // 32-element block of this sub-block
         const uint64_t codes = hh ? ((q_cur[g] >> 4) & 0x0F0F0F0F0F0F0F0Full) : (q_cur[g] & 0x0F0F0F0F0F0F0F0Full);
+        // loads from in-range addresses whatever the lane, then a select
+        // (no branches: the loads and MFMAs of neighbouring sub-blocks can
+        // be scheduled together)
         long A[3];
 #pragma unroll
         for (int l = 0; l < 3; ++l) {
-          const uint8_t* src = limbs + (l * nblk + jb) * (kMbMaxVec * kMbTokStride) + tok_a * kMbTokStride + 8 * kg;
-          A[l] = a_real ? *reinterpret_cast<const long*>(src) : 0l;
+          const uint8_t* src =
+              limbs + (l * nblk + jb) * (kMbMaxVec * kMbTokStride) + (tok_a & (kMbMaxVec - 1)) * kMbTokStride + 8 * kg;
+          const long v = *reinterpret_cast<const long*>(src);
+          A[l] = a_real ? v : 0l;
         }
         const i32x4v Ia = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[0], long(codes), i32x4v{}, 0, 0, 0);
         const i32x4v Ib = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[1], long(codes), i32x4v{}, 0, 0, 0);
         const i32x4v Ic = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[2], long(codes), i32x4v{}, 0, 0, 0);
-        const float dsc = d * ubyte<0>(hh ? (scp >> 8) : scp), dmm = dm * ubyte<0>(hh ? (mp >> 8) : mp);
-        f32x4 pk4 = {0.f, 0.f, 0.f, 0.f}, sx4 = {0.f, 0.f, 0.f, 0.f};
-        if (d_real) {
-          pk4 = *reinterpret_cast<const f32x4*>(pk + jb * kMbMaxVec + tok_d);
-          sx4 = *reinterpret_cast<const f32x4*>(sx + jb * kMbMaxVec + tok_d);
-        }
+        const int scj = int((hh ? (scp >> 8) : scp) & 0xFFu);
+        const float mj = float((hh ? (mp >> 8) : mp) & 0xFFu);
+        const f32x4 sx4 = *reinterpret_cast<const f32x4*>(sx + jb * kMbMaxVec + (tok_d & (kMbMaxVec - 1)));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float f = __builtin_fmaf(float(Ia[k]), 65536.f, float(Ib[k] * 256 + Ic[k]));
-          acc[k] = __builtin_fmaf(f, dsc * pk4[k], acc[k]);
-          acc[k] = __builtin_fmaf(-dmm, sx4[k], acc[k]);
+          // |integer dot| <= 15 * 32 * 128 and sc <= 63: 24-bit operands
+          ia[k] = __mul24(Ia[k], scj) + ia[k];
+          ib[k] = __mul24(Ib[k], scj) + ib[k];
+          ic[k] = __mul24(Ic[k], scj) + ic[k];
+          mn[k] = __builtin_fmaf(mj, sx4[k], mn[k]);
         }
       }
+    }
+    // |ia|, |ib|, |ic| <= 8 * 63 * 61440 < 2^25: f32 conversions within an ulp
+    const float d = h2f(h_cur.x), dm = h2f(h_cur.x >> 16);
+    // lanes holding padding vectors (tok_d >= 8) read vectors 0-3 and are never stored
+    const f32x4 pk4 = *reinterpret_cast<const f32x4*>(pk8 + sb * kMbMaxVec + (tok_d & (kMbMaxVec - 1)));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float f = __builtin_fmaf(float(ia[k]), 65536.f, __builtin_fmaf(float(ib[k]), 256.f, float(ic[k])));
+      acc[k] = __builtin_fmaf(f, d * pk4[k], acc[k]);
+      acc[k] = __builtin_fmaf(-dm, mn[k], acc[k]);
     }
     h_cur = h_nxt;
 #pragma unroll
@@ -212,11 +227,13 @@ hipError_t launch_gemv_mfma(const void* wv, int64_t rows, int64_t cols, const fl
                             int cu, hipStream_t s) {
   if (!gemv_mfma_ok(kQ4_K, rows, cols, batch)) return hipErrorInvalidValue;
   // T row tiles per workgroup so the tiles cover the CUs about once; the
-  // rest of 8 waves split the super-blocks into shares of PER <= 8
+  // workgroup's waves (12 for 3 or 4 tiles, 8 otherwise: one workgroup per
+  // CU, the activations' LDS allowing no more) split the super-blocks into
+  // shares of PER <= 8
   int T = int((rows + 16LL * cu - 1) / (16LL * cu));
   if (T < 1) T = 1;
   if (T > 4) T = 4;
-  const int S = T >= 3 ? 2 : 8 / T;  // T * S <= 8 waves
+  const int S = T >= 3 ? kMbMaxWaves / T : 8 / T;
   const int nsb = int(cols / 256);
   const int per = (nsb + S - 1) / S;  // <= 8: cols <= 4096 and S >= 2
   const int nblk = int(cols / 32);

@@ -100,10 +100,11 @@ def test_gemv_batch(backend, oracle, quant, cols, batch):
 
 
 @pytest.mark.parametrize("rows,cols,batch", [(100, 4096, 5), (17, 256, 8), (1, 512, 2), (12288, 4096, 8),
-                                             (4099, 1024, 7)])
+                                             (4099, 1024, 7), (16400, 1024, 8)])
 def test_gemv_batch_q4k_mfma_shapes(backend, oracle, rows, cols, batch):
     # the batched Q4_K path on int8 MFMA: partial 16-row tiles, shares of
-    # super-blocks with nothing to do, odd batches, a tall matrix
+    # super-blocks with nothing to do, odd batches, a tall matrix (16400
+    # rows: four row tiles per workgroup and three shares, one of them empty)
     say("gemv batch q4k mfma", rows, cols, batch)
     w = S.matrix(12, 77 + rows + cols, rows, cols)
     x = S.normal_f32(batch * 17 + rows, batch * cols).reshape(batch, cols)
@@ -113,6 +114,22 @@ def test_gemv_batch_q4k_mfma_shapes(backend, oracle, rows, cols, batch):
     sub = np.concatenate([w[i * rb:(i + 1) * rb] for i in idx])
     for b in range(batch):
         check(y[b][idx], oracle.gemv(12, len(idx), cols, sub, x[b]))
+
+
+def test_gemv_batch_q4k_mixed_block_magnitudes(backend, oracle):
+    """The batched Q4_K path scales each 256-element super-block of x by one
+    power of two: 32-element blocks whose magnitudes differ by up to 10^8
+    within a super-block still meet the tolerance against the f64 sums."""
+    rows, cols, batch = 256, 2048, 8
+    say("gemv batch q4k mixed block magnitudes")
+    w = S.matrix(12, 4321, rows, cols)
+    x = S.normal_f32(4322, batch * cols).reshape(batch, cols)
+    rng = np.random.default_rng(4323)
+    scale = (10.0 ** rng.uniform(-4, 4, size=(batch, cols // 32))).astype(np.float32)
+    x = (x.reshape(batch, cols // 32, 32) * scale[:, :, None]).reshape(batch, cols).astype(np.float32)
+    y = backend.gemv_batch(H.QuantTensor("bm_mixed", 12, rows, cols, w), x, batch)
+    for b in range(batch):
+        check(y[b], oracle.gemv(12, rows, cols, w, x[b]))
 
 
 def test_gemv_shape_errors(backend):
