@@ -21,8 +21,9 @@
 // LDS (double buffered, one barrier per 64-element chunk of K). In bf16 mode
 // the activation tile does too (mm_bf16_lds_kernel: global_load_lds copies
 // into a three-slot ring); the q8 kernel, and bf16 calls whose activations
-// exceed 32-bit byte offsets, load each wave's A fragments straight from
-// global memory (L2-resident) into registers. The MFMA's k order is
+// exceed 32-bit byte offsets, load each wave's activation fragments straight
+// from global memory (L2-resident) into registers (q8: in the fragment order
+// its pre-pass writes, one contiguous 1 KiB wave load each). The MFMA's k order is
 // free as long as A and B agree, so lane half h of k-step s holds chunk
 // elements [32h + 8s, +8) (bf16) or [32s + 16h, +16) (int8) of both operands,
 // which keeps every fragment one 16-byte load. Tiles are numbered so that the
@@ -257,11 +258,8 @@ __global__ void x_bf16_kernel(const float* __restrict__ x, uint32_t* __restrict_
 // X f32 -> Q8 blocks of 32: s = max|x| / 127 (f32 division), q = rne(x / s)
 // (0 where s == 0), plus u = s * sum(q) for the Q4_K min term. One thread
 // per block; `blocks` = m * cols / 32, scales indexed [token][block].
-__global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s_out,
-                            float* __restrict__ u_out, int64_t blocks) {
-  const int64_t b = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (b >= blocks) return;
-  const f32x4* xv = reinterpret_cast<const f32x4*>(x + 32 * b);
+__device__ __forceinline__ void q8_block(const float* __restrict__ x32, uint32_t* w, float& s_out, float& u_out) {
+  const f32x4* xv = reinterpret_cast<const f32x4*>(x32);
   float v[32];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -275,7 +273,6 @@ __global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
 #pragma unroll
   for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
   const float s = __fdiv_rn(amax, 127.f);
-  uint32_t w[8];
   int sum = 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -288,11 +285,49 @@ __global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
     }
     w[k] = word;
   }
+  s_out = s;
+  u_out = s * float(sum);
+}
+
+__global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ s_out,
+                            float* __restrict__ u_out, int64_t blocks) {
+  const int64_t b = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (b >= blocks) return;
+  uint32_t w[8];
+  float sv, uv;
+  q8_block(x + 32 * b, w, sv, uv);
   u32x4* qv = reinterpret_cast<u32x4*>(q + 32 * b);
   qv[0] = u32x4{w[0], w[1], w[2], w[3]};
   qv[1] = u32x4{w[4], w[5], w[6], w[7]};
-  s_out[b] = s;
-  u_out[b] = s * float(sum);
+  s_out[b] = sv;
+  u_out[b] = uv;
+}
+
+// The same blocks for the q8 matmul, in the order its waves load them
+// (tokens padded with zero blocks to a multiple of 32; T = token / 32,
+// l = token % 32, block j = 2c + s of chunk c):
+//   codes: 16-byte piece ((T * nch + c) * 2 + s) * 64 + 32 h + l holds codes
+//          [16h, 16h + 16) of the block (one 1 KiB wave load per fragment);
+//   s, u:  float (T * nblk + j) * 32 + l (one 128-byte run per block).
+__global__ void x_q8_tiled_kernel(const float* __restrict__ x, u32x4* __restrict__ qt, float* __restrict__ st,
+                                  float* __restrict__ ut, int m, int cols, int64_t blocks) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;  // (T, j, l)
+  if (i >= blocks) return;
+  const int nblk = cols / 32, nch = cols / kMmKC;
+  const int l = int(i & 31);
+  const int64_t tj = i >> 5;
+  const int j = int(tj % nblk);
+  const int64_t T = tj / nblk;
+  const int64_t t = 32 * T + l;
+  uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  float sv = 0.f, uv = 0.f;
+  if (t < m) q8_block(x + t * cols + 32 * j, w, sv, uv);
+  const int c = j >> 1, s = j & 1;
+  u32x4* dst = qt + ((T * nch + c) * 2 + s) * 64 + l;
+  dst[0] = u32x4{w[0], w[1], w[2], w[3]};
+  dst[32] = u32x4{w[4], w[5], w[6], w[7]};
+  st[i] = sv;
+  ut[i] = uv;
 }
 
 // --------------------------------------------------------------- tile order --
@@ -641,13 +676,18 @@ __global__ void __launch_bounds__(kMmThreads)
   const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
   const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
 
-  // this lane's tokens (one per M-subtile) and their code rows
-  int tok[2];
+  // this lane's token tiles (one per M-subtile): codes of fragment (T, c, s)
+  // at 16-byte piece ((T * nchunks + c) * 2 + s) * 64 + lane, scales and min
+  // sums of (T, block j) at float (T * nblk + j) * 32 + l32
+  const int n_tt = (m + 31) >> 5;
   const int8_t* xr[2];
+  const float *sr[2], *ur[2];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    tok[mi] = min(t0 + 64 * wave + 32 * mi + l32, m - 1);
-    xr[mi] = xq + int64_t(tok[mi]) * cols + 16 * half;
+    const int T = min((t0 + 64 * wave + 32 * mi) >> 5, n_tt - 1);
+    xr[mi] = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
+    sr[mi] = xs + int64_t(T) * nblk * 32 + l32;
+    ur[mi] = xu + int64_t(T) * nblk * 32 + l32;
   }
 
   f32x16 acc[2][3];
@@ -682,14 +722,14 @@ __global__ void __launch_bounds__(kMmThreads)
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 32 * s);
+    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 1024 * s);
   // the lane's tokens' block scales and min sums, a chunk ahead with the codes
   float sxc[2][2], umc[2];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) sxc[mi][s] = xs[int64_t(tok[mi]) * nblk + s];
-    umc[mi] = S::kMin ? xu[int64_t(tok[mi]) * nblk + half] : 0.f;
+    for (int s = 0; s < 2; ++s) sxc[mi][s] = sr[mi][32 * s];
+    umc[mi] = S::kMin ? ur[mi][32 * half] : 0.f;
   }
   __syncthreads();
 
@@ -706,12 +746,12 @@ __global__ void __launch_bounds__(kMmThreads)
           for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
             for (int s = 0; s < 2; ++s)
-              xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * kMmKC + 32 * s);
+              xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * 2048 + 1024 * s);
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) sxn[mi][s] = xs[int64_t(tok[mi]) * nblk + 2 * (c + 1) + s];
-            umn[mi] = S::kMin ? xu[int64_t(tok[mi]) * nblk + 2 * (c + 1) + half] : 0.f;
+            for (int s = 0; s < 2; ++s) sxn[mi][s] = sr[mi][32 * (2 * (c + 1) + s)];
+            umn[mi] = S::kMin ? ur[mi][32 * (2 * (c + 1) + half)] : 0.f;
           }
         }
         const int buf = c & 1;
@@ -817,8 +857,9 @@ bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint
 
 size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
   if (mode == 0) return align256(size_t(m) * size_t(cols) * 2);
-  const size_t blocks = size_t(m) * size_t(cols / 32);
-  return align256(size_t(m) * size_t(cols)) + 2 * align256(blocks * sizeof(float));
+  const size_t mp = size_t((m + 31) / 32 * 32);  // tokens padded to whole 32-token tiles
+  const size_t blocks = mp * size_t(cols / 32);
+  return align256(mp * size_t(cols)) + 2 * align256(blocks * sizeof(float));
 }
 
 template <class S>
@@ -835,10 +876,11 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
       hipLaunchKernelGGL(mm_bf16_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
                          reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
   } else if constexpr (S::kQ8) {
-    const size_t blocks = size_t(m) * size_t(cols / 32);
+    const size_t mp = size_t((m + 31) / 32 * 32);
+    const size_t blocks = mp * size_t(cols / 32);
     const int8_t* xq = reinterpret_cast<const int8_t*>(ws);
-    const float* xs = reinterpret_cast<const float*>(ws + align256(size_t(m) * size_t(cols)));
-    const float* xu = reinterpret_cast<const float*>(ws + align256(size_t(m) * size_t(cols)) +
+    const float* xs = reinterpret_cast<const float*>(ws + align256(mp * size_t(cols)));
+    const float* xu = reinterpret_cast<const float*>(ws + align256(mp * size_t(cols)) +
                                                      align256(blocks * sizeof(float)));
     hipLaunchKernelGGL(mm_q8_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb, xq, xs, xu, m, y,
                        ntm);
@@ -866,12 +908,12 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
     hipLaunchKernelGGL(x_bf16_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s, x,
                        reinterpret_cast<uint32_t*>(ws), n8);
   } else {
-    const size_t blocks = size_t(m) * size_t(cols / 32);
-    float* xs = reinterpret_cast<float*>(ws + align256(size_t(m) * size_t(cols)));
-    float* xu = reinterpret_cast<float*>(ws + align256(size_t(m) * size_t(cols)) +
-                                         align256(blocks * sizeof(float)));
-    hipError_t e = launch_quantize_q8(x, m * cols, reinterpret_cast<int8_t*>(ws), xs, xu, s);
-    if (e != hipSuccess) return e;
+    const size_t mp = size_t((m + 31) / 32 * 32);
+    const size_t blocks = mp * size_t(cols / 32);
+    float* xs = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)));
+    float* xu = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)) + align256(blocks * sizeof(float)));
+    hipLaunchKernelGGL(x_q8_tiled_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, x,
+                       reinterpret_cast<u32x4*>(ws), xs, xu, int(m), int(cols), int64_t(blocks));
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
