@@ -13,17 +13,21 @@
 // with weights d * sc_j * q - dmin * m_j in sub-block j:
 //   sum_e w_e x_e = d * 2^-k * (2^16 A + 2^8 B + C) - dmin * sum_j m_j * sx_j,
 //   A = sum_j sc_j * sum_{e in j} q_e a_e   (B, C likewise)
-// where each sub-block's integer sum is one exact v_mfma_i32_16x16x32_i8
-// (K = 32) and the 6-bit scales sc_j are applied in integers (v_mad_i32_i24),
-// so the f32 work is once per super-block; sx_j is the f32 sum of x over
-// sub-block j. x is represented to 2^-23 of its super-block's maximum.
+// where each sub-block's integer sums are exact v_mfma_i32_16x16x32_i8
+// products (K = 32) and the 6-bit scales sc_j are applied in integers
+// (v_mad_i32_i24), so the f32 work is once per super-block; sx_j is the f32
+// sum of x over sub-block j. x is represented to 2^-23 of its super-block's
+// maximum.
 //
-// Mapping: a wave owns a tile of 16 weight rows (the MFMA's B columns; the
-// vectors are its A rows, padded to 16) and a share of the super-blocks;
-// a workgroup is T row tiles x S super-block shares (T * S waves), with the
-// activations' limbs for every block and vector in LDS. The S shares of a
-// row tile are added through LDS at the end. Lane l of a wave holds, in D,
-// weight row l % 16 for vectors 4 * (l / 16) + i, i < 4.
+// Mapping: a wave owns a tile of 16 weight rows (the MFMA's B columns) and a
+// share of the super-blocks; the MFMA's 16 A rows are two limbs of the 8
+// vectors (rows 0-7 one limb, rows 8-15 another), so a sub-block takes two
+// MFMAs: (a | b) and (c | zero). A workgroup is T row tiles x S super-block
+// shares (T * S waves), with the activations' limbs for every block and
+// vector in LDS. The S shares of a row tile are added through LDS at the end.
+// Lane l of a wave holds, in D, weight row l % 16 for vectors
+// 4 * ((l / 16) & 1) + i, i < 4: the a and c sums in lanes 0-31, the b sums
+// in lanes 32-63.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -117,9 +121,16 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
   const int r16 = lane & 15, kg = lane >> 4;  // B column (weight row) and k group
   const int row = min(blockIdx.x * (16 * T) + 16 * rt + r16, rows - 1);
   const uint8_t* wr = w + int64_t(row) * row_bytes;
-  const int tok_a = r16;            // the vector this lane feeds as an A row
-  const bool a_real = tok_a < nb;
-  const int tok_d = 4 * kg;         // first vector of this lane's D values (kg 2, 3: padding)
+  // A rows 0-7 carry one limb of vectors 0-7 and rows 8-15 another limb of
+  // the same vectors: MFMA 1 takes limbs (a | b), MFMA 2 (c | zero). So lanes
+  // of k groups 0, 1 hold a and c sums of vectors 4 kg + i in D, lanes of k
+  // groups 2, 3 the b sums of the same vectors (kg - 2), exchanged once per
+  // super-block.
+  const int vec_a = r16 & 7;                  // the vector this lane feeds as an A row
+  const bool a_real = vec_a < nb;
+  const bool a_hi = r16 >= 8;                 // A rows 8-15: the second limb
+  const int tok_d = 4 * (kg & 1);             // first vector of this lane's D values
+  const bool d_out = kg < 2;                  // lanes whose D holds the a and c sums
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   u32x4 h_cur, h_nxt;
@@ -135,7 +146,7 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
     load_sb(sb + 1, h_nxt, q_nxt);  // the next super-block in flight (past the share: valid, unused)
     // per limb: sum over the sub-blocks of sc_j * (integer dot); and the
     // f32 min term sum_j m_j * sx_j
-    int ia[4] = {0, 0, 0, 0}, ib[4] = {0, 0, 0, 0}, ic[4] = {0, 0, 0, 0};
+    int i1[4] = {0, 0, 0, 0}, i2[4] = {0, 0, 0, 0};  // (a | b) and (c | 0) sums
     float mn[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -151,37 +162,36 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
         // loads from in-range addresses whatever the lane, then a select
         // (no branches: the loads and MFMAs of neighbouring sub-blocks can
         // be scheduled together)
-        long A[3];
-#pragma unroll
-        for (int l = 0; l < 3; ++l) {
-          const uint8_t* src =
-              limbs + (l * nblk + jb) * (kMbMaxVec * kMbTokStride) + (tok_a & (kMbMaxVec - 1)) * kMbTokStride + 8 * kg;
-          const long v = *reinterpret_cast<const long*>(src);
-          A[l] = a_real ? v : 0l;
-        }
-        const i32x4v Ia = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[0], long(codes), i32x4v{}, 0, 0, 0);
-        const i32x4v Ib = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[1], long(codes), i32x4v{}, 0, 0, 0);
-        const i32x4v Ic = __builtin_amdgcn_mfma_i32_16x16x32_i8(A[2], long(codes), i32x4v{}, 0, 0, 0);
+        const uint8_t* blk = limbs + jb * (kMbMaxVec * kMbTokStride) + vec_a * kMbTokStride + 8 * kg;
+        const int limb_stride = nblk * (kMbMaxVec * kMbTokStride);
+        const long v1 = *reinterpret_cast<const long*>(blk + (a_hi ? limb_stride : 0));  // a | b
+        const long v2 = *reinterpret_cast<const long*>(blk + 2 * limb_stride);           // c
+        const long A1 = a_real ? v1 : 0l;
+        const long A2 = a_real && !a_hi ? v2 : 0l;
+        const i32x4v I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(A1, long(codes), i32x4v{}, 0, 0, 0);
+        const i32x4v I2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(A2, long(codes), i32x4v{}, 0, 0, 0);
         const int scj = int((hh ? (scp >> 8) : scp) & 0xFFu);
         const float mj = float((hh ? (mp >> 8) : mp) & 0xFFu);
-        const f32x4 sx4 = *reinterpret_cast<const f32x4*>(sx + jb * kMbMaxVec + (tok_d & (kMbMaxVec - 1)));
+        const f32x4 sx4 = *reinterpret_cast<const f32x4*>(sx + jb * kMbMaxVec + tok_d);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           // |integer dot| <= 15 * 32 * 128 and sc <= 63: 24-bit operands
-          ia[k] = __mul24(Ia[k], scj) + ia[k];
-          ib[k] = __mul24(Ib[k], scj) + ib[k];
-          ic[k] = __mul24(Ic[k], scj) + ic[k];
+          i1[k] = __mul24(I1[k], scj) + i1[k];
+          i2[k] = __mul24(I2[k], scj) + i2[k];
           mn[k] = __builtin_fmaf(mj, sx4[k], mn[k]);
         }
       }
     }
-    // |ia|, |ib|, |ic| <= 8 * 63 * 61440 < 2^25: f32 conversions within an ulp
+    // the b sums from the lanes 32 apart; |a|, |b|, |c| sums <= 8 * 63 * 61440
+    // < 2^25: f32 conversions within an ulp
+    int ib[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ib[k] = __shfl_xor(i1[k], 32, kWave);
     const float d = h2f(h_cur.x), dm = h2f(h_cur.x >> 16);
-    // lanes holding padding vectors (tok_d >= 8) read vectors 0-3 and are never stored
-    const f32x4 pk4 = *reinterpret_cast<const f32x4*>(pk8 + sb * kMbMaxVec + (tok_d & (kMbMaxVec - 1)));
+    const f32x4 pk4 = *reinterpret_cast<const f32x4*>(pk8 + sb * kMbMaxVec + tok_d);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float f = __builtin_fmaf(float(ia[k]), 65536.f, __builtin_fmaf(float(ib[k]), 256.f, float(ic[k])));
+      const float f = __builtin_fmaf(float(i1[k]), 65536.f, __builtin_fmaf(float(ib[k]), 256.f, float(i2[k])));
       acc[k] = __builtin_fmaf(f, d * pk4[k], acc[k]);
       acc[k] = __builtin_fmaf(-dm, mn[k], acc[k]);
     }
@@ -204,7 +214,7 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
     if (r < rows) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (tok_d + i < nb) y[int64_t(tok_d + i) * rows + r] = t[i];
+        if (d_out && tok_d + i < nb) y[int64_t(tok_d + i) * rows + r] = t[i];
     }
   }
 }
