@@ -4,8 +4,9 @@
  *
  * The library replaces the matvec/matmul half of strata-core's
  * `trait ComputeBackend` (crates/strata-core/src/backend.rs:20-51) for the
- * GGUF types Q8_0, Q4_K and Q6_K. Weights stay packed in device memory in
- * their GGUF block layout; kernels dequantize in registers.
+ * GGUF types Q8_0, Q4_K and Q6_K (and F32 / F16 / BF16 for the plain matvec
+ * and dequant, the types router and gate tensors use). Weights stay packed in
+ * device memory in their GGUF block layout; kernels dequantize in registers.
  *
  * Conventions
  *  - Every function returns int: SH_OK (0) or a negative SH_ERR_* code, and
@@ -122,7 +123,8 @@ int sh_evict(sh_context* ctx, uint64_t key);
 
 /* ComputeBackend::gemv (backend.rs:25), semantics of ops::gemv
  * (crates/strata-core/src/ops.rs:14-28): y[r] = sum_c W[r][c] * x[c].
- * x_len must equal cols and y_len rows. */
+ * x_len must equal cols and y_len rows. Q8_0 / Q4_K / Q6_K, and F32 / F16 /
+ * BF16 (products and sums in f64, as ops::gemv does). */
 int sh_gemv(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint64_t x_len, float* y,
             uint64_t y_len);
 
@@ -161,6 +163,22 @@ int sh_moe_route(sh_context* ctx, const float* logits, uint32_t n_tok, uint32_t 
 int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view* up,
                const sh_expert_view* down, const float* logits, uint32_t n_tok, uint32_t top_k,
                const float* x, float* out);
+
+/* The whole MoE layer, MoeLayer::route + MoeLayer::combine
+ * (crates/strata-core/src/moe.rs:48-143), for n_tok tokens of x [n_tok]
+ * [n_embd]: logits = router . bf16(x) (route, moe.rs:55-56), the routed
+ * experts as sh_moe_ffn, then the always-on shared expert added plain:
+ * out += sigmoid(gate_inp_shexp . x) * down_shexp . (silu(gate_shexp . x) *
+ * (up_shexp . x)) (moe.rs:129-142). router [n_expert][n_embd], gate/up_shexp
+ * [n_ff_shexp][n_embd], down_shexp [n_embd][n_ff_shexp], gate_inp_shexp
+ * [1][n_embd] are ops::gemv matrices of any matvec type (F32 / F16 / BF16
+ * included); the expert views as in sh_moe_ffn. n_ff_shexp must be a
+ * multiple of 4. The weight budget must hold the eight tensors at once. */
+int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert_view* gate,
+                 const sh_expert_view* up, const sh_expert_view* down, const sh_quant_tensor* gate_shexp,
+                 const sh_quant_tensor* up_shexp, const sh_quant_tensor* down_shexp,
+                 const sh_quant_tensor* gate_inp_shexp, const float* x, uint32_t n_tok, uint32_t top_k,
+                 float* out);
 
 /* Batched prefill matmul: y[t][r] = sum_c W[r][c] * x[t][c] for t < m, x
  * [m][cols] and y [m][rows] row-major f32. The reference has no matmul
@@ -215,12 +233,28 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
                    uint32_t n_tok, uint32_t top_k, const float* x, float* out, void* workspace,
                    uint64_t workspace_bytes, void* stream);
 
+/* Bytes of device workspace sh_moe_layer_dev needs; quants[8] are the types
+ * of router, gate, up, down, gate_shexp, up_shexp, down_shexp,
+ * gate_inp_shexp. */
+int sh_moe_layer_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
+                                 uint64_t n_ff, uint64_t n_ff_shexp, const uint32_t* quants, uint64_t* bytes);
+
+/* sh_moe_layer on device pointers: tensors[8] in the order router, gate,
+ * up, down (expert tensors, as in sh_moe_ffn_dev), gate_shexp, up_shexp,
+ * down_shexp, gate_inp_shexp (row-major matrices); x (16-byte aligned) and
+ * out [n_tok][n_embd]; workspace at least sh_moe_layer_workspace_bytes()
+ * long and 256-byte aligned. Calls sharing one workspace must not overlap
+ * in time. */
+int sh_moe_layer_dev(const sh_expert_dev* tensors, uint64_t n_expert, uint64_t n_embd, uint64_t n_ff,
+                     uint64_t n_ff_shexp, uint32_t n_tok, uint32_t top_k, const float* x, float* out,
+                     void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* rows x cols of packed blocks at `w` -> out[rows][cols] f32, bit-exact. */
 int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                    float* out, void* stream);
 
 /* y[b][r] = sum_c W[r][c] x[b][c], b < batch (1..8); w at least 2-byte
- * aligned (4 for Q8_0), x 16-byte aligned. */
+ * aligned (4 for Q8_0 and F32), x 16-byte aligned. */
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream);
 

@@ -485,6 +485,63 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
   return rc;
 }
 
+/* ops.rs:90-92 */
+float sho_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* ---- the whole MoE layer for one token (moe.rs:48-143) -----------------
+ * route:   x_bf = bf16(x) (hyper.rs:22-24), logits = router . x_bf
+ *          (ops::gemv), then sho_moe_route;
+ * combine: the routed experts (sho_moe_routed), then the shared expert
+ *          g = gate_sh . x, p = up_sh . x, h = silu(g) * p, d = down_sh . h,
+ *          s = gate_inp . x, out += sigmoid(s) * d (f32, product then sum).
+ * router [n_expert][n_embd], gate_sh / up_sh [n_ff_sh][n_embd], down_sh
+ * [n_embd][n_ff_sh], gate_inp [1][n_embd] (ops::gemv orientation).
+ * q[8]: the types of router, gate, up, down, gate_sh, up_sh, down_sh,
+ * gate_inp; t[8] / nb[8] their bytes. out (n_embd) is overwritten. */
+int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                  int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                  float* out) {
+  float* xb = (float*)malloc((size_t)n_embd * sizeof(float));
+  float* logits = (float*)malloc((size_t)n_expert * sizeof(float));
+  int64_t* ids = (int64_t*)malloc((size_t)top_k * sizeof(int64_t));
+  float* w = (float*)malloc((size_t)top_k * sizeof(float));
+  float* g = (float*)malloc((size_t)n_ff_sh * sizeof(float));
+  float* part = (float*)malloc((size_t)n_ff_sh * sizeof(float));
+  float* d = (float*)malloc((size_t)n_embd * sizeof(float));
+  float s = 0.0f;
+  int rc = SHO_OK;
+  for (int64_t i = 0; i < n_embd; ++i) xb[i] = sho_bf16_round(x[i]);
+  rc = sho_gemv(q[0], n_expert, n_embd, t[0], nb[0], xb, logits);
+  int64_t k = 0;
+  if (rc == SHO_OK) {
+    k = sho_moe_route(logits, n_expert, top_k, ids, w);
+    rc = sho_moe_routed(q[1], q[2], q[3], n_expert, n_embd, n_ff, t[1], nb[1], t[2], nb[2], t[3], nb[3], ids,
+                        w, k, x, out);
+  }
+  if (rc == SHO_OK) rc = sho_gemv(q[4], n_ff_sh, n_embd, t[4], nb[4], x, g);
+  if (rc == SHO_OK) rc = sho_gemv(q[5], n_ff_sh, n_embd, t[5], nb[5], x, part);
+  if (rc == SHO_OK) {
+    for (int64_t i = 0; i < n_ff_sh; ++i) g[i] = sho_silu(g[i]) * part[i];
+    rc = sho_gemv(q[6], n_embd, n_ff_sh, t[6], nb[6], g, d);
+  }
+  if (rc == SHO_OK) rc = sho_gemv(q[7], 1, n_embd, t[7], nb[7], x, &s);
+  if (rc == SHO_OK) {
+    const float gate = sho_sigmoid(s);
+    for (int64_t i = 0; i < n_embd; ++i) {
+      float v = gate * d[i];
+      out[i] = out[i] + v;
+    }
+  }
+  free(xb);
+  free(logits);
+  free(ids);
+  free(w);
+  free(g);
+  free(part);
+  free(d);
+  return rc;
+}
+
 int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
                size_t nbytes, const float* x, int64_t m, float* y, int n_threads) {
   if (m < 0) return SHO_UNSUPPORTED;

@@ -11,6 +11,8 @@
  *   - gemv / expert_gemv      crates/strata-core/src/ops.rs:14-28,169-195
  *   - silu                    crates/strata-core/src/ops.rs:85-87
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
+ *   - the whole MoE layer     crates/strata-core/src/moe.rs:48-143 (router
+ *                             matvec on bf16(x), shared expert, sigmoid gate)
  *   - prefill matmul          no reference op: m independent ops::gemv calls
  *                             (crates/strata-core/src/generate.rs:116-117)
  *   - Q8 activation blocks    the quantization the int8 prefill mode applies
@@ -79,6 +81,7 @@ int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
                     int64_t e, const float* x, float* y);
 
 float sho_silu(float x);
+float sho_sigmoid(float x);
 
 int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
                   int64_t* ids, float* weights);
@@ -89,6 +92,9 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
                    size_t up_bytes, const uint8_t* down, size_t down_bytes,
                    const int64_t* ids, const float* weights, int64_t k,
                    const float* x, float* out);
+int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                  int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                  float* out);
 
 /* y[t][r] = gemv(W, x[t]) for t < m: m independent sho_gemv calls, each
  * row-parallel over n_threads (bit-identical to the sequential loop). */

@@ -59,6 +59,10 @@ def lib() -> C.CDLL:
         L.sho_moe_routed.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
                                      C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
                                      i64p, f32p, C.c_int64, f32p, f32p]
+        L.sho_sigmoid.argtypes = [C.c_float]
+        L.sho_sigmoid.restype = C.c_float
+        L.sho_moe_layer.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
+                                    C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, f32p, f32p]
         L.sho_matmul.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, C.c_int64, f32p,
                                  C.c_int]
         L.sho_quantize_q8.argtypes = [f32p, C.c_size_t, u8p, f32p, f32p]
@@ -184,6 +188,27 @@ def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, 
     _check(lib().sho_moe_routed(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
                                 _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
                                 _ptr(xv), _ptr(out)), "moe_routed")
+    return out
+
+
+def sigmoid(x: float) -> float:
+    return lib().sho_sigmoid(x)
+
+
+def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: int, x, top_k: int) -> np.ndarray:
+    """The whole MoE layer for one token (moe.rs:48-143): router matvec on
+    bf16(x), route, routed experts, then the shared expert added with its
+    sigmoid gate. quants / tensors: router, gate, up, down, gate_sh, up_sh,
+    down_sh, gate_inp."""
+    bufs = [_u8(t) for t in tensors]
+    xv = _f32(x)
+    assert xv.size == n_embd and len(bufs) == 8
+    out = np.empty(n_embd, dtype=np.float32)
+    q = (C.c_uint32 * 8)(*[int(v) for v in quants])
+    tp = (C.c_void_p * 8)(*[_ptr(b) for b in bufs])
+    nb = (C.c_size_t * 8)(*[b.nbytes for b in bufs])
+    _check(lib().sho_moe_layer(q, tp, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, _ptr(xv), _ptr(out)),
+           "moe_layer")
     return out
 
 

@@ -180,11 +180,13 @@ int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uin
 
 // Shape checks shared by the matrix entry points; mirrors what the
 // reference asserts (ops.rs:15-17) or reports (dequant.rs:50-55).
-int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert, uint64_t nbytes) {
+// `plain_ok`: the entry point also takes F32 / F16 / BF16 (the matvec ones).
+int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert, uint64_t nbytes,
+                 bool plain_ok = false) {
   sh::Geometry g = sh::geometry(quant);
   if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
-  if (!sh::device_quant(quant))
-    return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u has no device matvec", quant);
+  if (!sh::device_quant(quant) && !(plain_ok && sh::plain_quant(quant)))
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u has no device kernel here", quant);
   if (cols % uint64_t(g.block) != 0)
     return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of %lld-element blocks",
                 (unsigned long long)cols, (long long)g.block);
@@ -330,7 +332,7 @@ int sh_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, uint64_t x_
                                     (unsigned long long)x_len, (unsigned long long)w->cols);
   if (y_len != w->rows) return fail(SH_ERR_SHAPE, "gemv: y has %llu elements, rows is %llu",
                                     (unsigned long long)y_len, (unsigned long long)w->rows);
-  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes);
+  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes, true);
   if (rc) return rc;
   Guard g(c);
   return run_gemv(c, w, x, y, 1);
@@ -339,7 +341,7 @@ int sh_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, uint64_t x_
 int sh_gemv_batch(sh_context* c, const sh_quant_tensor* w, const float* x, float* y, uint32_t batch) {
   if (!c || !w || !x || !y) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
   if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);
-  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes);
+  int rc = check_matrix(w->quant, w->rows, w->cols, 1, w->nbytes, true);
   if (rc) return rc;
   Guard g(c);
   return run_gemv(c, w, x, y, batch);
@@ -492,6 +494,113 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
   return SH_OK;
 }
 
+// The layer's dense tensors against the routed views: router [n_expert][n_embd],
+// gate/up_shexp [n_ff_sh][n_embd], down_shexp [n_embd][n_ff_sh],
+// gate_inp_shexp [1][n_embd]; then the plan.
+static int moe_layer_check(uint64_t E, uint64_t n_embd, uint64_t n_ff, uint64_t n_sh, uint32_t n_tok,
+                           uint32_t top_k, const sh::MoeLayerTypes& q, sh::MoeLayerPlan* plan) {
+  int rc = moe_check(E, n_embd, n_ff, n_tok, top_k, q.gate, q.down, &plan->moe);
+  if (rc) return rc;
+  if (q.up != q.gate)
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", q.gate, q.up);
+  if (n_sh == 0 || n_sh > (1u << 20)) return fail(SH_ERR_UNSUPPORTED_SHAPE, "shared expert width %llu",
+                                                 (unsigned long long)n_sh);
+  if (!sh::moe_layer_plan(int(n_tok), int(top_k), int(E), int(n_embd), int(n_ff), int(n_sh), q, plan))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE,
+                "MoE layer: router %llux%llu (type %u) or shared expert %llu wide (types %u, %u, %u, gate %u) "
+                "is not a matvec shape the kernels take",
+                (unsigned long long)E, (unsigned long long)n_embd, q.router, (unsigned long long)n_sh, q.gate_sh,
+                q.up_sh, q.down_sh, q.gate_inp);
+  return SH_OK;
+}
+
+int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_view* gate,
+                 const sh_expert_view* up, const sh_expert_view* down, const sh_quant_tensor* gate_shexp,
+                 const sh_quant_tensor* up_shexp, const sh_quant_tensor* down_shexp,
+                 const sh_quant_tensor* gate_inp_shexp, const float* x, uint32_t n_tok, uint32_t top_k,
+                 float* out) {
+  if (!c || !router || !gate || !up || !down || !gate_shexp || !up_shexp || !down_shexp || !gate_inp_shexp ||
+      !x || !out)
+    return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols, n_sh = gate_shexp->rows;
+  if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
+      down->rows != n_ff || down->cols != n_embd)
+    return fail(SH_ERR_SHAPE, "MoE views disagree: gate/up [%llu][%llu][%llu], down [%llu][%llu][%llu]",
+                (unsigned long long)E, (unsigned long long)n_embd, (unsigned long long)n_ff,
+                (unsigned long long)down->n_expert, (unsigned long long)down->rows,
+                (unsigned long long)down->cols);
+  if (router->rows != E || router->cols != n_embd || gate_shexp->cols != n_embd || up_shexp->rows != n_sh ||
+      up_shexp->cols != n_embd || down_shexp->rows != n_embd || down_shexp->cols != n_sh ||
+      gate_inp_shexp->rows != 1 || gate_inp_shexp->cols != n_embd)
+    return fail(SH_ERR_SHAPE, "MoE layer: router or shared-expert shapes disagree with the %llu x %llu experts",
+                (unsigned long long)E, (unsigned long long)n_embd);
+  int rc;
+  if ((rc = check_matrix(gate->quant, n_embd, n_ff, E, gate->nbytes)) ||
+      (rc = check_matrix(up->quant, n_embd, n_ff, E, up->nbytes)) ||
+      (rc = check_matrix(down->quant, n_ff, n_embd, E, down->nbytes)))
+    return rc;
+  const sh_quant_tensor* dense[5] = {router, gate_shexp, up_shexp, down_shexp, gate_inp_shexp};
+  for (const sh_quant_tensor* t : dense)
+    if ((rc = check_matrix(t->quant, t->rows, t->cols, 1, t->nbytes, true))) return rc;
+  const sh::MoeLayerTypes q{router->quant, gate->quant, up->quant, down->quant,
+                            gate_shexp->quant, up_shexp->quant, down_shexp->quant, gate_inp_shexp->quant};
+  sh::MoeLayerPlan plan;
+  if ((rc = moe_layer_check(E, n_embd, n_ff, n_sh, n_tok, top_k, q, &plan))) return rc;
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  // all eight tensors resident at once: admit them twice (a budget eviction
+  // while admitting a later one may drop an earlier one), then check
+  struct Want {
+    uint64_t key;
+    uint32_t quant;
+    uint64_t n_expert, rows, cols;
+    const uint8_t* data;
+  };
+  const Want want[8] = {
+      {router->key, router->quant, 1, router->rows, router->cols, router->data},
+      {gate->key, gate->quant, E, n_embd, n_ff, gate->data},
+      {up->key, up->quant, E, n_embd, n_ff, up->data},
+      {down->key, down->quant, E, n_ff, n_embd, down->data},
+      {gate_shexp->key, gate_shexp->quant, 1, n_sh, n_embd, gate_shexp->data},
+      {up_shexp->key, up_shexp->quant, 1, n_sh, n_embd, up_shexp->data},
+      {down_shexp->key, down_shexp->quant, 1, n_embd, n_sh, down_shexp->data},
+      {gate_inp_shexp->key, gate_inp_shexp->quant, 1, 1, n_embd, gate_inp_shexp->data}};
+  void* dev[8] = {};
+  for (int pass = 0; pass < 2; ++pass)
+    for (int i = 0; i < 8; ++i) {
+      Resident* r = nullptr;
+      const uint64_t nb = want[i].n_expert * want[i].rows * uint64_t(sh::byte_size(want[i].quant, int64_t(want[i].cols)));
+      if ((rc = resident(c, want[i].key, want[i].quant, want[i].n_expert, want[i].rows, want[i].cols,
+                         want[i].data, nb, &r)))
+        return rc;
+      dev[i] = r->dev;
+    }
+  for (int i = 0; i < 8; ++i) {
+    auto it = c->weights.find(want[i].key);
+    if (it == c->weights.end() || it->second.dev != dev[i])
+      return fail(SH_ERR_OUT_OF_MEMORY, "the weight budget does not hold the layer's tensors at once");
+  }
+  const size_t xb = sizeof(float) * n_tok * n_embd;
+  if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(xb, "out buffer")) ||
+      (rc = c->d_blk.ensure(plan.bytes, "workspace")) || (rc = c->h_in.ensure(xb, "x staging")) ||
+      (rc = c->h_out.ensure(xb, "out staging")))
+    return rc;
+  memcpy(c->h_in.p, x, xb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
+  auto q6 = [](uint32_t flags) { return (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  const sh::MoeLayerTensors w{dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], dev[6], dev[7],
+                              q6(router->flags), q6(gate->flags), q6(up->flags), q6(down->flags),
+                              q6(gate_shexp->flags), q6(up_shexp->flags), q6(down_shexp->flags),
+                              q6(gate_inp_shexp->flags)};
+  HIP_TRY(sh::launch_moe_layer(plan, q, w, static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
+                               c->d_blk.p, c->stream),
+          "moe layer launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, xb, hipMemcpyDeviceToHost, c->stream), "out readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "moe layer");
+  memcpy(out, c->h_out.p, xb);
+  return SH_OK;
+}
+
 static int matmul_check(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t m, uint32_t mode) {
   if (mode > SH_MATMUL_Q8) return fail(SH_ERR_INVALID_ARGUMENT, "matmul mode %u", mode);
   if (!sh::device_quant(quant))
@@ -582,7 +691,7 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream) {
   if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);
-  int rc = check_matrix(quant, rows, cols, 1, ~uint64_t(0));
+  int rc = check_matrix(quant, rows, cols, 1, ~uint64_t(0), true);
   if (rc) return rc;
   if (rows == 0 || cols == 0)
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "empty matrix on the device path");
@@ -591,8 +700,8 @@ int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, ui
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "gemv %llux%llu of type %u (batch %u) is not supported",
                 (unsigned long long)rows, (unsigned long long)cols, quant, batch);
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
-      (quant == SH_QUANT_Q8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)))
-    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0; x 16)");
+      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(w) & 3u)))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0 and F32; x 16)");
   HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
                           (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
           "gemv launch");
@@ -636,6 +745,51 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
                          (down->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, logits, x, out, workspace,
                          static_cast<hipStream_t>(stream)),
           "moe launch");
+  return SH_OK;
+}
+
+int sh_moe_layer_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
+                                 uint64_t n_ff, uint64_t n_ff_shexp, const uint32_t* quants, uint64_t* bytes) {
+  if (!quants || !bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  const sh::MoeLayerTypes q{quants[0], quants[1], quants[2], quants[3], quants[4], quants[5], quants[6], quants[7]};
+  sh::MoeLayerPlan plan;
+  int rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &plan);
+  if (rc) return rc;
+  *bytes = plan.bytes;
+  return SH_OK;
+}
+
+int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd, uint64_t n_ff,
+                     uint64_t n_ff_shexp, uint32_t n_tok, uint32_t top_k, const float* x, float* out,
+                     void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!t || !x || !out || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  for (int i = 0; i < 8; ++i) {
+    if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
+    if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
+        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
+      return fail(SH_ERR_INVALID_ARGUMENT, "misaligned tensor %d", i);
+  }
+  if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(SH_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  const sh::MoeLayerTypes q{t[0].quant, t[1].quant, t[2].quant, t[3].quant,
+                            t[4].quant, t[5].quant, t[6].quant, t[7].quant};
+  int rc;
+  const uint64_t dims[8][2] = {{n_expert, n_embd}, {n_embd, n_ff}, {n_embd, n_ff}, {n_ff, n_embd},
+                               {n_ff_shexp, n_embd}, {n_ff_shexp, n_embd}, {n_embd, n_ff_shexp}, {1, n_embd}};
+  for (int i = 0; i < 8; ++i)
+    if ((rc = check_matrix(t[i].quant, dims[i][0], dims[i][1], 1, ~uint64_t(0), i == 0 || i >= 4))) return rc;
+  sh::MoeLayerPlan plan;
+  if ((rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &plan))) return rc;
+  if (workspace_bytes < plan.bytes)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed",
+                (unsigned long long)workspace_bytes, (unsigned long long)plan.bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  auto q6 = [](uint32_t flags) { return (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  const sh::MoeLayerTensors w{t[0].data, t[1].data, t[2].data, t[3].data, t[4].data, t[5].data, t[6].data,
+                              t[7].data, q6(t[0].flags), q6(t[1].flags), q6(t[2].flags), q6(t[3].flags),
+                              q6(t[4].flags), q6(t[5].flags), q6(t[6].flags), q6(t[7].flags)};
+  HIP_TRY(sh::launch_moe_layer(plan, q, w, x, out, workspace, static_cast<hipStream_t>(stream)),
+          "moe layer launch");
   return SH_OK;
 }
 

@@ -48,6 +48,8 @@ inline int64_t byte_size(uint32_t q, int64_t n) {
 
 // The quantized matvec kernels accept these.
 inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ6_K; }
+// Plain-float element types: matvec (f64 sums) and dequant only.
+inline bool plain_quant(uint32_t q) { return q == kF32 || q == kF16 || q == kBF16; }
 
 constexpr int kWave = 64;
 

@@ -879,6 +879,69 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
   }
 }
 
+// ------------------------------------------------------- F32 / F16 / BF16 --
+// Plain-float rows (quant.rs ids 0, 1, 30: the router and shared-expert gate
+// tensors real files carry). As ops::gemv (ops.rs:14-28) every product
+// w * x is exact in f64 and the row sum accumulates in f64 before the cast
+// to f32; here lane l sums columns l, l + 64, ... and the 64 lane sums are
+// added by a butterfly, so only the order of the f64 additions differs from
+// the sequential loop. A wave takes `rpw` consecutive rows; each weight is
+// loaded once for all NB vectors.
+template <int Q>
+__device__ __forceinline__ float plain_at(const uint8_t* row, int c) {
+  if constexpr (Q == kF32) return reinterpret_cast<const float*>(row)[c];
+  const uint32_t h = reinterpret_cast<const uint16_t*>(row)[c];
+  if constexpr (Q == kF16) return h2f(h);
+  return __builtin_bit_cast(float, h << 16);  // BF16
+}
+
+template <int Q, int NB>
+__global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restrict__ w, int rows, int cols,
+                                                         int64_t row_bytes, const float* __restrict__ x,
+                                                         float* __restrict__ y, int rpw) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int r0 = wave * rpw, r1 = min(rows, r0 + rpw);
+  for (int r = r0; r < r1; ++r) {
+    const uint8_t* row = w + int64_t(r) * row_bytes;
+    double acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.0;
+    for (int c = lane; c < cols; c += kWave) {
+      const double wv = double(plain_at<Q>(row, c));
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b] = __builtin_fma(wv, double(x[int64_t(b) * cols + c]), acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      double v = acc[b];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+      if (lane == 0) y[int64_t(b) * rows + r] = float(v);
+    }
+  }
+}
+
+template <int Q>
+static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int64_t row_bytes, const float* x,
+                               float* y, hipStream_t s) {
+  // about 4096 waves, at least one row each
+  const int rpw = max(1, (rows + 4095) / 4096);
+  const int waves = (rows + rpw - 1) / rpw;
+  const dim3 grid(unsigned((waves + 3) / 4)), block(256);
+  switch (nb) {
+    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
+    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw);
+  }
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launch --
 static int g_cu_count = 0;
 
@@ -899,7 +962,9 @@ constexpr size_t kMaxLds = 160 * 1024;
 static size_t lds_bytes(int cols, int nb) { return size_t(nb) * x_stride(cols) * sizeof(float); }
 
 bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
-  if (!device_quant(quant) || rows <= 0 || cols <= 0 || batch < 1 || batch > 8) return false;
+  if (rows <= 0 || cols <= 0 || batch < 1 || batch > 8) return false;
+  if (plain_quant(quant)) return rows <= (int64_t(1) << 31) - 1 && cols <= (int64_t(1) << 30);
+  if (!device_quant(quant)) return false;
   if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 20)) return false;
   if (cols % 64 != 0) return false;  // 64-column lane units (Q8_0 blocks in pairs)
   if (cols % geometry(quant).block != 0) return false;
@@ -981,6 +1046,15 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   if (!gemv_shape_ok(quant, rows, cols, batch)) return hipErrorInvalidValue;
   const uint8_t* w = static_cast<const uint8_t*>(wv);
   const int64_t row_bytes = byte_size(quant, cols);
+  if (plain_quant(quant)) {
+    // elements are read at their own alignment (4 bytes for F32, 2 otherwise)
+    if (reinterpret_cast<uintptr_t>(w) & uintptr_t(quant == kF32 ? 3 : 1)) return hipErrorInvalidValue;
+    switch (quant) {
+      case kF32: return launch_plain<kF32>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+      case kF16: return launch_plain<kF16>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+      default: return launch_plain<kBF16>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+    }
+  }
   // Q8_0 reads 68-byte block pairs with dword loads: rows must start on a
   // dword boundary (row_bytes is 68 * cols/64, so only the base matters).
   if (quant == kQ8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;

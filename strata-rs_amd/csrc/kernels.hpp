@@ -68,6 +68,27 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       hipStream_t s);
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
 
+// The whole MoE layer (router matvec on bf16-rounded x, routed experts,
+// shared expert with its sigmoid gate): the routed plan plus the layer's
+// intermediate buffers after it in the same workspace.
+struct MoeLayerTypes {
+  uint32_t router, gate, up, down, gate_sh, up_sh, down_sh, gate_inp;
+};
+struct MoeLayerTensors {
+  const void *router, *gate, *up, *down, *gate_sh, *up_sh, *down_sh, *gate_inp;
+  int q6_router, q6_gate, q6_up, q6_down, q6_gate_sh, q6_up_sh, q6_down_sh, q6_gate_inp;
+};
+struct MoeLayerPlan {
+  MoePlan moe;
+  int n_ff_sh;
+  size_t o_logits, o_xb, o_g, o_u, o_h, o_d, o_s;  // [n_tok][...] f32 each
+  size_t bytes;
+};
+bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, int n_ff_sh,
+                    const MoeLayerTypes& q, MoeLayerPlan* plan);
+hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const MoeLayerTensors& w,
+                            const float* x, float* out, void* workspace, hipStream_t s);
+
 // Prefill matmul Y[t][r] = sum_c W[r][c] X[t][c], t < m. mode 0: bf16
 // activations on bf16 MFMA; mode 1: Q8-quantized activations on int8 MFMA
 // (Q4_K and Q8_0 weights). `workspace` holds matmul_workspace_bytes().

@@ -1,0 +1,128 @@
+// The whole MoE layer on the device: MoeLayer::route and MoeLayer::combine
+// (crates/strata-core/src/moe.rs:48-143) for n_tok tokens.
+//
+//   route    x_bf = bf16(x), rounded to nearest even (hyper.rs:22-24), and
+//            logits = router . x_bf (ops::gemv, moe.rs:55-56); then the
+//            routed FFN of moe.hip: softmax, top-k, the experts, and
+//            out = sum over the token's experts (ascending id) of w * d;
+//   shared   g = gate_shexp . x, u = up_shexp . x, h = silu(g) * u,
+//            d = down_shexp . h, s = gate_inp_shexp . x (ops::gemv each,
+//            moe.rs:129-138);
+//   combine  out += sigmoid(s) * d, after the routed sum (moe.rs:139-142).
+// The matvecs are the library's gemv kernels (F32 / F16 / BF16 rows sum in
+// f64 as ops::gemv does; Q8_0 / Q4_K / Q6_K on the integer-limb path), up
+// to 8 tokens per launch.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace sh {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// bf16::from_f32(v).to_f32(): round to nearest even (v_cvt_pk_bf16_f32;
+// a NaN stays a NaN).
+__global__ void bf16_round_kernel(const float* __restrict__ x, float* __restrict__ xb, int64_t n) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) return;
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){x[i], 0.f}, bf16x2_t);
+  xb[i] = __builtin_bit_cast(float, uint32_t(__builtin_bit_cast(uint32_t, v) & 0xFFFFu) << 16);
+}
+
+// h = silu(g) * u with silu(v) = v / (1 + exp(-v)) in f32 (ops.rs:85-87).
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ h,
+                                int64_t n) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) return;
+  const float v = g[i];
+  h[i] = v / (1.f + expf(-v)) * u[i];
+}
+
+// out[t][i] += sigmoid(s[t]) * d[t][i], sigmoid(v) = 1 / (1 + exp(-v))
+// (ops.rs:90-92), one f32 product and one f32 add as moe.rs:139-142.
+__global__ void shexp_add_kernel(float* __restrict__ out, const float* __restrict__ d, const float* __restrict__ s,
+                                 int n_embd, int64_t n) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) return;
+  const float sv = s[i / n_embd];
+  const float gate = 1.f / (1.f + expf(-sv));
+  out[i] = __fadd_rn(out[i], __fmul_rn(gate, d[i]));
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, int n_ff_sh,
+                    const MoeLayerTypes& q, MoeLayerPlan* plan) {
+  MoeLayerPlan p{};
+  if (!moe_plan(n_tok, top_k, n_expert, n_embd, n_ff, q.gate, q.down, &p.moe)) return false;
+  if (q.up != q.gate || n_ff_sh <= 0) return false;
+  // the matvecs of the layer, at the shapes the gemv kernels take
+  if (!gemv_shape_ok(q.router, n_expert, n_embd, 1) || !gemv_shape_ok(q.gate_sh, n_ff_sh, n_embd, 1) ||
+      !gemv_shape_ok(q.up_sh, n_ff_sh, n_embd, 1) || !gemv_shape_ok(q.down_sh, n_embd, n_ff_sh, 1) ||
+      !gemv_shape_ok(q.gate_inp, 1, n_embd, 1))
+    return false;
+  if (n_ff_sh % 4 != 0) return false;  // h rows stay 16-byte aligned as gemv inputs
+  size_t o = align256(p.moe.bytes);
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  const size_t T = size_t(n_tok);
+  p.o_logits = take(sizeof(float) * T * n_expert);
+  p.o_xb = take(sizeof(float) * T * n_embd);
+  p.o_g = take(sizeof(float) * T * n_ff_sh);
+  p.o_u = take(sizeof(float) * T * n_ff_sh);
+  p.o_h = take(sizeof(float) * T * n_ff_sh);
+  p.o_d = take(sizeof(float) * T * n_embd);
+  p.o_s = take(sizeof(float) * T);
+  p.bytes = o;
+  p.n_ff_sh = n_ff_sh;
+  *plan = p;
+  return true;
+}
+
+// y[t] = W . x[t] for t < n_tok, 8 tokens per launch.
+static hipError_t gemv_tokens(uint32_t quant, const void* w, int rows, int cols, const float* x, float* y,
+                              int n_tok, int q6s, hipStream_t s) {
+  for (int t0 = 0; t0 < n_tok; t0 += 8) {
+    const int nb = n_tok - t0 < 8 ? n_tok - t0 : 8;
+    const hipError_t e = launch_gemv(quant, w, rows, cols, x + int64_t(t0) * cols, y + int64_t(t0) * rows, nb,
+                                     q6s, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const MoeLayerTensors& w,
+                            const float* x, float* out, void* workspace, hipStream_t s) {
+  const MoePlan& m = p.moe;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* logits = reinterpret_cast<float*>(ws + p.o_logits);
+  float* xb = reinterpret_cast<float*>(ws + p.o_xb);
+  float* g = reinterpret_cast<float*>(ws + p.o_g);
+  float* u = reinterpret_cast<float*>(ws + p.o_u);
+  float* h = reinterpret_cast<float*>(ws + p.o_h);
+  float* d = reinterpret_cast<float*>(ws + p.o_d);
+  float* sg = reinterpret_cast<float*>(ws + p.o_s);
+  const int T = m.n_tok, E = m.n_expert, n_embd = m.n_embd, n_sh = p.n_ff_sh;
+  const int64_t nx = int64_t(T) * n_embd, nh = int64_t(T) * n_sh;
+  auto blocks = [](int64_t n) { return dim3(unsigned((n + 255) / 256)); };
+  hipError_t e;
+  // route: router . bf16(x), then the routed experts into out
+  hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);
+  if ((e = gemv_tokens(q.router, w.router, E, n_embd, xb, logits, T, w.q6_router, s)) != hipSuccess) return e;
+  if ((e = launch_moe(m, q.gate, q.up, q.down, w.gate, w.up, w.down, w.q6_gate, w.q6_up, w.q6_down, logits, x,
+                      out, workspace, s)) != hipSuccess)
+    return e;
+  // shared expert
+  if ((e = gemv_tokens(q.gate_sh, w.gate_sh, n_sh, n_embd, x, g, T, w.q6_gate_sh, s)) != hipSuccess) return e;
+  if ((e = gemv_tokens(q.up_sh, w.up_sh, n_sh, n_embd, x, u, T, w.q6_up_sh, s)) != hipSuccess) return e;
+  hipLaunchKernelGGL(silu_mul_kernel, blocks(nh), dim3(256), 0, s, g, u, h, nh);
+  if ((e = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, s)) != hipSuccess) return e;
+  if ((e = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, s)) != hipSuccess) return e;
+  hipLaunchKernelGGL(shexp_add_kernel, blocks(nx), dim3(256), 0, s, out, d, sg, n_embd, nx);
+  return hipGetLastError();
+}
+
+}  // namespace sh

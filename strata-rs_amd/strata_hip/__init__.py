@@ -52,9 +52,10 @@ EXPORTS = (
     "sh_abi_version", "sh_last_error", "sh_device_count", "sh_quant_geometry",
     "sh_create", "sh_destroy", "sh_name", "sh_resident_bytes", "sh_evict",
     "sh_gemv", "sh_gemv_batch", "sh_expert_gemv", "sh_dequantize_row",
-    "sh_moe_route", "sh_moe_ffn", "sh_matmul",
+    "sh_moe_route", "sh_moe_ffn", "sh_moe_layer", "sh_matmul",
     "sh_moe_workspace_bytes", "sh_moe_ffn_dev", "sh_matmul_workspace_bytes", "sh_matmul_dev",
-    "sh_quantize_q8_dev", "sh_dequant_dev", "sh_gemv_dev",
+    "sh_quantize_q8_dev", "sh_moe_layer_workspace_bytes", "sh_moe_layer_dev", "sh_dequant_dev",
+    "sh_gemv_dev",
 )
 
 
@@ -151,6 +152,12 @@ def load_library() -> C.CDLL:
     L.sh_moe_workspace_bytes.argtypes = [u32, u32, u64, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
     L.sh_moe_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC), C.POINTER(_ExpertDevC),
                                  u64, u64, u64, vp, u32, u32, vp, vp, vp, u64, vp]
+    L.sh_moe_layer.argtypes = [vp, C.POINTER(_QuantTensorC), C.POINTER(_ExpertViewC), C.POINTER(_ExpertViewC),
+                               C.POINTER(_ExpertViewC), C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC),
+                               C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC), f32p, u32, u32, f32p]
+    L.sh_moe_layer_workspace_bytes.argtypes = [u32, u32, u64, u64, u64, u64, C.POINTER(C.c_uint32),
+                                               C.POINTER(C.c_uint64)]
+    L.sh_moe_layer_dev.argtypes = [C.POINTER(_ExpertDevC), u64, u64, u64, u64, u32, u32, vp, vp, vp, u64, vp]
     L.sh_matmul.argtypes = [vp, C.POINTER(_QuantTensorC), f32p, u32, f32p, u32]
     L.sh_matmul_workspace_bytes.argtypes = [u32, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
     L.sh_matmul_dev.argtypes = [u32, u32, vp, u64, u64, vp, u32, vp, u32, vp, u64, vp]
@@ -348,6 +355,21 @@ class HipBackend:
                                  top_k, xv.ctypes.data, out.ctypes.data))
         return out
 
+    def moe_layer(self, router: QuantTensor, gate: ExpertView, up: ExpertView, down: ExpertView,
+                  gate_shexp: QuantTensor, up_shexp: QuantTensor, down_shexp: QuantTensor,
+                  gate_inp_shexp: QuantTensor, x, top_k: int) -> np.ndarray:
+        """MoeLayer::route + MoeLayer::combine (moe.rs:48-143) for ``x [n_tok][n_embd]``:
+        router logits on bf16(x), the routed experts, and the shared expert
+        added with its sigmoid gate; returns ``[n_tok][n_embd]``."""
+        xv = np.ascontiguousarray(x, dtype=np.float32)
+        if xv.ndim == 1:
+            xv = xv[None, :]
+        out = np.empty_like(xv)
+        cs = [t._c() for t in (router, gate, up, down, gate_shexp, up_shexp, down_shexp, gate_inp_shexp)]
+        check(self._L.sh_moe_layer(self._ctx, *(C.byref(c) for c in cs), xv.ctypes.data, xv.shape[0], top_k,
+                                   out.ctypes.data))
+        return out
+
     def matmul(self, w: QuantTensor, x, mode: int = MATMUL_BF16) -> np.ndarray:
         """Prefill matmul ``y[t] = W x[t]`` for ``x [m][cols]`` -> ``[m][rows]``:
         m gemvs (ops.rs:14-28) with bf16 or Q8-block activations (``mode``)."""
@@ -399,6 +421,24 @@ def moe_ffn_dev(gate: tuple, up: tuple, down: tuple, n_expert: int, n_embd: int,
     check(load_library().sh_moe_ffn_dev(C.byref(g), C.byref(u), C.byref(d), n_expert, n_embd, n_ff,
                                         logits_ptr, n_tok, top_k, x_ptr, out_ptr, ws_ptr, ws_bytes,
                                         stream or None))
+
+
+def moe_layer_workspace_bytes(n_tok: int, top_k: int, n_expert: int, n_embd: int, n_ff: int, n_ff_shexp: int,
+                              quants) -> int:
+    """quants: the 8 types (router, gate, up, down, gate_shexp, up_shexp, down_shexp, gate_inp_shexp)."""
+    q = (C.c_uint32 * 8)(*[int(v) for v in quants])
+    v = C.c_uint64()
+    check(load_library().sh_moe_layer_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, n_ff_shexp, q,
+                                                      C.byref(v)))
+    return v.value
+
+
+def moe_layer_dev(tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_shexp: int, n_tok: int, top_k: int,
+                  x_ptr: int, out_ptr: int, ws_ptr: int, ws_bytes: int, stream: int = 0) -> None:
+    """tensors: 8 (quant, flags, device pointer) in sh_moe_layer_dev's order."""
+    arr = (_ExpertDevC * 8)(*[_ExpertDevC(int(q), f, p) for q, f, p in tensors])
+    check(load_library().sh_moe_layer_dev(arr, n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, x_ptr, out_ptr,
+                                          ws_ptr, ws_bytes, stream or None))
 
 
 def matmul_workspace_bytes(quant: int, rows: int, cols: int, m: int, mode: int = MATMUL_BF16) -> int:

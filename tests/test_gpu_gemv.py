@@ -144,8 +144,8 @@ def test_gemv_shape_errors(backend):
         backend.gemv(H.QuantTensor("short", 12, 4, 256, w[:-1]), np.zeros(256, np.float32),
                      np.zeros(4, np.float32))
     with pytest.raises(H.UnsupportedQuantError):
-        f32 = np.zeros((4, 8), np.float32)
-        backend.gemv(H.QuantTensor("f32", 0, 4, 8, f32), np.zeros(8, np.float32), np.zeros(4, np.float32))
+        q4_0 = np.zeros(4 * 18, np.uint8)  # Q4_0: not on this path
+        backend.gemv(H.QuantTensor("q4_0", 2, 4, 32, q4_0), np.zeros(32, np.float32), np.zeros(4, np.float32))
 
 
 def test_gemv_empty_shapes(backend):
@@ -168,3 +168,39 @@ def test_gemv_dev_pointers_on_torch_stream(oracle):
     H.gemv_dev(12, wd.data_ptr(), rows, cols, xd.data_ptr(), yd.data_ptr(), 1, s)
     torch.cuda.synchronize()
     check(yd.cpu().numpy(), oracle.gemv(12, rows, cols, w, x, threads=8))
+
+
+def plain_matrix(quant, seed, rows, cols):
+    """F32 / F16 / BF16 rows of N(0, 1) values, as packed bytes."""
+    v = S.normal_f32(seed, rows * cols)
+    if quant == H.QuantType.F32:
+        return v.view(np.uint8)
+    if quant == H.QuantType.F16:
+        return v.astype(np.float16).view(np.uint8)
+    bits = v.view(np.uint32)
+    rne = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)  # round to nearest even
+    return rne.view(np.uint8)
+
+
+@pytest.mark.parametrize("quant", [H.QuantType.F32, H.QuantType.F16, H.QuantType.BF16])
+@pytest.mark.parametrize("rows,cols,batch", [(128, 2048, 1), (1, 2048, 1), (300, 2049, 3), (5, 1, 8),
+                                             (4096, 4096, 2)])
+def test_gemv_plain_types(backend, oracle, quant, rows, cols, batch):
+    """Plain-float rows (router and shared-expert gate tensors): products and
+    sums in f64 as ops::gemv, so the f32 results equal the oracle's except
+    where the two summation orders straddle a rounding boundary (1 ulp)."""
+    say("gemv plain", int(quant), rows, cols, batch)
+    w = plain_matrix(quant, 900 + rows + cols, rows, cols)
+    x = S.normal_f32(901 + cols, batch * cols).reshape(batch, cols)
+    t = H.QuantTensor(f"p{int(quant)}_{rows}_{cols}", int(quant), rows, cols, w)
+    if batch == 1:
+        y = np.empty(rows, np.float32)
+        backend.gemv(t, x[0], y)
+        y = y[None]
+    else:
+        y = backend.gemv_batch(t, x, batch)
+    for b in range(batch):
+        ref = oracle.gemv(int(quant), rows, cols, w, x[b])
+        ulp = np.abs(y[b].view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+        assert ulp.max() <= 1, (b, int(ulp.max()))
+        assert np.mean(y[b] == ref) >= 0.99

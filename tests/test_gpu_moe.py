@@ -243,3 +243,110 @@ def test_moe_errors(backend):
         backend.moe_ffn(g, g, d_bad, np.zeros((1, 4), np.float32), np.zeros((1, 256), np.float32), 2)
     with pytest.raises(H.BackendError):
         backend.moe_route(np.zeros((1, 4), np.float32), 5)  # top_k > n_expert
+
+
+def layer_tensors(n_expert, n_embd, n_ff, n_sh, seed, q_router=0, q_inp=0, q_sh=(12, 12, 14)):
+    """Router and gate-input rows as plain floats (F32, or BF16 when asked),
+    experts as the MoE config (gate/up Q4_K, down Q6_K), the shared expert
+    in the given types."""
+    def plain(q, s, n):
+        v = S.normal_f32(s, n)
+        if q == 0:
+            return v.view(np.uint8)
+        bits = v.view(np.uint32)
+        return ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16).view(np.uint8)
+    quants = [q_router, 12, 12, 14, q_sh[0], q_sh[1], q_sh[2], q_inp]
+    tensors = [plain(q_router, seed, n_expert * n_embd),
+               S.matrix(12, seed + 1, n_expert * n_embd, n_ff), S.matrix(12, seed + 2, n_expert * n_embd, n_ff),
+               S.matrix(14, seed + 3, n_expert * n_ff, n_embd),
+               S.matrix(q_sh[0], seed + 4, n_sh, n_embd), S.matrix(q_sh[1], seed + 5, n_sh, n_embd),
+               S.matrix(q_sh[2], seed + 6, n_embd, n_sh), plain(q_inp, seed + 7, n_embd)]
+    return quants, tensors
+
+
+def layer_views(name, quants, tensors, n_expert, n_embd, n_ff, n_sh):
+    q, t = quants, tensors
+    return (H.QuantTensor(f"{name}.router", q[0], n_expert, n_embd, t[0]),
+            H.ExpertView(f"{name}.gate", q[1], n_expert, n_embd, n_ff, t[1]),
+            H.ExpertView(f"{name}.up", q[2], n_expert, n_embd, n_ff, t[2]),
+            H.ExpertView(f"{name}.down", q[3], n_expert, n_ff, n_embd, t[3]),
+            H.QuantTensor(f"{name}.gate_sh", q[4], n_sh, n_embd, t[4]),
+            H.QuantTensor(f"{name}.up_sh", q[5], n_sh, n_embd, t[5]),
+            H.QuantTensor(f"{name}.down_sh", q[6], n_embd, n_sh, t[6]),
+            H.QuantTensor(f"{name}.inp_sh", q[7], 1, n_embd, t[7]))
+
+
+@pytest.mark.parametrize("n_tok,q_router,q_inp,q_sh", [(1, 0, 0, (12, 12, 14)), (3, 30, 0, (8, 8, 8)),
+                                                       (9, 0, 30, (14, 14, 12))])
+def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh):
+    """The whole layer (moe.rs:48-143): router matvec on bf16(x) (F32 or
+    BF16 rows, f64 sums), routing, the routed experts and the shared expert
+    with its sigmoid gate, against the oracle token by token; 9 tokens take
+    two 8-token matvec launches."""
+    n_expert, n_embd, n_ff, n_sh, top_k = 32, 512, 256, 256, 6
+    say("moe layer", n_tok, q_router, q_inp, q_sh)
+    q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8400 + n_tok, q_router, q_inp, q_sh)
+    x = S.normal_f32(8500 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    views = layer_views(f"L{n_tok}", q, t, n_expert, n_embd, n_ff, n_sh)
+    out = backend.moe_layer(*views, x, top_k)
+    for i in range(n_tok):
+        ref = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[i], top_k)
+        assert rel_err(out[i], ref) <= 1e-3, (i, rel_err(out[i], ref))
+        assert elem_rel_err(out[i], ref, floor=1.0) <= 1e-3
+
+
+@pytest.fixture(scope="module")
+def layer_config_tensors():
+    # the MoE config (128 experts, hidden 2048, expert FFN 768, top-8) with a
+    # shared expert of width 768 (Q4_K gate/up, Q6_K down) and F32 router and
+    # gate-input rows
+    return layer_tensors(128, 2048, 768, 768, 8600)
+
+
+@pytest.mark.parametrize("n_tok", [1, 16])
+def test_moe_layer_config_shapes(backend, oracle, layer_config_tensors, n_tok):
+    n_expert, n_embd, n_ff, n_sh, top_k = 128, 2048, 768, 768, 8
+    say("moe layer config", n_tok)
+    q, t = layer_config_tensors
+    x = S.normal_f32(8700 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    out = backend.moe_layer(*layer_views("Lcfg", q, t, n_expert, n_embd, n_ff, n_sh), x, top_k)
+    for i in range(n_tok):
+        ref = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[i], top_k)
+        assert rel_err(out[i], ref) <= 1e-3, (i, rel_err(out[i], ref))
+        assert elem_rel_err(out[i], ref, floor=1.0) <= 1e-3
+
+
+def test_moe_layer_dev_matches_host_path(backend):
+    import torch
+    n_expert, n_embd, n_ff, n_sh, top_k, n_tok = 32, 512, 256, 256, 8, 4
+    say("moe layer dev")
+    q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8800)
+    x = S.normal_f32(8801, n_tok * n_embd).reshape(n_tok, n_embd)
+    host = backend.moe_layer(*layer_views("Ldev", q, t, n_expert, n_embd, n_ff, n_sh), x, top_k)
+    dev = torch.device("cuda:0")
+    td = [torch.from_numpy(a).to(dev) for a in t]
+    tx = torch.from_numpy(x).to(dev)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+    nb = H.moe_layer_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, n_sh, q)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    H.moe_layer_dev([(qq, 0, a.data_ptr()) for qq, a in zip(q, td)], n_expert, n_embd, n_ff, n_sh, n_tok,
+                    top_k, tx.data_ptr(), out.data_ptr(), ws.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), host)
+
+
+def test_moe_layer_errors(backend):
+    say("moe layer errors")
+    n_expert, n_embd, n_ff, n_sh = 8, 256, 256, 256
+    q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8900)
+    views = list(layer_views("Lerr", q, t, n_expert, n_embd, n_ff, n_sh))
+    x = np.zeros((1, n_embd), np.float32)
+    bad = list(views)
+    bad[0] = H.QuantTensor("Lerr.router_bad", 0, n_expert + 1, n_embd,
+                           S.normal_f32(1, (n_expert + 1) * n_embd).view(np.uint8))
+    with pytest.raises(H.ShapeError):
+        backend.moe_layer(*bad, x, 2)
+    bad = list(views)
+    bad[4] = H.QuantTensor("Lerr.gsh_q40", 2, n_sh, n_embd, np.zeros(n_sh * n_embd // 32 * 18, np.uint8))
+    with pytest.raises(H.UnsupportedQuantError):
+        backend.moe_layer(*bad, x, 2)

@@ -9,7 +9,11 @@
   of the same order bit for bit, and the threaded variant equals it too;
 * MoE routing invariants (crates/strata-core/src/moe.rs:58-90): weights sum
   to one, ids ascending, ties to the lower id, uniform logits give uniform
-  weights; the routed combine equals its composition from expert_gemv.
+  weights; the routed combine equals its composition from expert_gemv;
+* the whole MoE layer (moe.rs:48-143): with the shared expert off it is the
+  routed part on router . bf16(x) bit for bit; with the routed experts off
+  and a zero gate input it is exactly half the shared expert's output; a
+  tie that exists only after bf16 rounding routes to the lower id.
 """
 from fractions import Fraction
 
@@ -256,3 +260,84 @@ def test_bf16_round_matches_torch_and_scalar(oracle):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     for v in x[-7:]:
         assert np.float32(oracle.lib().sho_bf16_round(float(v))) == oracle.bf16_round_array(np.float32(v))
+
+
+def test_sigmoid_closed_form(oracle):
+    # ops.rs:90-92: 1 / (1 + exp(-x)) in f32
+    assert oracle.sigmoid(0.0) == 0.5
+    assert oracle.sigmoid(100.0) == 1.0
+    assert oracle.sigmoid(-100.0) < 1e-40
+    for v in (-3.0, -0.5, 0.25, 2.0):
+        assert abs(oracle.sigmoid(v) - 1.0 / (1.0 + np.exp(-v))) < 1e-7
+
+
+def moe_layer_tensors(n_expert, n_embd, n_ff, n_sh, seed):
+    f32 = lambda s, n: S.normal_f32(s, n).view(np.uint8)  # noqa: E731
+    router = f32(seed, n_expert * n_embd)
+    gate = S.matrix(12, seed + 1, n_expert * n_embd, n_ff)
+    up = S.matrix(12, seed + 2, n_expert * n_embd, n_ff)
+    down = S.matrix(14, seed + 3, n_expert * n_ff, n_embd)
+    g_sh = S.matrix(8, seed + 4, n_sh, n_embd)
+    u_sh = S.matrix(8, seed + 5, n_sh, n_embd)
+    d_sh = S.matrix(12, seed + 6, n_embd, n_sh)
+    inp = f32(seed + 7, n_embd)
+    return [0, 12, 12, 14, 8, 8, 12, 0], [router, gate, up, down, g_sh, u_sh, d_sh, inp]
+
+
+def test_moe_layer_without_shared_expert_is_the_routed_part(oracle):
+    """moe.rs:48-127: with the shared down matrix zero the layer is route on
+    router . bf16(x) plus the routed combine, bit for bit."""
+    n_expert, n_embd, n_ff, n_sh, k = 16, 256, 256, 256, 4
+    q, t = moe_layer_tensors(n_expert, n_embd, n_ff, n_sh, 8100)
+    t[6] = np.zeros_like(t[6])
+    x = S.normal_f32(8101, n_embd)
+    got = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x, k)
+    xb = np.array([oracle.lib().sho_bf16_round(float(v)) for v in x], np.float32)
+    logits = oracle.gemv(0, n_expert, n_embd, t[0], xb)
+    ids, w = oracle.moe_route(logits, k)
+    want = oracle.moe_routed(12, 12, 14, n_expert, n_embd, n_ff, t[1], t[2], t[3], ids, w, x)
+    assert np.array_equal(got, want)
+
+
+def test_moe_layer_shared_expert_half_gate(oracle):
+    """moe.rs:129-142: with every routed down matrix zero and a zero gate
+    input row (sigmoid(0) = 1/2 exactly), the layer is half the shared
+    expert's output: down_sh . (silu(gate_sh . x) * (up_sh . x)) / 2."""
+    n_expert, n_embd, n_ff, n_sh, k = 8, 256, 256, 512, 2
+    q, t = moe_layer_tensors(n_expert, n_embd, n_ff, n_sh, 8200)
+    t[3] = np.zeros_like(t[3])
+    t[7] = np.zeros_like(t[7])
+    x = S.normal_f32(8201, n_embd)
+    got = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x, k)
+    g = oracle.gemv(8, n_sh, n_embd, t[4], x)
+    u = oracle.gemv(8, n_sh, n_embd, t[5], x)
+    h = np.array([oracle.silu(float(a)) for a in g], np.float32) * u
+    d = oracle.gemv(12, n_embd, n_sh, t[6], h)
+    assert np.array_equal(got, np.float32(0.5) * d)
+    assert np.any(got != 0)
+
+
+def test_moe_layer_routes_on_bf16_rounded_x(oracle):
+    """moe.rs:55: the router sees bf16(x). Two experts whose logits are x[0]
+    and x[1]; x[1] = 1 + 2^-9 rounds to 1.0 = x[0], so the tie goes to
+    expert 0 (without the rounding expert 1 would win). Expert 1's down
+    matrix is zero and the shared expert is off, so a nonzero output shows
+    expert 0 was chosen."""
+    n_expert, n_embd, n_ff, n_sh, k = 2, 256, 256, 256, 1
+    q, t = moe_layer_tensors(n_expert, n_embd, n_ff, n_sh, 8300)
+    router = np.zeros((n_expert, n_embd), np.float32)
+    router[0, 0] = 1.0
+    router[1, 1] = 1.0
+    t[0] = router.view(np.uint8).reshape(-1)
+    rb = S.row_bytes(14, n_embd)
+    down = t[3].copy()
+    down[n_ff * rb:] = 0  # expert 1
+    t[3] = down
+    t[6] = np.zeros_like(t[6])
+    x = S.normal_f32(8301, n_embd)
+    x[0], x[1] = 1.0, np.float32(1.0 + 2.0 ** -9)
+    got = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x, k)
+    assert np.any(got != 0)
+    want = oracle.moe_routed(12, 12, 14, n_expert, n_embd, n_ff, t[1], t[2], t[3], np.array([0]),
+                             np.array([1.0], np.float32), x)
+    assert np.array_equal(got, want)
