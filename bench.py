@@ -218,6 +218,69 @@ def bench_moe(torch, H, S, steps):
     return res
 
 
+def bench_moe_layer(torch, H, S, steps):
+    """The whole MoE layer (router on bf16(x), routed experts, shared expert
+    and its gate) at the routed config plus a shared expert of width 768
+    (gate/up Q4_K, down Q6_K) and F32 router / gate-input rows; GB/s of the
+    packed bytes each call reads (the routed-to experts once each, the
+    shared expert, the router and gate-input rows)."""
+    import numpy as np
+    E, n_embd, n_ff, n_sh, top_k = 128, 2048, 768, 768, 8
+    gate = S.matrix(S.Q4_K, 0x5EED0041, E * n_embd, n_ff)
+    up = S.matrix(S.Q4_K, 0x5EED0042, E * n_embd, n_ff)
+    down = S.matrix(S.Q6_K, 0x5EED0043, E * n_ff, n_embd)
+    router = S.normal_f32(0x5EED0047, E * n_embd)
+    g_sh = S.matrix(S.Q4_K, 0x5EED0048, n_sh, n_embd)
+    u_sh = S.matrix(S.Q4_K, 0x5EED0049, n_sh, n_embd)
+    d_sh = S.matrix(S.Q6_K, 0x5EED004A, n_embd, n_sh)
+    inp = S.normal_f32(0x5EED004B, n_embd)
+    quants = [0, S.Q4_K, S.Q4_K, S.Q6_K, S.Q4_K, S.Q4_K, S.Q6_K, 0]
+    host = [router.view(np.uint8), gate, up, down, g_sh, u_sh, d_sh, inp.view(np.uint8)]
+    per_expert = (gate.nbytes + up.nbytes + down.nbytes) // E
+    fixed = router.nbytes + g_sh.nbytes + u_sh.nbytes + d_sh.nbytes + inp.nbytes
+    dev = torch.device("cuda:0")
+    sets = [[torch.from_numpy(a).to(dev) for a in host] for _ in range(3)]  # 3 x ~395 MB
+    rt = router.reshape(E, n_embd)
+    del gate, up, down
+    res = {}
+    for n_tok in (1, 16):
+        variants = 8
+        xs = [S.normal_f32(0x5EED004C + 97 * v + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+              for v in range(variants)]
+        uniq = []
+        for xv in xs:
+            # the experts each token routes to: top-k of router . bf16(x) (softmax keeps the order)
+            bits = xv.view(np.uint32)
+            xb = (((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+            lg = xb.astype(np.float64) @ rt.T.astype(np.float64)
+            ids = set()
+            for t in range(n_tok):
+                ids.update(np.argsort(-lg[t], kind="stable")[:top_k].tolist())
+            uniq.append(len(ids))
+        tx = [torch.from_numpy(xv).to(dev) for xv in xs]
+        out = torch.empty(n_tok * n_embd, dtype=torch.float32, device=dev)
+        nb = H.moe_layer_workspace_bytes(n_tok, top_k, E, n_embd, n_ff, n_sh, quants)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        calls, byts = [], 0
+        for v in range(variants * len(sets)):
+            ts, xv = sets[v % len(sets)], tx[v % variants]
+            byts += uniq[v % variants] * per_expert + fixed
+            calls.append(lambda st, ts=ts, xv=xv:
+                         H.moe_layer_dev([(q, 0, t.data_ptr()) for q, t in zip(quants, ts)], E, n_embd, n_ff,
+                                         n_sh, n_tok, top_k, xv.data_ptr(), out.data_ptr(), ws.data_ptr(), nb,
+                                         st))
+        ms = time_calls(torch, calls, steps, len(calls))
+        mean_bytes = byts / len(calls)
+        res[f"moe_layer_128x2048x768_top8_shexp768_{n_tok}tok"] = {
+            "us_per_call": round(ms * 1e3, 2), "mean_unique_experts": round(sum(uniq) / variants, 2),
+            "weight_GBps": round(mean_bytes / (ms * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(100 * mean_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+        del ws, tx, out
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(w, x, rows, cols, seconds):
     """The oracle (ops::gemv restated in C, one thread) on whole rows of the
     same matrix for about `seconds`; GB/s of packed weight bytes."""
@@ -294,7 +357,9 @@ def main():
         args.no_extra = True
         args.no_cpu = True
     elif args.only == "moe":
-        print(json.dumps(bench_moe(torch, H, S, args.steps)), flush=True)
+        res = bench_moe(torch, H, S, args.steps)
+        res.update(bench_moe_layer(torch, H, S, args.steps))
+        print(json.dumps(res), flush=True)
         return
     elif args.only == "prefill":
         wp = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
@@ -356,6 +421,8 @@ def main():
         del prefill_w
         print("[bench] extra moe", file=sys.stderr, flush=True)
         extra.update(bench_moe(torch, H, S, 240))
+        print("[bench] extra moe layer", file=sys.stderr, flush=True)
+        extra.update(bench_moe_layer(torch, H, S, 240))
         out["extra"] = extra
 
     if not args.no_cpu:

@@ -883,10 +883,11 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
 // Plain-float rows (quant.rs ids 0, 1, 30: the router and shared-expert gate
 // tensors real files carry). As ops::gemv (ops.rs:14-28) every product
 // w * x is exact in f64 and the row sum accumulates in f64 before the cast
-// to f32; here lane l sums columns l, l + 64, ... and the 64 lane sums are
-// added by a butterfly, so only the order of the f64 additions differs from
-// the sequential loop. A wave takes `rpw` consecutive rows; each weight is
-// loaded once for all NB vectors.
+// to f32; here a workgroup of 256 threads takes a row, thread t summing
+// columns t, t + 256, ... (eight loads in flight before their products),
+// and the 256 partial sums are added by wave butterflies and then in wave
+// order through LDS, so only the order of the f64 additions differs from
+// the sequential loop. Each weight is loaded once for all NB vectors.
 template <int Q>
 __device__ __forceinline__ float plain_at(const uint8_t* row, int c) {
   if constexpr (Q == kF32) return reinterpret_cast<const float*>(row)[c];
@@ -895,49 +896,66 @@ __device__ __forceinline__ float plain_at(const uint8_t* row, int c) {
   return __builtin_bit_cast(float, h << 16);  // BF16
 }
 
+constexpr int kPlainThreads = 256, kPlainUnroll = 8;
+
 template <int Q, int NB>
-__global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restrict__ w, int rows, int cols,
-                                                         int64_t row_bytes, const float* __restrict__ x,
-                                                         float* __restrict__ y, int rpw) {
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int r0 = wave * rpw, r1 = min(rows, r0 + rpw);
-  for (int r = r0; r < r1; ++r) {
-    const uint8_t* row = w + int64_t(r) * row_bytes;
-    double acc[NB];
+__global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t* __restrict__ w, int rows, int cols,
+                                                                  int64_t row_bytes, const float* __restrict__ x,
+                                                                  float* __restrict__ y) {
+  __shared__ double part[kPlainThreads / kWave][NB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x;
+  const uint8_t* row = w + int64_t(r) * row_bytes;
+  double acc[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = 0.0;
-    for (int c = lane; c < cols; c += kWave) {
-      const double wv = double(plain_at<Q>(row, c));
+  for (int b = 0; b < NB; ++b) acc[b] = 0.0;
+  constexpr int kStep = kPlainThreads * kPlainUnroll;
+  for (int c0 = 0; c0 < cols; c0 += kStep) {
+    float wv[kPlainUnroll], xv[kPlainUnroll][NB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) acc[b] = __builtin_fma(wv, double(x[int64_t(b) * cols + c]), acc[b]);
+    for (int k = 0; k < kPlainUnroll; ++k) {
+      const int c = min(c0 + k * kPlainThreads + tid, cols - 1);
+      wv[k] = plain_at<Q>(row, c);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xv[k][b] = x[int64_t(b) * cols + c];
     }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      double v = acc[b];
+    for (int k = 0; k < kPlainUnroll; ++k) {
+      if (c0 + k * kPlainThreads + tid < cols) {
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-      if (lane == 0) y[int64_t(b) * rows + r] = float(v);
+        for (int b = 0; b < NB; ++b) acc[b] = __builtin_fma(double(wv[k]), double(xv[k][b]), acc[b]);
+      }
     }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    double v = acc[b];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if (lane == 0) part[wave][b] = v;
+  }
+  __syncthreads();
+  if (tid < NB) {
+    double v = part[0][tid];
+#pragma unroll
+    for (int k = 1; k < kPlainThreads / kWave; ++k) v += part[k][tid];
+    y[int64_t(tid) * rows + r] = float(v);
   }
 }
 
 template <int Q>
 static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int64_t row_bytes, const float* x,
                                float* y, hipStream_t s) {
-  // about 4096 waves, at least one row each
-  const int rpw = max(1, (rows + 4095) / 4096);
-  const int waves = (rows + rpw - 1) / rpw;
-  const dim3 grid(unsigned((waves + 3) / 4)), block(256);
+  const dim3 grid = dim3(unsigned(rows)), block = dim3(kPlainThreads);
   switch (nb) {
-    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw); break;
-    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, rpw);
+    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8>), grid, block, 0, s, w, rows, cols, row_bytes, x, y);
   }
   return hipGetLastError();
 }

@@ -9,6 +9,8 @@
 //            d = down_shexp . h, s = gate_inp_shexp . x (ops::gemv each,
 //            moe.rs:129-138);
 //   combine  out += sigmoid(s) * d, after the routed sum (moe.rs:139-142).
+// The shared expert runs on a second stream, forked from and joined back to
+// the caller's, beside the route and the routed experts.
 // The matvecs are the library's gemv kernels (F32 / F16 / BF16 rows sum in
 // f64 as ops::gemv does; Q8_0 / Q4_K / Q6_K on the integer-limb path), up
 // to 8 tokens per launch.
@@ -94,6 +96,42 @@ static hipError_t gemv_tokens(uint32_t quant, const void* w, int rows, int cols,
   return hipSuccess;
 }
 
+// A second stream per (thread, device) for the shared expert: forked from
+// the caller's stream with an event and joined back before the final add,
+// so the shared expert runs beside the routed experts (under stream capture
+// the two become parallel branches of the graph). Thread-local, so
+// concurrent callers (and concurrent captures) never share it; default
+// priority, like every stream here. The streams live until the process
+// ends (no destructor: at exit the runtime may already be gone).
+namespace {
+struct SideStreams {
+  int dev[8] = {-1, -1, -1, -1, -1, -1, -1, -1};
+  hipStream_t s[8] = {};
+};
+thread_local SideStreams g_side;
+
+hipError_t side_stream(hipStream_t* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  for (int i = 0; i < 8; ++i) {
+    if (g_side.dev[i] == dev) {
+      *out = g_side.s[i];
+      return hipSuccess;
+    }
+    if (g_side.dev[i] < 0) {
+      e = hipStreamCreateWithFlags(&g_side.s[i], hipStreamNonBlocking);
+      if (e != hipSuccess) return e;
+      g_side.dev[i] = dev;
+      *out = g_side.s[i];
+      return hipSuccess;
+    }
+  }
+  *out = nullptr;  // more than 8 devices on one thread: no side stream
+  return hipSuccess;
+}
+}  // namespace
+
 hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const MoeLayerTensors& w,
                             const float* x, float* out, void* workspace, hipStream_t s) {
   const MoePlan& m = p.moe;
@@ -109,20 +147,47 @@ hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const
   const int64_t nx = int64_t(T) * n_embd, nh = int64_t(T) * n_sh;
   auto blocks = [](int64_t n) { return dim3(unsigned((n + 255) / 256)); };
   hipError_t e;
-  // route: router . bf16(x), then the routed experts into out
-  hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);
-  if ((e = gemv_tokens(q.router, w.router, E, n_embd, xb, logits, T, w.q6_router, s)) != hipSuccess) return e;
-  if ((e = launch_moe(m, q.gate, q.up, q.down, w.gate, w.up, w.down, w.q6_gate, w.q6_up, w.q6_down, logits, x,
-                      out, workspace, s)) != hipSuccess)
-    return e;
-  // shared expert
-  if ((e = gemv_tokens(q.gate_sh, w.gate_sh, n_sh, n_embd, x, g, T, w.q6_gate_sh, s)) != hipSuccess) return e;
-  if ((e = gemv_tokens(q.up_sh, w.up_sh, n_sh, n_embd, x, u, T, w.q6_up_sh, s)) != hipSuccess) return e;
-  hipLaunchKernelGGL(silu_mul_kernel, blocks(nh), dim3(256), 0, s, g, u, h, nh);
-  if ((e = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, s)) != hipSuccess) return e;
-  if ((e = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, s)) != hipSuccess) return e;
-  hipLaunchKernelGGL(shexp_add_kernel, blocks(nx), dim3(256), 0, s, out, d, sg, n_embd, nx);
-  return hipGetLastError();
+  // the shared expert on the side stream (on `s` itself without one)
+  hipStream_t side = nullptr;
+  if ((e = side_stream(&side)) != hipSuccess) return e;
+  hipEvent_t fork = nullptr, join = nullptr;
+  if (side) {
+    if ((e = hipEventCreateWithFlags(&fork, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&join, hipEventDisableTiming)) != hipSuccess) {
+      (void)hipEventDestroy(fork);
+      return e;
+    }
+  }
+  auto run = [&]() -> hipError_t {
+    hipError_t r;
+    hipStream_t ss = s;
+    if (side) {
+      if ((r = hipEventRecord(fork, s)) != hipSuccess) return r;
+      if ((r = hipStreamWaitEvent(side, fork, 0)) != hipSuccess) return r;
+      ss = side;
+    }
+    if ((r = gemv_tokens(q.gate_sh, w.gate_sh, n_sh, n_embd, x, g, T, w.q6_gate_sh, ss)) != hipSuccess) return r;
+    if ((r = gemv_tokens(q.up_sh, w.up_sh, n_sh, n_embd, x, u, T, w.q6_up_sh, ss)) != hipSuccess) return r;
+    hipLaunchKernelGGL(silu_mul_kernel, blocks(nh), dim3(256), 0, ss, g, u, h, nh);
+    if ((r = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, ss)) != hipSuccess) return r;
+    if ((r = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, ss)) != hipSuccess) return r;
+    if (side && (r = hipEventRecord(join, side)) != hipSuccess) return r;
+    // route: router . bf16(x), then the routed experts into out
+    hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);
+    if ((r = gemv_tokens(q.router, w.router, E, n_embd, xb, logits, T, w.q6_router, s)) != hipSuccess) return r;
+    if ((r = launch_moe(m, q.gate, q.up, q.down, w.gate, w.up, w.down, w.q6_gate, w.q6_up, w.q6_down, logits, x,
+                        out, workspace, s)) != hipSuccess)
+      return r;
+    if (side && (r = hipStreamWaitEvent(s, join, 0)) != hipSuccess) return r;
+    hipLaunchKernelGGL(shexp_add_kernel, blocks(nx), dim3(256), 0, s, out, d, sg, n_embd, nx);
+    return hipGetLastError();
+  };
+  e = run();
+  if (side) {
+    (void)hipEventDestroy(fork);
+    (void)hipEventDestroy(join);
+  }
+  return e;
 }
 
 }  // namespace sh

@@ -335,6 +335,49 @@ def test_moe_layer_dev_matches_host_path(backend):
     assert np.array_equal(out.cpu().numpy(), host)
 
 
+def test_moe_layer_graph_replays(backend):
+    """The layer forks its shared expert onto a second stream and joins it
+    back: captured in a HIP graph (two parallel branches), every replay, with
+    eager calls of other inputs between replays, equals the eager result."""
+    import torch
+    n_expert, n_embd, n_ff, n_sh, top_k, n_tok = 32, 512, 256, 256, 8, 3
+    say("moe layer graph")
+    q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 9000)
+    dev = torch.device("cuda:0")
+    td = [torch.from_numpy(a).to(dev) for a in t]
+    xs = [torch.from_numpy(S.normal_f32(9001 + i, n_tok * n_embd)).to(dev) for i in range(2)]
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+    nb = H.moe_layer_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, n_sh, q)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+
+    def call(x, stream):
+        H.moe_layer_dev([(qq, 0, a.data_ptr()) for qq, a in zip(q, td)], n_expert, n_embd, n_ff, n_sh, n_tok,
+                        top_k, x.data_ptr(), out.data_ptr(), ws.data_ptr(), nb, stream)
+
+    eager = []
+    for x in xs:
+        call(x, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        eager.append(out.cpu().numpy().copy())
+    assert not np.array_equal(eager[0], eager[1])
+    s = torch.cuda.Stream(dev)
+    with torch.cuda.stream(s):
+        call(xs[0], s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call(xs[0], torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[0]), rep
+        call(xs[1], torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[1]), rep
+
+
 def test_moe_layer_errors(backend):
     say("moe layer errors")
     n_expert, n_embd, n_ff, n_sh = 8, 256, 256, 256
