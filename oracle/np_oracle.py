@@ -6,13 +6,13 @@ than from the block loops, so a slip in one of the two (a swapped nibble, a
 wrong scale index, a fused multiply-add) shows up as a mismatch.
 
 References: crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :208-234 (Q6_K),
-:237-270 (Q4_K); crates/strata-core/src/ops.rs:14-28 (gemv).
+:237-270 (Q4_K), :272-302 (Q5_K); crates/strata-core/src/ops.rs:14-28 (gemv).
 """
 from __future__ import annotations
 
 import numpy as np
 
-F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
 
 
 def _f16(b: np.ndarray) -> np.ndarray:
@@ -65,6 +65,29 @@ def q4_k(data: np.ndarray) -> np.ndarray:
     return (prod - mm).astype(np.float32).reshape(n * 256)
 
 
+def q5_k(data: np.ndarray) -> np.ndarray:
+    b = data.reshape(-1, 176)
+    n = b.shape[0]
+    d = _f16(b[:, 0:2])
+    dmin = _f16(b[:, 2:4])
+    s, m = _k4_scales(b[:, 4:16])
+    qh = b[:, 16:48]
+    qs = b[:, 48:176]
+    # element i: sub-block i // 32; its nibble as Q4_K's; its fifth bit is
+    # bit (i // 32) of qh[i % 32] (sub-block k reads bit k).
+    i = np.arange(256)
+    byte = 32 * (i // 64) + (i % 32)
+    hi = (i % 64) >= 32
+    nib = np.where(hi[None, :], qs[:, byte] >> 4, qs[:, byte] & 0x0F)
+    fifth = (qh[:, i % 32] >> (i // 32)) & 1
+    q = (nib + 16 * fifth).astype(np.float32)
+    sub = i // 32
+    dsc = (d[:, None] * s[:, sub].astype(np.float32)).astype(np.float32)
+    mm = (dmin[:, None] * m[:, sub].astype(np.float32)).astype(np.float32)
+    prod = (dsc * q).astype(np.float32)
+    return (prod - mm).astype(np.float32).reshape(n * 256)
+
+
 def q6_k(data: np.ndarray, signed_scales: bool = False) -> np.ndarray:
     b = data.reshape(-1, 210)
     n = b.shape[0]
@@ -91,6 +114,8 @@ def dequantize(quant: int, data: np.ndarray, rows: int, cols: int,
         flat = q8_0(data)
     elif quant == Q4_K:
         flat = q4_k(data)
+    elif quant == Q5_K:
+        flat = q5_k(data)
     elif quant == Q6_K:
         flat = q6_k(data, signed_q6k_scales)
     elif quant == F32:

@@ -101,6 +101,7 @@ int64_t sho_block_size(uint32_t quant) {
     case SHO_Q8_0:
       return 32;
     case SHO_Q4_K:
+    case SHO_Q5_K:
     case SHO_Q6_K:
       return 256;
     default:
@@ -119,6 +120,8 @@ int64_t sho_type_size(uint32_t quant) {
       return 34;
     case SHO_Q4_K:
       return 144;
+    case SHO_Q5_K:
+      return 176;
     case SHO_Q6_K:
       return 210;
     default:
@@ -180,6 +183,37 @@ static void dq_q4_k(const uint8_t* b, float* out) {
   }
 }
 
+/* dequant.rs:272-302. As Q4_K with a fifth bit: group g's low-nibble half
+ * takes bit 2g of qh[l], its high-nibble half bit 2g + 1; the code q + 16h
+ * (exact in f32) is scaled by d1 and m1 subtracted, two roundings. */
+static void dq_q5_k(const uint8_t* b, float* out) {
+  float d = sho_f16_to_f32(rd16(b));
+  float mn = sho_f16_to_f32(rd16(b + 2));
+  const uint8_t* scales = b + 4;
+  const uint8_t* qh = b + 16;
+  const uint8_t* ql = b + 48;
+  for (int grp = 0; grp < 4; ++grp) {
+    uint8_t sc, m;
+    sho_get_scale_min_k4(2 * grp, scales, &sc, &m);
+    float d1 = d * (float)sc;
+    float m1 = mn * (float)m;
+    sho_get_scale_min_k4(2 * grp + 1, scales, &sc, &m);
+    float d2 = d * (float)sc;
+    float m2 = mn * (float)m;
+    const uint8_t u1 = (uint8_t)(1u << (2 * grp)), u2 = (uint8_t)(2u << (2 * grp));
+    const uint8_t* qq = ql + 32 * grp;
+    float* o = out + 64 * grp;
+    for (int l = 0; l < 32; ++l) {
+      float c1 = (float)(qq[l] & 0x0F) + ((qh[l] & u1) ? 16.0f : 0.0f);
+      float p1 = d1 * c1;
+      o[l] = p1 - m1;
+      float c2 = (float)(qq[l] >> 4) + ((qh[l] & u2) ? 16.0f : 0.0f);
+      float p2 = d2 * c2;
+      o[32 + l] = p2 - m2;
+    }
+  }
+}
+
 /* dequant.rs:208-234. Two halves of 128 elements; q = 6-bit code - 32 and
  * out = (d * sc) * q. The reference reads sc as u8 (F4); SHO_Q6K_SCALE_I8
  * gives ggml's int8_t reading for comparison. */
@@ -235,6 +269,9 @@ static int dq_block(uint32_t quant, const uint8_t* b, float* out, int q6_mode) {
       return SHO_OK;
     case SHO_Q4_K:
       dq_q4_k(b, out);
+      return SHO_OK;
+    case SHO_Q5_K:
+      dq_q5_k(b, out);
       return SHO_OK;
     case SHO_Q6_K:
       dq_q6_k(b, out, q6_mode);

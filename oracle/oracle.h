@@ -7,7 +7,7 @@
  *
  * It restates, in plain C, the reference's scalar CPU path:
  *   - block geometry          crates/strata-gguf/src/quant.rs:125-181
- *   - f16 -> f32, row dequant crates/strata-gguf/src/dequant.rs:28-61,123-128,208-270
+ *   - f16 -> f32, row dequant crates/strata-gguf/src/dequant.rs:28-61,123-128,208-302
  *   - gemv / expert_gemv      crates/strata-core/src/ops.rs:14-28,169-195
  *   - silu                    crates/strata-core/src/ops.rs:85-87
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
@@ -38,6 +38,7 @@ enum {
   SHO_F16 = 1,
   SHO_Q8_0 = 8,
   SHO_Q4_K = 12,
+  SHO_Q5_K = 13,
   SHO_Q6_K = 14,
   SHO_BF16 = 30,
 };

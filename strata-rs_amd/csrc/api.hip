@@ -180,12 +180,13 @@ int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uin
 
 // Shape checks shared by the matrix entry points; mirrors what the
 // reference asserts (ops.rs:15-17) or reports (dequant.rs:50-55).
-// `plain_ok`: the entry point also takes F32 / F16 / BF16 (the matvec ones).
+// `matvec`: the entry point runs on the matvec kernels, which also take
+// F32 / F16 / BF16 and Q5_K.
 int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert, uint64_t nbytes,
-                 bool plain_ok = false) {
+                 bool matvec = false) {
   sh::Geometry g = sh::geometry(quant);
   if (g.block == 0) return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u is not supported", quant);
-  if (!sh::device_quant(quant) && !(plain_ok && sh::plain_quant(quant)))
+  if (!sh::device_quant(quant) && !(matvec && (sh::plain_quant(quant) || sh::gemv_quant(quant))))
     return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u has no device kernel here", quant);
   if (cols % uint64_t(g.block) != 0)
     return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of %lld-element blocks",

@@ -4,6 +4,7 @@
 // (crates/strata-gguf/src/quant.rs:125-164):
 //   Q8_0  32 elements /  34 B: [d: f16][q: i8 x 32]
 //   Q4_K 256 elements / 144 B: [d: f16][dmin: f16][scales: 12 B][qs: 128 B]
+//   Q5_K 256 elements / 176 B: [d: f16][dmin: f16][scales: 12 B][qh: 32 B][qs: 128 B]
 //   Q6_K 256 elements / 210 B: [ql: 128 B][qh: 64 B][sc: 16 B][d: f16]
 #pragma once
 
@@ -17,6 +18,7 @@ enum QuantId : uint32_t {
   kF16 = 1,
   kQ8_0 = 8,
   kQ4_K = 12,
+  kQ5_K = 13,
   kQ6_K = 14,
   kBF16 = 30,
 };
@@ -34,6 +36,7 @@ inline Geometry geometry(uint32_t q) {
     case kBF16: return {1, 2};
     case kQ8_0: return {32, 34};
     case kQ4_K: return {256, 144};
+    case kQ5_K: return {256, 176};
     case kQ6_K: return {256, 210};
     default: return {0, 0};
   }
@@ -50,6 +53,9 @@ inline int64_t byte_size(uint32_t q, int64_t n) {
 inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ6_K; }
 // Plain-float element types: matvec (f64 sums) and dequant only.
 inline bool plain_quant(uint32_t q) { return q == kF32 || q == kF16 || q == kBF16; }
+// Types the matvec (and dequant) kernels take beyond device_quant: Q5_K has
+// a matvec of its own but no expert, MoE or matmul kernel.
+inline bool gemv_quant(uint32_t q) { return device_quant(q) || q == kQ5_K; }
 
 constexpr int kWave = 64;
 

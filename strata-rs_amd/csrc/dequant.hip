@@ -1,7 +1,7 @@
 // Bit-exact device dequantization: packed GGUF rows -> f32.
 //
-// Follows crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :208-234 (Q6_K)
-// and :237-270 (Q4_K) element for element, with the same rounding: every
+// Follows crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :208-234 (Q6_K),
+// :237-270 (Q4_K) and :272-302 (Q5_K) element for element, with the same rounding: every
 // product and difference is a separate f32 operation (contraction is off for
 // this file's arithmetic), f16 scales widen exactly.
 //
@@ -48,6 +48,27 @@ __device__ __forceinline__ float dq_q4_k(const uint8_t* blk, int j) {
   return p - m1;
 }
 
+// Q5_K element j: Q4_K's nibble plus 16 when bit `sub` of qh[j % 32] is set
+// (sub-block sub = j / 32 reads bit sub: 2*grp for the low nibbles, 2*grp + 1
+// for the high ones, dequant.rs:285-297). q + 16 is exact; then one product
+// and one difference, each rounded.
+__device__ __forceinline__ float dq_q5_k(const uint8_t* blk, int j) {
+#pragma clang fp contract(off)
+  float d = h2f(rd16(blk));
+  float mn = h2f(rd16(blk + 2));
+  int grp = j >> 6, k = j & 63;
+  int sub = 2 * grp + (k >> 5);
+  uint32_t sc, m;
+  scale_min_k4(sub, blk + 4, sc, m);
+  float d1 = d * static_cast<float>(sc);
+  float m1 = mn * static_cast<float>(m);
+  uint32_t byte = blk[48 + 32 * grp + (k & 31)];
+  uint32_t q = (k < 32) ? (byte & 0x0Fu) : (byte >> 4);
+  uint32_t h = (uint32_t(blk[16 + (k & 31)]) >> sub) & 1u;
+  float p = d1 * static_cast<float>(q + 16u * h);
+  return p - m1;
+}
+
 // Q6_K element j: half h, quarter t, lane l of dequant.rs:217-229.
 __device__ __forceinline__ float dq_q6_k(const uint8_t* blk, int j, int signed_scales) {
 #pragma clang fp contract(off)
@@ -75,6 +96,7 @@ __global__ void dequant_kernel(uint32_t quant, const uint8_t* __restrict__ w, in
     switch (quant) {
       case kQ8_0: v = dq_q8_0(row + (c >> 5) * 34, int(c & 31)); break;
       case kQ4_K: v = dq_q4_k(row + (c >> 8) * 144, int(c & 255)); break;
+      case kQ5_K: v = dq_q5_k(row + (c >> 8) * 176, int(c & 255)); break;
       case kQ6_K: v = dq_q6_k(row + (c >> 8) * 210, int(c & 255), q6_signed); break;
       case kF16: v = h2f(rd16(row + 2 * c)); break;
       case kBF16: v = __builtin_bit_cast(float, rd16(row + 2 * c) << 16); break;

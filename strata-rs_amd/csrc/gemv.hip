@@ -1,11 +1,12 @@
-// Fused dequant + matvec for Q8_0, Q4_K and Q6_K rows, read packed from HBM.
+// Fused dequant + matvec for Q8_0, Q4_K, Q5_K and Q6_K rows, read packed from
+// HBM.
 //
 // Semantics: crates/strata-core/src/ops.rs:14-28 (`gemv`): y[r] = sum_c
 // W[r][c] * x[c] with W[r][c] the strata-gguf dequantized value
-// (crates/strata-gguf/src/dequant.rs:123-128, :208-234, :237-270). The sum is
+// (crates/strata-gguf/src/dequant.rs:123-128, :208-234, :237-302). The sum is
 // formed in f32 in a different order from the reference's sequential f64
 // loop, and per-block scales are factored out:
-//   Q4_K  sum_sub (d*sc) * sum(q*x) - (dmin*m) * sum(x)
+//   Q4_K  sum_sub (d*sc) * sum(q*x) - (dmin*m) * sum(x)   (Q5_K alike, q 0..31)
 //   Q8_0  sum_blk  d * (sum((q+128)*x) - 128 * sum(x))
 //   Q6_K  sum_16   d*sc * (sum(q6*x) - 32 * sum(x))
 // so the outputs agree with the reference to f32 rounding, not bit for bit.
@@ -110,6 +111,71 @@ struct FmtQ4K {
     }
     const float x0 = x.s.x + x.s.y, x1 = x.s.z + x.s.w;
     const float qsum = ubyte<0>(scp) * (lo0 + lo1) + (ubyte<1>(scp) * 0.0625f) * (hi0 + hi1);
+    const float msum = ubyte<0>(mp) * x0 + ubyte<1>(mp) * x1;
+    return d * qsum - dm * msum;
+  }
+};
+
+// ------------------------------------------------------------------ Q5_K --
+// Unit u of a row: super-block u/4, group g = u%4, as FmtQ4K; each code also
+// takes a fifth bit from qh[l] (l = element % 32): bit 2g for the low-nibble
+// sub-block 2g, bit 2g+1 for the high-nibble sub-block 2g+1 (dequant.rs:
+// 285-297), so codes run 0..31. Every lane of a super-block reads its 16
+// header and 32 qh bytes.
+__device__ __forceinline__ void q5k_codes(uint32_t q, uint32_t qh, uint32_t g, uint32_t& lo, uint32_t& hi) {
+  const uint32_t t = qh >> (2u * g);  // bit 2g of byte j at bit 8j, bit 2g+1 at 8j+1
+  lo = (q & 0x0F0F0F0Fu) | ((t << 4) & 0x10101010u);
+  hi = ((q >> 4) & 0x0F0F0F0Fu) | ((t << 3) & 0x10101010u);
+}
+
+// (scale, min) of sub-blocks 2g and 2g+1 in the two low bytes of scp / mp,
+// from the 12 packed bytes in words h.y, h.z, h.w (dequant.rs:237-245).
+__device__ __forceinline__ void k4_pair(u32x4 h, int g, uint32_t& scp, uint32_t& mp) {
+  const uint32_t sh = (g & 1) << 4;
+  const uint32_t t1 = h.y >> sh, t2 = h.z >> sh, t3 = h.w >> sh;
+  scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+  mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
+}
+
+struct FmtQ5K {
+  static constexpr int kR = 2;
+  static constexpr int kRing = 4;
+  struct Load {
+    u32x4 h, h0, h1, a, b;
+  };
+  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
+    const uint8_t* sb = row + (u >> 2) * 176;
+    const int g = u & 3;
+    o.h = ld16(sb);
+    o.h0 = ld16(sb + 16);
+    o.h1 = ld16(sb + 32);
+    o.a = ld16(sb + 48 + 32 * g);
+    o.b = ld16(sb + 64 + 32 * g);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int u, int) {
+    const int g = u & 3;
+    uint32_t scp, mp;
+    k4_pair(L.h, g, scp, mp);
+    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
+    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
+    const uint32_t qh[8] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w};
+    float lo0 = 0.f, lo1 = 0.f, hi0 = 0.f, hi1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t lo, hi;
+      q5k_codes(q[k], qh[k], uint32_t(g), lo, hi);
+      const f32x4 xl = x.v[k], xh = x.v[8 + k];
+      lo0 = __builtin_fmaf(ubyte<0>(lo), xl.x, lo0);
+      lo1 = __builtin_fmaf(ubyte<1>(lo), xl.y, lo1);
+      lo0 = __builtin_fmaf(ubyte<2>(lo), xl.z, lo0);
+      lo1 = __builtin_fmaf(ubyte<3>(lo), xl.w, lo1);
+      hi0 = __builtin_fmaf(ubyte<0>(hi), xh.x, hi0);
+      hi1 = __builtin_fmaf(ubyte<1>(hi), xh.y, hi1);
+      hi0 = __builtin_fmaf(ubyte<2>(hi), xh.z, hi0);
+      hi1 = __builtin_fmaf(ubyte<3>(hi), xh.w, hi1);
+    }
+    const float x0 = x.s.x + x.s.y, x1 = x.s.z + x.s.w;
+    const float qsum = ubyte<0>(scp) * (lo0 + lo1) + ubyte<1>(scp) * (hi0 + hi1);
     const float msum = ubyte<0>(mp) * x0 + ubyte<1>(mp) * x1;
     return d * qsum - dm * msum;
   }
@@ -663,6 +729,48 @@ struct LimbQ4K {
   }
 };
 
+// Q5_K with integer dots: unit u as LimbQ4K; codes 0..31 (nibble plus the
+// fifth bit, q5k_codes) go into the dots unchanged.
+struct LimbQ5K {
+  struct Load {
+    u32x4 h, h0, h1, a, b;
+  };
+  static constexpr int kWinBytes = 16 * 176;
+  struct Off {
+    int h, q;
+  };
+  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 176, 48 + 32 * (u & 3)}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    L.h = ld16(row + o.h);
+    L.h0 = ld16(row + o.h + 16);
+    L.h1 = ld16(row + o.h + 32);
+    L.a = ld16(row + o.h + o.q);
+    L.b = ld16(row + o.h + o.q + 16);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
+    const int g = lane & 3;
+    uint32_t scp, mp;
+    k4_pair(L.h, g, scp, mp);
+    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
+    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
+    const uint32_t qh[8] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w};
+    int a0 = 0, a1 = 0;
+    uint32_t b0 = 0, b1 = 0, c0 = 0, c1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t lo, hi;
+      q5k_codes(q[k], qh[k], uint32_t(g), lo, hi);
+      dot_limbs(lo, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), a0, b0, c0);
+      dot_limbs(hi, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), a1, b1, c1);
+    }
+    const float s0 = limb_value(a0, b0, c0) * fw(x.i0.z);
+    const float s1 = limb_value(a1, b1, c1) * fw(x.i1.z);
+    const float qsum = ubyte<0>(scp) * s0 + ubyte<1>(scp) * s1;
+    const float msum = ubyte<0>(mp) * (fw(x.i0.x) + fw(x.i0.y)) + ubyte<1>(mp) * (fw(x.i1.x) + fw(x.i1.y));
+    return d * qsum - dm * msum;
+  }
+};
+
 // Q8_0 with integer dots: unit u = blocks 2u and 2u+1 (68 bytes from a
 // dword-aligned address). Codes are signed: the top limb (signed) takes them
 // as they are; against the unsigned low limbs they are biased to q + 128 and
@@ -982,7 +1090,7 @@ static size_t lds_bytes(int cols, int nb) { return size_t(nb) * x_stride(cols) *
 bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
   if (rows <= 0 || cols <= 0 || batch < 1 || batch > 8) return false;
   if (plain_quant(quant)) return rows <= (int64_t(1) << 31) - 1 && cols <= (int64_t(1) << 30);
-  if (!device_quant(quant)) return false;
+  if (!gemv_quant(quant)) return false;
   if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 20)) return false;
   if (cols % 64 != 0) return false;  // 64-column lane units (Q8_0 blocks in pairs)
   if (cols % geometry(quant).block != 0) return false;
@@ -1101,6 +1209,10 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
       case kQ8_0:
         e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
                     : launch_nb<FmtQ8>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
+        break;
+      case kQ5_K:
+        e = nb == 1 ? launch_limb<LimbQ5K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
+                    : launch_nb<FmtQ5K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       default:
         e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,

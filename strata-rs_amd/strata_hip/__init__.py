@@ -65,6 +65,7 @@ class QuantType(enum.IntEnum):
     F16 = 1
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
     BF16 = 30
 

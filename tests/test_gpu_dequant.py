@@ -44,7 +44,7 @@ def test_every_f16_scale_pattern(backend, oracle):
 
 
 @pytest.mark.parametrize("quant,cols", [(8, 4096), (12, 4096), (12, 12288), (14, 4096), (12, 768),
-                                        (14, 2048)])
+                                        (14, 2048), (13, 4096), (13, 768)])
 def test_random_rows_bit_exact(backend, oracle, quant, cols):
     say("dequant random rows", quant, cols)
     rows = 16

@@ -3,7 +3,7 @@
 Tolerance: max|y - ref| / max|ref| <= 1e-3 (the path's stated bound under
 f32 accumulation); the per-element error with a floor of rms(ref) is also
 held to 1e-3. Covers the reference's own gemv unit test, ragged row counts,
-one- and multi-window rows, batches 1..8, the Q6_K scale readings, the
+one- and multi-window rows, batches 1..8 (Q5_K too), the Q6_K scale readings, the
 configs' full shapes (the lm_head on a row sample) and the device-pointer
 entry point.
 """
@@ -46,6 +46,7 @@ def test_reference_q8_0_unit_case(backend):
     (12, 37, 256), (12, 1, 4096), (12, 129, 4096), (12, 64, 12288), (12, 33, 8192 + 256),
     (8, 37, 64), (8, 129, 4096), (8, 17, 4160), (8, 5, 12288),
     (14, 37, 256), (14, 129, 4096), (14, 9, 12288), (14, 3, 2048 + 256),
+    (13, 37, 256), (13, 129, 4096), (13, 9, 12288), (13, 3, 2048 + 256), (13, 4096, 4096),
 ])
 def test_gemv_shapes(backend, oracle, quant, rows, cols):
     say("gemv", quant, rows, cols)
@@ -87,7 +88,8 @@ def test_lm_head_q6_k_full_shape(backend, oracle, signed):
     backend.evict("lm_head" + ("_i8" if signed else ""))
 
 
-@pytest.mark.parametrize("quant,cols", [(12, 4096), (12, 12288), (8, 4096), (14, 4096)])
+@pytest.mark.parametrize("quant,cols", [(12, 4096), (12, 12288), (8, 4096), (14, 4096), (13, 4096),
+                                        (13, 12288)])
 @pytest.mark.parametrize("batch", [1, 2, 3, 8])
 def test_gemv_batch(backend, oracle, quant, cols, batch):
     rows = 96
@@ -146,6 +148,18 @@ def test_gemv_shape_errors(backend):
     with pytest.raises(H.UnsupportedQuantError):
         q4_0 = np.zeros(4 * 18, np.uint8)  # Q4_0: not on this path
         backend.gemv(H.QuantTensor("q4_0", 2, 4, 32, q4_0), np.zeros(32, np.float32), np.zeros(4, np.float32))
+
+
+def test_q5_k_is_matvec_only(backend):
+    """Q5_K rows run on the matvec (and dequant) kernels only: the expert,
+    MoE and matmul entry points report the type as unsupported."""
+    say("Q5_K outside the matvec")
+    w = S.matrix(13, 3, 2 * 256, 256)
+    with pytest.raises(H.UnsupportedQuantError):
+        backend.expert_gemv(H.ExpertView("q5e", 13, 2, 256, 256, w), 1, np.zeros(256, np.float32),
+                            np.zeros(256, np.float32))
+    with pytest.raises(H.UnsupportedQuantError):
+        backend.matmul(H.QuantTensor("q5m", 13, 512, 256, w), np.zeros((4, 256), np.float32))
 
 
 def test_gemv_empty_shapes(backend):

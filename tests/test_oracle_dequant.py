@@ -5,6 +5,8 @@
   :161-169 Q6_K) and its "finite values" fill (:187-244);
 * hand-derived Q4_K known answers (the reference has none) covering the
   direct (j < 4) and split (j >= 4) 6-bit scale packings;
+* hand-derived Q5_K known answers (none in the reference either) for the
+  fifth bit of every sub-block;
 * hand-derived negative Q6_K scales, u8 (reference) vs i8 (ggml) reading;
 * an encoder round trip for get_scale_min_k4 over every (j, sc, m);
 * the exhaustive binary16 -> binary32 table against numpy;
@@ -65,7 +67,7 @@ def _lcg_block(nbytes):
     return out
 
 
-@pytest.mark.parametrize("quant,elems", [(8, 32), (12, 256), (14, 256)])
+@pytest.mark.parametrize("quant,elems", [(8, 32), (12, 256), (13, 256), (14, 256)])
 def test_every_type_decodes_finite(oracle, quant, elems):
     # dequant_tests.rs:187-244 with its fill and its f16 0.125 at bytes 0..1
     b = _lcg_block(oracle.byte_size(quant, elems))
@@ -118,6 +120,48 @@ def test_q4_k_split_scales_last_subblock(oracle):
     qs[127] = 0xF0  # element 255 = group 3, high nibble 15
     out = oracle.dequantize_row(oracle.Q4_K, q4k_block(2.0, 0.25, sc, qs), 256)
     assert out[255] == 554.25   # (2*19)*15 - 0.25*63
+    assert out[224] == -15.75   # same sub-block, q = 0
+
+
+# ---- hand-derived Q5_K known answers ------------------------------------------
+
+def q5k_block(d, dmin, scales, qh, qs):
+    b = np.zeros(176, np.uint8)
+    b[0:2] = f16b(d)
+    b[2:4] = f16b(dmin)
+    b[4:16] = scales
+    b[16:48] = qh
+    b[48:176] = qs
+    return b
+
+
+def test_q5_k_fifth_bit_per_subblock(oracle):
+    """Sub-block k (elements 32k .. 32k+31) takes bit k of qh[l]: with scale
+    1 and min 0 everywhere and every nibble 0, element 32k + l is 16 exactly
+    when bit k of qh[l] is set."""
+    sc = encode_scale_min_k4([1] * 8, [0] * 8)
+    qh = np.zeros(32, np.uint8)
+    qh[3] = 0b00000101      # sub-blocks 0 and 2 at l = 3
+    qh[31] = 0b10000010     # sub-blocks 1 and 7 at l = 31
+    out = oracle.dequantize_row(oracle.Q5_K, q5k_block(1.0, 0.0, sc, qh, np.zeros(128, np.uint8)), 256)
+    want = np.zeros(256, np.float32)
+    want[[3, 64 + 3, 32 + 31, 224 + 31]] = 16.0
+    assert np.array_equal(out, want)
+
+
+def test_q5_k_nibbles_scales_and_mins(oracle):
+    sc = encode_scale_min_k4([3, 5, 0, 0, 0, 0, 0, 19], [2, 1, 0, 0, 0, 0, 0, 63])
+    qh = np.zeros(32, np.uint8)
+    qh[0] = 0x03            # element 0 and element 32 get +16
+    qh[31] = 0x80           # element 255 gets +16
+    qs = np.zeros(128, np.uint8)
+    qs[0] = 0x5A            # element 0: low nibble 10; element 32: high nibble 5
+    qs[127] = 0xF0          # element 255: high nibble 15, element 223: 0
+    out = oracle.dequantize_row(oracle.Q5_K, q5k_block(2.0, 0.25, sc, qh, qs), 256)
+    assert out[0] == 155.5      # (2*3)*(10+16) - 0.25*2
+    assert out[1] == -0.5       # (2*3)*0 - 0.5
+    assert out[32] == 209.75    # (2*5)*(5+16) - 0.25*1
+    assert out[255] == 1162.25  # (2*19)*(15+16) - 0.25*63
     assert out[224] == -15.75   # same sub-block, q = 0
 
 
@@ -233,6 +277,7 @@ def test_geometry_constants(oracle):
     # quant.rs:125-164; a 4096x4096 Q8_0 tensor is 17,825,792 bytes
     assert (oracle.block_size(8), oracle.type_size(8)) == (32, 34)
     assert (oracle.block_size(12), oracle.type_size(12)) == (256, 144)
+    assert (oracle.block_size(13), oracle.type_size(13)) == (256, 176)
     assert (oracle.block_size(14), oracle.type_size(14)) == (256, 210)
     assert oracle.byte_size(8, 4096 * 4096) == 17_825_792
     assert oracle.byte_size(12, 4096 * 12288) == 28_311_552
@@ -249,7 +294,7 @@ def test_truncated_rows(oracle):
 
 # ---- the independent numpy restatement --------------------------------------
 
-@pytest.mark.parametrize("quant", [8, 12, 14])
+@pytest.mark.parametrize("quant", [8, 12, 13, 14])
 def test_oracle_matches_numpy_restatement(oracle, quant):
     cols = 1024
     rows = 64
@@ -278,6 +323,25 @@ def test_q4_k_products_are_exact(oracle):
             sc, m = oracle.get_scale_min_k4(sub, blk[4:16])
             byte = blk[16 + 32 * (j // 64) + (k % 32)]
             q = (byte & 0xF) if k < 32 else (byte >> 4)
+            want[j] = d * sc * q - dm * m          # exact in f64
+        assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_q5_k_products_are_exact(oracle):
+    """As Q4_K: d1*q has at most 11 + 6 + 5 significant bits, exact in f32,
+    so d1*q - m1 is one rounding of the exact value."""
+    for seed in range(50):
+        blk = S.q5_k_blocks(1500 + seed, 1)
+        out = oracle.dequantize_row(oracle.Q5_K, blk, 256)
+        d = np.float64(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+        dm = np.float64(np.frombuffer(blk[2:4].tobytes(), np.float16)[0])
+        want = np.empty(256)
+        for j in range(256):
+            sub, k = j // 32, j % 64
+            sc, m = oracle.get_scale_min_k4(sub, blk[4:16])
+            byte = blk[48 + 32 * (j // 64) + (k % 32)]
+            q = (byte & 0xF) if k < 32 else (byte >> 4)
+            q += 16 * ((blk[16 + j % 32] >> sub) & 1)
             want[j] = d * sc * q - dm * m          # exact in f64
         assert np.array_equal(out, want.astype(np.float32))
 
