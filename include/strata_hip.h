@@ -4,9 +4,10 @@
  *
  * The library replaces the matvec/matmul half of strata-core's
  * `trait ComputeBackend` (crates/strata-core/src/backend.rs:20-51) for the
- * GGUF types Q8_0, Q4_K and Q6_K (and F32 / F16 / BF16 for the plain matvec
- * and dequant, the types router and gate tensors use). Weights stay packed in
- * device memory in their GGUF block layout; kernels dequantize in registers.
+ * GGUF types Q8_0, Q4_K and Q6_K (and, for the matvec and dequant only,
+ * Q5_K and F32 / F16 / BF16, the types router and gate tensors use).
+ * Weights stay packed in device memory in their GGUF block layout; kernels
+ * dequantize in registers.
  *
  * Conventions
  *  - Every function returns int: SH_OK (0) or a negative SH_ERR_* code, and
@@ -58,6 +59,7 @@ extern "C" {
 #define SH_QUANT_F16 1u
 #define SH_QUANT_Q8_0 8u
 #define SH_QUANT_Q4_K 12u
+#define SH_QUANT_Q5_K 13u /* matvec and dequant only */
 #define SH_QUANT_Q6_K 14u
 #define SH_QUANT_BF16 30u
 
@@ -99,6 +101,14 @@ typedef struct sh_expert_view {
   uint64_t nbytes;
 } sh_expert_view;
 
+/* RopeCfg (crates/strata-core/src/backend.rs:158-167). */
+typedef struct sh_rope_cfg {
+  uint64_t pos;      /* token position */
+  uint64_t n_rot;    /* leading head dims rotated (NEOX pairs) */
+  uint64_t head_dim; /* stride between heads */
+  double freq_base;  /* theta */
+} sh_rope_cfg;
+
 /* ---- library and context ----------------------------------------------- */
 int sh_abi_version(void);
 /* Message for the last failure on this thread ("" if none). */
@@ -123,8 +133,8 @@ int sh_evict(sh_context* ctx, uint64_t key);
 
 /* ComputeBackend::gemv (backend.rs:25), semantics of ops::gemv
  * (crates/strata-core/src/ops.rs:14-28): y[r] = sum_c W[r][c] * x[c].
- * x_len must equal cols and y_len rows. Q8_0 / Q4_K / Q6_K, and F32 / F16 /
- * BF16 (products and sums in f64, as ops::gemv does). */
+ * x_len must equal cols and y_len rows. Q8_0 / Q4_K / Q5_K / Q6_K, and F32 /
+ * F16 / BF16 (products and sums in f64, as ops::gemv does). */
 int sh_gemv(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint64_t x_len, float* y,
             uint64_t y_len);
 
@@ -139,6 +149,24 @@ int sh_gemv_batch(sh_context* ctx, const sh_quant_tensor* w, const float* x, flo
  * x_len must equal rows and y_len cols; e < n_expert. */
 int sh_expert_gemv(sh_context* ctx, const sh_expert_view* w, uint64_t e, const float* x,
                    uint64_t x_len, float* y, uint64_t y_len);
+
+/* ---- the trait's elementwise methods (host slices, synchronous) -------
+ * ComputeBackend::{rms_norm, rope_neox, softmax, l2_norm, add}
+ * (backend.rs:38-50) with the CPU bodies' arithmetic (ops.rs:46-165): f64
+ * sums and scales, one rounding to f32 per output as the Rust source. The
+ * sums run in a different order and expf / pow / sin / cos are the device
+ * library's, so outputs agree with the CPU backend to within an ulp. */
+
+/* ops::rms_norm (ops.rs:46-56): x = x * w / sqrt(mean(x^2) + eps), in place. */
+int sh_rms_norm(sh_context* ctx, float* x, const float* w, uint64_t n, double eps);
+/* ops::rope_neox (ops.rs:120-135) on one head of n floats, in place. */
+int sh_rope_neox(sh_context* ctx, float* head, uint64_t n, const sh_rope_cfg* cfg);
+/* ops::softmax (ops.rs:105-116), in place. */
+int sh_softmax(sh_context* ctx, float* xs, uint64_t n);
+/* ops::l2_norm (ops.rs:73-82), in place. */
+int sh_l2_norm(sh_context* ctx, float* head, uint64_t n, double eps);
+/* ops::add_into (ops.rs:161-165): a += b. */
+int sh_add(sh_context* ctx, float* a, const float* b, uint64_t n);
 
 /* dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device:
  * `n` f32 values from `nbytes` packed bytes, bit-exact. SH_ERR_TRUNCATED
@@ -171,8 +199,8 @@ int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view
  * out += sigmoid(gate_inp_shexp . x) * down_shexp . (silu(gate_shexp . x) *
  * (up_shexp . x)) (moe.rs:129-142). router [n_expert][n_embd], gate/up_shexp
  * [n_ff_shexp][n_embd], down_shexp [n_embd][n_ff_shexp], gate_inp_shexp
- * [1][n_embd] are ops::gemv matrices of any matvec type (F32 / F16 / BF16
- * included); the expert views as in sh_moe_ffn. n_ff_shexp must be a
+ * [1][n_embd] are ops::gemv matrices of any matvec type (Q5_K and F32 /
+ * F16 / BF16 included); the expert views as in sh_moe_ffn. n_ff_shexp must be a
  * multiple of 4. The weight budget must hold the eight tensors at once. */
 int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert_view* gate,
                  const sh_expert_view* up, const sh_expert_view* down, const sh_quant_tensor* gate_shexp,
@@ -257,6 +285,21 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
  * aligned (4 for Q8_0 and F32), x 16-byte aligned. */
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream);
+
+/* The elementwise methods batched over rows, on device pointers: the same
+ * arithmetic per row as the host-slice forms; enqueued on `stream`.
+ * rms_norm: x, out [rows][n] (out may equal x), w [n]. */
+int sh_rms_norm_dev(const float* x, const float* w, float* out, uint64_t rows, uint64_t n, double eps,
+                    void* stream);
+/* l2_norm and softmax of each row of x [rows][n], in place. */
+int sh_l2_norm_dev(float* x, uint64_t rows, uint64_t n, double eps, void* stream);
+int sh_softmax_dev(float* x, uint64_t rows, uint64_t n, void* stream);
+/* rope_neox of `rows` heads of cfg->head_dim floats (x [rows][head_dim]);
+ * head r is at position cfg->pos + r / heads_per_pos (heads_per_pos = the
+ * heads of one token, so a prefill batch of consecutive tokens is one call). */
+int sh_rope_neox_dev(float* x, uint64_t rows, uint64_t heads_per_pos, const sh_rope_cfg* cfg, void* stream);
+/* a[i] += b[i], i < n. */
+int sh_add_dev(float* a, const float* b, uint64_t n, void* stream);
 
 #ifdef __cplusplus
 }

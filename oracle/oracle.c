@@ -614,3 +614,67 @@ int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,
   }
   return SHO_OK;
 }
+
+/* ---- the trait's elementwise methods (backend.rs:38-50, ops.rs:46-165) --
+ * f64 where the reference works in f64; the sums run in its sequential
+ * order. pow / sin / cos are the C library's, as Rust's f64::powf and
+ * f64::sin_cos call the platform libm. */
+
+/* ops.rs:46-69 (rms_norm, rms_norm_into): ss = sum v*v (f64) / n,
+ * scale = 1 / sqrt(ss + eps), out[i] = (f32)((f64)x[i] * scale * (f64)w[i]).
+ * out may equal x. */
+void sho_rms_norm(const float* x, const float* w, size_t n, double eps, float* out) {
+  double ss = 0.0;
+  for (size_t i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+  ss /= (double)n;
+  const double scale = 1.0 / sqrt(ss + eps);
+  for (size_t i = 0; i < n; ++i) out[i] = (float)((double)x[i] * scale * (double)w[i]);
+}
+
+/* ops.rs:73-82: inv = 1 / sqrt(sum v*v + eps); v = (f32)((f64)v * inv). */
+void sho_l2_norm(float* head, size_t n, double eps) {
+  double ss = 0.0;
+  for (size_t i = 0; i < n; ++i) ss += (double)head[i] * (double)head[i];
+  const double inv = 1.0 / sqrt(ss + eps);
+  for (size_t i = 0; i < n; ++i) head[i] = (float)((double)head[i] * inv);
+}
+
+/* ops.rs:105-116: mx = max (f32, from -inf), v = expf(v - mx) in f32,
+ * sum in f64, inv = 1 / sum, v = (f32)((f64)v * inv). */
+void sho_softmax(float* xs, size_t n) {
+  float mx = -INFINITY;
+  for (size_t i = 0; i < n; ++i) mx = fmaxf(mx, xs[i]);
+  double sum = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    xs[i] = expf(xs[i] - mx);
+    sum += (double)xs[i];
+  }
+  const double inv = 1.0 / sum;
+  for (size_t i = 0; i < n; ++i) xs[i] = (float)((double)xs[i] * inv);
+}
+
+/* ops.rs:120-135: r = min(n_rot, head_dim, len) & ~1, half = r / 2; pair
+ * (i, i + half): theta = freq_base^(-2i / r), angle = theta * pos,
+ * a' = (f32)(a cos - b sin), b' = (f32)(a sin + b cos), all f64; dims from
+ * r on pass through. */
+void sho_rope_neox(float* head, size_t len, uint64_t pos, size_t n_rot, size_t head_dim,
+                   double freq_base) {
+  size_t r = n_rot < head_dim ? n_rot : head_dim;
+  if (len < r) r = len;
+  r &= ~(size_t)1;
+  const size_t half = r / 2;
+  const double p = (double)pos;
+  for (size_t i = 0; i < half; ++i) {
+    const double theta = pow(freq_base, -2.0 * (double)i / (double)r);
+    const double angle = theta * p;
+    const double s = sin(angle), c = cos(angle);
+    const double a = head[i], b = head[i + half];
+    head[i] = (float)(a * c - b * s);
+    head[i + half] = (float)(a * s + b * c);
+  }
+}
+
+/* ops.rs:161-165 (add_into): a[i] += b[i] in f32. */
+void sho_add(float* a, const float* b, size_t n) {
+  for (size_t i = 0; i < n; ++i) a[i] = a[i] + b[i];
+}

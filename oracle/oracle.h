@@ -13,6 +13,9 @@
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
  *   - the whole MoE layer     crates/strata-core/src/moe.rs:48-143 (router
  *                             matvec on bf16(x), shared expert, sigmoid gate)
+ *   - rms_norm, l2_norm, softmax, rope_neox, add
+ *                             crates/strata-core/src/ops.rs:46-165 (the
+ *                             trait's elementwise methods, backend.rs:38-50)
  *   - prefill matmul          no reference op: m independent ops::gemv calls
  *                             (crates/strata-core/src/generate.rs:116-117)
  *   - Q8 activation blocks    the quantization the int8 prefill mode applies
@@ -83,6 +86,14 @@ int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
 
 float sho_silu(float x);
 float sho_sigmoid(float x);
+
+/* the trait's elementwise methods, one row / head each */
+void sho_rms_norm(const float* x, const float* w, size_t n, double eps, float* out);
+void sho_l2_norm(float* head, size_t n, double eps);
+void sho_softmax(float* xs, size_t n);
+void sho_rope_neox(float* head, size_t len, uint64_t pos, size_t n_rot, size_t head_dim,
+                   double freq_base);
+void sho_add(float* a, const float* b, size_t n);
 
 int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
                   int64_t* ids, float* weights);

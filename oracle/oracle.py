@@ -66,6 +66,16 @@ def lib() -> C.CDLL:
         L.sho_matmul.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, C.c_int64, f32p,
                                  C.c_int]
         L.sho_quantize_q8.argtypes = [f32p, C.c_size_t, u8p, f32p, f32p]
+        L.sho_rms_norm.argtypes = [f32p, f32p, C.c_size_t, C.c_double, f32p]
+        L.sho_rms_norm.restype = None
+        L.sho_l2_norm.argtypes = [f32p, C.c_size_t, C.c_double]
+        L.sho_l2_norm.restype = None
+        L.sho_softmax.argtypes = [f32p, C.c_size_t]
+        L.sho_softmax.restype = None
+        L.sho_rope_neox.argtypes = [f32p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_size_t, C.c_double]
+        L.sho_rope_neox.restype = None
+        L.sho_add.argtypes = [f32p, f32p, C.c_size_t]
+        L.sho_add.restype = None
         _lib = L
     return _lib
 
@@ -193,6 +203,60 @@ def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, 
 
 def sigmoid(x: float) -> float:
     return lib().sho_sigmoid(x)
+
+
+# ---- the trait's elementwise methods (ops.rs:46-165), row by row -----------
+
+def _rows(x, n: int | None = None) -> np.ndarray:
+    v = np.array(x, dtype=np.float32, copy=True)
+    return v.reshape(-1, n if n is not None else v.shape[-1])
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """ops::rms_norm on each row of x ([rows][n]) with the weights w [n]."""
+    v = _rows(x)
+    wv = _f32(w)
+    assert wv.size == v.shape[1]
+    for r in range(v.shape[0]):
+        row = v[r]
+        lib().sho_rms_norm(_ptr(row), _ptr(wv), row.size, float(eps),
+                           _ptr(row))
+    return v.reshape(np.shape(x))
+
+
+def l2_norm(x, eps: float) -> np.ndarray:
+    """ops::l2_norm on each row (head) of x."""
+    v = _rows(x)
+    for r in range(v.shape[0]):
+        lib().sho_l2_norm(_ptr(v[r]), v.shape[1], float(eps))
+    return v.reshape(np.shape(x))
+
+
+def softmax(x) -> np.ndarray:
+    """ops::softmax on each row of x."""
+    v = _rows(x)
+    for r in range(v.shape[0]):
+        lib().sho_softmax(_ptr(v[r]), v.shape[1])
+    return v.reshape(np.shape(x))
+
+
+def rope_neox(x, pos: int, n_rot: int, head_dim: int, freq_base: float) -> np.ndarray:
+    """ops::rope_neox on each head_dim-long head of x (the whole buffer is
+    a run of heads, as the attention code passes them one at a time)."""
+    v = _rows(x, head_dim)
+    for r in range(v.shape[0]):
+        lib().sho_rope_neox(_ptr(v[r]), head_dim, int(pos), int(n_rot), int(head_dim),
+                            float(freq_base))
+    return v.reshape(np.shape(x))
+
+
+def add(a, b) -> np.ndarray:
+    """ops::add_into: a + b in f32."""
+    av = np.array(a, dtype=np.float32, copy=True).reshape(-1)
+    bv = _f32(b).reshape(-1)
+    assert av.size == bv.size
+    lib().sho_add(_ptr(av), _ptr(bv), av.size)
+    return av.reshape(np.shape(a))
 
 
 def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: int, x, top_k: int) -> np.ndarray:

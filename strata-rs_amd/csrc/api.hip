@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -834,5 +835,147 @@ int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales,
     return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (x and codes need 16 bytes)");
   HIP_TRY(sh::launch_quantize_q8(x, int64_t(n), codes, scales, code_sums, static_cast<hipStream_t>(stream)),
           "quantize launch");
+  return SH_OK;
+}
+
+// ---- the trait's elementwise methods ----------------------------------------
+
+namespace {
+
+int rowops_check(uint64_t rows, uint64_t n) {
+  if (!sh::rowops_shape_ok(int64_t(rows > (uint64_t(1) << 62) ? (uint64_t(1) << 62) : rows),
+                           int64_t(n > (uint64_t(1) << 62) ? (uint64_t(1) << 62) : n)))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "%llu rows of %llu floats is beyond the kernels' grids",
+                (unsigned long long)rows, (unsigned long long)n);
+  return SH_OK;
+}
+
+// Uploads `n` floats of each of up to two host slices into the context's
+// input buffer (16-byte aligned pieces), runs `launch` on the device
+// pointers, and copies the first piece back into `back`.
+template <class F>
+int run_rows(sh_context* c, const float* a, uint64_t na, const float* b, uint64_t nb, float* back,
+             const char* what, F launch) {
+  Guard gd(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  const size_t ab = sizeof(float) * na, bb = sizeof(float) * nb;
+  const size_t a_al = (ab + 255) & ~size_t(255);
+  int rc;
+  if ((rc = c->d_in.ensure(a_al + bb, "input buffer")) || (rc = c->h_in.ensure(a_al + bb, "input staging")) ||
+      (rc = c->h_out.ensure(ab, "output staging")))
+    return rc;
+  uint8_t* hi = static_cast<uint8_t*>(c->h_in.p);
+  memcpy(hi, a, ab);
+  if (nb) memcpy(hi + a_al, b, bb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, hi, a_al + bb, hipMemcpyHostToDevice, c->stream), "upload");
+  float* da = static_cast<float*>(c->d_in.p);
+  const float* db = reinterpret_cast<const float*>(static_cast<uint8_t*>(c->d_in.p) + a_al);
+  HIP_TRY(launch(da, db, c->stream), what);
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_in.p, ab, hipMemcpyDeviceToHost, c->stream), "readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), what);
+  memcpy(back, c->h_out.p, ab);
+  return SH_OK;
+}
+
+}  // namespace
+
+int sh_rms_norm(sh_context* c, float* x, const float* w, uint64_t n, double eps) {
+  if (!c || (n && (!x || !w))) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = rowops_check(1, n);
+  if (rc || n == 0) return rc;
+  return run_rows(c, x, n, w, n, x, "rms_norm", [&](float* dx, const float* dw, hipStream_t s) {
+    return sh::launch_rms_norm(dx, dw, dx, 1, int64_t(n), eps, s);
+  });
+}
+
+int sh_rope_neox(sh_context* c, float* head, uint64_t n, const sh_rope_cfg* cfg) {
+  if (!c || !cfg || (n && !head)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = rowops_check(1, n);
+  if (rc) return rc;
+  // r = min(n_rot, head_dim, n) & ~1 (ops.rs:123): the slice length bounds
+  // the rotated span, so the kernel's head_dim is n here
+  const uint64_t r = std::min(std::min(cfg->n_rot, cfg->head_dim), n) & ~uint64_t(1);
+  if (r == 0) return SH_OK;
+  return run_rows(c, head, n, nullptr, 0, head, "rope_neox", [&](float* dx, const float*, hipStream_t s) {
+    return sh::launch_rope_neox(dx, 1, int64_t(n), int64_t(r), cfg->pos, 1, cfg->freq_base, s);
+  });
+}
+
+int sh_softmax(sh_context* c, float* xs, uint64_t n) {
+  if (!c || (n && !xs)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = rowops_check(1, n);
+  if (rc || n == 0) return rc;
+  return run_rows(c, xs, n, nullptr, 0, xs, "softmax", [&](float* dx, const float*, hipStream_t s) {
+    return sh::launch_softmax(dx, 1, int64_t(n), s);
+  });
+}
+
+int sh_l2_norm(sh_context* c, float* head, uint64_t n, double eps) {
+  if (!c || (n && !head)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = rowops_check(1, n);
+  if (rc || n == 0) return rc;
+  return run_rows(c, head, n, nullptr, 0, head, "l2_norm", [&](float* dx, const float*, hipStream_t s) {
+    return sh::launch_l2_norm(dx, 1, int64_t(n), eps, s);
+  });
+}
+
+int sh_add(sh_context* c, float* a, const float* b, uint64_t n) {
+  if (!c || (n && (!a || !b))) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = rowops_check(1, n);
+  if (rc || n == 0) return rc;
+  return run_rows(c, a, n, b, n, a, "add", [&](float* da, const float* db, hipStream_t s) {
+    return sh::launch_add(da, db, int64_t(n), s);
+  });
+}
+
+int sh_rms_norm_dev(const float* x, const float* w, float* out, uint64_t rows, uint64_t n, double eps,
+                    void* stream) {
+  int rc = rowops_check(rows, n);
+  if (rc || rows == 0 || n == 0) return rc;
+  if (!x || !w || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  HIP_TRY(sh::launch_rms_norm(x, w, out, int64_t(rows), int64_t(n), eps, static_cast<hipStream_t>(stream)),
+          "rms_norm launch");
+  return SH_OK;
+}
+
+int sh_l2_norm_dev(float* x, uint64_t rows, uint64_t n, double eps, void* stream) {
+  int rc = rowops_check(rows, n);
+  if (rc || rows == 0 || n == 0) return rc;
+  if (!x) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  HIP_TRY(sh::launch_l2_norm(x, int64_t(rows), int64_t(n), eps, static_cast<hipStream_t>(stream)),
+          "l2_norm launch");
+  return SH_OK;
+}
+
+int sh_softmax_dev(float* x, uint64_t rows, uint64_t n, void* stream) {
+  int rc = rowops_check(rows, n);
+  if (rc || rows == 0 || n == 0) return rc;
+  if (!x) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  HIP_TRY(sh::launch_softmax(x, int64_t(rows), int64_t(n), static_cast<hipStream_t>(stream)), "softmax launch");
+  return SH_OK;
+}
+
+int sh_rope_neox_dev(float* x, uint64_t rows, uint64_t heads_per_pos, const sh_rope_cfg* cfg, void* stream) {
+  if (!cfg) return fail(SH_ERR_INVALID_ARGUMENT, "null cfg");
+  if (heads_per_pos == 0) return fail(SH_ERR_INVALID_ARGUMENT, "heads_per_pos is 0");
+  int rc = rowops_check(rows, cfg->head_dim);
+  if (rc) return rc;
+  const uint64_t r = std::min(cfg->n_rot, cfg->head_dim) & ~uint64_t(1);
+  if (rows == 0 || r == 0) return SH_OK;
+  if (!x) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if (rows * (r / 2) / 256 >= (uint64_t(1) << 31) || heads_per_pos > (uint64_t(1) << 62))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "rope over %llu heads is beyond the kernel's grid",
+                (unsigned long long)rows);
+  HIP_TRY(sh::launch_rope_neox(x, int64_t(rows), int64_t(cfg->head_dim), int64_t(r), cfg->pos,
+                               int64_t(heads_per_pos), cfg->freq_base, static_cast<hipStream_t>(stream)),
+          "rope launch");
+  return SH_OK;
+}
+
+int sh_add_dev(float* a, const float* b, uint64_t n, void* stream) {
+  int rc = rowops_check(1, n);
+  if (rc || n == 0) return rc;
+  if (!a || !b) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  HIP_TRY(sh::launch_add(a, b, int64_t(n), static_cast<hipStream_t>(stream)), "add launch");
   return SH_OK;
 }

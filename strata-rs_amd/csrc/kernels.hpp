@@ -102,4 +102,16 @@ hipError_t launch_matmul(uint32_t quant, const void* w, int64_t rows, int64_t co
 hipError_t launch_quantize_q8(const float* x, int64_t n, int8_t* q, float* scales, float* usum,
                               hipStream_t stream);
 
+// The trait's elementwise methods over `rows` rows of n floats (rope:
+// head_dim floats per row, row r at position pos0 + r / heads_per_pos).
+// rowops_shape_ok bounds rows and n for the grids.
+bool rowops_shape_ok(int64_t rows, int64_t n);
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t n, double eps,
+                           hipStream_t stream);
+hipError_t launch_l2_norm(float* x, int64_t rows, int64_t n, double eps, hipStream_t stream);
+hipError_t launch_softmax(float* x, int64_t rows, int64_t n, hipStream_t stream);
+hipError_t launch_rope_neox(float* x, int64_t rows, int64_t head_dim, int64_t n_rot, uint64_t pos0,
+                            int64_t heads_per_pos, double freq_base, hipStream_t stream);
+hipError_t launch_add(float* a, const float* b, int64_t n, hipStream_t stream);
+
 }  // namespace sh

@@ -1,0 +1,253 @@
+// The rest of ComputeBackend on the device: rms_norm, rope_neox, softmax,
+// l2_norm and add (crates/strata-core/src/backend.rs:38-50), with the CPU
+// bodies' arithmetic (crates/strata-core/src/ops.rs:46-165):
+//   rms_norm   ss = sum v*v (f64) / n; scale = 1 / sqrt(ss + eps);
+//              out = (f32)((f64)x * scale * (f64)w)
+//   l2_norm    inv = 1 / sqrt(sum v*v + eps); v = (f32)((f64)v * inv)
+//   softmax    mx = max (f32); e = expf(v - mx) (f32); sum e (f64);
+//              v = (f32)((f64)e * (1 / sum))
+//   rope_neox  r = min(n_rot, head_dim) & ~1; pair (i, i + r/2):
+//              theta = base^(-2i/r), angle = theta * pos, a' = (f32)(a cos -
+//              b sin), b' = (f32)(a sin + b cos), all f64
+//   add        a += b (f32)
+// Every operation is a separate rounding, as in the Rust source (contraction
+// is off in this file). Only the order of the f64 sums differs (a butterfly
+// over the lanes instead of a sequential loop), and pow / sin / cos are the
+// device library's f64 functions, within an ulp of the platform libm's; the
+// f32 exponential of softmax is the f64 one rounded to f32.
+//
+// Batched over rows: x is [rows][n] (rope: [rows][head_dim], each row one
+// head). A workgroup of 256 threads takes four rows of at most 1024
+// elements (a wave each) or one longer row (all four waves), so the many
+// short rows of per-head work (qk norms, rope) fill the chip as well as the
+// few long rows of per-token work.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace sh {
+
+constexpr int kRowThreads = 256;
+constexpr int64_t kShortRow = 1024;
+
+// Sums over the 64 lanes by butterfly: every lane ends with the same bits
+// (each step adds the same two operands in both lanes).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma clang fp contract(off)
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Row-wide reductions for W waves per row (W = 4: the whole workgroup, so
+// every thread must call them).
+template <int W>
+__device__ __forceinline__ double row_sum(double v, double* lds) {
+#pragma clang fp contract(off)
+  v = wave_sum_f64(v);
+  if constexpr (W == 1) {
+    return v;
+  } else {
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const double t = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+    __syncthreads();  // the slots are reused by the next reduction
+    return t;
+  }
+}
+
+template <int W>
+__device__ __forceinline__ float row_max(float v, float* lds) {
+  v = wave_max_f32(v);
+  if constexpr (W == 1) {
+    return v;
+  } else {
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+    __syncthreads();
+    return t;
+  }
+}
+
+// This thread's row and its index within the row's 64 * W threads.
+template <int W>
+__device__ __forceinline__ int64_t row_of_thread(int& t) {
+  if constexpr (W == 1) {
+    t = threadIdx.x & 63;
+    return int64_t(blockIdx.x) * (kRowThreads / 64) + (threadIdx.x >> 6);
+  } else {
+    t = threadIdx.x;
+    return blockIdx.x;
+  }
+}
+
+template <int W>
+__global__ void __launch_bounds__(kRowThreads) rms_norm_kernel(const float* x,  // may be out itself
+                                                               const float* __restrict__ w, float* out,
+                                                               int64_t rows, int64_t n, double eps) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  constexpr int T = 64 * W;
+  const float* xr = x + row * n;
+  double ss = 0.0;
+  for (int64_t i = t; i < n; i += T) {
+    const double v = xr[i];
+    ss += v * v;
+  }
+  ss = row_sum<W>(ss, lds);
+  const double scale = 1.0 / sqrt(ss / double(n) + eps);
+  float* o = out + row * n;
+  for (int64_t i = t; i < n; i += T) o[i] = float(double(xr[i]) * scale * double(w[i]));
+}
+
+template <int W>
+__global__ void __launch_bounds__(kRowThreads) l2_norm_kernel(float* x, int64_t rows, int64_t n, double eps) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  constexpr int T = 64 * W;
+  float* xr = x + row * n;
+  double ss = 0.0;
+  for (int64_t i = t; i < n; i += T) {
+    const double v = xr[i];
+    ss += v * v;
+  }
+  ss = row_sum<W>(ss, lds);
+  const double inv = 1.0 / sqrt(ss + eps);
+  for (int64_t i = t; i < n; i += T) xr[i] = float(double(xr[i]) * inv);
+}
+
+template <int W>
+__global__ void __launch_bounds__(kRowThreads) softmax_kernel(float* x, int64_t rows, int64_t n) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  __shared__ float ldm[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  constexpr int T = 64 * W;
+  float* xr = x + row * n;
+  float mx = -__builtin_inff();
+  for (int64_t i = t; i < n; i += T) mx = fmaxf(mx, xr[i]);
+  mx = row_max<W>(mx, ldm);
+  double sum = 0.0;
+  for (int64_t i = t; i < n; i += T) {
+    // the f32 exponential as the f64 one rounded once: within 0.5 ulp + a
+    // hair, as close to a correctly rounded expf as the platform libm's
+    const float e = float(exp(double(xr[i] - mx)));
+    xr[i] = e;
+    sum += double(e);
+  }
+  sum = row_sum<W>(sum, lds);
+  const double inv = 1.0 / sum;
+  for (int64_t i = t; i < n; i += T) xr[i] = float(double(xr[i]) * inv);
+}
+
+// One thread per (row, pair); row r is at position pos0 + r / heads_per_pos.
+__global__ void __launch_bounds__(kRowThreads) rope_neox_kernel(float* x, int64_t rows, int64_t head_dim, int r,
+                                                                uint64_t pos0, int64_t heads_per_pos,
+                                                                double freq_base) {
+#pragma clang fp contract(off)
+  const int half = r >> 1;
+  const int64_t gid = int64_t(blockIdx.x) * kRowThreads + threadIdx.x;
+  if (gid >= rows * half) return;
+  const int64_t row = gid / half;
+  const int i = int(gid - row * half);
+  const double p = double(pos0 + uint64_t(row / heads_per_pos));
+  const double theta = pow(freq_base, -2.0 * double(i) / double(r));
+  const double angle = theta * p;
+  const double s = sin(angle), c = cos(angle);
+  float* h = x + row * head_dim;
+  const double a = h[i], b = h[i + half];
+  const double ac = a * c, bs = b * s, as = a * s, bc = b * c;
+  h[i] = float(ac - bs);
+  h[i + half] = float(as + bc);
+}
+
+__global__ void __launch_bounds__(kRowThreads) add_kernel(float* __restrict__ a, const float* __restrict__ b,
+                                                          int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kRowThreads;
+  int64_t i = int64_t(blockIdx.x) * kRowThreads + threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(a) & 15u) == 0 && (reinterpret_cast<uintptr_t>(b) & 15u) == 0) {
+    const int64_t n4 = n >> 2;
+    f32x4* a4 = reinterpret_cast<f32x4*>(a);
+    const f32x4* b4 = reinterpret_cast<const f32x4*>(b);
+    for (int64_t k = i; k < n4; k += stride) a4[k] = a4[k] + b4[k];
+    for (int64_t k = 4 * n4 + i; k < n; k += stride) a[k] = a[k] + b[k];
+  } else {
+    for (int64_t k = i; k < n; k += stride) a[k] = a[k] + b[k];
+  }
+}
+
+static unsigned row_blocks(int64_t rows, int64_t n) {
+  return unsigned(n <= kShortRow ? (rows + 3) / 4 : rows);
+}
+
+bool rowops_shape_ok(int64_t rows, int64_t n) {
+  // grids of at most 2^31 workgroups; row offsets stay in int64
+  return rows >= 0 && n >= 0 && rows <= (int64_t(1) << 31) - 1 && n <= (int64_t(1) << 31) - 1 &&
+         (n == 0 || rows <= (int64_t(1) << 62) / n);
+}
+
+hipError_t launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t n, double eps,
+                           hipStream_t s) {
+  if (rows == 0 || n == 0) return hipSuccess;
+  if (n <= kShortRow)
+    hipLaunchKernelGGL(rms_norm_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, w, out, rows, n,
+                       eps);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<4>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, w, out, rows, n,
+                       eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_l2_norm(float* x, int64_t rows, int64_t n, double eps, hipStream_t s) {
+  if (rows == 0 || n == 0) return hipSuccess;
+  if (n <= kShortRow)
+    hipLaunchKernelGGL(l2_norm_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n, eps);
+  else
+    hipLaunchKernelGGL(l2_norm_kernel<4>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_softmax(float* x, int64_t rows, int64_t n, hipStream_t s) {
+  if (rows == 0 || n == 0) return hipSuccess;
+  if (n <= kShortRow)
+    hipLaunchKernelGGL(softmax_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n);
+  else
+    hipLaunchKernelGGL(softmax_kernel<4>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_neox(float* x, int64_t rows, int64_t head_dim, int64_t n_rot, uint64_t pos0,
+                            int64_t heads_per_pos, double freq_base, hipStream_t s) {
+  int64_t r = n_rot < head_dim ? n_rot : head_dim;
+  r &= ~int64_t(1);
+  if (rows == 0 || r == 0) return hipSuccess;
+  if (r > (int64_t(1) << 30) || heads_per_pos <= 0) return hipErrorInvalidValue;
+  const int64_t threads = rows * (r / 2);
+  const int64_t blocks = (threads + kRowThreads - 1) / kRowThreads;
+  if (blocks > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rope_neox_kernel, dim3(unsigned(blocks)), dim3(kRowThreads), 0, s, x, rows, head_dim, int(r),
+                     pos0, heads_per_pos, freq_base);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float* a, const float* b, int64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  int64_t blocks = ((n + 3) / 4 + kRowThreads - 1) / kRowThreads;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(add_kernel, dim3(unsigned(blocks)), dim3(kRowThreads), 0, s, a, b, n);
+  return hipGetLastError();
+}
+
+}  // namespace sh

@@ -55,7 +55,8 @@ EXPORTS = (
     "sh_moe_route", "sh_moe_ffn", "sh_moe_layer", "sh_matmul",
     "sh_moe_workspace_bytes", "sh_moe_ffn_dev", "sh_matmul_workspace_bytes", "sh_matmul_dev",
     "sh_quantize_q8_dev", "sh_moe_layer_workspace_bytes", "sh_moe_layer_dev", "sh_dequant_dev",
-    "sh_gemv_dev",
+    "sh_gemv_dev", "sh_rms_norm", "sh_rope_neox", "sh_softmax", "sh_l2_norm", "sh_add", "sh_rms_norm_dev",
+    "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev",
 )
 
 
@@ -116,6 +117,22 @@ class _ExpertViewC(C.Structure):
                 ("data", C.c_void_p), ("nbytes", C.c_uint64)]
 
 
+class _RopeCfgC(C.Structure):
+    _fields_ = [("pos", C.c_uint64), ("n_rot", C.c_uint64), ("head_dim", C.c_uint64), ("freq_base", C.c_double)]
+
+
+@dataclass
+class RopeCfg:
+    """backend.rs:158-167."""
+    pos: int
+    n_rot: int
+    head_dim: int
+    freq_base: float
+
+    def _c(self) -> _RopeCfgC:
+        return _RopeCfgC(self.pos, self.n_rot, self.head_dim, self.freq_base)
+
+
 _lib = None
 
 
@@ -165,6 +182,17 @@ def load_library() -> C.CDLL:
     L.sh_quantize_q8_dev.argtypes = [vp, u64, vp, vp, vp, vp]
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
+    dbl, ropep = C.c_double, C.POINTER(_RopeCfgC)
+    L.sh_rms_norm.argtypes = [vp, f32p, f32p, u64, dbl]
+    L.sh_rope_neox.argtypes = [vp, f32p, u64, ropep]
+    L.sh_softmax.argtypes = [vp, f32p, u64]
+    L.sh_l2_norm.argtypes = [vp, f32p, u64, dbl]
+    L.sh_add.argtypes = [vp, f32p, f32p, u64]
+    L.sh_rms_norm_dev.argtypes = [vp, vp, vp, u64, u64, dbl, vp]
+    L.sh_l2_norm_dev.argtypes = [vp, u64, u64, dbl, vp]
+    L.sh_softmax_dev.argtypes = [vp, u64, u64, vp]
+    L.sh_rope_neox_dev.argtypes = [vp, u64, u64, ropep, vp]
+    L.sh_add_dev.argtypes = [vp, vp, u64, vp]
     _lib = L
     return L
 
@@ -385,6 +413,34 @@ class HipBackend:
         check(self._L.sh_matmul(self._ctx, C.byref(wc), xv.ctypes.data, m, y.ctypes.data, int(mode)))
         return y
 
+    # ---- the trait's elementwise methods (backend.rs:38-50), in place ----
+    def rms_norm(self, x: np.ndarray, w, eps: float) -> None:
+        xv = _f32_out(x)
+        wv = _f32_in(w)
+        if wv.size != xv.size:
+            raise ShapeError(SH_ERR_SHAPE, f"w has {wv.size} elements, x {xv.size}")
+        check(self._L.sh_rms_norm(self._ctx, xv.ctypes.data, wv.ctypes.data, xv.size, float(eps)))
+
+    def rope_neox(self, head: np.ndarray, cfg: RopeCfg) -> None:
+        hv = _f32_out(head)
+        c = cfg._c()
+        check(self._L.sh_rope_neox(self._ctx, hv.ctypes.data, hv.size, C.byref(c)))
+
+    def softmax(self, xs: np.ndarray) -> None:
+        xv = _f32_out(xs)
+        check(self._L.sh_softmax(self._ctx, xv.ctypes.data, xv.size))
+
+    def l2_norm(self, head: np.ndarray, eps: float) -> None:
+        hv = _f32_out(head)
+        check(self._L.sh_l2_norm(self._ctx, hv.ctypes.data, hv.size, float(eps)))
+
+    def add(self, a: np.ndarray, b) -> None:
+        av = _f32_out(a)
+        bv = _f32_in(b)
+        if bv.size != av.size:
+            raise ShapeError(SH_ERR_SHAPE, f"b has {bv.size} elements, a {av.size}")
+        check(self._L.sh_add(self._ctx, av.ctypes.data, bv.ctypes.data, av.size))
+
     def dequantize_row(self, quant: int, block, out: np.ndarray, flags: int = 0) -> None:
         """dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device."""
         b = _bytes(block)
@@ -457,3 +513,24 @@ def matmul_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, m: int,
 def quantize_q8_dev(x_ptr: int, n: int, codes_ptr: int, scales_ptr: int, sums_ptr: int,
                     stream: int = 0) -> None:
     check(load_library().sh_quantize_q8_dev(x_ptr, n, codes_ptr, scales_ptr, sums_ptr, stream or None))
+
+
+def rms_norm_dev(x_ptr: int, w_ptr: int, out_ptr: int, rows: int, n: int, eps: float, stream: int = 0) -> None:
+    check(load_library().sh_rms_norm_dev(x_ptr, w_ptr, out_ptr, rows, n, float(eps), stream or None))
+
+
+def l2_norm_dev(x_ptr: int, rows: int, n: int, eps: float, stream: int = 0) -> None:
+    check(load_library().sh_l2_norm_dev(x_ptr, rows, n, float(eps), stream or None))
+
+
+def softmax_dev(x_ptr: int, rows: int, n: int, stream: int = 0) -> None:
+    check(load_library().sh_softmax_dev(x_ptr, rows, n, stream or None))
+
+
+def rope_neox_dev(x_ptr: int, rows: int, heads_per_pos: int, cfg: RopeCfg, stream: int = 0) -> None:
+    c = cfg._c()
+    check(load_library().sh_rope_neox_dev(x_ptr, rows, heads_per_pos, C.byref(c), stream or None))
+
+
+def add_dev(a_ptr: int, b_ptr: int, n: int, stream: int = 0) -> None:
+    check(load_library().sh_add_dev(a_ptr, b_ptr, n, stream or None))

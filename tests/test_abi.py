@@ -36,6 +36,7 @@ def test_abi_version_and_geometry():
     assert lib.sh_abi_version() == 1
     assert H.quant_geometry(H.QuantType.Q8_0) == (32, 34)
     assert H.quant_geometry(H.QuantType.Q4_K) == (256, 144)
+    assert H.quant_geometry(H.QuantType.Q5_K) == (256, 176)
     assert H.quant_geometry(H.QuantType.Q6_K) == (256, 210)
     assert H.byte_size(H.QuantType.Q4_K, 12288) == 6912
     with pytest.raises(H.UnsupportedQuantError):
