@@ -49,9 +49,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill"),
+    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
-                         "'moe' / 'prefill': that extra alone (for profiling; prints its JSON)")
+                         "'moe' / 'prefill' / 'rowops': that extra alone (for profiling; prints its JSON)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -281,6 +281,46 @@ def bench_moe_layer(torch, H, S, steps):
     return res
 
 
+def bench_rowops(torch, H, S, steps):
+    """The trait's elementwise methods at a decode step's shapes (hidden 4096,
+    32 heads of 128 with 64 rotated dims, a 4096-long attention row per head)
+    and a 16-token prefill's; 64 launches of one method captured in a graph
+    and replayed; us per launch and GB/s of the bytes each launch reads and
+    writes (the data stays in L2 between launches)."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    res = {}
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    w = t(S.normal_f32(0x5EED0061, 4096))
+    cases = []
+    for n_tok in (1, 16):
+        x = t(S.normal_f32(0x5EED0062 + n_tok, n_tok * 4096))
+        o = t(np.zeros(n_tok * 4096, np.float32))
+        q = t(S.normal_f32(0x5EED0063 + n_tok, n_tok * 32 * 128))
+        sc = t(S.normal_f32(0x5EED0064 + n_tok, n_tok * 32 * 4096))
+        cfg = H.RopeCfg(pos=1000, n_rot=64, head_dim=128, freq_base=1e7)
+        nb = 4 * n_tok * 4096
+        cases += [
+            (f"rms_norm_{n_tok}x4096", 2 * nb + 4 * 4096,
+             lambda st, x=x, o=o, n=n_tok: H.rms_norm_dev(x.data_ptr(), w.data_ptr(), o.data_ptr(), n, 4096, 1e-6, st)),
+            (f"rope_neox_{n_tok}x32x128_rot64", 2 * 4 * n_tok * 32 * 64,
+             lambda st, q=q, n=n_tok: H.rope_neox_dev(q.data_ptr(), n * 32, 32, cfg, st)),
+            (f"l2_norm_{n_tok}x32x128", 2 * 4 * n_tok * 32 * 128,
+             lambda st, q=q, n=n_tok: H.l2_norm_dev(q.data_ptr(), n * 32, 128, 1e-6, st)),
+            (f"softmax_{n_tok}x32x4096", 2 * 4 * n_tok * 32 * 4096,
+             lambda st, sc=sc, n=n_tok: H.softmax_dev(sc.data_ptr(), n * 32, 4096, st)),
+            (f"add_{n_tok}x4096", 3 * nb,
+             lambda st, x=x, o=o, n=n_tok: H.add_dev(o.data_ptr(), x.data_ptr(), n * 4096, st)),
+        ]
+    for name, nbytes, f in cases:
+        ms = time_calls(torch, [f] * 64, steps, 64)  # 64 launches per graph replay
+        res[name] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    return res
+
+
 def cpu_baseline(w, x, rows, cols, seconds):
     """The oracle (ops::gemv restated in C, one thread) on whole rows of the
     same matrix for about `seconds`; GB/s of packed weight bytes."""
@@ -361,6 +401,9 @@ def main():
         res.update(bench_moe_layer(torch, H, S, args.steps))
         print(json.dumps(res), flush=True)
         return
+    elif args.only == "rowops":
+        print(json.dumps(bench_rowops(torch, H, S, args.steps)), flush=True)
+        return
     elif args.only == "prefill":
         wp = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
         print(json.dumps(bench_prefill(torch, H, S, wp, 12288, 4096, 512, args.steps)), flush=True)
@@ -425,6 +468,8 @@ def main():
         extra.update(bench_moe(torch, H, S, 240))
         print("[bench] extra moe layer", file=sys.stderr, flush=True)
         extra.update(bench_moe_layer(torch, H, S, 240))
+        print("[bench] extra elementwise methods", file=sys.stderr, flush=True)
+        extra.update(bench_rowops(torch, H, S, 200))
         out["extra"] = extra
 
     if not args.no_cpu:

@@ -20,7 +20,12 @@
 // head). A workgroup of 256 threads takes four rows of at most 1024
 // elements (a wave each) or one longer row (all four waves), so the many
 // short rows of per-head work (qk norms, rope) fill the chip as well as the
-// few long rows of per-token work.
+// few long rows of per-token work. Rows of up to 8192 floats (n % 4 == 0,
+// 16-byte aligned) are held in registers between the reduction and the
+// write; longer or unaligned rows are streamed twice (three times for
+// softmax) through L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -152,6 +157,151 @@ __global__ void __launch_bounds__(kRowThreads) softmax_kernel(float* x, int64_t 
   for (int64_t i = t; i < n; i += T) xr[i] = float(double(xr[i]) * inv);
 }
 
+// ---- register-resident rows ---------------------------------------------
+// Rows of n % 4 == 0 floats at 16-byte aligned addresses, up to 8192 floats:
+// each thread loads its V float4 slots once (all loads in flight together),
+// reduces, and writes from registers, so a row costs one read and one write
+// and a single memory latency. Padding slots (past the row) are masked.
+template <int W, int V>
+__device__ __forceinline__ void load_slots(const float* row, int64_t n4, int t, f32x4 (&v)[V], float pad) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(row);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t i = t + int64_t(k) * 64 * W;
+    v[k] = i < n4 ? p[i] : f32x4{pad, pad, pad, pad};
+  }
+}
+
+template <int V>
+__device__ __forceinline__ double sum_squares(const f32x4 (&v)[V]) {
+#pragma clang fp contract(off)
+  double ss = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const double a = v[k].x, b = v[k].y, c = v[k].z, d = v[k].w;
+    ss += a * a;
+    ss += b * b;
+    ss += c * c;
+    ss += d * d;
+  }
+  return ss;
+}
+
+template <int W, int V>
+__global__ void __launch_bounds__(kRowThreads) rms_norm_reg_kernel(const float* x, const float* __restrict__ w,
+                                                                   float* out, int64_t rows, int64_t n,
+                                                                   double eps) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  const int64_t n4 = n >> 2;
+  f32x4 v[V], g[V];
+  load_slots<W, V>(x + row * n, n4, t, v, 0.f);
+  load_slots<W, V>(w, n4, t, g, 0.f);
+  const double ss = row_sum<W>(sum_squares(v), lds);
+  const double scale = 1.0 / sqrt(ss / double(n) + eps);
+  f32x4* o = reinterpret_cast<f32x4*>(out + row * n);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t i = t + int64_t(k) * 64 * W;
+    if (i < n4)
+      o[i] = f32x4{float(double(v[k].x) * scale * double(g[k].x)), float(double(v[k].y) * scale * double(g[k].y)),
+                   float(double(v[k].z) * scale * double(g[k].z)), float(double(v[k].w) * scale * double(g[k].w))};
+  }
+}
+
+template <int W, int V>
+__global__ void __launch_bounds__(kRowThreads) l2_norm_reg_kernel(float* x, int64_t rows, int64_t n, double eps) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  const int64_t n4 = n >> 2;
+  f32x4 v[V];
+  load_slots<W, V>(x + row * n, n4, t, v, 0.f);
+  const double ss = row_sum<W>(sum_squares(v), lds);
+  const double inv = 1.0 / sqrt(ss + eps);
+  f32x4* o = reinterpret_cast<f32x4*>(x + row * n);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t i = t + int64_t(k) * 64 * W;
+    if (i < n4)
+      o[i] = f32x4{float(double(v[k].x) * inv), float(double(v[k].y) * inv), float(double(v[k].z) * inv),
+                   float(double(v[k].w) * inv)};
+  }
+}
+
+template <int W, int V>
+__global__ void __launch_bounds__(kRowThreads) softmax_reg_kernel(float* x, int64_t rows, int64_t n) {
+#pragma clang fp contract(off)
+  __shared__ double lds[4];
+  __shared__ float ldm[4];
+  int t;
+  const int64_t row = row_of_thread<W>(t);
+  if (W == 1 && row >= rows) return;
+  const int64_t n4 = n >> 2;
+  f32x4 v[V];
+  load_slots<W, V>(x + row * n, n4, t, v, -__builtin_inff());  // padding leaves the max alone
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int k = 0; k < V; ++k) mx = fmaxf(fmaxf(fmaxf(mx, v[k].x), fmaxf(v[k].y, v[k].z)), v[k].w);
+  mx = row_max<W>(mx, ldm);
+  double sum = 0.0;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    if (t + int64_t(k) * 64 * W < n4) {
+      v[k].x = float(exp(double(v[k].x - mx)));
+      v[k].y = float(exp(double(v[k].y - mx)));
+      v[k].z = float(exp(double(v[k].z - mx)));
+      v[k].w = float(exp(double(v[k].w - mx)));
+      sum += double(v[k].x);
+      sum += double(v[k].y);
+      sum += double(v[k].z);
+      sum += double(v[k].w);
+    }
+  }
+  sum = row_sum<W>(sum, lds);
+  const double inv = 1.0 / sum;
+  f32x4* o = reinterpret_cast<f32x4*>(x + row * n);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t i = t + int64_t(k) * 64 * W;
+    if (i < n4)
+      o[i] = f32x4{float(double(v[k].x) * inv), float(double(v[k].y) * inv), float(double(v[k].z) * inv),
+                   float(double(v[k].w) * inv)};
+  }
+}
+
+// Calls f(W, V) with compile-time waves per row W and float4 slots per
+// thread V for a register-resident row of n floats; false when n does not
+// fit (then the streaming kernels above take the row).
+template <int A>
+using ic = std::integral_constant<int, A>;
+template <class F>
+static bool with_reg_shape(int64_t n, F&& f) {
+  if (n <= kShortRow) {
+    const int64_t per = (n / 4 + 63) / 64;
+    if (per <= 1) f(ic<1>{}, ic<1>{});
+    else if (per <= 2) f(ic<1>{}, ic<2>{});
+    else f(ic<1>{}, ic<4>{});
+    return true;
+  }
+  const int64_t per = (n / 4 + 255) / 256;
+  if (per <= 2) f(ic<4>{}, ic<2>{});
+  else if (per <= 4) f(ic<4>{}, ic<4>{});
+  else if (per <= 8) f(ic<4>{}, ic<8>{});
+  else return false;
+  return true;
+}
+
+static bool vec_row(int64_t n, const void* a, const void* b = nullptr, const void* c = nullptr) {
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  return n % 4 == 0 && al(a) && al(b) && al(c);
+}
+
 // One thread per (row, pair); row r is at position pos0 + r / heads_per_pos.
 __global__ void __launch_bounds__(kRowThreads) rope_neox_kernel(float* x, int64_t rows, int64_t head_dim, int r,
                                                                 uint64_t pos0, int64_t heads_per_pos,
@@ -201,6 +351,12 @@ bool rowops_shape_ok(int64_t rows, int64_t n) {
 hipError_t launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t n, double eps,
                            hipStream_t s) {
   if (rows == 0 || n == 0) return hipSuccess;
+  if (vec_row(n, x, w, out) && with_reg_shape(n, [&](auto w_, auto v_) {
+        constexpr int W = decltype(w_)::value, V = decltype(v_)::value;
+        hipLaunchKernelGGL((rms_norm_reg_kernel<W, V>), dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, w,
+                           out, rows, n, eps);
+      }))
+    return hipGetLastError();
   if (n <= kShortRow)
     hipLaunchKernelGGL(rms_norm_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, w, out, rows, n,
                        eps);
@@ -212,6 +368,12 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* out, int64_t r
 
 hipError_t launch_l2_norm(float* x, int64_t rows, int64_t n, double eps, hipStream_t s) {
   if (rows == 0 || n == 0) return hipSuccess;
+  if (vec_row(n, x) && with_reg_shape(n, [&](auto w_, auto v_) {
+        constexpr int W = decltype(w_)::value, V = decltype(v_)::value;
+        hipLaunchKernelGGL((l2_norm_reg_kernel<W, V>), dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows,
+                           n, eps);
+      }))
+    return hipGetLastError();
   if (n <= kShortRow)
     hipLaunchKernelGGL(l2_norm_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n, eps);
   else
@@ -221,6 +383,12 @@ hipError_t launch_l2_norm(float* x, int64_t rows, int64_t n, double eps, hipStre
 
 hipError_t launch_softmax(float* x, int64_t rows, int64_t n, hipStream_t s) {
   if (rows == 0 || n == 0) return hipSuccess;
+  if (vec_row(n, x) && with_reg_shape(n, [&](auto w_, auto v_) {
+        constexpr int W = decltype(w_)::value, V = decltype(v_)::value;
+        hipLaunchKernelGGL((softmax_reg_kernel<W, V>), dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows,
+                           n);
+      }))
+    return hipGetLastError();
   if (n <= kShortRow)
     hipLaunchKernelGGL(softmax_kernel<1>, dim3(row_blocks(rows, n)), dim3(kRowThreads), 0, s, x, rows, n);
   else
