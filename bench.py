@@ -445,9 +445,11 @@ def main():
         extra = {}
         shapes = [("q4k_gate_12288x4096_b1", S.Q4_K, 12288, 4096, 1),
                   ("q4k_gate_12288x4096_b8", S.Q4_K, 12288, 4096, 8),
+                  ("q4k_down_4096x12288_b8", S.Q4_K, 4096, 12288, 8),
                   ("q8_0_4096x4096_b1", S.Q8_0, 4096, 4096, 1),
                   ("q5k_4096x12288_b1", S.Q5_K, 4096, 12288, 1),
                   ("q5k_12288x4096_b8", S.Q5_K, 12288, 4096, 8),
+                  ("q5k_4096x12288_b8", S.Q5_K, 4096, 12288, 8),
                   ("q6k_lm_head_151936x4096_b1", S.Q6_K, 151936, 4096, 1)]
         prefill_w = None
         for name, q, r, c, b in shapes:

@@ -1187,7 +1187,7 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(x) & 15u))
     return hipErrorInvalidValue;
   if (batch >= 2 && gemv_mfma_ok(quant, rows, cols, batch))
-    return launch_gemv_mfma(w, rows, cols, x, y, batch, cu_count(), stream);
+    return launch_gemv_mfma(quant, w, rows, cols, x, y, batch, cu_count(), stream);
   // batch 1: 16 waves per CU for tall matrices whose rows are a single
   // 4096-column window (more waves hide more latency, and each still has
   // rows to stream); 8 otherwise (fewer workgroups stage x, and multi-window

@@ -19,11 +19,12 @@ bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
 hipError_t launch_gemv(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
                        float* y, int batch, int q6_signed, hipStream_t stream);
 
-// Batch 2..8 of Q4_K rows of at most 4096 columns on int8 MFMA (exact
-// integer activations); `cu` is the device's CU count.
+// Batch 2..8 of Q4_K or Q5_K rows on int8 MFMA (exact integer
+// activations, staged in LDS 4096 columns at a time); `cu` is the device's
+// CU count.
 bool gemv_mfma_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
-hipError_t launch_gemv_mfma(const void* w, int64_t rows, int64_t cols, const float* x, float* y, int batch,
-                            int cu, hipStream_t stream);
+hipError_t launch_gemv_mfma(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x, float* y,
+                            int batch, int cu, hipStream_t stream);
 
 // y[c] = sum_i x[i] * W[i][c] for one expert matrix W[rows = in][cols = out]
 // (reference orientation). `workspace` holds expert_workspace_bytes().

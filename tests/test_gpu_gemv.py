@@ -101,21 +101,24 @@ def test_gemv_batch(backend, oracle, quant, cols, batch):
         check(y[b], oracle.gemv(quant, rows, cols, w, x[b]))
 
 
+@pytest.mark.parametrize("quant", [12, 13])
 @pytest.mark.parametrize("rows,cols,batch", [(100, 4096, 5), (17, 256, 8), (1, 512, 2), (12288, 4096, 8),
-                                             (4099, 1024, 7), (16400, 1024, 8)])
-def test_gemv_batch_q4k_mfma_shapes(backend, oracle, rows, cols, batch):
-    # the batched Q4_K path on int8 MFMA: partial 16-row tiles, shares of
-    # super-blocks with nothing to do, odd batches, a tall matrix (16400
-    # rows: four row tiles per workgroup and three shares, one of them empty)
-    say("gemv batch q4k mfma", rows, cols, batch)
-    w = S.matrix(12, 77 + rows + cols, rows, cols)
+                                             (4099, 1024, 7), (16400, 1024, 8), (4096, 12288, 8),
+                                             (37, 4096 + 256, 3), (300, 8192 + 1024, 2)])
+def test_gemv_batch_kquant_mfma_shapes(backend, oracle, quant, rows, cols, batch):
+    # the batched Q4_K / Q5_K path on int8 MFMA: partial 16-row tiles, shares
+    # of super-blocks with nothing to do, odd batches, a tall matrix (16400
+    # rows: four row tiles per workgroup and three shares, one of them empty),
+    # rows of several 4096-column windows (the last one partial)
+    say("gemv batch mfma", quant, rows, cols, batch)
+    w = S.matrix(quant, 77 + rows + cols, rows, cols)
     x = S.normal_f32(batch * 17 + rows, batch * cols).reshape(batch, cols)
-    y = backend.gemv_batch(H.QuantTensor(f"bm_{rows}_{cols}", 12, rows, cols, w), x, batch)
+    y = backend.gemv_batch(H.QuantTensor(f"bm{quant}_{rows}_{cols}", quant, rows, cols, w), x, batch)
     idx = np.unique(np.linspace(0, rows - 1, min(rows, 512)).astype(np.int64))
-    rb = S.row_bytes(12, cols)
+    rb = S.row_bytes(quant, cols)
     sub = np.concatenate([w[i * rb:(i + 1) * rb] for i in idx])
     for b in range(batch):
-        check(y[b][idx], oracle.gemv(12, len(idx), cols, sub, x[b]))
+        check(y[b][idx], oracle.gemv(quant, len(idx), cols, sub, x[b]))
 
 
 def test_gemv_batch_q4k_mixed_block_magnitudes(backend, oracle):
