@@ -53,6 +53,13 @@ extern "C" {
 #define SH_ERR_NO_DEVICE (-6)        /* no usable HIP device                  */
 #define SH_ERR_DEVICE (-7)           /* HIP runtime failure                   */
 #define SH_ERR_OUT_OF_MEMORY (-8)    /* device or pinned allocation failed    */
+#define SH_ERR_FORMAT (-9)           /* malformed GGUF: reader.rs's BadMagic,
+                                        UnsupportedVersion, BadKeyLength,
+                                        StringNotUtf8, BadValueType,
+                                        WrongTensorDims, duplicate tensor     */
+#define SH_ERR_IO (-10)              /* the file cannot be opened or mapped   */
+#define SH_ERR_NOT_FOUND (-11)       /* no such tensor / key (or not of the
+                                        asked type): the reference's None     */
 
 /* ---- quant type ids (Strata's scheme, crates/strata-gguf/src/quant.rs:15-43) */
 #define SH_QUANT_F32 0u
@@ -108,6 +115,19 @@ typedef struct sh_rope_cfg {
   uint64_t head_dim; /* stride between heads */
   double freq_base;  /* theta */
 } sh_rope_cfg;
+
+/* An open GGUF file: GgufFile (crates/strata-gguf/src/reader.rs:200-445). */
+typedef struct sh_gguf sh_gguf;
+
+/* TensorInfo (reader.rs:179-197) plus its payload size. */
+typedef struct sh_gguf_tensor_info {
+  const char* name; /* valid until sh_gguf_close */
+  uint32_t n_dims;  /* 1..4 */
+  uint32_t type;    /* quant type id */
+  uint64_t shape[4]; /* GGUF order, dim 0 fastest; 1 past n_dims */
+  uint64_t offset;  /* from the start of the data section */
+  uint64_t nbytes;  /* tensor_payload_bytes (reader.rs:399-423); 0 for an unknown type */
+} sh_gguf_tensor_info;
 
 /* ---- library and context ----------------------------------------------- */
 int sh_abi_version(void);
@@ -285,6 +305,36 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
  * aligned (4 for Q8_0 and F32), x 16-byte aligned. */
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream);
+
+/* ---- GGUF weight source (host code; no device needed except the upload) */
+/* GgufFile::open (reader.rs:231-353): maps `path` read-only and parses the
+ * header, metadata and tensor directory with the reference's checks and
+ * limits; data_start is the directory's end rounded up to the alignment
+ * (general.alignment when an integer type and positive, else 32). */
+int sh_gguf_open(const char* path, sh_gguf** out);
+int sh_gguf_close(sh_gguf* gguf);
+int sh_gguf_header(const sh_gguf* gguf, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv,
+                   uint64_t* alignment, uint64_t* data_start, uint64_t* file_size);
+/* The index-th directory entry (file order). */
+int sh_gguf_tensor(const sh_gguf* gguf, uint64_t index, sh_gguf_tensor_info* out);
+/* GgufFile::find (reader.rs:387-389). */
+int sh_gguf_find(const sh_gguf* gguf, const char* name, uint64_t* index);
+/* GgufFile::tensor_data (reader.rs:425-445): the payload inside the mapping,
+ * bounds-checked (SH_ERR_TRUNCATED past the end of the file). */
+int sh_gguf_tensor_data(const sh_gguf* gguf, uint64_t index, const uint8_t** data, uint64_t* nbytes);
+/* Metadata (metadata.rs): the value's type tag, array element type and
+ * count; MetaValue::as_int (integer types; a u64 value reads as 0, as in
+ * the reference), as_float (numbers), as_str (strings, valid until close). */
+int sh_gguf_meta_type(const sh_gguf* gguf, const char* key, uint32_t* type, uint32_t* elem, uint64_t* count);
+int sh_gguf_meta_int(const sh_gguf* gguf, const char* key, int64_t* value);
+int sh_gguf_meta_float(const sh_gguf* gguf, const char* key, double* value);
+int sh_gguf_meta_str(const sh_gguf* gguf, const char* key, const char** s, uint64_t* len);
+/* Admits tensor `index` into ctx's resident store under `key`, packed as
+ * stored, copied from the mapping through pinned staging chunks. Dims map
+ * as [cols, rows, n_expert] (weights.rs:14-34), so a later sh_gemv /
+ * sh_expert_gemv / sh_moe_* call with the same key and shape finds it
+ * resident. Types with a device kernel only; 1 to 3 dims. */
+int sh_upload_gguf_tensor(sh_context* ctx, const sh_gguf* gguf, uint64_t index, uint64_t key);
 
 /* The elementwise methods batched over rows, on device pointers: the same
  * arithmetic per row as the host-slice forms; enqueued on `stream`.

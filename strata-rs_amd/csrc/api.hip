@@ -17,6 +17,7 @@
 
 #include "../../include/strata_hip.h"
 #include "common.hpp"
+#include "gguf.hpp"
 #include "kernels.hpp"
 
 namespace {
@@ -115,6 +116,8 @@ struct sh_context {
   std::unordered_map<uint64_t, Resident> weights;
   DevBuf d_in, d_out, d_blk;
   HostBuf h_in, h_out;
+  HostBuf stage[2];                      // pinned chunks of weight uploads
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
   std::mutex mu;
 };
 
@@ -123,6 +126,30 @@ namespace {
 void free_resident(Resident& r) {
   if (r.dev) (void)hipFree(r.dev);
   r.dev = nullptr;
+}
+
+// Copies n host bytes (e.g. an mmap'd GGUF payload, which is pageable) to
+// device memory through two pinned 8 MiB chunks: the host copy into one
+// chunk overlaps the DMA out of the other. Synchronous.
+constexpr size_t kStageChunk = size_t(8) << 20;
+int staged_upload(sh_context* c, void* dev, const uint8_t* src, uint64_t n) {
+  for (int b = 0; b < 2; ++b) {
+    int rc = c->stage[b].ensure(kStageChunk, "upload staging");
+    if (rc) return rc;
+    if (!c->stage_done[b]) HIP_TRY(hipEventCreateWithFlags(&c->stage_done[b], hipEventDisableTiming), "event");
+  }
+  uint8_t* d = static_cast<uint8_t*>(dev);
+  int k = 0;
+  for (uint64_t off = 0; off < n; off += kStageChunk, ++k) {
+    const int b = k & 1;
+    const size_t len = size_t(std::min<uint64_t>(kStageChunk, n - off));
+    if (k >= 2) HIP_TRY(hipEventSynchronize(c->stage_done[b]), "upload staging wait");  // chunk b is free
+    memcpy(c->stage[b].p, src + off, len);
+    HIP_TRY(hipMemcpyAsync(d + off, c->stage[b].p, len, hipMemcpyHostToDevice, c->stream), "weight upload");
+    HIP_TRY(hipEventRecord(c->stage_done[b], c->stream), "event");
+  }
+  HIP_TRY(hipStreamSynchronize(c->stream), "weight upload");
+  return SH_OK;
 }
 
 // Evicts least-recently-used entries until `incoming` more bytes fit, or the
@@ -166,11 +193,10 @@ int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uin
   r.bytes = nbytes;
   hipError_t e = hipMalloc(&r.dev, nbytes ? nbytes : 1);
   if (e != hipSuccess) return hip_fail(e, "uploading weight");
-  e = hipMemcpyAsync(r.dev, data, nbytes, hipMemcpyHostToDevice, c->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-  if (e != hipSuccess) {
+  const int rc = staged_upload(c, r.dev, data, nbytes);
+  if (rc != SH_OK) {
     (void)hipFree(r.dev);
-    return hip_fail(e, "uploading weight");
+    return rc;
   }
   r.used = ++c->clock;
   c->bytes += nbytes;
@@ -265,6 +291,10 @@ int sh_destroy(sh_context* c) {
     c->d_blk.release();
     c->h_in.release();
     c->h_out.release();
+    for (int b = 0; b < 2; ++b) {
+      c->stage[b].release();
+      if (c->stage_done[b]) (void)hipEventDestroy(c->stage_done[b]);
+    }
     (void)hipStreamDestroy(c->stream);
   }
   delete c;
@@ -978,4 +1008,155 @@ int sh_add_dev(float* a, const float* b, uint64_t n, void* stream) {
   if (!a || !b) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
   HIP_TRY(sh::launch_add(a, b, int64_t(n), static_cast<hipStream_t>(stream)), "add launch");
   return SH_OK;
+}
+
+// ---- GGUF weight source ---------------------------------------------------
+
+struct sh_gguf {
+  sh::GgufFile* f;
+};
+
+namespace {
+
+int gguf_fail(sh::GgufErr e, const std::string& msg) {
+  switch (e) {
+    case sh::GgufErr::kOk: return SH_OK;
+    case sh::GgufErr::kIo: return fail(SH_ERR_IO, "%s", msg.c_str());
+    case sh::GgufErr::kTruncated: return fail(SH_ERR_TRUNCATED, "%s", msg.c_str());
+    case sh::GgufErr::kUnsupportedQuant: return fail(SH_ERR_UNSUPPORTED_QUANT, "%s", msg.c_str());
+    default: return fail(SH_ERR_FORMAT, "%s", msg.c_str());
+  }
+}
+
+const sh::GgufMeta* meta_of(const sh_gguf* g, const char* key) {
+  if (!g || !key) return nullptr;
+  auto it = g->f->meta.find(key);
+  return it == g->f->meta.end() ? nullptr : &it->second;
+}
+
+bool meta_integer(uint32_t t) { return t <= 5 || t == 7 || t == 10 || t == 11; }  // MetaValue::as_int
+bool meta_number(uint32_t t) { return t != 8 && t != 9; }                          // MetaValue::is_num
+
+}  // namespace
+
+int sh_gguf_open(const char* path, sh_gguf** out) {
+  if (!path || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  sh::GgufFile* f = nullptr;
+  std::string msg;
+  const sh::GgufErr e = sh::gguf_open(path, &f, &msg);
+  if (e != sh::GgufErr::kOk) return gguf_fail(e, msg);
+  *out = new sh_gguf{f};
+  return SH_OK;
+}
+
+int sh_gguf_close(sh_gguf* g) {
+  if (g) {
+    delete g->f;
+    delete g;
+  }
+  return SH_OK;
+}
+
+int sh_gguf_header(const sh_gguf* g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv, uint64_t* alignment,
+                   uint64_t* data_start, uint64_t* file_size) {
+  if (!g) return fail(SH_ERR_INVALID_ARGUMENT, "null file");
+  if (version) *version = g->f->version;
+  if (n_tensors) *n_tensors = g->f->tensors.size();
+  if (n_kv) *n_kv = g->f->n_kv;
+  if (alignment) *alignment = g->f->alignment;
+  if (data_start) *data_start = g->f->data_start;
+  if (file_size) *file_size = g->f->size;
+  return SH_OK;
+}
+
+int sh_gguf_tensor(const sh_gguf* g, uint64_t index, sh_gguf_tensor_info* out) {
+  if (!g || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (index >= g->f->tensors.size())
+    return fail(SH_ERR_NOT_FOUND, "tensor %llu of %llu", (unsigned long long)index,
+                (unsigned long long)g->f->tensors.size());
+  const sh::GgufTensor& t = g->f->tensors[index];
+  out->name = t.name.c_str();
+  out->n_dims = uint32_t(t.shape.size());
+  out->type = t.ty;
+  for (int d = 0; d < 4; ++d) out->shape[d] = d < int(t.shape.size()) ? t.shape[d] : 1;
+  out->offset = t.offset;
+  std::string msg;
+  uint64_t nb = 0;
+  out->nbytes = sh::gguf_payload_bytes(t, &nb, &msg) == sh::GgufErr::kOk ? nb : 0;
+  return SH_OK;
+}
+
+int sh_gguf_find(const sh_gguf* g, const char* name, uint64_t* index) {
+  if (!g || !name || !index) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  auto it = g->f->index.find(name);
+  if (it == g->f->index.end()) return fail(SH_ERR_NOT_FOUND, "no tensor named %s", name);
+  *index = it->second;
+  return SH_OK;
+}
+
+int sh_gguf_tensor_data(const sh_gguf* g, uint64_t index, const uint8_t** data, uint64_t* nbytes) {
+  if (!g || !data || !nbytes) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (index >= g->f->tensors.size()) return fail(SH_ERR_NOT_FOUND, "tensor %llu", (unsigned long long)index);
+  std::string msg;
+  return gguf_fail(sh::gguf_tensor_data(*g->f, g->f->tensors[index], data, nbytes, &msg), msg);
+}
+
+int sh_gguf_meta_type(const sh_gguf* g, const char* key, uint32_t* type, uint32_t* elem, uint64_t* count) {
+  const sh::GgufMeta* m = meta_of(g, key);
+  if (!m) return fail(SH_ERR_NOT_FOUND, "no metadata key %s", key ? key : "(null)");
+  if (type) *type = m->ty;
+  if (elem) *elem = m->elem;
+  if (count) *count = m->count;
+  return SH_OK;
+}
+
+int sh_gguf_meta_int(const sh_gguf* g, const char* key, int64_t* value) {
+  const sh::GgufMeta* m = meta_of(g, key);
+  if (!m || !value || !meta_integer(m->ty))
+    return fail(SH_ERR_NOT_FOUND, "no integer metadata key %s", key ? key : "(null)");
+  *value = m->i;
+  return SH_OK;
+}
+
+int sh_gguf_meta_float(const sh_gguf* g, const char* key, double* value) {
+  const sh::GgufMeta* m = meta_of(g, key);
+  if (!m || !value || !meta_number(m->ty))
+    return fail(SH_ERR_NOT_FOUND, "no numeric metadata key %s", key ? key : "(null)");
+  *value = (m->ty == 6 || m->ty == 12) ? m->f : double(m->i);
+  return SH_OK;
+}
+
+int sh_gguf_meta_str(const sh_gguf* g, const char* key, const char** s, uint64_t* len) {
+  const sh::GgufMeta* m = meta_of(g, key);
+  if (!m || !s || m->ty != 8) return fail(SH_ERR_NOT_FOUND, "no string metadata key %s", key ? key : "(null)");
+  *s = m->s.c_str();
+  if (len) *len = m->s.size();
+  return SH_OK;
+}
+
+int sh_upload_gguf_tensor(sh_context* c, const sh_gguf* g, uint64_t index, uint64_t key) {
+  if (!c || !g) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (index >= g->f->tensors.size()) return fail(SH_ERR_NOT_FOUND, "tensor %llu", (unsigned long long)index);
+  const sh::GgufTensor& t = g->f->tensors[index];
+  if (!sh::gemv_quant(t.ty) && !sh::plain_quant(t.ty))
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "%s: type %u has no device kernel here", t.name.c_str(), t.ty);
+  if (t.shape.size() > 3)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "%s: %zu dims (matrices and expert stacks only)", t.name.c_str(),
+                t.shape.size());
+  const uint8_t* data = nullptr;
+  uint64_t nb = 0;
+  std::string msg;
+  const sh::GgufErr e = sh::gguf_tensor_data(*g->f, t, &data, &nb, &msg);
+  if (e != sh::GgufErr::kOk) return gguf_fail(e, msg);
+  // GGUF dims, fastest first: [cols, rows, n_expert] (weights.rs:14-34)
+  const uint64_t cols = t.shape[0];
+  const uint64_t rows = t.shape.size() > 1 ? t.shape[1] : 1;
+  const uint64_t n_expert = t.shape.size() > 2 ? t.shape[2] : 1;
+  if (cols % uint64_t(sh::geometry(t.ty).block) != 0)
+    return fail(SH_ERR_TRUNCATED, "%s: %llu columns are not whole blocks", t.name.c_str(), (unsigned long long)cols);
+  Guard gd(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident* r = nullptr;
+  return resident(c, key, t.ty, n_expert, rows, cols, data, nb, &r);
 }

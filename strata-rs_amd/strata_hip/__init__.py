@@ -42,6 +42,9 @@ SH_ERR_UNSUPPORTED_SHAPE = -5
 SH_ERR_NO_DEVICE = -6
 SH_ERR_DEVICE = -7
 SH_ERR_OUT_OF_MEMORY = -8
+SH_ERR_FORMAT = -9
+SH_ERR_IO = -10
+SH_ERR_NOT_FOUND = -11
 
 FLAG_Q6K_SIGNED_SCALES = 1
 MATMUL_BF16 = 0
@@ -56,7 +59,9 @@ EXPORTS = (
     "sh_moe_workspace_bytes", "sh_moe_ffn_dev", "sh_matmul_workspace_bytes", "sh_matmul_dev",
     "sh_quantize_q8_dev", "sh_moe_layer_workspace_bytes", "sh_moe_layer_dev", "sh_dequant_dev",
     "sh_gemv_dev", "sh_rms_norm", "sh_rope_neox", "sh_softmax", "sh_l2_norm", "sh_add", "sh_rms_norm_dev",
-    "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev",
+    "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev", "sh_gguf_open", "sh_gguf_close",
+    "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
+    "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor",
 )
 
 
@@ -93,11 +98,26 @@ class NoDeviceError(BackendError):
     pass
 
 
+class FormatError(BackendError):
+    """A malformed GGUF file (the reference reader's header errors)."""
+
+
+class NotFoundError(BackendError):
+    pass
+
+
+class IoError(BackendError):
+    pass
+
+
 _ERRORS = {
     SH_ERR_SHAPE: ShapeError,
     SH_ERR_TRUNCATED: TruncatedError,
     SH_ERR_UNSUPPORTED_QUANT: UnsupportedQuantError,
     SH_ERR_NO_DEVICE: NoDeviceError,
+    SH_ERR_FORMAT: FormatError,
+    SH_ERR_IO: IoError,
+    SH_ERR_NOT_FOUND: NotFoundError,
 }
 
 
@@ -115,6 +135,11 @@ class _ExpertViewC(C.Structure):
     _fields_ = [("key", C.c_uint64), ("quant", C.c_uint32), ("flags", C.c_uint32),
                 ("n_expert", C.c_uint64), ("rows", C.c_uint64), ("cols", C.c_uint64),
                 ("data", C.c_void_p), ("nbytes", C.c_uint64)]
+
+
+class _GgufTensorInfoC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("type", C.c_uint32), ("shape", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
 
 
 class _RopeCfgC(C.Structure):
@@ -193,6 +218,18 @@ def load_library() -> C.CDLL:
     L.sh_softmax_dev.argtypes = [vp, u64, u64, vp]
     L.sh_rope_neox_dev.argtypes = [vp, u64, u64, ropep, vp]
     L.sh_add_dev.argtypes = [vp, vp, u64, vp]
+    u64p, u32p = C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)
+    L.sh_gguf_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+    L.sh_gguf_close.argtypes = [vp]
+    L.sh_gguf_header.argtypes = [vp, u32p, u64p, u64p, u64p, u64p, u64p]
+    L.sh_gguf_tensor.argtypes = [vp, u64, C.POINTER(_GgufTensorInfoC)]
+    L.sh_gguf_find.argtypes = [vp, C.c_char_p, u64p]
+    L.sh_gguf_tensor_data.argtypes = [vp, u64, C.POINTER(vp), u64p]
+    L.sh_gguf_meta_type.argtypes = [vp, C.c_char_p, u32p, u32p, u64p]
+    L.sh_gguf_meta_int.argtypes = [vp, C.c_char_p, C.POINTER(C.c_int64)]
+    L.sh_gguf_meta_float.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double)]
+    L.sh_gguf_meta_str.argtypes = [vp, C.c_char_p, C.POINTER(C.c_char_p), u64p]
+    L.sh_upload_gguf_tensor.argtypes = [vp, vp, u64, u64]
     _lib = L
     return L
 
@@ -289,6 +326,97 @@ def _f32_out(y) -> np.ndarray:
     if not (isinstance(y, np.ndarray) and y.dtype == np.float32 and y.flags.c_contiguous):
         raise TypeError("output must be a C-contiguous float32 numpy array")
     return y
+
+
+@dataclass
+class GgufTensorInfo:
+    """TensorInfo (crates/strata-gguf/src/reader.rs:179-197) and its payload size."""
+    name: str
+    shape: list
+    type: int
+    offset: int
+    nbytes: int
+
+
+class GgufFile:
+    """GgufFile (reader.rs:200-445) over the library's reader: the file is
+    mapped until close(); tensor_data() views point into the mapping."""
+
+    def __init__(self, path: str):
+        self._L = load_library()
+        h = C.c_void_p()
+        check(self._L.sh_gguf_open(os.fsencode(path), C.byref(h)))
+        self._h = h
+        v, nt, nkv, al, ds, fs = C.c_uint32(), *(C.c_uint64() for _ in range(5))
+        check(self._L.sh_gguf_header(h, C.byref(v), C.byref(nt), C.byref(nkv), C.byref(al), C.byref(ds),
+                                     C.byref(fs)))
+        self.version, self.n_tensors, self.n_kv = v.value, nt.value, nkv.value
+        self.alignment, self.data_start, self.file_size = al.value, ds.value, fs.value
+
+    def close(self) -> None:
+        if self._h:
+            self._L.sh_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, index: int) -> GgufTensorInfo:
+        t = _GgufTensorInfoC()
+        check(self._L.sh_gguf_tensor(self._h, index, C.byref(t)))
+        return GgufTensorInfo(t.name.decode(), list(t.shape[:t.n_dims]), t.type, t.offset, t.nbytes)
+
+    def tensors(self) -> list:
+        return [self.tensor(i) for i in range(self.n_tensors)]
+
+    def find(self, name: str) -> int | None:
+        i = C.c_uint64()
+        rc = self._L.sh_gguf_find(self._h, name.encode(), C.byref(i))
+        if rc == SH_ERR_NOT_FOUND:
+            return None
+        check(rc)
+        return i.value
+
+    def tensor_data(self, index: int) -> np.ndarray:
+        p, n = C.c_void_p(), C.c_uint64()
+        check(self._L.sh_gguf_tensor_data(self._h, index, C.byref(p), C.byref(n)))
+        if n.value == 0:
+            return np.zeros(0, np.uint8)
+        v = np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p.value))
+        v.flags.writeable = False
+        return v
+
+    def meta_type(self, key: str):
+        t, e, c = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        rc = self._L.sh_gguf_meta_type(self._h, key.encode(), C.byref(t), C.byref(e), C.byref(c))
+        if rc == SH_ERR_NOT_FOUND:
+            return None
+        check(rc)
+        return t.value, e.value, c.value
+
+    def get_int(self, key: str):
+        v = C.c_int64()
+        rc = self._L.sh_gguf_meta_int(self._h, key.encode(), C.byref(v))
+        return None if rc == SH_ERR_NOT_FOUND else (check(rc), v.value)[1]
+
+    def get_float(self, key: str):
+        v = C.c_double()
+        rc = self._L.sh_gguf_meta_float(self._h, key.encode(), C.byref(v))
+        return None if rc == SH_ERR_NOT_FOUND else (check(rc), v.value)[1]
+
+    def get_str(self, key: str):
+        s, n = C.c_char_p(), C.c_uint64()
+        rc = self._L.sh_gguf_meta_str(self._h, key.encode(), C.byref(s), C.byref(n))
+        return None if rc == SH_ERR_NOT_FOUND else (check(rc), C.string_at(s, n.value).decode())[1]
 
 
 class HipBackend:
@@ -440,6 +568,11 @@ class HipBackend:
         if bv.size != av.size:
             raise ShapeError(SH_ERR_SHAPE, f"b has {bv.size} elements, a {av.size}")
         check(self._L.sh_add(self._ctx, av.ctypes.data, bv.ctypes.data, av.size))
+
+    def upload_gguf(self, f: GgufFile, index: int, name: str) -> None:
+        """Admits tensor `index` of an open GGUF file into the resident store
+        under `name` (the key later QuantTensor / ExpertView calls use)."""
+        check(self._L.sh_upload_gguf_tensor(self._ctx, f._h, index, name_key(name)))
 
     def dequantize_row(self, quant: int, block, out: np.ndarray, flags: int = 0) -> None:
         """dequantize_row (crates/strata-gguf/src/dequant.rs:45-61) on the device."""
