@@ -329,6 +329,20 @@ int sh_gguf_meta_type(const sh_gguf* gguf, const char* key, uint32_t* type, uint
 int sh_gguf_meta_int(const sh_gguf* gguf, const char* key, int64_t* value);
 int sh_gguf_meta_float(const sh_gguf* gguf, const char* key, double* value);
 int sh_gguf_meta_str(const sh_gguf* gguf, const char* key, const char** s, uint64_t* len);
+/* A whole model: GgufModel (reader.rs:450-522). `any_shard` of a split
+ * model `<name>-NNNNN-of-MMMMM.gguf` opens every shard (split_paths,
+ * reader.rs:524-572; a missing one is SH_ERR_IO naming it); any other path
+ * is a single shard. Metadata lives in shard 0. The shard handles are
+ * borrowed: valid until sh_gguf_model_close (sh_gguf_close on them is a
+ * no-op). A tensor name in two shards is SH_ERR_FORMAT. */
+typedef struct sh_gguf_model sh_gguf_model;
+int sh_gguf_model_open(const char* any_shard, sh_gguf_model** out);
+int sh_gguf_model_close(sh_gguf_model* model);
+int sh_gguf_model_shards(const sh_gguf_model* model, uint64_t* n_shards);
+int sh_gguf_model_shard(sh_gguf_model* model, uint64_t i, sh_gguf** shard);
+/* GgufModel::find (reader.rs:496-501): the shard and its tensor index. */
+int sh_gguf_model_find(const sh_gguf_model* model, const char* name, uint64_t* shard, uint64_t* index);
+
 /* Admits tensor `index` into ctx's resident store under `key`, packed as
  * stored, copied from the mapping through pinned staging chunks. Dims map
  * as [cols, rows, n_expert] (weights.rs:14-34), so a later sh_gemv /

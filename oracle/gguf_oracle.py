@@ -227,3 +227,24 @@ def open_file(path: str) -> GgufFile:
     except OSError as e:
         raise GgufError("io", str(e)) from e
     return parse(data)
+
+
+def split_paths(any_path: str) -> list:
+    """reader.rs:524-572."""
+    import os
+    at = any_path.rfind("-of-")
+    if at < 0 or at < 6 or any_path[at - 6] != "-" or len(any_path) != at + 14 or any_path[at + 9:at + 14] != ".gguf":
+        return [any_path]
+    a, b = any_path[at - 5:at], any_path[at + 4:at + 9]
+    if not (a.isascii() and a.isdigit() and b.isascii() and b.isdigit()):
+        return [any_path]
+    no, n = int(a), int(b)
+    if n < 1 or no < 1 or no > n:
+        return [any_path]
+    out = []
+    for i in range(1, n + 1):
+        p = any_path[:at - 5] + f"{i:05d}" + any_path[at:]
+        if not os.path.exists(p):
+            raise GgufError("io", f"{p}: missing model shard {i} of {n}")
+        out.append(p)
+    return out

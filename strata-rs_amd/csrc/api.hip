@@ -1033,6 +1033,12 @@ int sh_add_dev(float* a, const float* b, uint64_t n, void* stream) {
 
 struct sh_gguf {
   sh::GgufFile* f;
+  bool owned;  // false for a shard handle lent out by a model
+};
+
+struct sh_gguf_model {
+  sh::GgufModel* m;
+  std::vector<sh_gguf> shards;  // borrowed handles onto m's files
 };
 
 namespace {
@@ -1065,15 +1071,58 @@ int sh_gguf_open(const char* path, sh_gguf** out) {
   std::string msg;
   const sh::GgufErr e = sh::gguf_open(path, &f, &msg);
   if (e != sh::GgufErr::kOk) return gguf_fail(e, msg);
-  *out = new sh_gguf{f};
+  *out = new sh_gguf{f, true};
   return SH_OK;
 }
 
 int sh_gguf_close(sh_gguf* g) {
-  if (g) {
+  if (g && g->owned) {
     delete g->f;
     delete g;
   }
+  return SH_OK;
+}
+
+int sh_gguf_model_open(const char* any_shard, sh_gguf_model** out) {
+  if (!any_shard || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  sh::GgufModel* m = nullptr;
+  std::string msg;
+  const sh::GgufErr e = sh::gguf_model_open(any_shard, &m, &msg);
+  if (e != sh::GgufErr::kOk) return gguf_fail(e, msg);
+  sh_gguf_model* h = new sh_gguf_model{m, {}};
+  for (sh::GgufFile* f : m->shards) h->shards.push_back(sh_gguf{f, false});
+  *out = h;
+  return SH_OK;
+}
+
+int sh_gguf_model_close(sh_gguf_model* m) {
+  if (m) {
+    delete m->m;
+    delete m;
+  }
+  return SH_OK;
+}
+
+int sh_gguf_model_shards(const sh_gguf_model* m, uint64_t* n) {
+  if (!m || !n) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  *n = m->shards.size();
+  return SH_OK;
+}
+
+int sh_gguf_model_shard(sh_gguf_model* m, uint64_t i, sh_gguf** shard) {
+  if (!m || !shard) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (i >= m->shards.size()) return fail(SH_ERR_NOT_FOUND, "shard %llu of %zu", (unsigned long long)i, m->shards.size());
+  *shard = &m->shards[i];
+  return SH_OK;
+}
+
+int sh_gguf_model_find(const sh_gguf_model* m, const char* name, uint64_t* shard, uint64_t* index) {
+  if (!m || !name || !shard || !index) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  auto it = m->m->index.find(name);
+  if (it == m->m->index.end()) return fail(SH_ERR_NOT_FOUND, "no tensor named %s", name);
+  *shard = it->second.first;
+  *index = it->second.second;
   return SH_OK;
 }
 

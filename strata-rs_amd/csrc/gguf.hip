@@ -332,4 +332,76 @@ GgufErr gguf_tensor_data(const GgufFile& f, const GgufTensor& t, const uint8_t**
   return GgufErr::kOk;
 }
 
+static bool is_digit(char c) { return c >= '0' && c <= '9'; }
+
+GgufErr gguf_split_paths(const std::string& s, std::vector<std::string>* out, std::string* msg) {
+  out->clear();
+  const size_t at = s.rfind("-of-");
+  const bool shape = at != std::string::npos && at >= 6 && s[at - 6] == '-' && s.size() == at + 14 &&
+                     s.compare(at + 9, 5, ".gguf") == 0;
+  size_t no = 0, n = 0;
+  bool digits = shape;
+  for (int i = 0; shape && i < 5; ++i) {
+    const char a = s[at - 5 + i], b = s[at + 4 + i];
+    if (!is_digit(a) || !is_digit(b)) {
+      digits = false;
+      break;
+    }
+    no = no * 10 + size_t(a - '0');
+    n = n * 10 + size_t(b - '0');
+  }
+  if (!digits || n < 1 || no < 1 || no > n) {
+    out->push_back(s);
+    return GgufErr::kOk;
+  }
+  for (size_t i = 1; i <= n; ++i) {
+    char num[8];
+    snprintf(num, sizeof num, "%05zu", i);
+    std::string p = s;
+    p.replace(at - 5, 5, num);
+    struct stat st;
+    if (stat(p.c_str(), &st) != 0) {
+      out->clear();
+      *msg = p + ": missing model shard " + std::to_string(i) + " of " + std::to_string(n) +
+             " (is the download complete?)";
+      return GgufErr::kIo;
+    }
+    out->push_back(p);
+  }
+  return GgufErr::kOk;
+}
+
+GgufModel::~GgufModel() {
+  for (GgufFile* f : shards) delete f;
+}
+
+GgufErr gguf_model_open(const char* any_shard, GgufModel** out, std::string* msg) {
+  *out = nullptr;
+  std::vector<std::string> paths;
+  GgufErr e = gguf_split_paths(any_shard, &paths, msg);
+  if (e != GgufErr::kOk) return e;
+  GgufModel* m = new GgufModel;
+  for (const std::string& p : paths) {
+    GgufFile* f = nullptr;
+    e = gguf_open(p.c_str(), &f, msg);
+    if (e != GgufErr::kOk) {
+      delete m;
+      return e;
+    }
+    m->shards.push_back(f);
+  }
+  for (size_t si = 0; si < m->shards.size(); ++si) {
+    const std::vector<GgufTensor>& ts = m->shards[si]->tensors;
+    for (size_t ti = 0; ti < ts.size(); ++ti) {
+      if (!m->index.emplace(ts[ti].name, std::make_pair(si, ti)).second) {
+        *msg = "tensor " + ts[ti].name + " is in two shards";
+        delete m;
+        return GgufErr::kDuplicateTensor;
+      }
+    }
+  }
+  *out = m;
+  return GgufErr::kOk;
+}
+
 }  // namespace sh

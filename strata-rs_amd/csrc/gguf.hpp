@@ -73,4 +73,18 @@ GgufErr gguf_payload_bytes(const GgufTensor& t, uint64_t* bytes, std::string* ms
 GgufErr gguf_tensor_data(const GgufFile& f, const GgufTensor& t, const uint8_t** data, uint64_t* bytes,
                          std::string* msg);
 
+// split_paths (reader.rs:524-572): the shards of `<name>-NNNNN-of-MMMMM.gguf`
+// in split order; any other path is a single-shard model. A missing shard is
+// kIo with a message naming it.
+GgufErr gguf_split_paths(const std::string& any, std::vector<std::string>* out, std::string* msg);
+
+// GgufModel (reader.rs:450-522): every shard, one name index across them (a
+// name in two shards is kDuplicateTensor).
+struct GgufModel {
+  std::vector<GgufFile*> shards;
+  std::unordered_map<std::string, std::pair<size_t, size_t>> index;  // name -> (shard, tensor)
+  ~GgufModel();
+};
+GgufErr gguf_model_open(const char* any_shard, GgufModel** out, std::string* msg);
+
 }  // namespace sh

@@ -61,7 +61,8 @@ EXPORTS = (
     "sh_gemv_dev", "sh_rms_norm", "sh_rope_neox", "sh_softmax", "sh_l2_norm", "sh_add", "sh_rms_norm_dev",
     "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev", "sh_gguf_open", "sh_gguf_close",
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
-    "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor",
+    "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
+    "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find",
 )
 
 
@@ -230,6 +231,11 @@ def load_library() -> C.CDLL:
     L.sh_gguf_meta_float.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double)]
     L.sh_gguf_meta_str.argtypes = [vp, C.c_char_p, C.POINTER(C.c_char_p), u64p]
     L.sh_upload_gguf_tensor.argtypes = [vp, vp, u64, u64]
+    L.sh_gguf_model_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+    L.sh_gguf_model_close.argtypes = [vp]
+    L.sh_gguf_model_shards.argtypes = [vp, u64p]
+    L.sh_gguf_model_shard.argtypes = [vp, u64, C.POINTER(vp)]
+    L.sh_gguf_model_find.argtypes = [vp, C.c_char_p, u64p, u64p]
     _lib = L
     return L
 
@@ -342,10 +348,14 @@ class GgufFile:
     """GgufFile (reader.rs:200-445) over the library's reader: the file is
     mapped until close(); tensor_data() views point into the mapping."""
 
-    def __init__(self, path: str):
+    def __init__(self, path: str | None = None, _borrowed=None):
         self._L = load_library()
-        h = C.c_void_p()
-        check(self._L.sh_gguf_open(os.fsencode(path), C.byref(h)))
+        self._owned = _borrowed is None
+        if self._owned:
+            h = C.c_void_p()
+            check(self._L.sh_gguf_open(os.fsencode(path), C.byref(h)))
+        else:
+            h = _borrowed
         self._h = h
         v, nt, nkv, al, ds, fs = C.c_uint32(), *(C.c_uint64() for _ in range(5))
         check(self._L.sh_gguf_header(h, C.byref(v), C.byref(nt), C.byref(nkv), C.byref(al), C.byref(ds),
@@ -354,9 +364,9 @@ class GgufFile:
         self.alignment, self.data_start, self.file_size = al.value, ds.value, fs.value
 
     def close(self) -> None:
-        if self._h:
+        if self._h and self._owned:
             self._L.sh_gguf_close(self._h)
-            self._h = None
+        self._h = None
 
     def __enter__(self):
         return self
@@ -417,6 +427,65 @@ class GgufFile:
         s, n = C.c_char_p(), C.c_uint64()
         rc = self._L.sh_gguf_meta_str(self._h, key.encode(), C.byref(s), C.byref(n))
         return None if rc == SH_ERR_NOT_FOUND else (check(rc), C.string_at(s, n.value).decode())[1]
+
+
+class GgufModel:
+    """GgufModel (reader.rs:450-522): every shard of a split model, one name
+    index; shard(i) lends a GgufFile valid until close()."""
+
+    def __init__(self, any_shard: str):
+        self._L = load_library()
+        h = C.c_void_p()
+        check(self._L.sh_gguf_model_open(os.fsencode(any_shard), C.byref(h)))
+        self._h = h
+        n = C.c_uint64()
+        check(self._L.sh_gguf_model_shards(h, C.byref(n)))
+        self._shards = []
+        for i in range(n.value):
+            sh = C.c_void_p()
+            check(self._L.sh_gguf_model_shard(h, i, C.byref(sh)))
+            self._shards.append(GgufFile(_borrowed=sh))
+
+    @property
+    def n_shards(self) -> int:
+        return len(self._shards)
+
+    def shard(self, i: int) -> GgufFile:
+        return self._shards[i]
+
+    def meta(self) -> GgufFile:
+        return self._shards[0]
+
+    def find(self, name: str):
+        si, ti = C.c_uint64(), C.c_uint64()
+        rc = self._L.sh_gguf_model_find(self._h, name.encode(), C.byref(si), C.byref(ti))
+        if rc == SH_ERR_NOT_FOUND:
+            return None
+        check(rc)
+        return si.value, ti.value
+
+    def tensor_data(self, name: str):
+        f = self.find(name)
+        return None if f is None else self._shards[f[0]].tensor_data(f[1])
+
+    def close(self) -> None:
+        if self._h:
+            for sh in self._shards:
+                sh.close()
+            self._L.sh_gguf_model_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class HipBackend:

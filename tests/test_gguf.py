@@ -291,3 +291,51 @@ def test_last_key_wins(tmp_path):
     raw = Writer().kv("k", U32, 1).kv("k", STRING, "two").finish()
     f = compare(write(tmp_path, "dupkey", raw), raw)
     assert f.get_str("k") == "two" and f.n_kv == 2
+
+
+# ---- split models (reader.rs:450-572) ------------------------------------------
+
+def test_split_paths_resolves_siblings(tmp_path):
+    # reader_tests.rs:282-290, with the library's model open as the probe
+    single = str(tmp_path / "qwen4exp-q2_0.gguf")
+    assert G.split_paths(single) == [single]
+    missing = str(tmp_path / "model-00001-of-00002.gguf")
+    with pytest.raises(G.GgufError) as e:
+        G.split_paths(missing)
+    assert e.value.kind == "io"
+    (tmp_path / "model-00001-of-00002.gguf").write_bytes(Writer().finish())
+    with pytest.raises(H.IoError) as e:
+        H.GgufModel(missing)
+    assert "00002" in str(e.value)
+    # shapes that are not a split suffix are single files
+    for odd in ("m-00001-of-0000x.gguf", "m-00003-of-00002.gguf", "m-00000-of-00002.gguf", "m00001-of-00002.gguf",
+                "m-00001-of-00002.ggml", "m-0001-of-00002.gguf"):
+        assert G.split_paths(str(tmp_path / odd)) == [str(tmp_path / odd)]
+
+
+def test_multi_shard_model_reads_tensors_across_shards(tmp_path):
+    # reader_tests.rs:292-331
+    w1 = Writer()
+    qwen4exp_metadata(w1)
+    w1.kv("split.count", U32, 2).kv("split.no", U32, 0).kv("split.tensors.count", U32, 2)
+    w1.tensor("token_embd.weight", [32], 0, b"\0" * 128)
+    w2 = Writer()
+    w2.kv("split.count", U32, 2).kv("split.no", U32, 1).kv("split.tensors.count", U32, 2)
+    w2.tensor("output.weight", [32], 0, b"\1" * 128)
+    p1 = tmp_path / "strata-rs-test-model-00001-of-00002.gguf"
+    p2 = tmp_path / "strata-rs-test-model-00002-of-00002.gguf"
+    p1.write_bytes(w1.finish())
+    p2.write_bytes(w2.finish())
+    assert G.split_paths(str(p2)) == [str(p1), str(p2)]
+    with H.GgufModel(str(p2)) as m:
+        assert m.n_shards == 2
+        assert m.meta().get_str("general.architecture") == "qwen4exp"
+        assert m.find("token_embd.weight") == (0, 0)
+        assert m.find("output.weight") == (1, 0)
+        assert m.find("nope") is None
+        assert m.tensor_data("output.weight")[0] == 1
+    # a name in both shards is refused
+    w3 = Writer().kv("split.no", U32, 1).tensor("token_embd.weight", [32], 0, b"\0" * 128)
+    p2.write_bytes(w3.finish())
+    with pytest.raises(H.FormatError):
+        H.GgufModel(str(p1))
