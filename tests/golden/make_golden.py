@@ -16,8 +16,9 @@ reference_kats.json
 seeded_cases.npz
     Small seeded cases with the oracle's outputs (the C restatement of the
     reference, sequential f64 sums): dequantized rows and gemv outputs for
-    Q8_0, Q4_K and Q6_K (both scale readings), an expert gemv, MoE routing,
-    the routed MoE FFN and the Q8 activation quantizer. They let a machine
+    Q8_0, Q4_K, Q5_K and Q6_K (both scale readings), an expert gemv, MoE
+    routing, the routed MoE FFN, the Q8 activation quantizer, and the
+    elementwise methods (rms_norm, l2_norm, softmax, rope_neox) on rows. They let a machine
     without the oracle check the device path against fixed numbers. The MoE
     expert tensors are stored as the seeds of strata_hip.synth.matrix (their
     bytes would be most of the file); every other input is stored as data.
@@ -103,7 +104,7 @@ MOE_SEEDS = (0x601D0401, 0x601D0402, 0x601D0403)
 
 def seeded_cases():
     out = {}
-    for quant, rows, cols in ((8, 16, 256), (12, 16, 512), (14, 16, 512)):
+    for quant, rows, cols in ((8, 16, 256), (12, 16, 512), (14, 16, 512), (13, 16, 512)):
         w = S.matrix(quant, 0x601D0000 + quant, rows, cols)
         x = S.normal_f32(0x601D0100 + quant, cols)
         out[f"gemv_{quant}_w"] = w
@@ -143,6 +144,13 @@ def seeded_cases():
     xa[:32] = 0.0
     q, s, us = O.quantize_q8(xa)
     out.update(q8_x=xa, q8_codes=q, q8_scales=s, q8_sums=us)
+    # the elementwise methods: 3 rows of 1024 (rms_norm, softmax), 8 heads of
+    # 128 (l2_norm; rope with 64 rotated dims at position 4097, base 1e7)
+    xr = S.normal_f32(0x601D0600, 3 * 1024).reshape(3, 1024) * np.float32(2.0)
+    wr = S.normal_f32(0x601D0601, 1024)
+    hr = S.normal_f32(0x601D0602, 8 * 128).reshape(8, 128)
+    out.update(row_x=xr, row_w=wr, row_heads=hr, row_rms=O.rms_norm(xr, wr, 1e-6), row_softmax=O.softmax(xr),
+               row_l2=O.l2_norm(hr, 1e-6), row_rope=O.rope_neox(hr, 4097, 64, 128, 1e7))
     return out
 
 

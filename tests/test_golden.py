@@ -42,7 +42,7 @@ def test_reference_kat(oracle, k):
         assert abs(float(y[0]) - kat["expect"][0]) < kat["tol"]
 
 
-@pytest.mark.parametrize("quant,rows,cols", [(8, 16, 256), (12, 16, 512), (14, 16, 512)])
+@pytest.mark.parametrize("quant,rows,cols", [(8, 16, 256), (12, 16, 512), (14, 16, 512), (13, 16, 512)])
 def test_seeded_gemv_and_dequant(oracle, quant, rows, cols):
     c = cases()
     w, x = c[f"gemv_{quant}_w"], c[f"gemv_{quant}_x"]
@@ -72,3 +72,11 @@ def test_seeded_expert_moe_and_q8(oracle):
     q, s, us = oracle.quantize_q8(c["q8_x"])
     assert np.array_equal(q, c["q8_codes"]) and np.array_equal(s, c["q8_scales"])
     assert np.array_equal(us, c["q8_sums"])
+
+
+def test_seeded_row_methods(oracle):
+    c = cases()
+    assert np.array_equal(oracle.rms_norm(c["row_x"], c["row_w"], 1e-6), c["row_rms"])
+    assert np.array_equal(oracle.softmax(c["row_x"]), c["row_softmax"])
+    assert np.array_equal(oracle.l2_norm(c["row_heads"], 1e-6), c["row_l2"])
+    assert np.array_equal(oracle.rope_neox(c["row_heads"], 4097, 64, 128, 1e7), c["row_rope"])

@@ -39,7 +39,7 @@ def test_reference_dequant_kats(backend):
             assert out[int(i)] == v, (kat["source"], i)
 
 
-@pytest.mark.parametrize("quant,rows,cols", [(8, 16, 256), (12, 16, 512), (14, 16, 512)])
+@pytest.mark.parametrize("quant,rows,cols", [(8, 16, 256), (12, 16, 512), (14, 16, 512), (13, 16, 512)])
 def test_golden_gemv_and_dequant(backend, quant, rows, cols):
     say("golden gemv", quant)
     c = cases()
@@ -95,3 +95,32 @@ def test_golden_q8_quantizer(backend):
     assert np.array_equal(q.cpu().numpy(), c["q8_codes"])
     assert np.array_equal(s.cpu().numpy().view(np.uint32), c["q8_scales"].view(np.uint32))
     assert np.array_equal(u.cpu().numpy().view(np.uint32), c["q8_sums"].view(np.uint32))
+
+
+def test_golden_row_methods(backend):
+    """The elementwise methods on the host-slice entry points against the
+    fixtures: within one ulp (softmax two), as their parity tests."""
+    say("golden row methods")
+    c = cases()
+
+    def ulps(a, b):
+        a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+        b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+        a = np.where(a < 0, -(a & 0x7FFFFFFF), a)
+        b = np.where(b < 0, -(b & 0x7FFFFFFF), b)
+        return int(np.abs(a - b).max())
+
+    for r in range(3):
+        x = c["row_x"][r].copy()
+        backend.rms_norm(x, c["row_w"], 1e-6)
+        assert ulps(x, c["row_rms"][r]) <= 1
+        x = c["row_x"][r].copy()
+        backend.softmax(x)
+        assert ulps(x, c["row_softmax"][r]) <= 2
+    for h in range(8):
+        x = c["row_heads"][h].copy()
+        backend.l2_norm(x, 1e-6)
+        assert ulps(x, c["row_l2"][h]) <= 1
+        x = c["row_heads"][h].copy()
+        backend.rope_neox(x, H.RopeCfg(pos=4097, n_rot=64, head_dim=128, freq_base=1e7))
+        assert ulps(x, c["row_rope"][h]) <= 1
