@@ -59,6 +59,15 @@ inline bool gemv_quant(uint32_t q) { return device_quant(q) || q == kQ5_K; }
 
 constexpr int kWave = 64;
 
+// bf16::from_f32(v).to_f32() (crates/strata-core/src/hyper.rs:22-24): round
+// to nearest even with v_cvt_pk_bf16_f32 (a NaN stays a NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float bf16_rne(float v) {
+  const bf16x2_t b = __builtin_convertvector((f32x2_t){v, 0.f}, bf16x2_t);
+  return __builtin_bit_cast(float, uint32_t(__builtin_bit_cast(uint32_t, b) & 0xFFFFu) << 16);
+}
+
 // A 16-byte vector that only promises 4-byte alignment: GGUF blocks of 34 and
 // 210 bytes start at 2-byte boundaries, so every wide load below goes through
 // a dword-aligned address and a realignment.

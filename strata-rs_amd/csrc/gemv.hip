@@ -1006,7 +1006,7 @@ __device__ __forceinline__ float plain_at(const uint8_t* row, int c) {
 
 constexpr int kPlainThreads = 256, kPlainUnroll = 8;
 
-template <int Q, int NB>
+template <int Q, int NB, bool XB>
 __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t* __restrict__ w, int rows, int cols,
                                                                   int64_t row_bytes, const float* __restrict__ x,
                                                                   float* __restrict__ y) {
@@ -1025,7 +1025,10 @@ __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t
       const int c = min(c0 + k * kPlainThreads + tid, cols - 1);
       wv[k] = plain_at<Q>(row, c);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) xv[k][b] = x[int64_t(b) * cols + c];
+      for (int b = 0; b < NB; ++b) {
+        const float v = x[int64_t(b) * cols + c];
+        xv[k][b] = XB ? bf16_rne(v) : v;  // XB: the matvec of bf16(x)
+      }
     }
 #pragma unroll
     for (int k = 0; k < kPlainUnroll; ++k) {
@@ -1051,19 +1054,19 @@ __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t
   }
 }
 
-template <int Q>
+template <int Q, bool XB>
 static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int64_t row_bytes, const float* x,
                                float* y, hipStream_t s) {
   const dim3 grid = dim3(unsigned(rows)), block = dim3(kPlainThreads);
   switch (nb) {
-    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8>), grid, block, 0, s, w, rows, cols, row_bytes, x, y);
+    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
+    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y);
   }
   return hipGetLastError();
 }
@@ -1176,9 +1179,9 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
     // elements are read at their own alignment (4 bytes for F32, 2 otherwise)
     if (reinterpret_cast<uintptr_t>(w) & uintptr_t(quant == kF32 ? 3 : 1)) return hipErrorInvalidValue;
     switch (quant) {
-      case kF32: return launch_plain<kF32>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
-      case kF16: return launch_plain<kF16>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
-      default: return launch_plain<kBF16>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+      case kF32: return launch_plain<kF32, false>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+      case kF16: return launch_plain<kF16, false>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+      default: return launch_plain<kBF16, false>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     }
   }
   // Q8_0 reads 68-byte block pairs with dword loads: rows must start on a
@@ -1222,6 +1225,19 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,
+                                   float* y, int batch, hipStream_t stream) {
+  if (!plain_quant(quant) || !gemv_shape_ok(quant, rows, cols, batch)) return hipErrorInvalidValue;
+  const uint8_t* w = static_cast<const uint8_t*>(wv);
+  if (reinterpret_cast<uintptr_t>(w) & uintptr_t(quant == kF32 ? 3 : 1)) return hipErrorInvalidValue;
+  const int64_t row_bytes = byte_size(quant, cols);
+  switch (quant) {
+    case kF32: return launch_plain<kF32, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+    case kF16: return launch_plain<kF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+    default: return launch_plain<kBF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+  }
 }
 
 }  // namespace sh

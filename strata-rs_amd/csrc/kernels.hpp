@@ -18,6 +18,9 @@ hipError_t launch_dequant(uint32_t quant, const void* w, int64_t rows, int64_t c
 bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
 hipError_t launch_gemv(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
                        float* y, int batch, int q6_signed, hipStream_t stream);
+// The same for F32 / F16 / BF16 rows against bf16(x) (rounded as loaded).
+hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
+                                   float* y, int batch, hipStream_t stream);
 
 // Batch 2..8 of Q4_K or Q5_K rows on int8 MFMA (exact integer
 // activations, staged in LDS 4096 columns at a time); `cu` is the device's
@@ -63,10 +66,17 @@ struct MoePlan {
 
 bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t q_gateup,
               uint32_t q_down, MoePlan* plan);
+// The shared expert's part of the layer's combine: out[t] += sigmoid(s[t])
+// * d[t] after the routed sum, once `join` (if any) has completed.
+struct MoeShared {
+  const float* d;
+  const float* s;
+  hipEvent_t join;
+};
 hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, const void* gate,
                       const void* up, const void* down, int q6g, int q6u, int q6d,
                       const float* logits, const float* x, float* out, void* workspace,
-                      hipStream_t s);
+                      hipStream_t s, const MoeShared* shared = nullptr);
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
 
 // The whole MoE layer (router matvec on bf16-rounded x, routed experts,

@@ -629,7 +629,8 @@ __global__ void __launch_bounds__(kMoeThreads)
 // skipping w == 0 (moe.rs:112-126).
 __device__ __forceinline__ void combine_cols(const MoePlan& plan, const float* __restrict__ part,
                                              const int* qa, const float* wa, int t, int col0,
-                                             float* __restrict__ out, float (*dsum)[32]) {
+                                             float* __restrict__ out, float (*dsum)[32],
+                                             const float* sh_d = nullptr, const float* sh_s = nullptr) {
   const int cl = threadIdx.x & 31, al = threadIdx.x >> 5;
   for (int a = al; a < plan.top_k; a += 8) {
     const float* src = part + int64_t(qa[a]) * plan.nch_b * plan.n_embd + col0 + cl;
@@ -648,19 +649,29 @@ __device__ __forceinline__ void combine_cols(const MoePlan& plan, const float* _
       const float wv = wa[a];
       if (wv != 0.f) acc = __fadd_rn(acc, __fmul_rn(wv, dsum[a][cl]));
     }
+    if (sh_d) {
+      // the shared expert: sigmoid(v) = 1 / (1 + exp(-v)) (ops.rs:90-92), then
+      // one f32 product and one f32 add (moe.rs:139-142)
+      const float sv = sh_s[t];
+      const float gate = 1.f / (1.f + expf(-sv));
+      acc = __fadd_rn(acc, __fmul_rn(gate, sh_d[int64_t(t) * plan.n_embd + col0 + cl]));
+    }
     out[int64_t(t) * plan.n_embd + col0 + cl] = acc;
   }
 }
 
 // Block: 32 columns of one token.
+// With sh_d set (the whole layer), the shared expert's gated output is added
+// after the routed sum.
 __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const uint8_t* ws,
-                                                          float* __restrict__ out) {
+                                                          float* __restrict__ out, const float* __restrict__ sh_d,
+                                                          const float* __restrict__ sh_s) {
   __shared__ float dsum[kMoeMaxTopK][32];
   const int blocks_per_tok = plan.n_embd / 32;
   const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
   combine_cols(plan, reinterpret_cast<const float*>(ws + plan.o_part_b),
                reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k,
-               reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum);
+               reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum, sh_d, sh_s);
 }
 
 // ------------------------------------------------------------------- host --
@@ -790,7 +801,7 @@ static void launch_down(const MoePlan& p, const void* down, uint8_t* ws, int q6d
 hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, const void* gate,
                       const void* up, const void* down, int q6g, int q6u, int q6d,
                       const float* logits, const float* x, float* out, void* workspace,
-                      hipStream_t s) {
+                      hipStream_t s, const MoeShared* shared) {
   if (qg != qu) return hipErrorInvalidValue;  // gate and up share one kernel
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   // one token (decode): gate/up routes it itself; otherwise the route kernel
@@ -810,8 +821,12 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
     case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
     default: launch_down<HxQ6K>(p, down, ws, q6d, s);
   }
+  if (shared && shared->join) {
+    const hipError_t e = hipStreamWaitEvent(s, shared->join, 0);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned(p.n_tok * (p.n_embd / 32))), dim3(256), 0, s, p,
-                     ws, out);
+                     ws, out, shared ? shared->d : nullptr, shared ? shared->s : nullptr);
   return hipGetLastError();
 }
 

@@ -8,9 +8,11 @@
 //   shared   g = gate_shexp . x, u = up_shexp . x, h = silu(g) * u,
 //            d = down_shexp . h, s = gate_inp_shexp . x (ops::gemv each,
 //            moe.rs:129-138);
-//   combine  out += sigmoid(s) * d, after the routed sum (moe.rs:139-142).
+//   combine  out += sigmoid(s) * d, after the routed sum (moe.rs:139-142),
+//            inside the routed combine kernel.
 // The shared expert runs on a second stream, forked from and joined back to
-// the caller's, beside the route and the routed experts.
+// the caller's (just before the combine), beside the route and the routed
+// experts. A plain-float router rounds x to bf16 as its matvec loads it.
 // The matvecs are the library's gemv kernels (F32 / F16 / BF16 rows sum in
 // f64 as ops::gemv does; Q8_0 / Q4_K / Q6_K on the integer-limb path), up
 // to 8 tokens per launch.
@@ -19,16 +21,12 @@
 
 namespace sh {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// bf16::from_f32(v).to_f32(): round to nearest even (v_cvt_pk_bf16_f32;
-// a NaN stays a NaN).
+// bf16(x) for a quantized router (a plain-float router rounds x as it loads
+// it, inside the matvec).
 __global__ void bf16_round_kernel(const float* __restrict__ x, float* __restrict__ xb, int64_t n) {
   const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
   if (i >= n) return;
-  const bf16x2_t v = __builtin_convertvector((f32x2_t){x[i], 0.f}, bf16x2_t);
-  xb[i] = __builtin_bit_cast(float, uint32_t(__builtin_bit_cast(uint32_t, v) & 0xFFFFu) << 16);
+  xb[i] = bf16_rne(x[i]);
 }
 
 // h = silu(g) * u with silu(v) = v / (1 + exp(-v)) in f32 (ops.rs:85-87).
@@ -38,17 +36,6 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
   if (i >= n) return;
   const float v = g[i];
   h[i] = v / (1.f + expf(-v)) * u[i];
-}
-
-// out[t][i] += sigmoid(s[t]) * d[t][i], sigmoid(v) = 1 / (1 + exp(-v))
-// (ops.rs:90-92), one f32 product and one f32 add as moe.rs:139-142.
-__global__ void shexp_add_kernel(float* __restrict__ out, const float* __restrict__ d, const float* __restrict__ s,
-                                 int n_embd, int64_t n) {
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= n) return;
-  const float sv = s[i / n_embd];
-  const float gate = 1.f / (1.f + expf(-sv));
-  out[i] = __fadd_rn(out[i], __fmul_rn(gate, d[i]));
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -84,13 +71,16 @@ bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, in
   return true;
 }
 
-// y[t] = W . x[t] for t < n_tok, 8 tokens per launch.
+// y[t] = W . x[t] for t < n_tok, 8 tokens per launch; `xbf16`: W . bf16(x[t])
+// (plain-float W only).
 static hipError_t gemv_tokens(uint32_t quant, const void* w, int rows, int cols, const float* x, float* y,
-                              int n_tok, int q6s, hipStream_t s) {
+                              int n_tok, int q6s, hipStream_t s, bool xbf16 = false) {
   for (int t0 = 0; t0 < n_tok; t0 += 8) {
     const int nb = n_tok - t0 < 8 ? n_tok - t0 : 8;
-    const hipError_t e = launch_gemv(quant, w, rows, cols, x + int64_t(t0) * cols, y + int64_t(t0) * rows, nb,
-                                     q6s, s);
+    const float* xt = x + int64_t(t0) * cols;
+    float* yt = y + int64_t(t0) * rows;
+    const hipError_t e = xbf16 ? launch_gemv_plain_bf16x(quant, w, rows, cols, xt, yt, nb, s)
+                               : launch_gemv(quant, w, rows, cols, xt, yt, nb, q6s, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -172,14 +162,18 @@ hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const
     if ((r = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, ss)) != hipSuccess) return r;
     if ((r = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, ss)) != hipSuccess) return r;
     if (side && (r = hipEventRecord(join, side)) != hipSuccess) return r;
-    // route: router . bf16(x), then the routed experts into out
-    hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);
-    if ((r = gemv_tokens(q.router, w.router, E, n_embd, xb, logits, T, w.q6_router, s)) != hipSuccess) return r;
+    // route: router . bf16(x), then the routed experts into out; the combine
+    // waits for the shared expert and adds sigmoid(s) * d after the routed sum
+    if (plain_quant(q.router)) {
+      if ((r = gemv_tokens(q.router, w.router, E, n_embd, x, logits, T, 0, s, true)) != hipSuccess) return r;
+    } else {
+      hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);
+      if ((r = gemv_tokens(q.router, w.router, E, n_embd, xb, logits, T, w.q6_router, s)) != hipSuccess) return r;
+    }
+    const MoeShared shared{d, sg, side ? join : nullptr};
     if ((r = launch_moe(m, q.gate, q.up, q.down, w.gate, w.up, w.down, w.q6_gate, w.q6_up, w.q6_down, logits, x,
-                        out, workspace, s)) != hipSuccess)
+                        out, workspace, s, &shared)) != hipSuccess)
       return r;
-    if (side && (r = hipStreamWaitEvent(s, join, 0)) != hipSuccess) return r;
-    hipLaunchKernelGGL(shexp_add_kernel, blocks(nx), dim3(256), 0, s, out, d, sg, n_embd, nx);
     return hipGetLastError();
   };
   e = run();
