@@ -170,6 +170,17 @@ int sh_gemv_batch(sh_context* ctx, const sh_quant_tensor* w, const float* x, flo
 int sh_expert_gemv(sh_context* ctx, const sh_expert_view* w, uint64_t e, const float* x,
                    uint64_t x_len, float* y, uint64_t y_len);
 
+/* Admits a packed tensor into the resident store under `key` ahead of use
+ * (what the first matvec call with that key would do): idempotent, a key
+ * already resident with the same type and shape is left as it is, one with
+ * another is replaced; LRU under the budget. Layout as sh_expert_view /
+ * sh_quant_tensor (n_expert = 1 for a matrix). src_row_pitch: bytes from one
+ * row start to the next in `data` (0 = packed rows of byte_size(quant,
+ * cols)); rows are stored packed on the device. Later calls with the key
+ * may pass data = NULL. Types with a device kernel only. */
+int sh_weight_upload(sh_context* ctx, uint64_t key, uint32_t quant, uint64_t n_expert, uint64_t rows,
+                     uint64_t cols, const uint8_t* data, uint64_t src_row_pitch);
+
 /* ---- the trait's elementwise methods (host slices, synchronous) -------
  * ComputeBackend::{rms_norm, rope_neox, softmax, l2_norm, add}
  * (backend.rs:38-50) with the CPU bodies' arithmetic (ops.rs:46-165): f64

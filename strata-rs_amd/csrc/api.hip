@@ -15,6 +15,7 @@
 #include <string>
 #include <thread>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/strata_hip.h"
 #include "common.hpp"
@@ -1227,4 +1228,35 @@ int sh_upload_gguf_tensor(sh_context* c, const sh_gguf* g, uint64_t index, uint6
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   Resident* r = nullptr;
   return resident(c, key, t.ty, n_expert, rows, cols, data, nb, &r);
+}
+
+int sh_weight_upload(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uint64_t rows, uint64_t cols,
+                     const uint8_t* data, uint64_t src_row_pitch) {
+  if (!c || !data) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (!sh::gemv_quant(quant) && !sh::plain_quant(quant))
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "quant type id %u has no device kernel here", quant);
+  const sh::Geometry g = sh::geometry(quant);
+  if (cols % uint64_t(g.block) != 0)
+    return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of blocks", (unsigned long long)cols);
+  const uint64_t rb = cols / uint64_t(g.block) * uint64_t(g.bytes);
+  const uint64_t n_rows = n_expert * rows;
+  if (n_expert == 0 || (rows && n_rows / rows != n_expert) || (rb && n_rows > ~uint64_t(0) / rb))
+    return fail(SH_ERR_INVALID_ARGUMENT, "bad tensor shape");
+  if (src_row_pitch != 0 && src_row_pitch < rb)
+    return fail(SH_ERR_INVALID_ARGUMENT, "row pitch %llu is below the row size %llu",
+                (unsigned long long)src_row_pitch, (unsigned long long)rb);
+  Guard gd(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  Resident* r = nullptr;
+  if (src_row_pitch == 0 || src_row_pitch == rb || n_rows <= 1)
+    return resident(c, key, quant, n_expert, rows, cols, data, n_rows * rb, &r);
+  // pitched rows: packed into a host copy first
+  std::vector<uint8_t> packed;
+  try {
+    packed.resize(size_t(n_rows * rb));
+  } catch (const std::bad_alloc&) {
+    return fail(SH_ERR_OUT_OF_MEMORY, "host memory for re-pitching %llu rows", (unsigned long long)n_rows);
+  }
+  for (uint64_t i = 0; i < n_rows; ++i) memcpy(packed.data() + i * rb, data + i * src_row_pitch, size_t(rb));
+  return resident(c, key, quant, n_expert, rows, cols, packed.data(), n_rows * rb, &r);
 }

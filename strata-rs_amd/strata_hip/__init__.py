@@ -62,7 +62,7 @@ EXPORTS = (
     "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev", "sh_gguf_open", "sh_gguf_close",
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
-    "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find",
+    "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
 )
 
 
@@ -236,6 +236,7 @@ def load_library() -> C.CDLL:
     L.sh_gguf_model_shards.argtypes = [vp, u64p]
     L.sh_gguf_model_shard.argtypes = [vp, u64, C.POINTER(vp)]
     L.sh_gguf_model_find.argtypes = [vp, C.c_char_p, u64p, u64p]
+    L.sh_weight_upload.argtypes = [vp, u64, u32, u64, u64, u64, vp, u64]
     _lib = L
     return L
 
@@ -637,6 +638,14 @@ class HipBackend:
         if bv.size != av.size:
             raise ShapeError(SH_ERR_SHAPE, f"b has {bv.size} elements, a {av.size}")
         check(self._L.sh_add(self._ctx, av.ctypes.data, bv.ctypes.data, av.size))
+
+    def upload(self, name: str, quant: int, n_expert: int, rows: int, cols: int, data, row_pitch: int = 0) -> None:
+        """Admits a packed tensor under `name` ahead of its first use
+        (idempotent per name and shape); `row_pitch` bytes between row starts
+        in `data` (0: packed)."""
+        b = _bytes(data)
+        check(self._L.sh_weight_upload(self._ctx, name_key(name), int(quant), n_expert, rows, cols, b.ctypes.data,
+                                       row_pitch))
 
     def upload_gguf(self, f: GgufFile, index: int, name: str) -> None:
         """Admits tensor `index` of an open GGUF file into the resident store

@@ -81,3 +81,33 @@ def test_upload_from_gguf_then_matvec(tmp_path, oracle):
         check(y, oracle.expert_gemv(14, 4, 256, 512, ex, 2, x))
     finally:
         be.close()
+
+
+def test_weight_upload_pitched_and_idempotent(oracle):
+    """sh_weight_upload: rows given with a pitch (16 pad bytes after each
+    2304-byte Q4_K row) are stored packed; a second upload of the key is a
+    no-op; later calls pass a zero stand-in and still read the real rows."""
+    say("weight upload, pitched rows")
+    rows, cols = 96, 4096
+    w = S.matrix(12, 21, rows, cols)
+    rb = S.row_bytes(12, cols)
+    pitched = np.zeros((rows, rb + 16), np.uint8)
+    pitched[:, :rb] = w.reshape(rows, rb)
+    pitched[:, rb:] = 0xAB
+    be = H.HipBackend(0, 1 << 30)
+    try:
+        be.upload("pitched", 12, 1, rows, cols, pitched, row_pitch=rb + 16)
+        before = be.resident_bytes()
+        assert before == rows * rb
+        be.upload("pitched", 12, 1, rows, cols, pitched, row_pitch=rb + 16)
+        assert be.resident_bytes() == before
+        x = S.normal_f32(22, cols)
+        y = np.empty(rows, np.float32)
+        be.gemv(H.QuantTensor("pitched", 12, rows, cols, np.zeros(w.nbytes, np.uint8)), x, y)
+        check(y, oracle.gemv(12, rows, cols, w, x))
+        with pytest.raises(H.BackendError):
+            be.upload("bad", 12, 1, rows, cols, pitched, row_pitch=rb - 1)
+        with pytest.raises(H.UnsupportedQuantError):
+            be.upload("iq", 23, 1, 2, 256, np.zeros(272, np.uint8))
+    finally:
+        be.close()
