@@ -49,9 +49,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops"),
+    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
-                         "'moe' / 'prefill' / 'rowops': that extra alone (for profiling; prints its JSON)")
+                         "'moe' / 'prefill' / 'rowops' / 'ffn': that extra alone (for profiling; prints its JSON)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -321,6 +321,36 @@ def bench_rowops(torch, H, S, steps):
     return res
 
 
+def bench_ffn(torch, H, S, steps):
+    """The dense FFN half of a layer (rms_norm, gate, up, silu * up, down,
+    residual) at the dense config, Q4_K, hidden 4096, FFN 12288, one token,
+    over rotating copies of the three matrices (3 x 28.3 MB); us per call and
+    GB/s of the packed weights each call reads."""
+    import numpy as np
+    n_embd, n_ff = 4096, 12288
+    mats = [S.matrix(S.Q4_K, 0x5EED0071 + i, *((n_ff, n_embd) if i < 2 else (n_embd, n_ff))) for i in range(3)]
+    wbytes = sum(m.nbytes for m in mats)
+    dev = torch.device("cuda:0")
+    n_copies = 12  # 1.02 GB of weights: beyond the Infinity Cache
+    sets = [[torch.from_numpy(m).to(dev) for m in mats]] + [None] * (n_copies - 1)
+    for i in range(1, n_copies):
+        sets[i] = [t.clone() for t in sets[0]]
+    x = torch.from_numpy(S.normal_f32(0x5EED0074, n_embd)).to(dev)
+    norm = torch.from_numpy(S.normal_f32(0x5EED0075, n_embd)).to(dev)
+    out = torch.empty_like(x)
+    nb = H.ffn_workspace_bytes(1, n_embd, n_ff)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    calls = [lambda st, ts=ts: H.ffn_dev([(S.Q4_K, 0, t.data_ptr()) for t in ts], n_embd, n_ff, 1, x.data_ptr(),
+                                         norm.data_ptr(), 1e-6, out.data_ptr(), ws.data_ptr(), nb, st)
+             for ts in sets]
+    ms = time_calls(torch, calls, steps, len(calls))
+    del sets, ws
+    torch.cuda.empty_cache()
+    return {"ffn_q4k_4096x12288_1tok": {"us_per_call": round(ms * 1e3, 2),
+                                        "weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                                        "pct_hbm_peak": round(100 * wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}}
+
+
 def cpu_baseline(w, x, rows, cols, seconds):
     """The oracle (ops::gemv restated in C, one thread) on whole rows of the
     same matrix for about `seconds`; GB/s of packed weight bytes."""
@@ -401,6 +431,9 @@ def main():
         res.update(bench_moe_layer(torch, H, S, args.steps))
         print(json.dumps(res), flush=True)
         return
+    elif args.only == "ffn":
+        print(json.dumps(bench_ffn(torch, H, S, args.steps)), flush=True)
+        return
     elif args.only == "rowops":
         print(json.dumps(bench_rowops(torch, H, S, args.steps)), flush=True)
         return
@@ -470,6 +503,8 @@ def main():
         extra.update(bench_moe(torch, H, S, 240))
         print("[bench] extra moe layer", file=sys.stderr, flush=True)
         extra.update(bench_moe_layer(torch, H, S, 240))
+        print("[bench] extra dense ffn", file=sys.stderr, flush=True)
+        extra.update(bench_ffn(torch, H, S, 240))
         print("[bench] extra elementwise methods", file=sys.stderr, flush=True)
         extra.update(bench_rowops(torch, H, S, 200))
         out["extra"] = extra

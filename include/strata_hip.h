@@ -361,6 +361,21 @@ int sh_gguf_model_find(const sh_gguf_model* model, const char* name, uint64_t* s
  * resident. Types with a device kernel only; 1 to 3 dims. */
 int sh_upload_gguf_tensor(sh_context* ctx, const sh_gguf* gguf, uint64_t index, uint64_t key);
 
+/* The dense FFN half of a decoder layer (crates/strata-core/src/qwen35.rs:
+ * 112-129) for n_tok tokens on device pointers: mixed = rms_norm(x,
+ * post_norm, eps) (ops.rs:59-69); g = gate . mixed; u = up . mixed;
+ * h = g / (1 + exp(-g)) * u (f32); out = x + down . h (f32). tensors[3]:
+ * gate, up [n_ff][n_embd] and down [n_embd][n_ff], any matvec types; x, out
+ * [n_tok][n_embd] (out may equal x: the residual add in place); post_norm
+ * [n_embd]; workspace >= sh_ffn_workspace_bytes, 256-byte aligned. One token
+ * with one quantized type runs in three launches (rms_norm; gate and up
+ * together; down with silu(g) * u staged and the residual added). No
+ * reference counterpart as one call: it replaces the six steps above. */
+int sh_ffn_workspace_bytes(uint32_t n_tok, uint64_t n_embd, uint64_t n_ff, uint64_t* bytes);
+int sh_ffn_dev(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
+               const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
+               void* stream);
+
 /* The elementwise methods batched over rows, on device pointers: the same
  * arithmetic per row as the host-slice forms; enqueued on `stream`.
  * rms_norm: x, out [rows][n] (out may equal x), w [n]. */

@@ -678,3 +678,35 @@ void sho_rope_neox(float* head, size_t len, uint64_t pos, size_t n_rot, size_t h
 void sho_add(float* a, const float* b, size_t n) {
   for (size_t i = 0; i < n; ++i) a[i] = a[i] + b[i];
 }
+
+/* ---- the dense FFN half of a layer (qwen35.rs:112-129), one token ----------
+ * mixed = rms_norm_into(x, post_norm, eps); g = gate . mixed; u = up . mixed;
+ * h[i] = g[i] / (1 + expf(-g[i])) * u[i] (f32); m = down . h; out = x + m
+ * (f32). gate / up [n_ff][n_embd], down [n_embd][n_ff]. out may equal x. */
+int sho_dense_ffn(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_embd, int64_t n_ff,
+                  const float* x, const float* post_norm, double eps, float* out) {
+  float* mixed = malloc(sizeof(float) * (size_t)n_embd);
+  float* g = malloc(sizeof(float) * (size_t)n_ff);
+  float* u = malloc(sizeof(float) * (size_t)n_ff);
+  float* m = malloc(sizeof(float) * (size_t)n_embd);
+  int rc = (mixed && g && u && m) ? SHO_OK : SHO_TRUNCATED;
+  if (rc == SHO_OK) {
+    sho_rms_norm(x, post_norm, (size_t)n_embd, eps, mixed);
+    rc = sho_gemv(q[0], n_ff, n_embd, t[0], nb[0], mixed, g);
+  }
+  if (rc == SHO_OK) rc = sho_gemv(q[1], n_ff, n_embd, t[1], nb[1], mixed, u);
+  if (rc == SHO_OK) {
+    for (int64_t i = 0; i < n_ff; ++i) {
+      const float gv = g[i];
+      g[i] = gv / (1.0f + expf(-gv)) * u[i];
+    }
+    rc = sho_gemv(q[2], n_embd, n_ff, t[2], nb[2], g, m);
+  }
+  if (rc == SHO_OK)
+    for (int64_t i = 0; i < n_embd; ++i) out[i] = x[i] + m[i];
+  free(mixed);
+  free(g);
+  free(u);
+  free(m);
+  return rc;
+}

@@ -13,6 +13,7 @@
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
  *   - the whole MoE layer     crates/strata-core/src/moe.rs:48-143 (router
  *                             matvec on bf16(x), shared expert, sigmoid gate)
+ *   - dense FFN half      crates/strata-core/src/qwen35.rs:112-129
  *   - rms_norm, l2_norm, softmax, rope_neox, add
  *                             crates/strata-core/src/ops.rs:46-165 (the
  *                             trait's elementwise methods, backend.rs:38-50)
@@ -94,6 +95,11 @@ void sho_softmax(float* xs, size_t n);
 void sho_rope_neox(float* head, size_t len, uint64_t pos, size_t n_rot, size_t head_dim,
                    double freq_base);
 void sho_add(float* a, const float* b, size_t n);
+
+/* the dense FFN half of a layer, one token (qwen35.rs:112-129): q, t, nb
+ * for gate, up, down */
+int sho_dense_ffn(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_embd, int64_t n_ff,
+                  const float* x, const float* post_norm, double eps, float* out);
 
 int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
                   int64_t* ids, float* weights);

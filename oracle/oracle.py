@@ -76,6 +76,8 @@ def lib() -> C.CDLL:
         L.sho_rope_neox.restype = None
         L.sho_add.argtypes = [f32p, f32p, C.c_size_t]
         L.sho_add.restype = None
+        L.sho_dense_ffn.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
+                                    C.c_int64, C.c_int64, f32p, f32p, C.c_double, f32p]
         _lib = L
     return _lib
 
@@ -308,3 +310,21 @@ def bf16_round_array(a) -> np.ndarray:
     u = _f32(a).view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
     return r.view(np.float32).reshape(np.shape(a))
+
+
+def dense_ffn(quants, tensors, n_embd: int, n_ff: int, x, post_norm, eps: float) -> np.ndarray:
+    """The dense FFN half of a layer for each row of x (qwen35.rs:112-129);
+    quants / tensors: gate, up, down."""
+    bufs = [_u8(t) for t in tensors]
+    q = (C.c_uint32 * 3)(*[int(v) for v in quants])
+    ptrs = (C.c_void_p * 3)(*[b.ctypes.data for b in bufs])
+    nbs = (C.c_size_t * 3)(*[b.nbytes for b in bufs])
+    xv = np.array(x, dtype=np.float32, copy=True).reshape(-1, n_embd)
+    nw = _f32(post_norm)
+    out = np.empty_like(xv)
+    for r in range(xv.shape[0]):
+        row = np.ascontiguousarray(xv[r])
+        o = np.empty(n_embd, np.float32)
+        _check(lib().sho_dense_ffn(q, ptrs, nbs, n_embd, n_ff, _ptr(row), _ptr(nw), float(eps), _ptr(o)), "dense_ffn")
+        out[r] = o
+    return out.reshape(np.shape(x))

@@ -1260,3 +1260,43 @@ int sh_weight_upload(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_exp
   for (uint64_t i = 0; i < n_rows; ++i) memcpy(packed.data() + i * rb, data + i * src_row_pitch, size_t(rb));
   return resident(c, key, quant, n_expert, rows, cols, packed.data(), n_rows * rb, &r);
 }
+
+int sh_ffn_workspace_bytes(uint32_t n_tok, uint64_t n_embd, uint64_t n_ff, uint64_t* bytes) {
+  if (!bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null bytes");
+  if (n_tok == 0 || n_embd == 0 || n_ff == 0 || n_embd > (uint64_t(1) << 20) || n_ff > (uint64_t(1) << 20))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "ffn shape");
+  *bytes = sh::ffn_workspace_bytes(n_tok, int64_t(n_embd), int64_t(n_ff));
+  return SH_OK;
+}
+
+int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
+               const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
+               void* stream) {
+  if (!t || !x || !post_norm || !out || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  uint64_t need = 0;
+  int rc = sh_ffn_workspace_bytes(n_tok, n_embd, n_ff, &need);
+  if (rc) return rc;
+  if (workspace_bytes < need)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+  const uint64_t dims[3][2] = {{n_ff, n_embd}, {n_ff, n_embd}, {n_embd, n_ff}};
+  for (int i = 0; i < 3; ++i) {
+    if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
+    if ((rc = check_matrix(t[i].quant, dims[i][0], dims[i][1], 1, ~uint64_t(0), true))) return rc;
+    if (!sh::gemv_shape_ok(t[i].quant, int64_t(dims[i][0]), int64_t(dims[i][1]), 1))
+      return fail(SH_ERR_UNSUPPORTED_SHAPE, "ffn tensor %d: %llux%llu of type %u", i,
+                  (unsigned long long)dims[i][0], (unsigned long long)dims[i][1], t[i].quant);
+    if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
+        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
+      return fail(SH_ERR_INVALID_ARGUMENT, "misaligned tensor %d", i);
+  }
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u) || n_embd % 4 != 0 || n_ff % 4 != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned x, out or workspace (or n_embd, n_ff not multiples of 4)");
+  auto q6 = [](uint32_t f) { return (f & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  HIP_TRY(sh::launch_ffn(t[0].quant, t[1].quant, t[2].quant, t[0].data, t[1].data, t[2].data, q6(t[0].flags),
+                         q6(t[1].flags), q6(t[2].flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), x, post_norm,
+                         eps, out, workspace, static_cast<hipStream_t>(stream)),
+          "ffn launch");
+  return SH_OK;
+}

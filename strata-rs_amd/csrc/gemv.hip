@@ -689,6 +689,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // Q4_K with integer dots: unit u = (super-block u/4, group g = u%4) as in
 // FmtQ4K; low nibbles are sub-block 2g (x block 2u), high nibbles 2g+1.
 struct LimbQ4K {
+  static constexpr uint32_t kQuant = kQ4_K;
   struct Load {
     u32x4 h, a, b;
   };
@@ -732,6 +733,7 @@ struct LimbQ4K {
 // Q5_K with integer dots: unit u as LimbQ4K; codes 0..31 (nibble plus the
 // fifth bit, q5k_codes) go into the dots unchanged.
 struct LimbQ5K {
+  static constexpr uint32_t kQuant = kQ5_K;
   struct Load {
     u32x4 h, h0, h1, a, b;
   };
@@ -776,6 +778,7 @@ struct LimbQ5K {
 // as they are; against the unsigned low limbs they are biased to q + 128 and
 // the bias 128 * K is removed in integers before the one f32 conversion.
 struct LimbQ8 {
+  static constexpr uint32_t kQuant = kQ8_0;
   struct Load {
     u32x4 a, b, c, d;
     uint32_t e;
@@ -825,6 +828,7 @@ struct LimbQ8 {
 // FmtQ6K; the 6-bit codes 0..63 go straight into the dots and the -32
 // offset is taken off with the per-16 sums of x.
 struct LimbQ6K {
+  static constexpr uint32_t kQuant = kQ6_K;
   using Load = FmtQ6K::Load;
   static constexpr int kWinBytes = 16 * 210;
   struct Off {
@@ -881,11 +885,22 @@ struct LimbQ6K {
 // double-buffered (A/B ping-pong, both refills unconditional so the loop
 // latch never drains the load queue), and the first item is requested
 // before x is staged, so weight bytes are in flight from the first cycles.
-template <class F, int R, int MAXQ>
+//
+// MODE bits (compile-time; 0 for the plain matvec) let the dense FFN run in
+// two launches: kLimbTwoMat reads rows [0, rows1) from w and [rows1, rows)
+// from w2 (gate and up in one launch, x staged once); kLimbSiluX stages
+// silu(x) * xu, with silu(v) = v / (1 + exp(-v)) in f32 (qwen35.rs:120-124),
+// instead of x; kLimbResid writes y = xres + sum (one f32 add, qwen35.rs:127-129).
+constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4;
+
+template <class F, int R, int MAXQ, int MODE = 0>
 __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restrict__ w, int rows,
                                                         int cols, int64_t row_bytes,
                                                         const float* __restrict__ x,
-                                                        float* __restrict__ y, int per, int flags) {
+                                                        float* y, int per, int flags,
+                                                        const uint8_t* __restrict__ w2, int rows1,
+                                                        const float* __restrict__ xu,
+                                                        const float* xres) {  // xres may be y (in place)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
@@ -916,7 +931,10 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int row = min((rg0 + qq) * R + r, rows - 1);
-      F::load(w + int64_t(row) * row_bytes, o, L[r]);
+      const uint8_t* base = w + int64_t(row) * row_bytes;
+      if constexpr ((MODE & kLimbTwoMat) != 0)
+        base = row >= rows1 ? w2 + int64_t(row - rows1) * row_bytes : base;
+      F::load(base, o, L[r]);
     }
     if (++pq == my) {
       pq = 0;
@@ -935,7 +953,20 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     const int g = g0 + tid;
     const int gl = min(g, groups - 1);
     const f32x4* src = reinterpret_cast<const f32x4*>(x + 16 * gl);
-    limb_group(lds8, cols, g, g < groups, src[0], src[1], src[2], src[3]);
+    if constexpr ((MODE & kLimbSiluX) != 0) {
+      const f32x4* su = reinterpret_cast<const f32x4*>(xu + 16 * gl);
+      f32x4 h[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+#pragma clang fp contract(off)
+        const f32x4 gv = src[k], uv = su[k];
+        h[k] = f32x4{gv.x / (1.f + expf(-gv.x)) * uv.x, gv.y / (1.f + expf(-gv.y)) * uv.y,
+                     gv.z / (1.f + expf(-gv.z)) * uv.z, gv.w / (1.f + expf(-gv.w)) * uv.w};
+      }
+      limb_group(lds8, cols, g, g < groups, h[0], h[1], h[2], h[3]);
+    } else {
+      limb_group(lds8, cols, g, g < groups, src[0], src[1], src[2], src[3]);
+    }
   }
   __syncthreads();
   if (n_items == 0) return;
@@ -981,7 +1012,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
       for (int r = 0; r < R; ++r) {
         const float t = wave_sum_dpp(acc[q][r]);
         const int row = (rg0 + q) * R + r;
-        if (lane == 63 && row < rows) y[row] = t;
+        if (lane == 63 && row < rows) y[row] = (MODE & kLimbResid) != 0 ? __fadd_rn(xres[row], t) : t;
       }
     }
   }
@@ -1121,10 +1152,11 @@ static hipError_t launch_one(const uint8_t* w, int rows, int cols, int64_t row_b
 
 // Row groups spread over `waves_per_cu` waves per CU; multi-window rows keep
 // at most MAXQ row groups per wave (their sums live in registers).
-template <class F, int R, int MAXQ>
+template <class F, int R, int MAXQ, int MODE = 0>
 static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_bytes,
                               const float* x, float* y, hipStream_t stream, int threads,
-                              int waves_per_cu, int flags = 0) {
+                              int waves_per_cu, int flags = 0, const uint8_t* w2 = nullptr, int rows1 = 0,
+                              const float* xu = nullptr, const float* xres = nullptr) {
   const int wpg = threads / 64;
   const int n_rg = (rows + R - 1) / R;
   const int units = cols >> 6, nwin = (units + 63) >> 6;
@@ -1134,8 +1166,9 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   if (nwin == 1 && per > MAXQ) per = MAXQ;
   const int waves = (n_rg + per - 1) / per;
   const int blocks = (waves + wpg - 1) / wpg;
-  hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ>), dim3(unsigned(blocks)), dim3(threads),
-                     size_t(limb_lds_bytes(cols)), stream, w, rows, cols, row_bytes, x, y, per, flags);
+  hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE>), dim3(unsigned(blocks)), dim3(threads),
+                     size_t(limb_lds_bytes(cols)), stream, w, rows, cols, row_bytes, x, y, per, flags, w2, rows1, xu,
+                     xres);
   return hipGetLastError();
 }
 
@@ -1237,6 +1270,40 @@ hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* wv, int64_t rows,
     case kF32: return launch_plain<kF32, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     case kF16: return launch_plain<kF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     default: return launch_plain<kBF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+  }
+}
+
+// One token through the dense FFN's two matvec launches (limb kernels):
+// [g; u] = [gate; up] . x (both n_ff x n_embd, one launch, x staged once),
+// then out = xres + down . (silu(g) * u) (silu and the residual add inside).
+template <class F>
+static hipError_t launch_ffn1(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_embd, int n_ff,
+                              const float* x, float* gu, const float* xres, float* out, int q6s, hipStream_t s) {
+  const int64_t rb1 = byte_size(F::kQuant, n_embd), rb2 = byte_size(F::kQuant, n_ff);
+  hipError_t e = launch_limb<F, 1, 4, kLimbTwoMat>(gate, 2 * n_ff, n_embd, rb1, x, gu, s, 512, 8, q6s, up, n_ff);
+  if (e != hipSuccess) return e;
+  return launch_limb<F, 1, 4, kLimbSiluX | kLimbResid>(down, n_embd, n_ff, rb2, gu, out, s, 512, 8, q6s, nullptr,
+                                                       0, gu + n_ff, xres);
+}
+
+bool ffn_fused_ok(uint32_t quant, int64_t n_embd, int64_t n_ff) {
+  return (quant == kQ4_K || quant == kQ8_0 || quant == kQ5_K || quant == kQ6_K) &&
+         gemv_shape_ok(quant, 2 * n_ff, n_embd, 1) && gemv_shape_ok(quant, n_embd, n_ff, 1) &&
+         n_ff % 4 == 0 && 2 * n_ff <= (int64_t(1) << 30);
+}
+
+hipError_t launch_ffn_one(uint32_t quant, const void* gate, const void* up, const void* down, int64_t n_embd,
+                          int64_t n_ff, const float* x, float* gu, const float* xres, float* out, int q6s,
+                          hipStream_t s) {
+  if (!ffn_fused_ok(quant, n_embd, n_ff)) return hipErrorInvalidValue;
+  const auto* g = static_cast<const uint8_t*>(gate);
+  const auto* u = static_cast<const uint8_t*>(up);
+  const auto* d = static_cast<const uint8_t*>(down);
+  switch (quant) {
+    case kQ4_K: return launch_ffn1<LimbQ4K>(g, u, d, int(n_embd), int(n_ff), x, gu, xres, out, q6s, s);
+    case kQ8_0: return launch_ffn1<LimbQ8>(g, u, d, int(n_embd), int(n_ff), x, gu, xres, out, q6s, s);
+    case kQ5_K: return launch_ffn1<LimbQ5K>(g, u, d, int(n_embd), int(n_ff), x, gu, xres, out, q6s, s);
+    default: return launch_ffn1<LimbQ6K>(g, u, d, int(n_embd), int(n_ff), x, gu, xres, out, q6s, s);
   }
 }
 

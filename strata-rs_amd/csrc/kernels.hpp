@@ -18,6 +18,24 @@ hipError_t launch_dequant(uint32_t quant, const void* w, int64_t rows, int64_t c
 bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
 hipError_t launch_gemv(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
                        float* y, int batch, int q6_signed, hipStream_t stream);
+// One token of the dense FFN (qwen35.rs:112-129) after its rms_norm, in two
+// matvec launches: gu = [gate . x; up . x] (2 * n_ff floats), then
+// out = xres + down . (silu(g) * u). All three matrices of type `quant`
+// (Q8_0 / Q4_K / Q5_K / Q6_K); ffn_fused_ok checks the shapes.
+bool ffn_fused_ok(uint32_t quant, int64_t n_embd, int64_t n_ff);
+hipError_t launch_ffn_one(uint32_t quant, const void* gate, const void* up, const void* down, int64_t n_embd,
+                          int64_t n_ff, const float* x, float* gu, const float* xres, float* out, int q6s,
+                          hipStream_t stream);
+// h = silu(g) * u elementwise (ops.rs:85-87, f32).
+hipError_t launch_silu_mul(const float* g, const float* u, float* h, int64_t n, hipStream_t stream);
+
+// The dense FFN half of a layer for n_tok tokens (rms_norm, gate, up, silu,
+// down, residual); workspace of ffn_workspace_bytes.
+size_t ffn_workspace_bytes(int64_t n_tok, int64_t n_embd, int64_t n_ff);
+hipError_t launch_ffn(uint32_t q_gate, uint32_t q_up, uint32_t q_down, const void* gate, const void* up,
+                      const void* down, int q6g, int q6u, int q6d, int64_t n_embd, int64_t n_ff, int n_tok,
+                      const float* x, const float* post_norm, double eps, float* out, void* workspace,
+                      hipStream_t stream);
 // The same for F32 / F16 / BF16 rows against bf16(x) (rounded as loaded).
 hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
                                    float* y, int batch, hipStream_t stream);
@@ -124,5 +142,6 @@ hipError_t launch_softmax(float* x, int64_t rows, int64_t n, hipStream_t stream)
 hipError_t launch_rope_neox(float* x, int64_t rows, int64_t head_dim, int64_t n_rot, uint64_t pos0,
                             int64_t heads_per_pos, double freq_base, hipStream_t stream);
 hipError_t launch_add(float* a, const float* b, int64_t n, hipStream_t stream);
+hipError_t launch_add_out(float* out, const float* a, const float* b, int64_t n, hipStream_t stream);
 
 }  // namespace sh

@@ -38,6 +38,12 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
   h[i] = v / (1.f + expf(-v)) * u[i];
 }
 
+hipError_t launch_silu_mul(const float* g, const float* u, float* h, int64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, g, u, h, n);
+  return hipGetLastError();
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, int n_ff_sh,

@@ -338,6 +338,13 @@ __global__ void __launch_bounds__(kRowThreads) add_kernel(float* __restrict__ a,
   }
 }
 
+// out = a + b (f32), out distinct from b.
+__global__ void __launch_bounds__(kRowThreads) add_out_kernel(float* out, const float* a, const float* __restrict__ b,
+                                                              int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kRowThreads;
+  for (int64_t k = int64_t(blockIdx.x) * kRowThreads + threadIdx.x; k < n; k += stride) out[k] = a[k] + b[k];
+}
+
 static unsigned row_blocks(int64_t rows, int64_t n) {
   return unsigned(n <= kShortRow ? (rows + 3) / 4 : rows);
 }
@@ -415,6 +422,14 @@ hipError_t launch_add(float* a, const float* b, int64_t n, hipStream_t s) {
   int64_t blocks = ((n + 3) / 4 + kRowThreads - 1) / kRowThreads;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(add_kernel, dim3(unsigned(blocks)), dim3(kRowThreads), 0, s, a, b, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_out(float* out, const float* a, const float* b, int64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  int64_t blocks = (n + kRowThreads - 1) / kRowThreads;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(add_out_kernel, dim3(unsigned(blocks)), dim3(kRowThreads), 0, s, out, a, b, n);
   return hipGetLastError();
 }
 

@@ -63,6 +63,7 @@ EXPORTS = (
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
     "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
+    "sh_ffn_workspace_bytes", "sh_ffn_dev",
 )
 
 
@@ -237,6 +238,8 @@ def load_library() -> C.CDLL:
     L.sh_gguf_model_shard.argtypes = [vp, u64, C.POINTER(vp)]
     L.sh_gguf_model_find.argtypes = [vp, C.c_char_p, u64p, u64p]
     L.sh_weight_upload.argtypes = [vp, u64, u32, u64, u64, u64, vp, u64]
+    L.sh_ffn_workspace_bytes.argtypes = [u32, u64, u64, u64p]
+    L.sh_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), u64, u64, u32, vp, vp, dbl, vp, vp, u64, vp]
     _lib = L
     return L
 
@@ -745,3 +748,18 @@ def rope_neox_dev(x_ptr: int, rows: int, heads_per_pos: int, cfg: RopeCfg, strea
 
 def add_dev(a_ptr: int, b_ptr: int, n: int, stream: int = 0) -> None:
     check(load_library().sh_add_dev(a_ptr, b_ptr, n, stream or None))
+
+
+def ffn_workspace_bytes(n_tok: int, n_embd: int, n_ff: int) -> int:
+    v = C.c_uint64()
+    check(load_library().sh_ffn_workspace_bytes(n_tok, n_embd, n_ff, C.byref(v)))
+    return v.value
+
+
+def ffn_dev(tensors, n_embd: int, n_ff: int, n_tok: int, x_ptr: int, norm_ptr: int, eps: float, out_ptr: int,
+            ws_ptr: int, ws_bytes: int, stream: int = 0) -> None:
+    """The dense FFN half of a layer (qwen35.rs:112-129); tensors: gate, up,
+    down as (quant, flags, device pointer)."""
+    arr = (_ExpertDevC * 3)(*[_ExpertDevC(int(q), f, p) for q, f, p in tensors])
+    check(load_library().sh_ffn_dev(arr, n_embd, n_ff, n_tok, x_ptr, norm_ptr, float(eps), out_ptr, ws_ptr, ws_bytes,
+                                    stream or None))

@@ -1,0 +1,73 @@
+"""The dense FFN half of a layer on the device (sh_ffn_dev) vs the oracle's
+sho_dense_ffn (crates/strata-core/src/qwen35.rs:112-129: rms_norm, gate, up,
+silu * up, down, residual add).
+
+Tolerance: the matvec bound, 1e-3, on out - x (the FFN's own output, which
+the residual add would otherwise hide) relative to its largest magnitude,
+and per element with the rms floor; the residual add itself is checked at
+f32 rounding. Covers the config's dense shape (Q4_K, hidden 4096, FFN 12288)
+on the fused one-token path (three launches), three tokens and mixed types
+on the general path, in-place output, and Q8_0 / Q5_K / Q6_K fused.
+"""
+import numpy as np
+import pytest
+
+import strata_hip as H
+from conftest import elem_rel_err, rel_err
+from strata_hip import synth as S
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def run_ffn(quants, mats, n_embd, n_ff, x, norm, eps, in_place=False):
+    import torch
+    dev = [torch.from_numpy(np.ascontiguousarray(m)).cuda() for m in mats]
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    nd = torch.from_numpy(np.ascontiguousarray(norm)).cuda()
+    n_tok = x.shape[0]
+    out = xd if in_place else torch.empty_like(xd)
+    nb = H.ffn_workspace_bytes(n_tok, n_embd, n_ff)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    H.ffn_dev([(q, 0, t.data_ptr()) for q, t in zip(quants, dev)], n_embd, n_ff, n_tok, xd.data_ptr(),
+              nd.data_ptr(), eps, out.data_ptr(), ws.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check(got, want, x):
+    dg, dw = got.astype(np.float64) - x, want.astype(np.float64) - x
+    assert rel_err(dg, dw) <= TOL, rel_err(dg, dw)
+    assert elem_rel_err(dg, dw, floor=1.0) <= TOL
+
+
+@pytest.mark.parametrize("quants,n_embd,n_ff,n_tok,in_place", [
+    ((12, 12, 12), 4096, 12288, 1, False),   # the dense config, fused
+    ((12, 12, 12), 4096, 12288, 1, True),
+    ((12, 12, 12), 2048, 4096, 3, False),    # general path
+    ((12, 12, 14), 2048, 4096, 1, True),     # mixed types: general path
+    ((8, 8, 8), 2048, 4096, 1, False),       # fused Q8_0
+    ((13, 13, 13), 2048, 4096, 1, False),    # fused Q5_K
+    ((14, 14, 14), 2048, 4096, 1, False),    # fused Q6_K
+])
+def test_ffn_matches_oracle(oracle, quants, n_embd, n_ff, n_tok, in_place):
+    say("ffn", quants, n_embd, n_ff, n_tok, in_place)
+    mats = [S.matrix(quants[0], 31, n_ff, n_embd), S.matrix(quants[1], 32, n_ff, n_embd),
+            S.matrix(quants[2], 33, n_embd, n_ff)]
+    x = S.normal_f32(34 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    norm = S.normal_f32(35, n_embd)
+    got = run_ffn(quants, mats, n_embd, n_ff, x, norm, 1e-6, in_place)
+    want = oracle.dense_ffn(quants, mats, n_embd, n_ff, x, norm, 1e-6)
+    check(got, want, x)
+
+
+def test_ffn_errors():
+    say("ffn errors")
+    with pytest.raises(H.BackendError):
+        H.ffn_workspace_bytes(0, 4096, 12288)
+    with pytest.raises(H.BackendError):
+        H.ffn_dev([(12, 0, 256), (12, 0, 256), (12, 0, 256)], 4096, 12288, 1, 16, 16, 1e-6, 16, 256, 0)

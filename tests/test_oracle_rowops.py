@@ -149,3 +149,32 @@ def test_rope_odd_n_rot_and_short_head(oracle):
     b = oracle.rope_neox(h0, pos=3, n_rot=4, head_dim=6, freq_base=1e4)
     assert np.array_equal(a, b)
     assert a[4] == 5.0 and a[5] == 6.0
+
+
+# ---- the dense FFN half of a layer (qwen35.rs:112-129) ---------------------------
+
+def test_dense_ffn_hand_computed(oracle):
+    # F32 identity matrices: mixed = x * w / rms, g = u = mixed,
+    # h = silu(mixed) * mixed, out = x + h
+    eye = np.eye(2, dtype=np.float32).view(np.uint8)
+    x = np.array([3.0, 4.0], np.float32)
+    out = oracle.dense_ffn([0, 0, 0], [eye, eye, eye], 2, 2, x, [2.0, 2.0], 0.0)
+    for i, v in enumerate((3.0, 4.0)):
+        m = v * 2.0 / math.sqrt(12.5)
+        assert abs(out[i] - (v + m / (1 + math.exp(-m)) * m)) < 1e-5
+
+
+def test_dense_ffn_zero_paths_give_x(oracle):
+    from strata_hip import synth as S
+    n_embd, n_ff = 256, 512
+    gate = S.matrix(12, 1, n_ff, n_embd)
+    up = S.matrix(12, 2, n_ff, n_embd)
+    down = S.matrix(14, 3, n_embd, n_ff)
+    x = S.normal_f32(4, n_embd)
+    # a zero norm weight zeroes mixed, so g = u = h = 0 and out = x exactly
+    out = oracle.dense_ffn([12, 12, 14], [gate, up, down], n_embd, n_ff, x, np.zeros(n_embd, np.float32), 1e-6)
+    assert np.array_equal(out, x)
+    # zero up rows (all-zero blocks decode to 0) also leave out = x
+    out = oracle.dense_ffn([12, 12, 14], [gate, np.zeros_like(up), down], n_embd, n_ff, x, S.normal_f32(5, n_embd),
+                           1e-6)
+    assert np.array_equal(out, x)
