@@ -144,12 +144,19 @@ void parallel_copy(uint8_t* dst, const uint8_t* src, size_t n) {
   }
   const size_t part = (n / kStageThreads + 4095) & ~size_t(4095);
   std::thread t[kStageThreads - 1];
-  for (int i = 1; i < kStageThreads; ++i) {
-    const size_t a = std::min(n, part * i), b = std::min(n, part * (i + 1));
-    t[i - 1] = std::thread([=] { memcpy(dst + a, src + a, b - a); });
+  int started = 1;  // parts [0, started) are copied by this thread or a helper
+  try {
+    for (; started < kStageThreads; ++started) {
+      const size_t a = std::min(n, part * started), b = std::min(n, part * (started + 1));
+      t[started - 1] = std::thread([=] { memcpy(dst + a, src + a, b - a); });
+    }
+  } catch (const std::exception&) {
+    // no thread to be had: the parts not handed out are copied here
   }
   memcpy(dst, src, std::min(n, part));
-  for (auto& th : t) th.join();
+  const size_t rest = std::min(n, part * started);
+  if (rest < n) memcpy(dst + rest, src + rest, n - rest);
+  for (int i = 1; i < started; ++i) t[i - 1].join();
 }
 
 int staged_upload(sh_context* c, void* dev, const uint8_t* src, uint64_t n) {
