@@ -250,6 +250,8 @@ def layer_tensors(n_expert, n_embd, n_ff, n_sh, seed, q_router=0, q_inp=0, q_sh=
     experts as the MoE config (gate/up Q4_K, down Q6_K), the shared expert
     in the given types."""
     def plain(q, s, n):
+        if q not in (0, 30):  # a quantized router or gate input: rows of n_embd
+            return S.matrix(q, s, n // n_embd, n_embd)
         v = S.normal_f32(s, n)
         if q == 0:
             return v.view(np.uint8)
@@ -277,12 +279,14 @@ def layer_views(name, quants, tensors, n_expert, n_embd, n_ff, n_sh):
 
 
 @pytest.mark.parametrize("n_tok,q_router,q_inp,q_sh", [(1, 0, 0, (12, 12, 14)), (3, 30, 0, (8, 8, 8)),
-                                                       (9, 0, 30, (14, 14, 12))])
+                                                       (9, 0, 30, (14, 14, 12)), (2, 8, 13, (13, 13, 14)),
+                                                       (1, 12, 0, (12, 12, 14))])
 def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh):
     """The whole layer (moe.rs:48-143): router matvec on bf16(x) (F32 or
-    BF16 rows, f64 sums), routing, the routed experts and the shared expert
-    with its sigmoid gate, against the oracle token by token; 9 tokens take
-    two 8-token matvec launches."""
+    BF16 rows with f64 sums, rounding x as they load it; or quantized rows
+    after a rounding pass), routing, the routed experts and the shared
+    expert with its sigmoid gate, against the oracle token by token; 9
+    tokens take two 8-token matvec launches."""
     n_expert, n_embd, n_ff, n_sh, top_k = 32, 512, 256, 256, 6
     say("moe layer", n_tok, q_router, q_inp, q_sh)
     q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8400 + n_tok, q_router, q_inp, q_sh)
