@@ -221,3 +221,29 @@ def test_gemv_plain_types(backend, oracle, quant, rows, cols, batch):
         ulp = np.abs(y[b].view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
         assert ulp.max() <= 1, (b, int(ulp.max()))
         assert np.mean(y[b] == ref) >= 0.99
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_gemv_random_shapes(backend, oracle, seed):
+    """Seeded random shapes across every matvec type and batch 1..8: rows
+    1..3000, columns any multiple of the type's block (and of 64) up to
+    20480, so partial 16-row tiles, partial windows and several windows all
+    occur against the oracle."""
+    rng = np.random.default_rng(9000 + seed)
+    for case in range(8):
+        quant = int(rng.choice([8, 12, 13, 14, 0, 1, 30]))
+        step = 256 if quant in (12, 13, 14) else 64
+        cols = step * int(rng.integers(1, 20480 // step + 1))
+        rows = int(rng.integers(1, 3001))
+        batch = int(rng.integers(1, 9))
+        say("gemv random", seed, case, quant, rows, cols, batch)
+        if quant in (0, 1, 30):
+            w = plain_matrix(quant, seed * 100 + case, rows, cols)
+        else:
+            w = S.matrix(quant, seed * 100 + case, rows, cols)
+        x = S.normal_f32(seed * 100 + case + 7, batch * cols).reshape(batch, cols)
+        t = H.QuantTensor(f"rand{seed}_{case}", quant, rows, cols, w)
+        y = backend.gemv_batch(t, x, batch)
+        for b in range(batch):
+            check(y[b], oracle.gemv(quant, rows, cols, w, x[b], threads=8))
+        backend.evict(f"rand{seed}_{case}")
