@@ -397,3 +397,31 @@ def test_moe_layer_errors(backend):
     bad[4] = H.QuantTensor("Lerr.gsh_q40", 2, n_sh, n_embd, np.zeros(n_sh * n_embd // 32 * 18, np.uint8))
     with pytest.raises(H.UnsupportedQuantError):
         backend.moe_layer(*bad, x, 2)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_moe_ffn_random_configs(backend, oracle, seed):
+    """Seeded random routed-FFN configurations: 4..128 experts, hidden and
+    expert widths of several multiples of 256, top-1..8, 1..12 tokens,
+    Q4_K / Q8_0 gate-up with Q6_K / Q4_K / Q8_0 down, against the oracle."""
+    rng = np.random.default_rng(7000 + seed)
+    n_expert = int(rng.choice([4, 16, 64, 128]))
+    n_embd = 256 * int(rng.integers(1, 5))
+    n_ff = 256 * int(rng.integers(1, 4))
+    top_k = int(rng.integers(1, min(8, n_expert) + 1))
+    n_tok = int(rng.integers(1, 13))
+    qa = int(rng.choice([12, 8]))
+    qd = int(rng.choice([14, 12, 8]))
+    say("moe random", seed, n_expert, n_embd, n_ff, top_k, n_tok, qa, qd)
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, qa, qd, 7100 + seed)
+    logits = S.router_logits(7200 + seed, n_tok, n_expert)
+    x = S.normal_f32(7300 + seed, n_tok * n_embd).reshape(n_tok, n_embd)
+    out = backend.moe_ffn(H.ExpertView(f"rg{seed}", qa, n_expert, n_embd, n_ff, gate),
+                          H.ExpertView(f"ru{seed}", qa, n_expert, n_embd, n_ff, up),
+                          H.ExpertView(f"rd{seed}", qd, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    ref = oracle_moe(oracle, qa, qd, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    for t in range(n_tok):
+        assert rel_err(out[t], ref[t]) <= 1e-3, (t, rel_err(out[t], ref[t]))
+        assert elem_rel_err(out[t], ref[t], floor=1.0) <= 1e-3
+    for name in (f"rg{seed}", f"ru{seed}", f"rd{seed}"):
+        backend.evict(name)
