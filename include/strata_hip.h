@@ -74,6 +74,12 @@ extern "C" {
 /* Q6_K sub-block scales as ggml's int8_t instead of strata-gguf's u8 reading
  * (crates/strata-gguf/src/dequant.rs:211,224-227 reads them as u8). */
 #define SH_FLAG_Q6K_SIGNED_SCALES 1u
+/* sh_expert_view in ggml's orientation, as llama.cpp GGUF files store
+ * expert stacks: [n_expert][rows = out][cols = in] with blocks along the
+ * input, so sh_expert_gemv computes y[r] = sum_c W_e[r][c] x[c] (x_len =
+ * cols, y_len = rows) with the matvec kernels. The reference's in-major
+ * orientation (weights.rs:14-34) is the default. sh_expert_gemv only. */
+#define SH_FLAG_EXPERT_OUT_MAJOR 2u
 
 /* ---- matmul modes ------------------------------------------------------ */
 #define SH_MATMUL_BF16 0u /* bf16 activations, dequant-to-bf16 LDS tiles, bf16 MFMA */

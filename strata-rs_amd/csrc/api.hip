@@ -409,6 +409,48 @@ int sh_gemv_batch(sh_context* c, const sh_quant_tensor* w, const float* x, float
 int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const float* x,
                    uint64_t x_len, float* y, uint64_t y_len) {
   if (!c || !w || (!x && x_len) || (!y && y_len)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if (w->flags & SH_FLAG_EXPERT_OUT_MAJOR) {
+    // ggml orientation: expert e is an ordinary [rows = out][cols = in]
+    // matrix, run by the matvec kernels on its slice of the resident stack
+    if (x_len != w->cols) return fail(SH_ERR_SHAPE, "expert_gemv: x has %llu elements, cols is %llu",
+                                      (unsigned long long)x_len, (unsigned long long)w->cols);
+    if (y_len != w->rows) return fail(SH_ERR_SHAPE, "expert_gemv: y has %llu elements, rows is %llu",
+                                      (unsigned long long)y_len, (unsigned long long)w->rows);
+    if (e >= w->n_expert) return fail(SH_ERR_SHAPE, "expert %llu of %llu", (unsigned long long)e,
+                                      (unsigned long long)w->n_expert);
+    int rc = check_matrix(w->quant, w->rows, w->cols, w->n_expert, w->nbytes, true);
+    if (rc) return rc;
+    const uint64_t rows = w->rows, cols = w->cols;
+    if (rows == 0) return SH_OK;
+    if (cols == 0) {
+      memset(y, 0, sizeof(float) * rows);
+      return SH_OK;
+    }
+    if (!sh::gemv_shape_ok(w->quant, int64_t(rows), int64_t(cols), 1))
+      return fail(SH_ERR_UNSUPPORTED_SHAPE, "expert_gemv %llux%llu of type %u is not supported",
+                  (unsigned long long)rows, (unsigned long long)cols, w->quant);
+    Guard g(c);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    Resident* r = nullptr;
+    const uint64_t rb = uint64_t(sh::byte_size(w->quant, int64_t(cols)));
+    rc = resident(c, w->key, w->quant, w->n_expert, rows, cols, w->data, w->n_expert * rows * rb, &r);
+    if (rc) return rc;
+    const size_t xb = sizeof(float) * cols, yb = sizeof(float) * rows;
+    if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(yb, "y buffer")) ||
+        (rc = c->h_in.ensure(xb, "x staging")) || (rc = c->h_out.ensure(yb, "y staging")))
+      return rc;
+    const uint8_t* we = static_cast<const uint8_t*>(r->dev) + e * rows * rb;
+    memcpy(c->h_in.p, x, xb);
+    HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
+    HIP_TRY(sh::launch_gemv(w->quant, we, int64_t(rows), int64_t(cols), static_cast<const float*>(c->d_in.p),
+                            static_cast<float*>(c->d_out.p), 1, (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                            c->stream),
+            "expert_gemv launch");
+    HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
+    HIP_TRY(hipStreamSynchronize(c->stream), "expert_gemv");
+    memcpy(y, c->h_out.p, yb);
+    return SH_OK;
+  }
   if (x_len != w->rows) return fail(SH_ERR_SHAPE, "expert_gemv: x has %llu elements, rows is %llu",
                                     (unsigned long long)x_len, (unsigned long long)w->rows);
   if (y_len != w->cols) return fail(SH_ERR_SHAPE, "expert_gemv: y has %llu elements, cols is %llu",

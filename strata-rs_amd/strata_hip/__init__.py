@@ -47,6 +47,7 @@ SH_ERR_IO = -10
 SH_ERR_NOT_FOUND = -11
 
 FLAG_Q6K_SIGNED_SCALES = 1
+FLAG_EXPERT_OUT_MAJOR = 2
 MATMUL_BF16 = 0
 MATMUL_Q8 = 1
 

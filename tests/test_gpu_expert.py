@@ -60,3 +60,20 @@ def test_expert_gemv_errors(backend):
     with pytest.raises(H.TruncatedError):
         short = H.ExpertView("errs_short", 12, 2, 8, 256, w[:-144])
         backend.expert_gemv(short, 0, np.zeros(8, np.float32), np.zeros(256, np.float32))
+
+
+
+@pytest.mark.parametrize("quant", [12, 8, 13, 14])
+def test_expert_gemv_ggml_orientation(backend, oracle, quant):
+    """SH_FLAG_EXPERT_OUT_MAJOR: experts stored as llama.cpp GGUFs do,
+    [n_expert][out][in], each expert an ordinary matvec of its slice."""
+    n_expert, rows, cols = 4, 768, 2048
+    w = S.matrix(quant, 8800 + quant, n_expert * rows, cols)
+    x = S.normal_f32(8900 + quant, cols)
+    v = H.ExpertView(f"ggml{quant}", quant, n_expert, rows, cols, w, flags=H.FLAG_EXPERT_OUT_MAJOR)
+    rb = S.row_bytes(quant, cols)
+    for e in (0, 3):
+        y = np.empty(rows, np.float32)
+        backend.expert_gemv(v, e, x, y)
+        want = oracle.gemv(quant, rows, cols, w[e * rows * rb:(e + 1) * rows * rb], x)
+        assert rel_err(y, want) <= 1e-3
