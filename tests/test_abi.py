@@ -70,3 +70,27 @@ def test_dev_entry_points_validate_before_launch():
     assert lib.sh_gemv_dev(2, 0, None, 16, 256, None, None, 1, None) == H.SH_ERR_UNSUPPORTED_QUANT
     assert lib.sh_gemv_dev(12, 0, None, 16, 200, None, None, 1, None) == H.SH_ERR_TRUNCATED
     assert lib.sh_dequant_dev(12, 0, None, 4, 256, None, None) == H.SH_ERR_INVALID_ARGUMENT
+
+
+def test_header_is_plain_c_and_links(tmp_path):
+    """include/strata_hip.h is a C99 header (what a cgo / bindgen / ctypes
+    binding reads), and a C program calling through it links against the
+    library: every declared symbol resolves at link time."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    header = os.path.join(root, "include", "strata_hip.h")
+    names = declared_symbols()
+    src = tmp_path / "use.c"
+    src.write_text('#include "strata_hip.h"\n#include <stdio.h>\n'
+                   'int main(void) {\n  void* p[] = {' + ", ".join(f"(void*)&{n}" for n in names) + '};\n'
+                   '  printf("%d %d\\n", sh_abi_version(), (int)(sizeof p / sizeof p[0]));\n  return 0;\n}\n')
+    lib = H.library_path()
+    exe = tmp_path / "use"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(header), str(src), "-o", str(exe),
+                    lib, "-Wl,-rpath," + os.path.dirname(lib)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()
+    assert out == [str(H.load_library().sh_abi_version()), str(len(names))]
