@@ -378,6 +378,12 @@ int sh_upload_gguf_tensor(sh_context* ctx, const sh_gguf* gguf, uint64_t index, 
  * together; down with silu(g) * u staged and the residual added). No
  * reference counterpart as one call: it replaces the six steps above. */
 int sh_ffn_workspace_bytes(uint32_t n_tok, uint64_t n_embd, uint64_t n_ff, uint64_t* bytes);
+/* The same on host slices, in place as the reference's `*x += *m`: x
+ * [n_tok][n_embd] holds the layer input and receives the output; gate / up
+ * [n_ff][n_embd] and down [n_embd][n_ff] are resident weights (admitted on
+ * first use; the budget must hold all three). Synchronous. */
+int sh_ffn(sh_context* ctx, const sh_quant_tensor* gate, const sh_quant_tensor* up, const sh_quant_tensor* down,
+           const float* post_norm, double eps, uint32_t n_tok, float* x);
 int sh_ffn_dev(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
                const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
                void* stream);

@@ -1349,3 +1349,60 @@ int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t 
           "ffn launch");
   return SH_OK;
 }
+
+int sh_ffn(sh_context* c, const sh_quant_tensor* gate, const sh_quant_tensor* up, const sh_quant_tensor* down,
+           const float* post_norm, double eps, uint32_t n_tok, float* x) {
+  if (!c || !gate || !up || !down || !post_norm || (!x && n_tok)) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  const uint64_t n_embd = gate->cols, n_ff = gate->rows;
+  if (up->rows != n_ff || up->cols != n_embd || down->rows != n_embd || down->cols != n_ff)
+    return fail(SH_ERR_SHAPE, "ffn: gate/up must be [n_ff][n_embd] and down [n_embd][n_ff]");
+  const sh_quant_tensor* t[3] = {gate, up, down};
+  int rc;
+  for (int i = 0; i < 3; ++i)
+    if ((rc = check_matrix(t[i]->quant, t[i]->rows, t[i]->cols, 1, t[i]->nbytes, true))) return rc;
+  if (n_tok == 0 || n_embd == 0 || n_ff == 0) return SH_OK;
+  uint64_t need = 0;
+  if ((rc = sh_ffn_workspace_bytes(n_tok, n_embd, n_ff, &need))) return rc;
+  for (int i = 0; i < 3; ++i)
+    if (!sh::gemv_shape_ok(t[i]->quant, int64_t(t[i]->rows), int64_t(t[i]->cols), 1))
+      return fail(SH_ERR_UNSUPPORTED_SHAPE, "ffn tensor %d: %llux%llu of type %u", i,
+                  (unsigned long long)t[i]->rows, (unsigned long long)t[i]->cols, t[i]->quant);
+  if (n_embd % 4 != 0 || n_ff % 4 != 0) return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_embd and n_ff must be multiples of 4");
+  Guard g(c);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  // the three matrices resident at once (admitted twice, as sh_moe_layer)
+  void* dev[3] = {};
+  for (int pass = 0; pass < 2; ++pass)
+    for (int i = 0; i < 3; ++i) {
+      Resident* r = nullptr;
+      const uint64_t nb = t[i]->rows * uint64_t(sh::byte_size(t[i]->quant, int64_t(t[i]->cols)));
+      if ((rc = resident(c, t[i]->key, t[i]->quant, 1, t[i]->rows, t[i]->cols, t[i]->data, nb, &r))) return rc;
+      dev[i] = r->dev;
+    }
+  for (int i = 0; i < 3; ++i) {
+    auto it = c->weights.find(t[i]->key);
+    if (it == c->weights.end() || it->second.dev != dev[i])
+      return fail(SH_ERR_OUT_OF_MEMORY, "the weight budget does not hold the FFN's matrices at once");
+  }
+  // x and post_norm in one upload (post_norm 256-byte aligned after x)
+  const size_t xb = sizeof(float) * n_tok * n_embd, nb = sizeof(float) * n_embd;
+  const size_t x_al = (xb + 255) & ~size_t(255);
+  if ((rc = c->d_in.ensure(x_al + nb, "x buffer")) || (rc = c->d_blk.ensure(need, "workspace")) ||
+      (rc = c->h_in.ensure(x_al + nb, "x staging")) || (rc = c->h_out.ensure(xb, "out staging")))
+    return rc;
+  uint8_t* hi = static_cast<uint8_t*>(c->h_in.p);
+  memcpy(hi, x, xb);
+  memcpy(hi + x_al, post_norm, nb);
+  HIP_TRY(hipMemcpyAsync(c->d_in.p, hi, x_al + nb, hipMemcpyHostToDevice, c->stream), "x upload");
+  float* dx = static_cast<float*>(c->d_in.p);
+  const float* dn = reinterpret_cast<const float*>(static_cast<uint8_t*>(c->d_in.p) + x_al);
+  auto q6 = [](uint32_t f) { return (f & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  HIP_TRY(sh::launch_ffn(gate->quant, up->quant, down->quant, dev[0], dev[1], dev[2], q6(gate->flags), q6(up->flags),
+                         q6(down->flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), dx, dn, eps, dx, c->d_blk.p,
+                         c->stream),
+          "ffn launch");
+  HIP_TRY(hipMemcpyAsync(c->h_out.p, dx, xb, hipMemcpyDeviceToHost, c->stream), "x readback");
+  HIP_TRY(hipStreamSynchronize(c->stream), "ffn");
+  memcpy(x, c->h_out.p, xb);
+  return SH_OK;
+}

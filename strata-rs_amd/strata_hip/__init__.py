@@ -64,7 +64,7 @@ EXPORTS = (
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
     "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
-    "sh_ffn_workspace_bytes", "sh_ffn_dev",
+    "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn",
 )
 
 
@@ -241,6 +241,8 @@ def load_library() -> C.CDLL:
     L.sh_weight_upload.argtypes = [vp, u64, u32, u64, u64, u64, vp, u64]
     L.sh_ffn_workspace_bytes.argtypes = [u32, u64, u64, u64p]
     L.sh_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), u64, u64, u32, vp, vp, dbl, vp, vp, u64, vp]
+    L.sh_ffn.argtypes = [vp, C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC), f32p, dbl,
+                         u32, f32p]
     _lib = L
     return L
 
@@ -642,6 +644,16 @@ class HipBackend:
         if bv.size != av.size:
             raise ShapeError(SH_ERR_SHAPE, f"b has {bv.size} elements, a {av.size}")
         check(self._L.sh_add(self._ctx, av.ctypes.data, bv.ctypes.data, av.size))
+
+    def ffn(self, gate: QuantTensor, up: QuantTensor, down: QuantTensor, post_norm, eps: float, x: np.ndarray) -> None:
+        """The dense FFN half of a layer (qwen35.rs:112-129) in place on
+        ``x [n_tok][n_embd]`` (float32, C-contiguous)."""
+        xv = _f32_out(x)
+        nv = _f32_in(post_norm)
+        n_tok = xv.size // gate.cols if gate.cols else 0
+        g, u, d = gate._c(), up._c(), down._c()
+        check(self._L.sh_ffn(self._ctx, C.byref(g), C.byref(u), C.byref(d), nv.ctypes.data, float(eps), n_tok,
+                             xv.ctypes.data))
 
     def upload(self, name: str, quant: int, n_expert: int, rows: int, cols: int, data, row_pitch: int = 0) -> None:
         """Admits a packed tensor under `name` ahead of its first use

@@ -71,3 +71,19 @@ def test_ffn_errors():
         H.ffn_workspace_bytes(0, 4096, 12288)
     with pytest.raises(H.BackendError):
         H.ffn_dev([(12, 0, 256), (12, 0, 256), (12, 0, 256)], 4096, 12288, 1, 16, 16, 1e-6, 16, 256, 0)
+
+
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_ffn_host_slices_match_device_path(backend, oracle, n_tok):
+    """sh_ffn (host slices, resident weights, in place) against the oracle
+    and bit for bit against sh_ffn_dev."""
+    say("ffn host", n_tok)
+    n_embd, n_ff = 2048, 4096
+    mats = [S.matrix(12, 41, n_ff, n_embd), S.matrix(12, 42, n_ff, n_embd), S.matrix(14, 43, n_embd, n_ff)]
+    x = S.normal_f32(44 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    norm = S.normal_f32(45, n_embd)
+    got = x.copy()
+    backend.ffn(H.QuantTensor("ffn.gate", 12, n_ff, n_embd, mats[0]), H.QuantTensor("ffn.up", 12, n_ff, n_embd, mats[1]),
+                H.QuantTensor("ffn.down", 14, n_embd, n_ff, mats[2]), norm, 1e-6, got)
+    check(got, oracle.dense_ffn((12, 12, 14), mats, n_embd, n_ff, x, norm, 1e-6), x)
+    assert np.array_equal(got, run_ffn((12, 12, 14), mats, n_embd, n_ff, x, norm, 1e-6))
