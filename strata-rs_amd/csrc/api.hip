@@ -21,6 +21,7 @@
 #include "common.hpp"
 #include "gguf.hpp"
 #include "kernels.hpp"
+#include "store.hpp"
 
 namespace {
 
@@ -53,6 +54,7 @@ struct Resident {
   void* dev = nullptr;
   uint64_t bytes = 0;
   uint64_t used = 0;
+  uint64_t pin = 0;  // the call that last admitted or hit it (never evicted by that call)
   uint32_t quant = 0;
   uint64_t rows = 0, cols = 0, n_expert = 0;
 };
@@ -115,6 +117,7 @@ struct sh_context {
   uint64_t budget = 0;
   uint64_t bytes = 0;
   uint64_t clock = 0;
+  uint64_t call = 0;  // numbers the locked calls; admissions pin their entry to it
   std::unordered_map<uint64_t, Resident> weights;
   DevBuf d_in, d_out, d_blk;
   HostBuf h_in, h_out;
@@ -181,19 +184,33 @@ int staged_upload(sh_context* c, void* dev, const uint8_t* src, uint64_t n) {
 
 // Evicts least-recently-used entries until `incoming` more bytes fit, or the
 // store is empty (gpu.rs:88-112): a single tensor larger than the budget is
-// still admitted, alone.
-void make_room(sh_context* c, uint64_t incoming) {
-  while (!c->weights.empty() && c->bytes + incoming > c->budget) {
-    auto victim = c->weights.begin();
-    for (auto it = c->weights.begin(); it != c->weights.end(); ++it)
-      if (it->second.used < victim->second.used) victim = it;
-    c->bytes -= victim->second.bytes;
-    free_resident(victim->second);
-    c->weights.erase(victim);
+// still admitted, alone. Entries the current call has admitted are never
+// evicted (sh::plan_eviction); when they keep the store over budget the
+// admission fails with SH_ERR_OUT_OF_MEMORY and nothing is evicted.
+int make_room(sh_context* c, uint64_t key, uint64_t incoming) {
+  std::vector<sh::StoreEntry> entries;
+  entries.reserve(c->weights.size());
+  for (const auto& kv : c->weights) entries.push_back({kv.first, kv.second.bytes, kv.second.used, kv.second.pin});
+  std::vector<uint64_t> victims;
+  if (!sh::plan_eviction(entries, c->bytes, c->budget, incoming, c->call, &victims))
+    return fail(SH_ERR_OUT_OF_MEMORY,
+                "weight %llu (%llu bytes): the budget of %llu bytes does not hold it beside the %llu bytes "
+                "this call already uses",
+                (unsigned long long)key, (unsigned long long)incoming, (unsigned long long)c->budget,
+                (unsigned long long)c->bytes);
+  for (uint64_t v : victims) {
+    auto it = c->weights.find(v);
+    c->bytes -= it->second.bytes;
+    free_resident(it->second);
+    c->weights.erase(it);
   }
+  return SH_OK;
 }
 
-// The device copy of a weight, uploading the packed bytes on first use.
+// The device copy of a weight, uploading the packed bytes on first use. The
+// entry is pinned to the current call: later admissions of the same call do
+// not evict it, so every pointer a call has obtained stays valid until it
+// returns.
 int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uint64_t rows,
              uint64_t cols, const uint8_t* data, uint64_t nbytes, Resident** out) {
   auto it = c->weights.find(key);
@@ -202,16 +219,21 @@ int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uin
     if (r.quant == quant && r.rows == rows && r.cols == cols && r.n_expert == n_expert &&
         r.bytes == nbytes) {
       r.used = ++c->clock;
+      r.pin = c->call;
       *out = &r;
       return SH_OK;
     }
+    if (r.pin == c->call)  // replacing it would free memory this call holds
+      return fail(SH_ERR_INVALID_ARGUMENT, "weight key %llu names two different tensors in one call",
+                  (unsigned long long)key);
     // same key, different tensor: replace it
     c->bytes -= r.bytes;
     free_resident(r);
     c->weights.erase(it);
   }
   if (!data) return fail(SH_ERR_INVALID_ARGUMENT, "weight %llu: null data", (unsigned long long)key);
-  make_room(c, nbytes);
+  int rc = make_room(c, key, nbytes);
+  if (rc) return rc;
   Resident r;
   r.quant = quant;
   r.rows = rows;
@@ -220,12 +242,13 @@ int resident(sh_context* c, uint64_t key, uint32_t quant, uint64_t n_expert, uin
   r.bytes = nbytes;
   hipError_t e = hipMalloc(&r.dev, nbytes ? nbytes : 1);
   if (e != hipSuccess) return hip_fail(e, "uploading weight");
-  const int rc = staged_upload(c, r.dev, data, nbytes);
+  rc = staged_upload(c, r.dev, data, nbytes);
   if (rc != SH_OK) {
     (void)hipFree(r.dev);
     return rc;
   }
   r.used = ++c->clock;
+  r.pin = c->call;
   c->bytes += nbytes;
   auto ins = c->weights.emplace(key, r);
   *out = &ins.first->second;
@@ -245,17 +268,24 @@ int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert
   if (cols % uint64_t(g.block) != 0)
     return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of %lld-element blocks",
                 (unsigned long long)cols, (long long)g.block);
-  uint64_t need = n_expert * rows * (cols / uint64_t(g.block)) * uint64_t(g.bytes);
+  uint64_t need = 0;
+  if (__builtin_mul_overflow(n_expert, rows, &need) ||
+      __builtin_mul_overflow(need, cols / uint64_t(g.block), &need) ||
+      __builtin_mul_overflow(need, uint64_t(g.bytes), &need))
+    return fail(SH_ERR_INVALID_ARGUMENT, "tensor of %llu x %llu x %llu elements: byte size overflows 64 bits",
+                (unsigned long long)n_expert, (unsigned long long)rows, (unsigned long long)cols);
   if (nbytes < need)
     return fail(SH_ERR_TRUNCATED, "%llu bytes for a tensor that needs %llu", (unsigned long long)nbytes,
                 (unsigned long long)need);
   return SH_OK;
 }
 
+// Holds the context lock for one call and numbers the call, so the weights
+// it admits are pinned until it returns.
 struct Guard {
   sh_context* c;
   std::lock_guard<std::mutex> lk;
-  explicit Guard(sh_context* ctx) : c(ctx), lk(ctx->mu) {}
+  explicit Guard(sh_context* ctx) : c(ctx), lk(ctx->mu) { ++c->call; }
 };
 
 }  // namespace
@@ -544,6 +574,8 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
                const float* x, float* out) {
   if (!c || !gate || !up || !down || !logits || !x || !out)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
   const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols;
   if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
       down->rows != n_ff || down->cols != n_embd)
@@ -568,9 +600,6 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
   if ((rc = resident(c, gate->key, gate->quant, E, n_embd, n_ff, gate->data, ga, &rg))) return rc;
   if ((rc = resident(c, up->key, up->quant, E, n_embd, n_ff, up->data, ga, &ru))) return rc;
   if ((rc = resident(c, down->key, down->quant, E, n_ff, n_embd, down->data, db, &rd))) return rc;
-  // a budget eviction while admitting a later view may have dropped an earlier one
-  if ((rc = resident(c, gate->key, gate->quant, E, n_embd, n_ff, gate->data, ga, &rg))) return rc;
-  if ((rc = resident(c, up->key, up->quant, E, n_embd, n_ff, up->data, ga, &ru))) return rc;
   const size_t lb = sizeof(float) * n_tok * E, xb = sizeof(float) * n_tok * n_embd;
   const size_t lb_al = (lb + 255) & ~size_t(255);
   if ((rc = c->d_in.ensure(lb_al + xb, "inputs")) || (rc = c->d_out.ensure(xb, "out buffer")) ||
@@ -623,6 +652,8 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
   if (!c || !router || !gate || !up || !down || !gate_shexp || !up_shexp || !down_shexp || !gate_inp_shexp ||
       !x || !out)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
   const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols, n_sh = gate_shexp->rows;
   if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
       down->rows != n_ff || down->cols != n_embd)
@@ -649,8 +680,8 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
   if ((rc = moe_layer_check(E, n_embd, n_ff, n_sh, n_tok, top_k, q, &plan))) return rc;
   Guard g(c);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
-  // all eight tensors resident at once: admit them twice (a budget eviction
-  // while admitting a later one may drop an earlier one), then check
+  // all eight tensors resident at once (each admission is pinned to this
+  // call, so a later one cannot evict an earlier one)
   struct Want {
     uint64_t key;
     uint32_t quant;
@@ -667,19 +698,13 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
       {down_shexp->key, down_shexp->quant, 1, n_embd, n_sh, down_shexp->data},
       {gate_inp_shexp->key, gate_inp_shexp->quant, 1, 1, n_embd, gate_inp_shexp->data}};
   void* dev[8] = {};
-  for (int pass = 0; pass < 2; ++pass)
-    for (int i = 0; i < 8; ++i) {
-      Resident* r = nullptr;
-      const uint64_t nb = want[i].n_expert * want[i].rows * uint64_t(sh::byte_size(want[i].quant, int64_t(want[i].cols)));
-      if ((rc = resident(c, want[i].key, want[i].quant, want[i].n_expert, want[i].rows, want[i].cols,
-                         want[i].data, nb, &r)))
-        return rc;
-      dev[i] = r->dev;
-    }
   for (int i = 0; i < 8; ++i) {
-    auto it = c->weights.find(want[i].key);
-    if (it == c->weights.end() || it->second.dev != dev[i])
-      return fail(SH_ERR_OUT_OF_MEMORY, "the weight budget does not hold the layer's tensors at once");
+    Resident* r = nullptr;
+    const uint64_t nb = want[i].n_expert * want[i].rows * uint64_t(sh::byte_size(want[i].quant, int64_t(want[i].cols)));
+    if ((rc = resident(c, want[i].key, want[i].quant, want[i].n_expert, want[i].rows, want[i].cols,
+                       want[i].data, nb, &r)))
+      return rc;
+    dev[i] = r->dev;
   }
   const size_t xb = sizeof(float) * n_tok * n_embd;
   if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(xb, "out buffer")) ||
@@ -826,6 +851,8 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
   if (!gate || !up || !down || !gate->data || !up->data || !down->data || !logits || !x || !out ||
       !workspace)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
   if (gate->quant != up->quant)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", gate->quant, up->quant);
   sh::MoePlan plan;
@@ -864,6 +891,8 @@ int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd,
                      uint64_t n_ff_shexp, uint32_t n_tok, uint32_t top_k, const float* x, float* out,
                      void* workspace, uint64_t workspace_bytes, void* stream) {
   if (!t || !x || !out || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  if ((t[1].flags | t[2].flags | t[3].flags) & SH_FLAG_EXPERT_OUT_MAJOR)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
   for (int i = 0; i < 8; ++i) {
     if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
     if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
@@ -1370,19 +1399,13 @@ int sh_ffn(sh_context* c, const sh_quant_tensor* gate, const sh_quant_tensor* up
   if (n_embd % 4 != 0 || n_ff % 4 != 0) return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_embd and n_ff must be multiples of 4");
   Guard g(c);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
-  // the three matrices resident at once (admitted twice, as sh_moe_layer)
+  // the three matrices resident at once (pinned to this call)
   void* dev[3] = {};
-  for (int pass = 0; pass < 2; ++pass)
-    for (int i = 0; i < 3; ++i) {
-      Resident* r = nullptr;
-      const uint64_t nb = t[i]->rows * uint64_t(sh::byte_size(t[i]->quant, int64_t(t[i]->cols)));
-      if ((rc = resident(c, t[i]->key, t[i]->quant, 1, t[i]->rows, t[i]->cols, t[i]->data, nb, &r))) return rc;
-      dev[i] = r->dev;
-    }
   for (int i = 0; i < 3; ++i) {
-    auto it = c->weights.find(t[i]->key);
-    if (it == c->weights.end() || it->second.dev != dev[i])
-      return fail(SH_ERR_OUT_OF_MEMORY, "the weight budget does not hold the FFN's matrices at once");
+    Resident* r = nullptr;
+    const uint64_t nb = t[i]->rows * uint64_t(sh::byte_size(t[i]->quant, int64_t(t[i]->cols)));
+    if ((rc = resident(c, t[i]->key, t[i]->quant, 1, t[i]->rows, t[i]->cols, t[i]->data, nb, &r))) return rc;
+    dev[i] = r->dev;
   }
   // x and post_norm in one upload (post_norm 256-byte aligned after x)
   const size_t xb = sizeof(float) * n_tok * n_embd, nb = sizeof(float) * n_embd;

@@ -24,6 +24,8 @@
 //     one; row sums are reduced across the wave with cross-lane shuffles.
 // Weight bytes are read exactly once per launch with 16-byte loads of the
 // block layout; nothing is dequantized to memory.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -1103,18 +1105,18 @@ static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int
 }
 
 // ---------------------------------------------------------------- launch --
-static int g_cu_count = 0;
-
+// CU count of the current device, queried once per device. The cache is
+// atomic: the entry points are called from several threads at once.
 static int cu_count() {
-  if (g_cu_count == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      g_cu_count = n;
-    else
-      g_cu_count = 256;
-  }
-  return g_cu_count;
+  constexpr int kDevs = 64;
+  static std::atomic<int> cache[kDevs];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  int n = dev < kDevs ? cache[dev].load(std::memory_order_relaxed) : 0;
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < kDevs) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 constexpr size_t kMaxLds = 160 * 1024;

@@ -113,6 +113,15 @@ class IoError(BackendError):
     pass
 
 
+class UnsupportedShapeError(BackendError):
+    pass
+
+
+class OutOfMemoryError(BackendError):
+    """A device or pinned allocation failed, or the weight budget cannot hold
+    the tensors one call needs at once."""
+
+
 _ERRORS = {
     SH_ERR_SHAPE: ShapeError,
     SH_ERR_TRUNCATED: TruncatedError,
@@ -121,6 +130,8 @@ _ERRORS = {
     SH_ERR_FORMAT: FormatError,
     SH_ERR_IO: IoError,
     SH_ERR_NOT_FOUND: NotFoundError,
+    SH_ERR_UNSUPPORTED_SHAPE: UnsupportedShapeError,
+    SH_ERR_OUT_OF_MEMORY: OutOfMemoryError,
 }
 
 
@@ -650,7 +661,11 @@ class HipBackend:
         ``x [n_tok][n_embd]`` (float32, C-contiguous)."""
         xv = _f32_out(x)
         nv = _f32_in(post_norm)
-        n_tok = xv.size // gate.cols if gate.cols else 0
+        if nv.size != gate.cols:
+            raise ShapeError(SH_ERR_SHAPE, f"post_norm has {nv.size} elements, n_embd is {gate.cols}")
+        if gate.cols == 0 or xv.size == 0 or xv.size % gate.cols != 0:
+            raise ShapeError(SH_ERR_SHAPE, f"x has {xv.size} elements, not a positive multiple of {gate.cols}")
+        n_tok = xv.size // gate.cols
         g, u, d = gate._c(), up._c(), down._c()
         check(self._L.sh_ffn(self._ctx, C.byref(g), C.byref(u), C.byref(d), nv.ctypes.data, float(eps), n_tok,
                              xv.ctypes.data))

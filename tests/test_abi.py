@@ -72,6 +72,17 @@ def test_dev_entry_points_validate_before_launch():
     assert lib.sh_dequant_dev(12, 0, None, 4, 256, None, None) == H.SH_ERR_INVALID_ARGUMENT
 
 
+def test_tensor_byte_size_overflow_is_refused():
+    # rows * (cols / 256) * 144 past 2^64: refused as an invalid argument, not
+    # wrapped to a small size (which would admit a short buffer)
+    lib = H.load_library()
+    assert lib.sh_gemv_dev(12, 0, None, 1 << 60, 256 << 10, None, None, 1, None) == H.SH_ERR_INVALID_ARGUMENT
+    assert "overflows" in H.last_error()
+    # a product that fits is not an overflow (refused later, for the null pointers)
+    assert lib.sh_gemv_dev(12, 0, None, 1 << 40, 256, None, None, 1, None) == H.SH_ERR_INVALID_ARGUMENT
+    assert "overflows" not in H.last_error()
+
+
 def test_header_is_plain_c_and_links(tmp_path):
     """include/strata_hip.h is a C99 header (what a cgo / bindgen / ctypes
     binding reads), and a C program calling through it links against the

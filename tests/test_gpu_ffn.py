@@ -87,3 +87,39 @@ def test_ffn_host_slices_match_device_path(backend, oracle, n_tok):
                 H.QuantTensor("ffn.down", 14, n_embd, n_ff, mats[2]), norm, 1e-6, got)
     check(got, oracle.dense_ffn((12, 12, 14), mats, n_embd, n_ff, x, norm, 1e-6), x)
     assert np.array_equal(got, run_ffn((12, 12, 14), mats, n_embd, n_ff, x, norm, 1e-6))
+
+
+def test_ffn_budget_holding_two_of_three_refuses(oracle):
+    """Three matrices against a budget that holds two: the call fails with
+    OutOfMemoryError instead of evicting a matrix it already holds, and the
+    context keeps working."""
+    say("ffn budget two of three")
+    n_embd, n_ff = 1024, 2048
+    mats = [S.matrix(12, 51, n_ff, n_embd), S.matrix(12, 52, n_ff, n_embd), S.matrix(12, 53, n_embd, n_ff)]
+    x = S.normal_f32(54, n_embd).reshape(1, n_embd)
+    norm = S.normal_f32(55, n_embd)
+    ts = (H.QuantTensor("bud.gate", 12, n_ff, n_embd, mats[0]), H.QuantTensor("bud.up", 12, n_ff, n_embd, mats[1]),
+          H.QuantTensor("bud.down", 12, n_embd, n_ff, mats[2]))
+    budget = mats[0].nbytes + mats[1].nbytes + mats[2].nbytes // 2
+    with H.HipBackend(0, budget) as be:
+        got = x.copy()
+        with pytest.raises(H.OutOfMemoryError):
+            be.ffn(*ts, norm, 1e-6, got)
+        assert np.array_equal(got, x)  # untouched: nothing ran
+        assert be.resident_bytes() <= budget
+    with H.HipBackend(0, sum(m.nbytes for m in mats)) as be:
+        got = x.copy()
+        be.ffn(*ts, norm, 1e-6, got)
+    check(got, oracle.dense_ffn((12, 12, 12), mats, n_embd, n_ff, x, norm, 1e-6), x)
+
+
+def test_ffn_host_shape_errors(backend):
+    say("ffn host shape errors")
+    n_embd, n_ff = 1024, 2048
+    mats = [S.matrix(12, 61, n_ff, n_embd), S.matrix(12, 62, n_ff, n_embd), S.matrix(12, 63, n_embd, n_ff)]
+    ts = (H.QuantTensor("se.gate", 12, n_ff, n_embd, mats[0]), H.QuantTensor("se.up", 12, n_ff, n_embd, mats[1]),
+          H.QuantTensor("se.down", 12, n_embd, n_ff, mats[2]))
+    with pytest.raises(H.ShapeError):  # short post_norm
+        backend.ffn(*ts, np.ones(n_embd - 4, np.float32), 1e-6, np.zeros(n_embd, np.float32))
+    with pytest.raises(H.ShapeError):  # ragged x
+        backend.ffn(*ts, np.ones(n_embd, np.float32), 1e-6, np.zeros(n_embd + 4, np.float32))

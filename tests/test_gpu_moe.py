@@ -425,3 +425,49 @@ def test_moe_ffn_random_configs(backend, oracle, seed):
         assert elem_rel_err(out[t], ref[t], floor=1.0) <= 1e-3
     for name in (f"rg{seed}", f"ru{seed}", f"rd{seed}"):
         backend.evict(name)
+
+
+def test_moe_ffn_budget_holding_two_of_three_refuses(oracle, moe_config_tensors):
+    # gate and up (Q4_K, 113 MB each) and down (Q6_K, 165 MB) of the MoE
+    # config; the budget holds any two of them but not all three, so the
+    # call must fail before any launch rather than evict a tensor it holds
+    gate, up, down = moe_config_tensors
+    n_expert, n_embd, n_ff, top_k = 128, 2048, 768, 8
+    say("moe ffn budget two of three")
+    budget = gate.nbytes + down.nbytes
+    assert budget < gate.nbytes + up.nbytes + down.nbytes
+    logits = S.router_logits(4150, 1, n_expert)
+    x = S.normal_f32(4250, n_embd).reshape(1, n_embd)
+    g = H.ExpertView("bud.gate", 12, n_expert, n_embd, n_ff, gate)
+    u = H.ExpertView("bud.up", 12, n_expert, n_embd, n_ff, up)
+    d = H.ExpertView("bud.down", 14, n_expert, n_ff, n_embd, down)
+    with H.HipBackend(0, budget) as be:
+        for _ in range(2):  # the second attempt starts with gate and up resident
+            with pytest.raises(H.OutOfMemoryError):
+                be.moe_ffn(g, u, d, logits, x, top_k)
+            assert be.resident_bytes() <= budget
+        # the context still serves calls that fit: expert 5 of down alone
+        xe = S.normal_f32(4260, n_ff)
+        y = np.empty(n_embd, np.float32)
+        be.expert_gemv(d, 5, xe, y)
+        want = oracle.expert_gemv(14, n_expert, n_ff, n_embd, down, 5, xe)
+        assert rel_err(y, want) <= 1e-3
+    # and a budget that holds all three runs the call
+    with H.HipBackend(0, gate.nbytes + up.nbytes + down.nbytes) as be:
+        out = be.moe_ffn(g, u, d, logits, x, top_k)
+    ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    assert rel_err(out, ref) <= 1e-3
+
+
+def test_fused_moe_refuses_out_major_views(backend):
+    n_expert, n_embd, n_ff, top_k, n_tok = 8, 256, 256, 2, 1
+    say("moe ffn out-major refused")
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 6300)
+    logits = S.router_logits(6310, n_tok, n_expert)
+    x = S.normal_f32(6320, n_tok * n_embd).reshape(n_tok, n_embd)
+    om = H.FLAG_EXPERT_OUT_MAJOR
+    g = H.ExpertView("om.g", 12, n_expert, n_ff, n_embd, gate, flags=om)
+    u = H.ExpertView("om.u", 12, n_expert, n_ff, n_embd, up, flags=om)
+    d = H.ExpertView("om.d", 14, n_expert, n_embd, n_ff, down, flags=om)
+    with pytest.raises(H.UnsupportedShapeError):
+        backend.moe_ffn(g, u, d, logits, x, top_k)
