@@ -58,10 +58,48 @@ def parse():
     return ap.parse_args()
 
 
+def _graph_of(torch, stream, calls, n):
+    """A HIP graph of exactly n calls, cycling through `calls`."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        h = torch.cuda.current_stream().cuda_stream
+        for i in range(n):
+            calls[i % len(calls)](h)
+    return g
+
+
+def _time_graph_calls(torch, stream, calls, steps, warmup):
+    """Runs `warmup` calls untimed, then times exactly `steps` calls, each
+    set captured as one HIP graph and replayed once; events on `stream`.
+    Returns ms per call."""
+    with torch.cuda.stream(stream):  # eager pass: the calls are accepted
+        for f in calls:
+            f(stream.cuda_stream)
+    torch.cuda.synchronize()
+    if warmup > 0:
+        gw = _graph_of(torch, stream, calls, warmup)
+        with torch.cuda.stream(stream):
+            gw.replay()
+        torch.cuda.synchronize()
+        del gw
+    g = _graph_of(torch, stream, calls, steps)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del g
+    return ms
+
+
 def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags=0):
-    """Mean ms per launch over `steps` launches (graph replays), rotating over
-    copies of the weights; returns (ms, n_copies, launches_timed)."""
-    import numpy as np
+    """Mean ms per launch over exactly `steps` launches (one graph replay)
+    after `warmup` untimed ones, rotating over copies of the weights; returns
+    (ms, n_copies, launches_timed)."""
     from strata_hip import synth as S
 
     nbytes = w_host.nbytes
@@ -74,68 +112,23 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
     stream = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
 
-    def launch_all(s):
-        for c in copies:
-            H.gemv_dev(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch, s, flags)
+    def call(c):
+        return lambda s: H.gemv_dev(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch, s, flags)
 
-    # eager warm-up (also checks the launch is accepted before capture)
-    with torch.cuda.stream(stream):
-        launch_all(stream.cuda_stream)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        launch_all(torch.cuda.current_stream().cuda_stream)
-    reps_w = max(1, -(-warmup // n_copies))
-    reps = max(1, -(-steps // n_copies))
-    with torch.cuda.stream(stream):
-        for _ in range(reps_w):
-            g.replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    with torch.cuda.stream(stream):
-        for _ in range(reps):
-            g.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / (reps * n_copies)
-    del g, copies, base
+    ms = _time_graph_calls(torch, stream, [call(c) for c in copies], steps, warmup)
+    del copies, base
     torch.cuda.empty_cache()
-    return ms, n_copies, reps * n_copies
+    return ms, n_copies, steps
 
 
 def time_calls(torch, calls, steps, warmup):
-    """Mean ms per call of a list of enqueue functions f(stream_handle),
-    captured once in a HIP graph and replayed; calls are cycled in order."""
+    """Mean ms per call of a list of enqueue functions f(stream_handle):
+    exactly `steps` calls, cycled in order, captured in one HIP graph and
+    replayed once after `warmup` untimed calls."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for f in calls:
-            f(stream.cuda_stream)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        for f in calls:
-            f(torch.cuda.current_stream().cuda_stream)
-    n = len(calls)
-    with torch.cuda.stream(stream):
-        for _ in range(max(1, -(-warmup // n))):
-            g.replay()
-    torch.cuda.synchronize()
-    reps = max(1, -(-steps // n))
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    with torch.cuda.stream(stream):
-        for _ in range(reps):
-            g.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / (reps * n)
-    del g
-    return ms
+    return _time_graph_calls(torch, stream, calls, steps, warmup)
 
 
 def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):

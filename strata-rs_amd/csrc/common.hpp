@@ -160,6 +160,17 @@ __device__ __forceinline__ void transpose_bytes(uint32_t v0, uint32_t v1, uint32
   p2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);  // byte 2
 }
 
+// Lane exchanges inside a quad of lanes as DPP moves (VALU, no LDS round
+// trip): the value of lane i ^ 1, and of lane i ^ 2.
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ float dpp_xor1(float v) { return __builtin_bit_cast(float, dpp_xor1(__builtin_bit_cast(uint32_t, v))); }
+__device__ __forceinline__ float dpp_xor2(float v) { return __builtin_bit_cast(float, dpp_xor2(__builtin_bit_cast(uint32_t, v))); }
+
 // bytes [shift, shift + 4) of the 8-byte little-endian pair (lo, hi).
 __device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
   return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);

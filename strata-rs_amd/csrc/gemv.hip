@@ -585,21 +585,25 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 __host__ __device__ inline int plane_stride(int cols) { return cols + cols / 4; }
 __host__ __device__ inline int limb_lds_bytes(int cols) { return 3 * plane_stride(cols) + (cols / 32) * 16; }
 
-// Converts one 16-column group held in registers and writes it to LDS. The
-// thread handling group g ^ 1 (the other half of the 32-column block) is the
-// neighbouring lane, which shares the block maximum and sum.
-__device__ __forceinline__ void limb_group(uint8_t* lds, int cols, int g, bool valid, f32x4 a, f32x4 b,
-                                           f32x4 c, f32x4 d) {
-  const float xs[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w,
-                        c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+// Converts 8 consecutive columns held in registers (elements 8t .. 8t + 7,
+// t the thread) and writes them to LDS. The four lanes of a 32-column block
+// are t & ~3 .. t | 3, neighbours in one quad of the wave: they exchange the
+// block's maximum and sums with DPP moves, and lane t & ~3 writes the block's
+// record. K (the integer sum of the low limbs) is formed only when LOW is
+// set: signed Q8_0 codes need it; the unsigned codes of the k-quants do not.
+template <bool LOW>
+__device__ __forceinline__ void limb_group8(uint8_t* lds, int cols, int t, bool valid, f32x4 a, f32x4 b) {
+  const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   float m = 0.f, s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8; ++i) {
     m = fmaxf(m, fabsf(xs[i]));
     s += xs[i];
   }
-  m = fmaxf(m, __shfl_xor(m, 1, kWave));
-  const float s_other = __shfl_xor(s, 1, kWave);
+  m = fmaxf(m, dpp_xor1(m));
+  m = fmaxf(m, dpp_xor2(m));
+  const float s16 = s + dpp_xor1(s);  // the lane pair's 16 columns
+  const float s16_other = dpp_xor2(s16);
   // k with m * 2^k < 2^22; for m == 0 any k works
   // (clamped so 2^k stays finite for blocks whose maximum is below 2^-104)
   int e = 0;
@@ -608,31 +612,34 @@ __device__ __forceinline__ void limb_group(uint8_t* lds, int cols, int g, bool v
   const float up = ldexpf(1.f, k);
   // a NaN or infinite block keeps its NaN through the scale
   const float down = (m - m == 0.f) ? ldexpf(1.f, -k) : __builtin_nanf("");
-  uint32_t v[16];
-  uint32_t low = 0;  // sum of (v & 0xFFFF) over the group
+  uint32_t v[8];
+  uint32_t low = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 8; ++i) {
     // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
-    const float t = __builtin_fmaf(xs[i], up, 12582912.0f);
-    v[i] = __builtin_bit_cast(uint32_t, t) - 0x4B400000u;
-    low += v[i] & 0xFFFFu;
+    const float tt = __builtin_fmaf(xs[i], up, 12582912.0f);
+    v[i] = __builtin_bit_cast(uint32_t, tt) - 0x4B400000u;
+    if constexpr (LOW) low += v[i] & 0xFFFFu;
   }
-  const uint32_t low_other = __shfl_xor(low, 1, kWave);
+  if constexpr (LOW) {
+    low += dpp_xor1(low);
+    low += dpp_xor2(low);
+  }
   if (!valid) return;
-  const int e0 = 16 * g;
+  const int e0 = 8 * t;
   const int off = e0 + 16 * (e0 >> 6);
   const int ps = plane_stride(cols);
-  uint32_t pc[4], pb[4], pa[4];
+  uint32_t pc[2], pb[2], pa[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) transpose_bytes(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], pc[q], pb[q], pa[q]);
-  *reinterpret_cast<u32x4*>(lds + off) = u32x4{pa[0], pa[1], pa[2], pa[3]};
-  *reinterpret_cast<u32x4*>(lds + ps + off) = u32x4{pb[0], pb[1], pb[2], pb[3]};
-  *reinterpret_cast<u32x4*>(lds + 2 * ps + off) = u32x4{pc[0], pc[1], pc[2], pc[3]};
-  if ((g & 1) == 0) {
-    *reinterpret_cast<u32x4*>(lds + 3 * ps + 16 * (g >> 1)) =
-        u32x4{__builtin_bit_cast(uint32_t, s), __builtin_bit_cast(uint32_t, s_other),
-              __builtin_bit_cast(uint32_t, down), low + low_other};
-  }
+  for (int q = 0; q < 2; ++q) transpose_bytes(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], pc[q], pb[q], pa[q]);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(lds + off) = u32x2{pa[0], pa[1]};
+  *reinterpret_cast<u32x2*>(lds + ps + off) = u32x2{pb[0], pb[1]};
+  *reinterpret_cast<u32x2*>(lds + 2 * ps + off) = u32x2{pc[0], pc[1]};
+  if ((t & 3) == 0)
+    *reinterpret_cast<u32x4*>(lds + 3 * ps + 16 * (t >> 2)) =
+        u32x4{__builtin_bit_cast(uint32_t, s16), __builtin_bit_cast(uint32_t, s16_other),
+              __builtin_bit_cast(uint32_t, down), low};
 }
 
 // The lane's 64 columns: limb dwords for elements 4j..4j+3 and the two
@@ -895,7 +902,7 @@ struct LimbQ6K {
 // instead of x; kLimbResid writes y = xres + sum (one f32 add, qwen35.rs:127-129).
 constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4;
 
-template <class F, int R, int MAXQ, int MODE = 0>
+template <class F, int R, int MAXQ, int MODE = 0, int NPRE = 1>
 __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restrict__ w, int rows,
                                                         int cols, int64_t row_bytes,
                                                         const float* __restrict__ x,
@@ -904,6 +911,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
                                                         const float* __restrict__ xu,
                                                         const float* xres) {  // xres may be y (in place)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  constexpr bool kLow = F::kQuant == kQ8_0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
   const int units = cols >> 6;
@@ -943,32 +951,55 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
       ++pw;
     }
   };
+
+  // x as limbs, 8 columns per thread and round (4096 columns a round). The
+  // x loads of the first NPRE rounds are issued before the first weight
+  // item's, so the wait for them does not wait for the weights; their
+  // conversion is branch-free (a round's idle threads convert a clamped
+  // copy and skip the write), which keeps the loads ahead of the weight
+  // loads. Rounds past NPRE (rows wider than NPRE * 4096 columns) load and
+  // convert in a loop after the first item is requested.
+  const int n8 = cols >> 3;
+  const int nthr = blockDim.x;
+  f32x4 xv[NPRE][2], uv[NPRE][2];
+#pragma unroll
+  for (int k = 0; k < NPRE; ++k) {
+    const int t = min(tid + k * nthr, n8 - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + 8 * t);
+    xv[k][0] = src[0];
+    xv[k][1] = src[1];
+    if constexpr ((MODE & kLimbSiluX) != 0) {
+      const f32x4* su = reinterpret_cast<const f32x4*>(xu + 8 * t);
+      uv[k][0] = su[0];
+      uv[k][1] = su[1];
+    }
+  }
   typename F::Load A[R], B[R];
   issue(A);
-
-  // stage x as limbs (a wave whose 64 groups all lie past the end skips the
-  // round: the last round is usually partial)
-  const int groups = cols >> 4;
-  const int wave_first = tid & ~63;
-  for (int g0 = 0; g0 < groups; g0 += blockDim.x) {
-    if (g0 + wave_first >= groups) break;
-    const int g = g0 + tid;
-    const int gl = min(g, groups - 1);
-    const f32x4* src = reinterpret_cast<const f32x4*>(x + 16 * gl);
+  auto stage = [&](int t, f32x4 a, f32x4 b, f32x4 ua, f32x4 ub) {
     if constexpr ((MODE & kLimbSiluX) != 0) {
-      const f32x4* su = reinterpret_cast<const f32x4*>(xu + 16 * gl);
-      f32x4 h[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
 #pragma clang fp contract(off)
-        const f32x4 gv = src[k], uv = su[k];
-        h[k] = f32x4{gv.x / (1.f + expf(-gv.x)) * uv.x, gv.y / (1.f + expf(-gv.y)) * uv.y,
-                     gv.z / (1.f + expf(-gv.z)) * uv.z, gv.w / (1.f + expf(-gv.w)) * uv.w};
-      }
-      limb_group(lds8, cols, g, g < groups, h[0], h[1], h[2], h[3]);
+      const f32x4 h0{a.x / (1.f + expf(-a.x)) * ua.x, a.y / (1.f + expf(-a.y)) * ua.y,
+                     a.z / (1.f + expf(-a.z)) * ua.z, a.w / (1.f + expf(-a.w)) * ua.w};
+      const f32x4 h1{b.x / (1.f + expf(-b.x)) * ub.x, b.y / (1.f + expf(-b.y)) * ub.y,
+                     b.z / (1.f + expf(-b.z)) * ub.z, b.w / (1.f + expf(-b.w)) * ub.w};
+      limb_group8<kLow>(lds8, cols, t, t < n8, h0, h1);
     } else {
-      limb_group(lds8, cols, g, g < groups, src[0], src[1], src[2], src[3]);
+      limb_group8<kLow>(lds8, cols, t, t < n8, a, b);
     }
+  };
+#pragma unroll
+  for (int k = 0; k < NPRE; ++k) stage(tid + k * nthr, xv[k][0], xv[k][1], uv[k][0], uv[k][1]);
+  for (int t0 = NPRE * nthr; t0 < n8; t0 += nthr) {
+    const int t = min(t0 + tid, n8 - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + 8 * t);
+    f32x4 ua{}, ub{};
+    if constexpr ((MODE & kLimbSiluX) != 0) {
+      const f32x4* su = reinterpret_cast<const f32x4*>(xu + 8 * t);
+      ua = su[0];
+      ub = su[1];
+    }
+    stage(t0 + tid, src[0], src[1], ua, ub);
   }
   __syncthreads();
   if (n_items == 0) return;
@@ -1168,9 +1199,19 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   if (nwin == 1 && per > MAXQ) per = MAXQ;
   const int waves = (n_rg + per - 1) / per;
   const int blocks = (waves + wpg - 1) / wpg;
-  hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE>), dim3(unsigned(blocks)), dim3(threads),
-                     size_t(limb_lds_bytes(cols)), stream, w, rows, cols, row_bytes, x, y, per, flags, w2, rows1, xu,
-                     xres);
+  // x rounds (threads * 8 columns each) whose loads go ahead of the weights
+  const int rounds = (cols + threads * 8 - 1) / (threads * 8);
+  const dim3 grid = dim3(unsigned(blocks)), block = dim3(unsigned(threads));
+  const size_t lds = size_t(limb_lds_bytes(cols));
+  if (rounds <= 1)
+    hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 1>), grid, block, lds, stream, w, rows, cols, row_bytes, x,
+                       y, per, flags, w2, rows1, xu, xres);
+  else if (rounds == 2)
+    hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 2>), grid, block, lds, stream, w, rows, cols, row_bytes, x,
+                       y, per, flags, w2, rows1, xu, xres);
+  else
+    hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 3>), grid, block, lds, stream, w, rows, cols, row_bytes, x,
+                       y, per, flags, w2, rows1, xu, xres);
   return hipGetLastError();
 }
 

@@ -247,3 +247,4 @@ def test_gemv_random_shapes(backend, oracle, seed):
         for b in range(batch):
             check(y[b], oracle.gemv(quant, rows, cols, w, x[b], threads=8))
         backend.evict(f"rand{seed}_{case}")
+
