@@ -1347,16 +1347,13 @@ int sh_ffn_workspace_bytes(uint32_t n_tok, uint64_t n_embd, uint64_t n_ff, uint6
   return SH_OK;
 }
 
-int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
-               const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
-               void* stream) {
-  if (!t || !x || !post_norm || !out || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
-  uint64_t need = 0;
-  int rc = sh_ffn_workspace_bytes(n_tok, n_embd, n_ff, &need);
+// Validation shared by sh_ffn_dev and sh_ffn_dev_noalloc (everything but
+// the workspace, which each checks itself).
+static int ffn_dev_check(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
+                         const float* post_norm, const float* out, uint64_t* need) {
+  if (!t || !x || !post_norm || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
+  int rc = sh_ffn_workspace_bytes(n_tok, n_embd, n_ff, need);
   if (rc) return rc;
-  if (workspace_bytes < need)
-    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed", (unsigned long long)workspace_bytes,
-                (unsigned long long)need);
   const uint64_t dims[3][2] = {{n_ff, n_embd}, {n_ff, n_embd}, {n_embd, n_ff}};
   for (int i = 0; i < 3; ++i) {
     if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
@@ -1368,14 +1365,34 @@ int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t 
         ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
       return fail(SH_ERR_INVALID_ARGUMENT, "misaligned tensor %d", i);
   }
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 255u) || n_embd % 4 != 0 || n_ff % 4 != 0)
-    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned x, out or workspace (or n_embd, n_ff not multiples of 4)");
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u) || n_embd % 4 != 0 ||
+      n_ff % 4 != 0)
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned x or out (or n_embd, n_ff not multiples of 4)");
+  return SH_OK;
+}
+
+static hipError_t ffn_dev_launch(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
+                                 const float* x, const float* post_norm, double eps, float* out, void* workspace,
+                                 void* stream) {
   auto q6 = [](uint32_t f) { return (f & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
-  HIP_TRY(sh::launch_ffn(t[0].quant, t[1].quant, t[2].quant, t[0].data, t[1].data, t[2].data, q6(t[0].flags),
-                         q6(t[1].flags), q6(t[2].flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), x, post_norm,
-                         eps, out, workspace, static_cast<hipStream_t>(stream)),
-          "ffn launch");
+  return sh::launch_ffn(t[0].quant, t[1].quant, t[2].quant, t[0].data, t[1].data, t[2].data, q6(t[0].flags),
+                        q6(t[1].flags), q6(t[2].flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), x, post_norm, eps,
+                        out, workspace, static_cast<hipStream_t>(stream));
+}
+
+int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
+               const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
+               void* stream) {
+  uint64_t need = 0;
+  int rc = ffn_dev_check(t, n_embd, n_ff, n_tok, x, post_norm, out, &need);
+  if (rc) return rc;
+  if (!workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null workspace");
+  if (workspace_bytes < need)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  HIP_TRY(ffn_dev_launch(t, n_embd, n_ff, n_tok, x, post_norm, eps, out, workspace, stream), "ffn launch");
   return SH_OK;
 }
 
