@@ -387,6 +387,18 @@ int sh_ffn(sh_context* ctx, const sh_quant_tensor* gate, const sh_quant_tensor* 
 int sh_ffn_dev(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
                const float* post_norm, double eps, float* out, void* workspace, uint64_t workspace_bytes,
                void* stream);
+/* sh_ffn_dev without a workspace argument, and without allocating anything:
+ * its intermediates live in a fixed 4 MiB device array inside the library
+ * (one per GPU, held until the process ends). No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Shapes whose sh_ffn_workspace_bytes exceed 4 MiB are refused with
+ * SH_ERR_UNSUPPORTED_SHAPE (at n_embd 4096, n_ff 12288: up to 23 tokens).
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must not be issued. Same
+ * results as sh_ffn_dev, bit for bit. */
+int sh_ffn_dev_noalloc(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
+                       const float* x, const float* post_norm, double eps, float* out, void* stream);
 
 /* The elementwise methods batched over rows, on device pointers: the same
  * arithmetic per row as the host-slice forms; enqueued on `stream`.

@@ -23,6 +23,14 @@
 #include "kernels.hpp"
 #include "store.hpp"
 
+// Device scratch of the allocation-free entry point (sh_ffn_dev_noalloc):
+// a fixed array in the library's code object, so using it allocates
+// nothing. Each device holds its own copy until the process ends. Host code
+// never passes `scratch` itself (a host-side name, not a device address):
+// it passes the per-device address from hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
 
 thread_local std::string t_error;
@@ -49,6 +57,11 @@ int hip_fail(hipError_t e, const char* what) {
     hipError_t e_ = (expr);                  \
     if (e_ != hipSuccess) return hip_fail(e_, what); \
   } while (0)
+
+// Per-device addresses of `scratch` (hipGetSymbolAddress, once per device).
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices];
 
 struct Resident {
   void* dev = nullptr;
@@ -1393,6 +1406,40 @@ int sh_ffn_dev(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t 
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   HIP_TRY(ffn_dev_launch(t, n_embd, n_ff, n_tok, x, post_norm, eps, out, workspace, stream), "ffn launch");
+  return SH_OK;
+}
+
+// The current device's address of `scratch`, looked up once per device (with
+// that device current) and kept.
+static int scratch_address(void** out) {
+  static_assert(sizeof(scratch) == kScratchBytes, "scratch size");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices) return fail(SH_ERR_NO_DEVICE, "device %d: no scratch slot", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(SH_ERR_DEVICE, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SH_OK;
+}
+
+int sh_ffn_dev_noalloc(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok, const float* x,
+                       const float* post_norm, double eps, float* out, void* stream) {
+  uint64_t need = 0;
+  int rc = ffn_dev_check(t, n_embd, n_ff, n_tok, x, post_norm, out, &need);
+  if (rc) return rc;
+  if (need > kScratchBytes)
+    return fail(SH_ERR_UNSUPPORTED_SHAPE,
+                "ffn of %u tokens at %llu x %llu needs %llu bytes of scratch; the allocation-free path has %llu",
+                n_tok, (unsigned long long)n_embd, (unsigned long long)n_ff, (unsigned long long)need,
+                (unsigned long long)kScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  HIP_TRY(ffn_dev_launch(t, n_embd, n_ff, n_tok, x, post_norm, eps, out, ws, stream), "ffn launch");
   return SH_OK;
 }
 

@@ -64,7 +64,7 @@ EXPORTS = (
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
     "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
-    "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn",
+    "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn", "sh_ffn_dev_noalloc",
 )
 
 
@@ -252,6 +252,7 @@ def load_library() -> C.CDLL:
     L.sh_weight_upload.argtypes = [vp, u64, u32, u64, u64, u64, vp, u64]
     L.sh_ffn_workspace_bytes.argtypes = [u32, u64, u64, u64p]
     L.sh_ffn_dev.argtypes = [C.POINTER(_ExpertDevC), u64, u64, u32, vp, vp, dbl, vp, vp, u64, vp]
+    L.sh_ffn_dev_noalloc.argtypes = [C.POINTER(_ExpertDevC), u64, u64, u32, vp, vp, dbl, vp, vp]
     L.sh_ffn.argtypes = [vp, C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC), C.POINTER(_QuantTensorC), f32p, dbl,
                          u32, f32p]
     _lib = L
@@ -791,3 +792,12 @@ def ffn_dev(tensors, n_embd: int, n_ff: int, n_tok: int, x_ptr: int, norm_ptr: i
     arr = (_ExpertDevC * 3)(*[_ExpertDevC(int(q), f, p) for q, f, p in tensors])
     check(load_library().sh_ffn_dev(arr, n_embd, n_ff, n_tok, x_ptr, norm_ptr, float(eps), out_ptr, ws_ptr, ws_bytes,
                                     stream or None))
+
+
+def ffn_dev_noalloc(tensors, n_embd: int, n_ff: int, n_tok: int, x_ptr: int, norm_ptr: int, eps: float, out_ptr: int,
+                    stream: int = 0) -> None:
+    """ffn_dev with the library's fixed device scratch (no allocation; at
+    most 4 MiB of intermediates; overlapping calls on one GPU race)."""
+    arr = (_ExpertDevC * 3)(*[_ExpertDevC(int(q), f, p) for q, f, p in tensors])
+    check(load_library().sh_ffn_dev_noalloc(arr, n_embd, n_ff, n_tok, x_ptr, norm_ptr, float(eps), out_ptr,
+                                            stream or None))
