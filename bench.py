@@ -14,7 +14,9 @@ Prints ONE JSON line (rank 0):
   roofline       algorithmic bytes (weights + x + y) per launch over the mean
                  launch time, against MI355X's 8 TB/s; `traffic` is the HBM
                  bytes per launch measured with rocprofv3 counters, when a
-                 summary exists under profiles/
+                 summary exists under profiles/; `measured_ceiling_GBps` is a
+                 plain streaming read of the same bytes over the same rotating
+                 copies in the same graph harness
   cpu_baseline   the reference's CPU path (the C restatement of ops::gemv,
                  single thread, sequential f64) timed on this host on a
                  bounded sample of the same workload
@@ -24,7 +26,8 @@ Prints ONE JSON line (rank 0):
                  16 tokens, routing varied per call, 3 copies of the expert
                  set rotated); the prefill matmul (Q4_K 12288x4096 times 512
                  tokens, bf16 and Q8 activation modes, activation pre-pass
-                 included)
+                 included); the host-slice sh_gemv (the trait drop-in, PCIe
+                 round trip included) at the headline shape
 """
 from __future__ import annotations
 
@@ -96,10 +99,12 @@ def _time_graph_calls(torch, stream, calls, steps, warmup):
     return ms
 
 
-def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags=0):
+def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags=0, ceiling=None):
     """Mean ms per launch over exactly `steps` launches (one graph replay)
     after `warmup` untimed ones, rotating over copies of the weights; returns
-    (ms, n_copies, launches_timed)."""
+    (ms, n_copies, launches_timed). With `ceiling` (a dict), a plain
+    streaming read of the same copies (sh_stream_read_dev) is timed the same
+    way and its ms per launch stored under ceiling["ms"]."""
     from strata_hip import synth as S
 
     nbytes = w_host.nbytes
@@ -116,6 +121,13 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
         return lambda s: H.gemv_dev(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch, s, flags)
 
     ms = _time_graph_calls(torch, stream, [call(c) for c in copies], steps, warmup)
+    if ceiling is not None:
+        folds = torch.empty(H.STREAM_READ_BLOCKS, dtype=torch.int32, device=dev)
+
+        def read(c):
+            return lambda s: H.stream_read_dev(c.data_ptr(), nbytes, folds.data_ptr(), s)
+
+        ceiling["ms"] = _time_graph_calls(torch, stream, [read(c) for c in copies], steps, warmup)
     del copies, base
     torch.cuda.empty_cache()
     return ms, n_copies, steps
@@ -364,7 +376,7 @@ def cpu_baseline(w, x, rows, cols, seconds):
         times.append(time.perf_counter() - t0)
     t = sorted(times)[2]
     gbs = n_rows * rb / t / 1e9
-    nthreads = os.cpu_count() or 1
+    nthreads = min(16, os.cpu_count() or 1)  # the box's CPU share per GPU
     t0 = time.perf_counter()
     O.gemv(O.Q4_K, rows, cols, w, x, threads=nthreads)
     t_mt = time.perf_counter() - t0
@@ -378,7 +390,37 @@ def cpu_baseline(w, x, rows, cols, seconds):
                   f"as the reference runs)",
         "all_cores": {"value": round(rows * rb / t_mt / 1e9, 4), "cores": nthreads,
                       "sample": "the whole matrix once, rows split over threads"},
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
     }
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def host_slice_gemv(H, S, w, x, rows, cols, calls):
+    """The trait drop-in path end to end: sh_gemv on host slices (x copied in
+    through pinned staging, the launch, y read back, a synchronisation) with
+    the weights already resident; microseconds per call."""
+    import numpy as np
+    y = np.empty(rows, np.float32)
+    with H.HipBackend(0) as be:
+        t = H.QuantTensor("bench.host_slice", S.Q4_K, rows, cols, w)
+        for _ in range(10):
+            be.gemv(t, x, y)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            be.gemv(t, x, y)
+        return (time.perf_counter() - t0) / calls * 1e6
 
 
 def load_traffic(name):
@@ -440,10 +482,13 @@ def main():
     wbytes = w.nbytes
     print(f"[bench] Q4_K {rows}x{cols} ({wbytes} B) batch 1: warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
-    ms, n_copies, launches = timed_graph(torch, H, S.Q4_K, rows, cols, w, 1, args.steps, args.warmup)
+    ceiling = {}
+    ms, n_copies, launches = timed_graph(torch, H, S.Q4_K, rows, cols, w, 1, args.steps, args.warmup,
+                                         ceiling=ceiling)
     gbs = wbytes / (ms * 1e-3) / 1e9
     alg = wbytes + 4 * cols + 4 * rows
     achieved = alg / (ms * 1e-3) / 1e9
+    ceil_gbs = wbytes / (ceiling["ms"] * 1e-3) / 1e9
     out = {
         "metric": "Q4_K fused matvec packed-weight GB/s + % HBM peak (4096x12288, batch 1)",
         "value": round(gbs, 2),
@@ -451,6 +496,7 @@ def main():
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "n_gpus": 1,
         "steps": launches,
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
@@ -463,7 +509,12 @@ def main():
                    "rows": rows, "cols": cols, "batch": 1, "weight_bytes": wbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("gemv_q4k_4096x12288_b1.traffic.json")},
+                     "traffic": load_traffic("gemv_q4k_4096x12288_b1.traffic.json"),
+                     "measured_ceiling_GBps": round(ceil_gbs, 2),
+                     "frac_of_measured_ceiling": round(gbs / ceil_gbs, 4),
+                     "ceiling": "plain streaming read of the same 28,311,552 bytes (sh_stream_read_dev: 16-byte "
+                                "loads, 2048 x 256 threads) over the same rotating copies, one HIP graph, "
+                                f"{ceiling['ms'] * 1e3:.3f} us per launch"},
     }
     print(f"[bench] {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
 
@@ -486,6 +537,8 @@ def main():
             extra[name] = {"us_per_launch": round(t * 1e3, 3),
                            "weight_GBps": round(wm.nbytes / (t * 1e-3) / 1e9, 1),
                            "pct_hbm_peak": round(100 * wm.nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+            if q == S.Q6_K:
+                extra[name]["scale_reading"] = "u8, as strata-gguf reads the Q6_K sub-block scales (dequant.rs:211)"
             if name == "q4k_gate_12288x4096_b1":
                 prefill_w = wm
             del wm
@@ -500,6 +553,12 @@ def main():
         extra.update(bench_ffn(torch, H, S, 240))
         print("[bench] extra elementwise methods", file=sys.stderr, flush=True)
         extra.update(bench_rowops(torch, H, S, 200))
+        print("[bench] extra host-slice gemv", file=sys.stderr, flush=True)
+        us = host_slice_gemv(H, S, w, S.normal_f32(7, cols), rows, cols, 200)
+        extra["host_slice_gemv_q4k_4096x12288_b1"] = {
+            "us_per_call": round(us, 2),
+            "note": "sh_gemv on host slices (the ComputeBackend::gemv drop-in): x in through pinned staging, "
+                    "launch, y back, synchronise; weights resident; 200 calls, wall clock"}
         out["extra"] = extra
 
     if not args.no_cpu:

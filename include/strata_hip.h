@@ -323,6 +323,13 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream);
 
+/* A plain streaming read of `nbytes` at `data` (16-byte aligned, a multiple
+ * of 16 bytes), the read-bandwidth ceiling the matvecs are measured against:
+ * 2048 workgroups of 256 threads, one 16-byte load per lane per step;
+ * out[2048] receives per-workgroup XOR folds of the 32-bit words read (their
+ * XOR is the XOR of all words). No reference counterpart. */
+int sh_stream_read_dev(const void* data, uint64_t nbytes, uint32_t* out, void* stream);
+
 /* ---- GGUF weight source (host code; no device needed except the upload) */
 /* GgufFile::open (reader.rs:231-353): maps `path` read-only and parses the
  * header, metadata and tensor directory with the reference's checks and

@@ -827,6 +827,14 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
   return SH_OK;
 }
 
+int sh_stream_read_dev(const void* data, uint64_t nbytes, uint32_t* out, void* stream) {
+  if ((!data && nbytes) || !out) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(data) & 15u) || (nbytes & 15u))
+    return fail(SH_ERR_INVALID_ARGUMENT, "data must be 16-byte aligned and a multiple of 16 bytes long");
+  HIP_TRY(sh::launch_stream_read(data, nbytes, out, static_cast<hipStream_t>(stream)), "stream read launch");
+  return SH_OK;
+}
+
 int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols,
                 const float* x, float* y, uint32_t batch, void* stream) {
   if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);

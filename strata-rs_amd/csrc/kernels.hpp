@@ -144,4 +144,10 @@ hipError_t launch_rope_neox(float* x, int64_t rows, int64_t head_dim, int64_t n_
 hipError_t launch_add(float* a, const float* b, int64_t n, hipStream_t stream);
 hipError_t launch_add_out(float* out, const float* a, const float* b, int64_t n, hipStream_t stream);
 
+// A plain streaming read of n bytes (16-byte aligned, a multiple of 16):
+// workgroup b of kStreamBlocks writes the XOR of the 32-bit words it read to
+// out[b]; the XOR of out[] is the XOR of all words.
+constexpr int kStreamBlocks = 2048;
+hipError_t launch_stream_read(const void* data, uint64_t nbytes, uint32_t* out, hipStream_t stream);
+
 }  // namespace sh

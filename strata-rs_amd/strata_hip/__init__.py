@@ -64,7 +64,7 @@ EXPORTS = (
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
     "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
-    "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn", "sh_ffn_dev_noalloc",
+    "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn", "sh_ffn_dev_noalloc", "sh_stream_read_dev",
 )
 
 
@@ -221,6 +221,7 @@ def load_library() -> C.CDLL:
     L.sh_quantize_q8_dev.argtypes = [vp, u64, vp, vp, vp, vp]
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
+    L.sh_stream_read_dev.argtypes = [vp, u64, vp, vp]
     dbl, ropep = C.c_double, C.POINTER(_RopeCfgC)
     L.sh_rms_norm.argtypes = [vp, f32p, f32p, u64, dbl]
     L.sh_rope_neox.argtypes = [vp, f32p, u64, ropep]
@@ -697,6 +698,15 @@ class HipBackend:
 def dequant_dev(quant: int, w_ptr: int, rows: int, cols: int, out_ptr: int, stream: int = 0,
                 flags: int = 0) -> None:
     check(load_library().sh_dequant_dev(int(quant), flags, w_ptr, rows, cols, out_ptr, stream or None))
+
+
+STREAM_READ_BLOCKS = 2048
+
+
+def stream_read_dev(data_ptr: int, nbytes: int, out_ptr: int, stream: int = 0) -> None:
+    """sh_stream_read_dev: a plain streaming read (the bandwidth ceiling);
+    out_ptr receives STREAM_READ_BLOCKS uint32 XOR folds."""
+    check(load_library().sh_stream_read_dev(data_ptr, nbytes, out_ptr, stream or None))
 
 
 def gemv_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, y_ptr: int, batch: int = 1,

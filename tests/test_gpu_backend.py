@@ -73,3 +73,20 @@ def test_threads_share_one_context(backend, oracle):
     for t in ts:
         t.join()
     assert not errors
+
+
+def test_stream_read_folds_every_word():
+    """sh_stream_read_dev (the bandwidth ceiling the benchmark reports): the
+    XOR of its per-workgroup folds equals the XOR of every 32-bit word, so
+    every byte is read (a ragged length that is not a multiple of the grid's
+    stride included)."""
+    import torch
+    say("stream read")
+    for n in (16, 4096 * 16 + 48, 28_311_552):
+        data = np.random.default_rng(n).integers(0, 2**32, n // 4, dtype=np.uint32)
+        d = torch.from_numpy(data.view(np.int32)).cuda()
+        out = torch.zeros(H.STREAM_READ_BLOCKS, dtype=torch.int32, device="cuda")
+        H.stream_read_dev(d.data_ptr(), n, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+        assert int(got) == int(np.bitwise_xor.reduce(data))
