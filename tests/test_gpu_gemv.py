@@ -1,8 +1,9 @@
 """Fused dequant-matvec on the device vs the oracle (ops::gemv).
 
-Tolerance: max|y - ref| / max|ref| <= 1e-3 (the path's stated bound under
-f32 accumulation); the per-element error with a floor of rms(ref) is also
-held to 1e-3. Covers the reference's own gemv unit test, ragged row counts,
+Tolerance (conftest.check_parity): max|y - ref| / max|ref| <= 1e-3 (the
+path's stated bound under f32 accumulation), and per element
+|y_i - ref_i| / max(|ref_i|, 1e-3 rms(ref)) <= 2e-3 (f32 arithmetic itself
+scores about 6e-4 there at 12288 inputs). Covers the reference's own gemv unit test, ragged row counts,
 one- and multi-window rows, batches 1..8 (Q5_K too), the Q6_K scale readings, the
 configs' full shapes (the lm_head on a row sample) and the device-pointer
 entry point.
@@ -11,7 +12,7 @@ import numpy as np
 import pytest
 
 import strata_hip as H
-from conftest import elem_rel_err, rel_err
+from conftest import check_parity
 from strata_hip import synth as S
 
 pytestmark = pytest.mark.gpu
@@ -22,9 +23,8 @@ def say(*a):
     print("[case]", *a, flush=True)
 
 
-def check(got, want):
-    assert rel_err(got, want) <= TOL, rel_err(got, want)
-    assert elem_rel_err(got, want, floor=1.0) <= TOL
+def check(got, want, label=""):
+    check_parity(got, want, label)
 
 
 def test_reference_q8_0_unit_case(backend):

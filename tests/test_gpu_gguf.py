@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import strata_hip as H
-from conftest import elem_rel_err, rel_err
+from conftest import check_parity
 from gguf_writer import STRING, U32, Writer
 from strata_hip import synth as S
 
@@ -24,8 +24,7 @@ def say(*a):
 
 
 def check(got, want):
-    assert rel_err(got, want) <= TOL
-    assert elem_rel_err(got, want, floor=1.0) <= TOL
+    check_parity(got, want, "gguf")
 
 
 def test_upload_from_gguf_then_matvec(tmp_path, oracle):

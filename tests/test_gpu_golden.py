@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import strata_hip as H
-from conftest import rel_err
+from conftest import check_parity
 from strata_hip import synth as S
 
 pytestmark = pytest.mark.gpu
@@ -46,7 +46,7 @@ def test_golden_gemv_and_dequant(backend, quant, rows, cols):
     w, x = c[f"gemv_{quant}_w"], c[f"gemv_{quant}_x"]
     y = np.empty(rows, np.float32)
     backend.gemv(H.QuantTensor(f"golden{quant}", quant, rows, cols, w), x, y)
-    assert rel_err(y, c[f"gemv_{quant}_y"]) <= 1e-3
+    check_parity(y, c[f"gemv_{quant}_y"], "golden")
     rb = H.byte_size(quant, cols)
     for r in range(rows):
         out = np.empty(cols, np.float32)
@@ -60,7 +60,7 @@ def test_golden_q6k_signed_gemv(backend):
     y = np.empty(16, np.float32)
     backend.gemv(H.QuantTensor("golden14s", 14, 16, 512, c["gemv_14s_w"], flags=H.FLAG_Q6K_SIGNED_SCALES),
                  c["gemv_14s_x"], y)
-    assert rel_err(y, c["gemv_14s_y"]) <= 1e-3
+    check_parity(y, c["gemv_14s_y"], "golden")
 
 
 def test_golden_expert_and_moe(backend):
@@ -68,7 +68,7 @@ def test_golden_expert_and_moe(backend):
     c = cases()
     y = np.empty(256, np.float32)
     backend.expert_gemv(H.ExpertView("golden_exp", 12, 3, 64, 256, c["expert_w"]), 1, c["expert_x"], y)
-    assert rel_err(y, c["expert_y"]) <= 1e-3
+    check_parity(y, c["expert_y"], "golden")
     ids, w = backend.moe_route(c["moe_logits"], 4)
     assert ids.tolist() == c["moe_ids"].tolist()
     assert np.abs(w - c["moe_wts"]).max() <= 4e-7
@@ -76,7 +76,7 @@ def test_golden_expert_and_moe(backend):
     out = backend.moe_ffn(H.ExpertView("gg", 12, 16, 256, 256, g), H.ExpertView("gu", 12, 16, 256, 256, u),
                           H.ExpertView("gd", 14, 16, 256, 256, d), c["moe_logits"], c["moe_x"], 4)
     for t in range(3):
-        assert rel_err(out[t], c["moe_out"][t]) <= 1e-3
+        check_parity(out[t], c["moe_out"][t], "golden")
 
 
 def test_golden_q8_quantizer(backend):

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import strata_hip as H
-from conftest import elem_rel_err, rel_err
+from conftest import STRICT_TOL, check_parity, rel_err
 from strata_hip import synth as S
 
 pytestmark = pytest.mark.gpu
@@ -37,9 +37,15 @@ def bf16_operand_ref(oracle, quant, rows, cols, w, x, scale_mode=0):
     return (xb @ Wb.T).astype(np.float32)
 
 
-def check_rows(got, want, tol):
-    worst = max(rel_err(got[t], want[t]) for t in range(want.shape[0]))
-    assert worst <= tol, worst
+def check_rows(got, want, tol, strict_tol=None):
+    """Every token row against its reference at the normwise bound `tol`;
+    the per-element metric is recorded, and asserted when `strict_tol` is
+    given (against the same rounded operands: the MFMA modes' own rounding
+    of x and W is the spec's 2e-2 allowance, not an error of the kernel)."""
+    worst = 0.0
+    for t in range(want.shape[0]):
+        worst = max(worst, rel_err(got[t], want[t]))
+        check_parity(got[t], want[t], f"row {t}", norm_tol=tol, strict_tol=strict_tol)
     return worst
 
 
@@ -54,7 +60,7 @@ def test_matmul_bf16(backend, oracle, quant, rows, cols, m):
     w = S.matrix(quant, 900 + rows, rows, cols)
     x = S.normal_f32(901 + m, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor(f"mm{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_BF16)
-    check_rows(y, bf16_operand_ref(oracle, quant, rows, cols, w, x), TOL_EXACT_OPERANDS)
+    check_rows(y, bf16_operand_ref(oracle, quant, rows, cols, w, x), TOL_EXACT_OPERANDS, STRICT_TOL)
     check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
 
 
@@ -65,7 +71,7 @@ def test_matmul_bf16_q6k_signed_scales(backend, oracle):
     x = S.normal_f32(912, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor("mm_q6s", 14, rows, cols, w, flags=H.FLAG_Q6K_SIGNED_SCALES), x,
                        H.MATMUL_BF16)
-    check_rows(y, bf16_operand_ref(oracle, 14, rows, cols, w, x, scale_mode=1), TOL_EXACT_OPERANDS)
+    check_rows(y, bf16_operand_ref(oracle, 14, rows, cols, w, x, scale_mode=1), TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
 @pytest.mark.parametrize("quant,rows,cols,m", [s for s in SHAPES if s[0] != 14])
@@ -75,7 +81,7 @@ def test_matmul_q8(backend, oracle, quant, rows, cols, m):
     x = S.normal_f32(921 + m, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor(f"mq{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_Q8)
     xq = oracle.dequantize_q8_activations(x)
-    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
     check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
 
 
@@ -99,9 +105,7 @@ def test_matmul_prefill_config(backend, oracle, prefill_weight, mode):
         exact = oracle.matmul(12, rows, cols, w, oracle.dequantize_q8_activations(x), threads=16)
     else:
         exact = bf16_operand_ref(oracle, 12, rows, cols, w, x)
-    check_rows(y, exact, TOL_EXACT_OPERANDS)
-    # per element, |y - r| / max(|r|, rms(r)), against the same-operand sums
-    assert elem_rel_err(y, exact, floor=1.0) <= TOL_EXACT_OPERANDS
+    check_rows(y, exact, TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
 def test_quantize_q8_dev_bit_exact(backend, oracle):

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import strata_hip as H
-from conftest import elem_rel_err, rel_err
+from conftest import check_parity, rel_err
 from strata_hip import synth as S
 
 pytestmark = pytest.mark.gpu
@@ -78,8 +78,7 @@ def test_moe_ffn_config_shapes(backend, oracle, moe_config_tensors, n_tok):
     out = backend.moe_ffn(g, u, d, logits, x, top_k)
     ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
     for t in range(n_tok):
-        assert rel_err(out[t], ref[t]) <= 1e-3, (t, rel_err(out[t], ref[t]))
-        assert elem_rel_err(out[t], ref[t], floor=1.0) <= 1e-3
+        check_parity(out[t], ref[t], "moe")
 
 
 def test_moe_ffn_q8_gate_up_small(backend, oracle):
@@ -92,7 +91,7 @@ def test_moe_ffn_q8_gate_up_small(backend, oracle):
                           H.ExpertView("u8", 8, n_expert, n_embd, n_ff, up),
                           H.ExpertView("d8", 14, n_expert, n_ff, n_embd, down), logits, x, top_k)
     ref = oracle_moe(oracle, 8, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
-    assert rel_err(out, ref) <= 1e-3
+    check_parity(out, ref, "moe")
 
 
 def test_moe_ffn_dev_matches_host_path(backend):
@@ -130,7 +129,7 @@ def test_moe_ffn_one_token_many_experts(backend, oracle):
                           H.ExpertView("um", 12, n_expert, n_embd, n_ff, up),
                           H.ExpertView("dm", 14, n_expert, n_ff, n_embd, down), logits, x, top_k)
     ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
-    assert rel_err(out, ref) <= 1e-3
+    check_parity(out, ref, "moe")
 
 
 @pytest.mark.parametrize("n_tok", [1, 4])
@@ -182,8 +181,7 @@ def test_moe_ffn_one_token_formats(backend, oracle, qg, qd):
                           H.ExpertView(f"uf{qg}{qd}", qg, n_expert, n_embd, n_ff, up),
                           H.ExpertView(f"df{qg}{qd}", qd, n_expert, n_ff, n_embd, down), logits, x, top_k)
     ref = oracle_moe(oracle, qg, qd, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
-    assert rel_err(out, ref) <= 1e-3, rel_err(out, ref)
-    assert elem_rel_err(out[0], ref[0], floor=1.0) <= 1e-3
+    check_parity(out, ref, "moe")
 
 
 def test_moe_ffn_one_token_repeat_and_graph(backend):
@@ -295,8 +293,7 @@ def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh)
     out = backend.moe_layer(*views, x, top_k)
     for i in range(n_tok):
         ref = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[i], top_k)
-        assert rel_err(out[i], ref) <= 1e-3, (i, rel_err(out[i], ref))
-        assert elem_rel_err(out[i], ref, floor=1.0) <= 1e-3
+        check_parity(out[i], ref, "moe")
 
 
 @pytest.fixture(scope="module")
@@ -316,8 +313,7 @@ def test_moe_layer_config_shapes(backend, oracle, layer_config_tensors, n_tok):
     out = backend.moe_layer(*layer_views("Lcfg", q, t, n_expert, n_embd, n_ff, n_sh), x, top_k)
     for i in range(n_tok):
         ref = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[i], top_k)
-        assert rel_err(out[i], ref) <= 1e-3, (i, rel_err(out[i], ref))
-        assert elem_rel_err(out[i], ref, floor=1.0) <= 1e-3
+        check_parity(out[i], ref, "moe")
 
 
 def test_moe_layer_dev_matches_host_path(backend):
@@ -421,8 +417,7 @@ def test_moe_ffn_random_configs(backend, oracle, seed):
                           H.ExpertView(f"rd{seed}", qd, n_expert, n_ff, n_embd, down), logits, x, top_k)
     ref = oracle_moe(oracle, qa, qd, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
     for t in range(n_tok):
-        assert rel_err(out[t], ref[t]) <= 1e-3, (t, rel_err(out[t], ref[t]))
-        assert elem_rel_err(out[t], ref[t], floor=1.0) <= 1e-3
+        check_parity(out[t], ref[t], "moe")
     for name in (f"rg{seed}", f"ru{seed}", f"rd{seed}"):
         backend.evict(name)
 
@@ -451,12 +446,12 @@ def test_moe_ffn_budget_holding_two_of_three_refuses(oracle, moe_config_tensors)
         y = np.empty(n_embd, np.float32)
         be.expert_gemv(d, 5, xe, y)
         want = oracle.expert_gemv(14, n_expert, n_ff, n_embd, down, 5, xe)
-        assert rel_err(y, want) <= 1e-3
+        check_parity(y, want, "moe")
     # and a budget that holds all three runs the call
     with H.HipBackend(0, gate.nbytes + up.nbytes + down.nbytes) as be:
         out = be.moe_ffn(g, u, d, logits, x, top_k)
     ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
-    assert rel_err(out, ref) <= 1e-3
+    check_parity(out, ref, "moe")
 
 
 def test_fused_moe_refuses_out_major_views(backend):
