@@ -1135,6 +1135,76 @@ static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int
   return hipGetLastError();
 }
 
+// --------------------------------------------------- Q8_0, odd blocks --
+// Q8_0 rows with an odd number of 32-element blocks (cols % 64 == 32, e.g.
+// the reference's one-block gemv case, ops_tests.rs:44-61): the 64-column
+// lane units above do not fit them, and such rows start on 2-byte
+// boundaries. A wave per row, lane l taking blocks l, l + 64, ... with
+// 2-byte loads of the 34-byte block; each weight is dequantized as
+// strata-gguf does (one f32 product q * d, dequant.rs:123-128) and the dot
+// is summed in f64 as ops::gemv (ops.rs:14-28), the lanes' sums added by a
+// butterfly: only the order of the f64 additions differs from the
+// sequential loop.
+template <int NB>
+__global__ void __launch_bounds__(256) gemv_q8_odd_kernel(const uint8_t* __restrict__ w, int rows, int nblk,
+                                                          int64_t row_bytes, const float* __restrict__ x,
+                                                          float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // wave-uniform
+  const uint8_t* row = w + int64_t(r) * row_bytes;
+  const int64_t cols = int64_t(nblk) * 32;
+  double acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.0;
+  for (int k = lane; k < nblk; k += kWave) {
+    const uint8_t* blk = row + int64_t(k) * 34;
+    const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+#pragma unroll 4
+    for (int j = 0; j < 32; j += 2) {
+      const uint32_t q2 = *reinterpret_cast<const uint16_t*>(blk + 2 + j);
+      const float w0 = float(int8_t(q2 & 0xFFu)) * d, w1 = float(int8_t(q2 >> 8)) * d;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float* xb = x + b * cols + int64_t(k) * 32 + j;
+        acc[b] = __builtin_fma(double(w0), double(xb[0]), acc[b]);
+        acc[b] = __builtin_fma(double(w1), double(xb[1]), acc[b]);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    double v = acc[b];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if (lane == 0) y[int64_t(b) * rows + r] = float(v);
+  }
+}
+
+template <int NB>
+static hipError_t launch_q8_odd_nb(const uint8_t* w, int rows, int nblk, int64_t row_bytes, const float* x, float* y,
+                                   hipStream_t s) {
+  hipLaunchKernelGGL((gemv_q8_odd_kernel<NB>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, s, w, rows, nblk,
+                     row_bytes, x, y);
+  return hipGetLastError();
+}
+
+static hipError_t launch_q8_odd(int nb, const uint8_t* w, int rows, int cols, const float* x, float* y,
+                                hipStream_t s) {
+  const int nblk = cols / 32;
+  const int64_t rb = int64_t(nblk) * 34;
+  switch (nb) {
+    case 1: return launch_q8_odd_nb<1>(w, rows, nblk, rb, x, y, s);
+    case 2: return launch_q8_odd_nb<2>(w, rows, nblk, rb, x, y, s);
+    case 3: return launch_q8_odd_nb<3>(w, rows, nblk, rb, x, y, s);
+    case 4: return launch_q8_odd_nb<4>(w, rows, nblk, rb, x, y, s);
+    case 5: return launch_q8_odd_nb<5>(w, rows, nblk, rb, x, y, s);
+    case 6: return launch_q8_odd_nb<6>(w, rows, nblk, rb, x, y, s);
+    case 7: return launch_q8_odd_nb<7>(w, rows, nblk, rb, x, y, s);
+    default: return launch_q8_odd_nb<8>(w, rows, nblk, rb, x, y, s);
+  }
+}
+
 // ---------------------------------------------------------------- launch --
 // CU count of the current device, queried once per device. The cache is
 // atomic: the entry points are called from several threads at once.
@@ -1159,8 +1229,9 @@ bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
   if (plain_quant(quant)) return rows <= (int64_t(1) << 31) - 1 && cols <= (int64_t(1) << 30);
   if (!gemv_quant(quant)) return false;
   if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 20)) return false;
-  if (cols % 64 != 0) return false;  // 64-column lane units (Q8_0 blocks in pairs)
   if (cols % geometry(quant).block != 0) return false;
+  if (quant == kQ8_0 && cols % 64 == 32) return true;  // odd blocks: gemv_q8_odd_kernel
+  if (cols % 64 != 0) return false;  // 64-column lane units (Q8_0 blocks in pairs)
   return lds_bytes(int(cols), 1) <= kMaxLds;
 }
 
@@ -1260,6 +1331,11 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
       default: return launch_plain<kBF16, false>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     }
   }
+  // Q8_0 rows of an odd number of blocks (2-byte aligned rows, 2-byte loads)
+  if (quant == kQ8_0 && cols % 64 == 32) {
+    if ((reinterpret_cast<uintptr_t>(w) & 1u)) return hipErrorInvalidValue;
+    return launch_q8_odd(batch, w, int(rows), int(cols), x, y, stream);
+  }
   // Q8_0 reads 68-byte block pairs with dword loads: rows must start on a
   // dword boundary (row_bytes is 68 * cols/64, so only the base matters).
   if (quant == kQ8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
@@ -1331,6 +1407,7 @@ static hipError_t launch_ffn1(const uint8_t* gate, const uint8_t* up, const uint
 
 bool ffn_fused_ok(uint32_t quant, int64_t n_embd, int64_t n_ff) {
   return (quant == kQ4_K || quant == kQ8_0 || quant == kQ5_K || quant == kQ6_K) &&
+         n_embd % 64 == 0 && n_ff % 64 == 0 &&  // the limb kernels' 64-column units
          gemv_shape_ok(quant, 2 * n_ff, n_embd, 1) && gemv_shape_ok(quant, n_embd, n_ff, 1) &&
          n_ff % 4 == 0 && 2 * n_ff <= (int64_t(1) << 30);
 }

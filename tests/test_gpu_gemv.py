@@ -28,18 +28,30 @@ def check(got, want, label=""):
 
 
 def test_reference_q8_0_unit_case(backend):
-    # ops_tests.rs:44-61: one Q8_0 block is too narrow for the device
-    # kernels' 64-column units, so the block is repeated in a 2-block row
-    # with the second block's x zeroed: the same sum.
+    # ops_tests.rs:44-61 as the reference runs it: one 34-byte Q8_0 block
+    # (d = 0.5, q = j % 7 - 3), a 32-element x, one output row
     from test_oracle_ops import q8_single_block
     b, x = q8_single_block()
-    w = H.QuantTensor("q8unit", H.QuantType.Q8_0, 1, 64, np.concatenate([b, b]))
-    xx = np.concatenate([x, np.zeros(32, np.float32)])
+    w = H.QuantTensor("q8unit", H.QuantType.Q8_0, 1, 32, b)
     y = np.zeros(1, np.float32)
-    say("gemv reference Q8_0 unit case")
-    backend.gemv(w, xx, y)
+    say("gemv reference Q8_0 unit case (one block)")
+    backend.gemv(w, x, y)
     expect = sum(float(j % 7 - 3) * 0.5 * float(x[j]) for j in range(32))
     assert abs(float(y[0]) - expect) < 1e-4
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(1, 32, 1), (7, 96, 1), (300, 4128, 1), (33, 12320, 3),
+                                             (1000, 4064, 8), (5, 32, 8)])
+def test_gemv_q8_0_odd_block_rows(backend, oracle, rows, cols, batch):
+    """Q8_0 rows of an odd number of 32-element blocks (any multiple of 32
+    columns, as quant.rs:125-136 allows): 34-byte rows alternate 4- and
+    2-byte alignment, every batch size."""
+    say("gemv Q8_0 odd blocks", rows, cols, batch)
+    w = S.matrix(8, 4000 + rows + cols, rows, cols)
+    x = S.normal_f32(4001 + cols, batch * cols).reshape(batch, cols)
+    y = backend.gemv_batch(H.QuantTensor(f"q8odd_{rows}_{cols}", 8, rows, cols, w), x, batch)
+    for i in range(batch):
+        check(y[i], oracle.gemv(8, rows, cols, w, x[i]), f"q8 odd b{i}")
 
 
 @pytest.mark.parametrize("quant,rows,cols", [
@@ -232,7 +244,7 @@ def test_gemv_random_shapes(backend, oracle, seed):
     rng = np.random.default_rng(9000 + seed)
     for case in range(8):
         quant = int(rng.choice([8, 12, 13, 14, 0, 1, 30]))
-        step = 256 if quant in (12, 13, 14) else 64
+        step = 256 if quant in (12, 13, 14) else 32 if quant == 8 else 64
         cols = step * int(rng.integers(1, 20480 // step + 1))
         rows = int(rng.integers(1, 3001))
         batch = int(rng.integers(1, 9))
