@@ -114,10 +114,15 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
     copies = [base] + [base.clone() for _ in range(n_copies - 1)]
     x = torch.from_numpy(S.normal_f32(7, batch * cols)).to(dev)
     y = torch.empty(batch * rows, dtype=torch.float32, device=dev)
+    nws = H.gemv_workspace_bytes(quant, rows, cols, batch)
+    ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
     stream = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
 
     def call(c):
+        if nws:  # batches: the activations converted once per call into the workspace
+            return lambda s: H.gemv_dev_ws(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch,
+                                           ws.data_ptr(), nws, s, flags)
         return lambda s: H.gemv_dev(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch, s, flags)
 
     ms = _time_graph_calls(torch, stream, [call(c) for c in copies], steps, warmup)

@@ -415,11 +415,14 @@ static int run_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, flo
   if ((rc = c->d_in.ensure(xb, "x buffer")) || (rc = c->d_out.ensure(yb, "y buffer")) ||
       (rc = c->h_in.ensure(xb, "x staging")) || (rc = c->h_out.ensure(yb, "y staging")))
     return rc;
+  const size_t wsb = sh::gemv_workspace_bytes(w->quant, int64_t(rows), int64_t(cols), int(batch));
+  if (wsb && (rc = c->d_blk.ensure(wsb, "workspace"))) return rc;
   memcpy(c->h_in.p, x, xb);
   HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
   HIP_TRY(sh::launch_gemv(w->quant, r->dev, int64_t(rows), int64_t(cols),
                           static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
-                          int(batch), (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+                          int(batch), (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream,
+                          wsb ? c->d_blk.p : nullptr),
           "gemv launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
   HIP_TRY(hipStreamSynchronize(c->stream), "gemv");
@@ -851,6 +854,40 @@ int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, ui
     return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0 and F32; x 16)");
   HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
                           (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
+          "gemv launch");
+  return SH_OK;
+}
+
+int sh_gemv_workspace_bytes(uint32_t quant, uint64_t rows, uint64_t cols, uint32_t batch, uint64_t* bytes) {
+  if (!bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null bytes");
+  if (batch < 1 || batch > 8) return fail(SH_ERR_INVALID_ARGUMENT, "batch %u is outside 1..8", batch);
+  int rc = check_matrix(quant, rows, cols, 1, ~uint64_t(0), true);
+  if (rc) return rc;
+  if (rows && cols && !sh::gemv_shape_ok(quant, int64_t(rows), int64_t(cols), int(batch)))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "gemv %llux%llu of type %u (batch %u) is not supported",
+                (unsigned long long)rows, (unsigned long long)cols, quant, batch);
+  *bytes = rows && cols ? sh::gemv_workspace_bytes(quant, int64_t(rows), int64_t(cols), int(batch)) : 0;
+  return SH_OK;
+}
+
+int sh_gemv_dev_ws(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols, const float* x,
+                   float* y, uint32_t batch, void* workspace, uint64_t workspace_bytes, void* stream) {
+  uint64_t need = 0;
+  int rc = sh_gemv_workspace_bytes(quant, rows, cols, batch, &need);
+  if (rc) return rc;
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed", (unsigned long long)workspace_bytes,
+                (unsigned long long)need);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  if (rows == 0 || cols == 0) return fail(SH_ERR_UNSUPPORTED_SHAPE, "empty matrix on the device path");
+  if (!w || !x || !y) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
+      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(w) & 3u)))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0 and F32; x 16)");
+  HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
+                          (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream),
+                          need ? workspace : nullptr),
           "gemv launch");
   return SH_OK;
 }

@@ -1317,8 +1317,16 @@ static hipError_t launch_nb(int nb, const uint8_t* w, int rows, int cols, int64_
   }
 }
 
+// Batches of rows wider than one 4096-column window run split-K over the
+// windows with their activations converted once per call (the workspace);
+// narrower rows gain nothing from the extra launch and take none.
+size_t gemv_workspace_bytes(uint32_t quant, int64_t rows, int64_t cols, int batch) {
+  return batch >= 2 && cols > 4096 && gemv_mfma_ok(quant, rows, cols, batch) ? gemv_mfma_workspace_bytes(rows, cols)
+                                                                               : 0;
+}
+
 hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,
-                       float* y, int batch, int q6_signed, hipStream_t stream) {
+                       float* y, int batch, int q6_signed, hipStream_t stream, void* ws) {
   if (!gemv_shape_ok(quant, rows, cols, batch)) return hipErrorInvalidValue;
   const uint8_t* w = static_cast<const uint8_t*>(wv);
   const int64_t row_bytes = byte_size(quant, cols);
@@ -1342,7 +1350,7 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(x) & 15u))
     return hipErrorInvalidValue;
   if (batch >= 2 && gemv_mfma_ok(quant, rows, cols, batch))
-    return launch_gemv_mfma(quant, w, rows, cols, x, y, batch, cu_count(), stream);
+    return launch_gemv_mfma(quant, w, rows, cols, x, y, batch, cu_count(), stream, ws);
   // batch 1: 16 waves per CU for tall matrices whose rows are a single
   // 4096-column window (more waves hide more latency, and each still has
   // rows to stream); 8 otherwise (fewer workgroups stage x, and multi-window

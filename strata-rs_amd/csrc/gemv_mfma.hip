@@ -28,9 +28,16 @@
 // vector of one window of up to 4096 columns in LDS; wider rows take their
 // windows in turn (restaging the limbs), the accumulators carried across.
 // The S shares of a row tile are added through LDS at the end.
+//
+// With a workspace, the activations are converted once per call by
+// mb_prep_kernel (a thread per vector and 32-element block) into the
+// workspace, and each workgroup copies a window's limbs, scales and sums
+// from there (L2) into LDS instead of converting them itself.
 // Lane l of a wave holds, in D, weight row l % 16 for vectors
 // 4 * ((l / 16) & 1) + i, i < 4: the a and c sums in lanes 0-31, the b sums
 // in lanes 32-63.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -46,13 +53,136 @@ __host__ __device__ inline int mb_limb_bytes(int nblk) { return 3 * nblk * kMbMa
 
 constexpr int kMbMaxWaves = 12;  // waves per workgroup (T * S)
 
+// DPP lane exchanges inside 8 adjacent lanes (a super-block's 8 blocks):
+// xor 1 and xor 2 as quad permutes; the other quad of the 8 through the
+// half-row mirror (lane i <-> 7 - i), which for values already uniform over
+// each quad is the same as xor 4.
+__device__ __forceinline__ float max8_dpp(float m) {
+  m = fmaxf(m, dpp_xor1(m));
+  m = fmaxf(m, dpp_xor2(m));
+  return fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, m), 0x141, 0xF, 0xF,
+                                                                          false)));  // row_half_mirror
+}
+
+// One 32-element block of one vector -> the three limb rows (32 bytes each),
+// its 2^-k (per 256-element super-block: the 8 adjacent lanes of a
+// super-block share their maximum) and its sum of x.
+__device__ __forceinline__ void mb_convert_block(const float* src, uint32_t* wa, uint32_t* wb, uint32_t* wc,
+                                                 float& down, float& sum) {
+  float v[32];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const f32x4 t = reinterpret_cast<const f32x4*>(src)[k];
+    v[4 * k] = t.x;
+    v[4 * k + 1] = t.y;
+    v[4 * k + 2] = t.z;
+    v[4 * k + 3] = t.w;
+  }
+  float m = 0.f, s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    m = fmaxf(m, fabsf(v[k]));
+    s += v[k];
+  }
+  m = max8_dpp(m);
+  int e = 0;
+  (void)frexpf(m, &e);
+  const int kk = m > 0.f ? min(22 - e, 126) : 0;
+  const float up = ldexpf(1.f, kk);
+  down = (m - m == 0.f) ? ldexpf(1.f, -kk) : __builtin_nanf("");
+  sum = s;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22),
+    // less 0x4B400000 plus 0x808080: u = v + 0x808080, whose bytes less 128
+    // are the balanced digits c, b, a
+    uint32_t u[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      u[q] = __builtin_bit_cast(uint32_t, __builtin_fmaf(v[4 * k + q], up, 12582912.0f)) - 0x4ABF7F80u;
+    uint32_t pc, pb, pa;
+    transpose_bytes(u[0], u[1], u[2], u[3], pc, pb, pa);
+    wa[k] = pa ^ 0x80808080u;
+    wb[k] = pb ^ 0x80808080u;
+    wc[k] = pc ^ 0x80808080u;
+  }
+}
+
+// Workspace layout, per window of nblk = min(cols, 4096) / 32 blocks (the
+// last window may use fewer): limbs [3][nblk][8 vectors][32 bytes], then
+// 2^-k [nblk / 8][8], then sums of x [nblk][8].
+__host__ __device__ inline size_t mb_win_bytes(int nblk) {
+  return size_t(3) * nblk * kMbMaxVec * 32 + size_t(nblk / 8) * kMbMaxVec * 4 + size_t(nblk) * kMbMaxVec * 4;
+}
+
+// The whole workspace: row-block counters of the split-K combine (zeroed
+// by mb_prep_kernel on every call), the windows' partial sums
+// [nwin][8][rows] (rows wider than one window), then the windows' images.
+static size_t mb_align(size_t v) { return (v + 255) & ~size_t(255); }
+static size_t mb_counters_bytes(int64_t rows) { return mb_align(size_t((rows + 15) / 16) * 4); }
+static size_t mb_part_bytes(int64_t rows, int64_t cols) {
+  const int64_t nwin = (cols + kMbMaxCols - 1) / kMbMaxCols;
+  return nwin > 1 ? mb_align(size_t(nwin) * kMbMaxVec * size_t(rows) * 4) : 0;
+}
+
+size_t gemv_mfma_workspace_bytes(int64_t rows, int64_t cols) {
+  const int nblk = int((cols < kMbMaxCols ? cols : kMbMaxCols) / 32);
+  const int64_t nwin = (cols + kMbMaxCols - 1) / kMbMaxCols;
+  return mb_counters_bytes(rows) + mb_part_bytes(rows, cols) + size_t(nwin) * mb_win_bytes(nblk);
+}
+
+// The activations of a call, converted once: thread p takes vector
+// p / (cols / 32) and block p % (cols / 32); threads p < n_count also clear
+// the split-K counters for the matvec launch that follows.
+__global__ void __launch_bounds__(256) mb_prep_kernel(const float* __restrict__ x, int cols, int nb,
+                                                      uint8_t* __restrict__ ws, uint32_t* __restrict__ count,
+                                                      int n_count) {
+  const int nblk_all = cols >> 5;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < n_count) count[p] = 0u;
+  const int pc = min(p, nb * nblk_all - 1);  // past the end: a valid copy of the last block, not written
+  const int b = pc / nblk_all, jg = pc - b * nblk_all;
+  uint32_t wa[8], wb[8], wc[8];
+  float down, sum;
+  mb_convert_block(x + int64_t(b) * cols + 32 * jg, wa, wb, wc, down, sum);
+  if (p >= nb * nblk_all) return;
+  const int nblk = min(cols, kMbMaxCols) >> 5;
+  const int win = jg / nblk, j = jg - win * nblk;
+  uint8_t* img = ws + size_t(win) * mb_win_bytes(nblk);
+  u32x4* da = reinterpret_cast<u32x4*>(img + ((size_t(0) * nblk + j) * kMbMaxVec + b) * 32);
+  u32x4* db = reinterpret_cast<u32x4*>(img + ((size_t(1) * nblk + j) * kMbMaxVec + b) * 32);
+  u32x4* dc = reinterpret_cast<u32x4*>(img + ((size_t(2) * nblk + j) * kMbMaxVec + b) * 32);
+  da[0] = u32x4{wa[0], wa[1], wa[2], wa[3]};
+  da[1] = u32x4{wa[4], wa[5], wa[6], wa[7]};
+  db[0] = u32x4{wb[0], wb[1], wb[2], wb[3]};
+  db[1] = u32x4{wb[4], wb[5], wb[6], wb[7]};
+  dc[0] = u32x4{wc[0], wc[1], wc[2], wc[3]};
+  dc[1] = u32x4{wc[4], wc[5], wc[6], wc[7]};
+  float* pkw = reinterpret_cast<float*>(img + size_t(3) * nblk * kMbMaxVec * 32);
+  float* sxw = pkw + (nblk / 8) * kMbMaxVec;
+  if ((j & 7) == 0) pkw[(j >> 3) * kMbMaxVec + b] = down;
+  sxw[j * kMbMaxVec + b] = sum;
+}
+
 // Q: kQ4_K (144-byte super-blocks, codes at byte 16) or kQ5_K (176 bytes:
 // qh at 16, codes at 48). ONE: the row is a single window (cols <= 4096),
 // which lets the compiler drop the window loop.
-template <int Q, int PER, bool ONE>
+//
+// SPLIT (with PREP, rows of two or more windows): workgroup b takes window
+// b % nwin of row block b / nwin only, so it copies one window's limbs; the
+// row block's sums per window go to part[win][vector][row] with
+// device-scope (L2-bypassing) stores, the workgroup counts itself in on
+// count[row block] once its stores are complete, and the last of the nwin
+// workgroups adds the windows' sums in window order (deterministic) and
+// writes y. No workgroup waits on another.
+constexpr int kMbCopyRounds = 12;  // 16-byte chunks per thread of one window's copy (6144 / 512)
+
+template <int Q, int PER, bool ONE, bool PREP, bool SPLIT>
 __global__ void __launch_bounds__(64 * kMbMaxWaves)
     gemv_mfma_kq_kernel(const uint8_t* __restrict__ w, int rows, int cols, int64_t row_bytes,
-                        const float* __restrict__ x, float* __restrict__ y, int nb, int T, int S) {
+                        const float* __restrict__ x, float* __restrict__ y, int nb, int T, int S,
+                        const uint8_t* __restrict__ ws, float* part, uint32_t* count) {
+  static_assert(!SPLIT || PREP, "the split-K combine needs the prepared workspace");
   constexpr int kSbBytes = Q == kQ5_K ? 176 : 144;
   constexpr int kCodes = Q == kQ5_K ? 48 : 16;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -65,10 +195,14 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
   float* sx = pk + nblk * kMbMaxVec;                                     // [nblk][8]: sum of x
   float* red = sx + nblk * kMbMaxVec;                                    // [T][S][64][4]
 
-  // ---- this wave's row tile and super-block share
+  // ---- this workgroup's row block (and window, SPLIT); this wave's row
+  // tile and super-block share
+  const int nwin = (cols + kMbMaxCols - 1) / kMbMaxCols;
+  const int rtb = SPLIT ? blockIdx.x / nwin : blockIdx.x;
+  const int win = SPLIT ? blockIdx.x - rtb * nwin : 0;
   const int rt = wave % T, sh_ = wave / T;
   const int r16 = lane & 15, kg = lane >> 4;  // B column (weight row) and k group
-  const int row = min(blockIdx.x * (16 * T) + 16 * rt + r16, rows - 1);
+  const int row = min(rtb * (16 * T) + 16 * rt + r16, rows - 1);
   const uint8_t* wr = w + int64_t(row) * row_bytes;
   // A rows 0-7 carry one limb of vectors 0-7 and rows 8-15 another limb of
   // the same vectors: MFMA 1 takes limbs (a | b), MFMA 2 (c | zero). So lanes
@@ -85,64 +219,76 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
 
   // ---- column windows of up to 4096: stage the window's limbs, then each
   // wave accumulates its share of the window's super-blocks
-  for (int c0 = 0; c0 < (ONE ? 1 : cols); c0 += kMbMaxCols) {
+  for (int c0 = SPLIT ? win * kMbMaxCols : 0; c0 < (ONE ? 1 : SPLIT ? win * kMbMaxCols + 1 : cols);
+       c0 += kMbMaxCols) {
     const int nblk_w = ONE ? nblk : min(cols - c0, kMbMaxCols) >> 5, nsb_w = nblk_w >> 3;
     if (c0 > 0) __syncthreads();  // every wave is done with the previous window's limbs
     // ---- activations -> limbs: one (vector, block) pair per thread per round;
     // the 8 blocks of a super-block are 8 adjacent lanes (nblk_w and the
     // workgroup size are multiples of 8), which share its maximum
     float* pk8 = pk;  // [nsb_w][8]: 2^-k of (super-block, vector)
-    for (int p = tid; p < nb * nblk_w; p += nthreads) {
-      const int b = p / nblk_w, j = p - b * nblk_w;
-      const f32x4* src = reinterpret_cast<const f32x4*>(x + int64_t(b) * cols + c0 + 32 * j);
-      float v[32];
+    if constexpr (PREP) {
+      // copy the window's image from the workspace: 16-byte chunks (half a
+      // limb row) to their 40-byte LDS slots, then the scales and sums; all
+      // of a thread's loads are issued before its stores
+      const uint8_t* img = ws + size_t(ONE ? 0 : c0 / kMbMaxCols) * mb_win_bytes(nblk);
+      const int nchunk = 3 * nblk_w * nb * 2;
+      u32x4 cv[kMbCopyRounds];
+      size_t cdst[kMbCopyRounds];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const f32x4 t = src[k];
-        v[4 * k] = t.x;
-        v[4 * k + 1] = t.y;
-        v[4 * k + 2] = t.z;
-        v[4 * k + 3] = t.w;
+      for (int k = 0; k < kMbCopyRounds; ++k) {
+        const int q = min(tid + k * nthreads, nchunk - 1);
+        const int half = q & 1, r = q >> 1;               // r: (limb, block, vector) record
+        const int b = r % nb, lj = r / nb;                  // lj = limb * nblk_w + block
+        const int l = lj / nblk_w, j = lj - l * nblk_w;
+        const size_t rec = (size_t(l) * nblk + j) * kMbMaxVec + b;
+        cv[k] = *reinterpret_cast<const u32x4*>(img + rec * 32 + 16 * half);
+        cdst[k] = rec * kMbTokStride + 16 * half;
       }
-      float m = 0.f, s = 0.f;
 #pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        m = fmaxf(m, fabsf(v[k]));
-        s += v[k];
+      for (int k = 0; k < kMbCopyRounds; ++k) {
+        if (tid + k * nthreads < nchunk) {
+          uint64_t* d = reinterpret_cast<uint64_t*>(limbs + cdst[k]);
+          d[0] = uint64_t(cv[k].x) | (uint64_t(cv[k].y) << 32);
+          d[1] = uint64_t(cv[k].z) | (uint64_t(cv[k].w) << 32);
+        }
       }
-      m = fmaxf(m, __shfl_xor(m, 1, kWave));
-      m = fmaxf(m, __shfl_xor(m, 2, kWave));
-      m = fmaxf(m, __shfl_xor(m, 4, kWave));
-      int e = 0;
-      (void)frexpf(m, &e);
-      const int kk = m > 0.f ? min(22 - e, 126) : 0;
-      const float up = ldexpf(1.f, kk);
-      if ((j & 7) == 0) pk8[(j >> 3) * kMbMaxVec + b] = (m - m == 0.f) ? ldexpf(1.f, -kk) : __builtin_nanf("");
-      sx[j * kMbMaxVec + b] = s;
-      uint32_t wa[8], wb[8], wc[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22),
-        // less 0x4B400000 plus 0x808080: u = v + 0x808080, whose bytes less 128
-        // are the balanced digits c, b, a
-        uint32_t u[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          u[q] = __builtin_bit_cast(uint32_t, __builtin_fmaf(v[4 * k + q], up, 12582912.0f)) - 0x4ABF7F80u;
-        uint32_t pc, pb, pa;
-        transpose_bytes(u[0], u[1], u[2], u[3], pc, pb, pa);
-        wa[k] = pa ^ 0x80808080u;
-        wb[k] = pb ^ 0x80808080u;
-        wc[k] = pc ^ 0x80808080u;
+      for (int q = tid + kMbCopyRounds * nthreads; q < nchunk; q += nthreads) {  // larger workgroup shapes
+        const int half = q & 1, r = q >> 1;
+        const int b = r % nb, lj = r / nb;
+        const int l = lj / nblk_w, j = lj - l * nblk_w;
+        const size_t rec = (size_t(l) * nblk + j) * kMbMaxVec + b;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(img + rec * 32 + 16 * half);
+        uint64_t* d = reinterpret_cast<uint64_t*>(limbs + rec * kMbTokStride + 16 * half);
+        d[0] = uint64_t(v.x) | (uint64_t(v.y) << 32);
+        d[1] = uint64_t(v.z) | (uint64_t(v.w) << 32);
       }
-      uint8_t* da = limbs + (0 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
-      uint8_t* db = limbs + (1 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
-      uint8_t* dc = limbs + (2 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+      const float* pkw = reinterpret_cast<const float*>(img + size_t(3) * nblk * kMbMaxVec * 32);
+      const float* sxw = pkw + (nblk / 8) * kMbMaxVec;
+      for (int q = tid; q < nblk_w * kMbMaxVec; q += nthreads) {
+        sx[q] = sxw[q];
+        if (q < (nblk_w / 8) * kMbMaxVec) pk8[q] = pkw[q];
+      }
+    } else {
+      // ---- activations -> limbs: one (vector, block) pair per thread per
+      // round; the 8 blocks of a super-block are 8 adjacent lanes (nblk_w and
+      // the workgroup size are multiples of 8), which share its maximum
+      for (int p = tid; p < nb * nblk_w; p += nthreads) {
+        const int b = p / nblk_w, j = p - b * nblk_w;
+        uint32_t wa[8], wb[8], wc[8];
+        float down, sum;
+        mb_convert_block(x + int64_t(b) * cols + c0 + 32 * j, wa, wb, wc, down, sum);
+        if ((j & 7) == 0) pk8[(j >> 3) * kMbMaxVec + b] = down;
+        sx[j * kMbMaxVec + b] = sum;
+        uint8_t* da = limbs + (0 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+        uint8_t* db = limbs + (1 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
+        uint8_t* dc = limbs + (2 * nblk + j) * (kMbMaxVec * kMbTokStride) + b * kMbTokStride;
 #pragma unroll
-      for (int k = 0; k < 8; k += 2) {
-        *reinterpret_cast<uint64_t*>(da + 4 * k) = uint64_t(wa[k]) | (uint64_t(wa[k + 1]) << 32);
-        *reinterpret_cast<uint64_t*>(db + 4 * k) = uint64_t(wb[k]) | (uint64_t(wb[k + 1]) << 32);
-        *reinterpret_cast<uint64_t*>(dc + 4 * k) = uint64_t(wc[k]) | (uint64_t(wc[k + 1]) << 32);
+        for (int k = 0; k < 8; k += 2) {
+          *reinterpret_cast<uint64_t*>(da + 4 * k) = uint64_t(wa[k]) | (uint64_t(wa[k + 1]) << 32);
+          *reinterpret_cast<uint64_t*>(db + 4 * k) = uint64_t(wb[k]) | (uint64_t(wb[k + 1]) << 32);
+          *reinterpret_cast<uint64_t*>(dc + 4 * k) = uint64_t(wc[k]) | (uint64_t(wc[k + 1]) << 32);
+        }
       }
     }
     __syncthreads();
@@ -232,11 +378,37 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
       const f32x4 v = *reinterpret_cast<const f32x4*>(red + ((rt * S + s2) * 64 + lane) * 4);
       t = f32x4{t.x + v.x, t.y + v.y, t.z + v.z, t.w + v.w};
     }
-    const int r = blockIdx.x * (16 * T) + 16 * rt + r16;
+    const int r = rtb * (16 * T) + 16 * rt + r16;
     if (r < rows) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (d_out && tok_d + i < nb) y[int64_t(tok_d + i) * rows + r] = t[i];
+      for (int i = 0; i < 4; ++i) {
+        if (d_out && tok_d + i < nb) {
+          if constexpr (SPLIT)
+            __hip_atomic_store(part + (int64_t(win) * kMbMaxVec + tok_d + i) * rows + r, t[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          else
+            y[int64_t(tok_d + i) * rows + r] = t[i];
+        }
+      }
+    }
+  }
+  if constexpr (SPLIT) {
+    __shared__ uint32_t s_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial sums are in memory
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(count + rtb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_last != uint32_t(nwin - 1)) return;
+    // the last workgroup of the row block: the windows' sums in window order
+    const int r0 = rtb * (16 * T), nr = min(16 * T, rows - r0);
+    for (int i = tid; i < nb * nr; i += nthreads) {
+      const int b = i / nr, r = r0 + (i - b * nr);
+      float v = __hip_atomic_load(part + int64_t(b) * rows + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int k = 1; k < nwin; ++k)
+        v += __hip_atomic_load(part + (int64_t(k) * kMbMaxVec + b) * rows + r, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      y[int64_t(b) * rows + r] = v;
     }
   }
 }
@@ -246,38 +418,61 @@ bool gemv_mfma_ok(uint32_t quant, int64_t rows, int64_t cols, int batch) {
          cols <= (int64_t(1) << 20) && rows > 0 && rows <= (int64_t(1) << 31) - 1;
 }
 
-template <int PER>
+template <int PER, bool PREP, bool SPLIT>
 static void launch_mb(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x, float* y,
-                      int batch, int T, int S, size_t lds, hipStream_t s) {
-  const unsigned blocks = unsigned((rows + 16 * T - 1) / (16 * T));
+                      int batch, int T, int S, size_t lds, const uint8_t* ws, float* part, uint32_t* count,
+                      hipStream_t s) {
+  const int64_t nwin = (cols + kMbMaxCols - 1) / kMbMaxCols;
+  const unsigned blocks = unsigned((rows + 16 * T - 1) / (16 * T) * (SPLIT ? nwin : 1));
   const uint8_t* w = static_cast<const uint8_t*>(wv);
   const int64_t rb = byte_size(quant, cols);
   const bool one = cols <= kMbMaxCols;
+  const dim3 grid = dim3(blocks), block = dim3(unsigned(64 * T * S));
   if (quant == kQ5_K) {
     if (one)
-      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ5_K, PER, true>), dim3(blocks), dim3(64 * T * S), lds, s, w,
-                         int(rows), int(cols), rb, x, y, batch, T, S);
+      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ5_K, PER, true, PREP, false>), grid, block, lds, s, w, int(rows),
+                         int(cols), rb, x, y, batch, T, S, ws, part, count);
     else
-      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ5_K, PER, false>), dim3(blocks), dim3(64 * T * S), lds, s, w,
-                         int(rows), int(cols), rb, x, y, batch, T, S);
+      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ5_K, PER, false, PREP, SPLIT>), grid, block, lds, s, w, int(rows),
+                         int(cols), rb, x, y, batch, T, S, ws, part, count);
   } else {
     if (one)
-      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ4_K, PER, true>), dim3(blocks), dim3(64 * T * S), lds, s, w,
-                         int(rows), int(cols), rb, x, y, batch, T, S);
+      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ4_K, PER, true, PREP, false>), grid, block, lds, s, w, int(rows),
+                         int(cols), rb, x, y, batch, T, S, ws, part, count);
     else
-      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ4_K, PER, false>), dim3(blocks), dim3(64 * T * S), lds, s, w,
-                         int(rows), int(cols), rb, x, y, batch, T, S);
+      hipLaunchKernelGGL((gemv_mfma_kq_kernel<kQ4_K, PER, false, PREP, SPLIT>), grid, block, lds, s, w, int(rows),
+                         int(cols), rb, x, y, batch, T, S, ws, part, count);
+  }
+}
+
+template <bool PREP, bool SPLIT>
+static void launch_mb_per(int per, uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,
+                          float* y, int batch, int T, int S, size_t lds, const uint8_t* ws, float* part,
+                          uint32_t* count, hipStream_t s) {
+  switch (per) {
+    case 1: launch_mb<1, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 2: launch_mb<2, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 3: launch_mb<3, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 4: launch_mb<4, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 5: launch_mb<5, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 6: launch_mb<6, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    case 7: launch_mb<7, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
+    default: launch_mb<8, PREP, SPLIT>(quant, wv, rows, cols, x, y, batch, T, S, lds, ws, part, count, s); break;
   }
 }
 
 hipError_t launch_gemv_mfma(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x, float* y,
-                            int batch, int cu, hipStream_t s) {
+                            int batch, int cu, hipStream_t s, void* ws) {
   if (!gemv_mfma_ok(quant, rows, cols, batch)) return hipErrorInvalidValue;
-  // T row tiles per workgroup so the tiles cover the CUs about once; the
-  // workgroup's waves (12 for 3 or 4 tiles, 8 otherwise: one workgroup per
-  // CU, the activations' LDS allowing no more) split the super-blocks into
-  // shares of PER <= 8
-  int T = int((rows + 16LL * cu - 1) / (16LL * cu));
+  if (ws && (reinterpret_cast<uintptr_t>(ws) & 255u)) return hipErrorInvalidValue;
+  const int64_t nwin = (cols + kMbMaxCols - 1) / kMbMaxCols;
+  const bool split = ws && nwin > 1;
+  // T row tiles per workgroup so the tiles cover the CUs about once (with
+  // the split, the row blocks times the windows); the workgroup's waves (12
+  // for 3 or 4 tiles, 8 otherwise: one workgroup per CU, the activations'
+  // LDS allowing no more) split the super-blocks into shares of PER <= 8
+  const int64_t slots = split ? (cu / nwin > 0 ? cu / nwin : 1) : cu;
+  int T = int((rows + 16LL * slots - 1) / (16LL * slots));
   if (T < 1) T = 1;
   if (T > 4) T = 4;
   const int S = T >= 3 ? kMbMaxWaves / T : 8 / T;
@@ -287,15 +482,23 @@ hipError_t launch_gemv_mfma(uint32_t quant, const void* wv, int64_t rows, int64_
   const int nblk = int(wcols / 32);
   const size_t lds = size_t(mb_limb_bytes(nblk)) + 2 * sizeof(float) * nblk * kMbMaxVec +
                      sizeof(float) * T * S * 64 * 4;
-  switch (per) {
-    case 1: launch_mb<1>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 2: launch_mb<2>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 3: launch_mb<3>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 4: launch_mb<4>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 5: launch_mb<5>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 6: launch_mb<6>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    case 7: launch_mb<7>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
-    default: launch_mb<8>(quant, wv, rows, cols, x, y, batch, T, S, lds, s); break;
+  if (ws) {
+    // the activations converted once for every workgroup (and the split-K
+    // counters cleared)
+    uint8_t* wsb = static_cast<uint8_t*>(ws);
+    uint32_t* count = reinterpret_cast<uint32_t*>(wsb);
+    float* part = reinterpret_cast<float*>(wsb + mb_counters_bytes(rows));
+    const uint8_t* img = wsb + mb_counters_bytes(rows) + mb_part_bytes(rows, cols);
+    const int n_count = int((rows + 16 * T - 1) / (16 * T));
+    const int64_t n = std::max<int64_t>(int64_t(batch) * (cols / 32), n_count);
+    hipLaunchKernelGGL(mb_prep_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, int(cols), batch,
+                       const_cast<uint8_t*>(img), count, n_count);
+    if (split)
+      launch_mb_per<true, true>(per, quant, wv, rows, cols, x, y, batch, T, S, lds, img, part, count, s);
+    else
+      launch_mb_per<true, false>(per, quant, wv, rows, cols, x, y, batch, T, S, lds, img, nullptr, nullptr, s);
+  } else {
+    launch_mb_per<false, false>(per, quant, wv, rows, cols, x, y, batch, T, S, lds, nullptr, nullptr, nullptr, s);
   }
   return hipGetLastError();
 }

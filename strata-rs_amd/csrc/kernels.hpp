@@ -16,8 +16,11 @@ hipError_t launch_dequant(uint32_t quant, const void* w, int64_t rows, int64_t c
 // hipErrorInvalidValue for shapes the kernels do not take (checked by
 // gemv_shape_ok first).
 bool gemv_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
+// `ws`: optional workspace of gemv_workspace_bytes() for batches of 2..8
+// (the activations are then converted once per call); null: none.
 hipError_t launch_gemv(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
-                       float* y, int batch, int q6_signed, hipStream_t stream);
+                       float* y, int batch, int q6_signed, hipStream_t stream, void* ws = nullptr);
+size_t gemv_workspace_bytes(uint32_t quant, int64_t rows, int64_t cols, int batch);
 // One token of the dense FFN (qwen35.rs:112-129) after its rms_norm, in two
 // matvec launches: gu = [gate . x; up . x] (2 * n_ff floats), then
 // out = xres + down . (silu(g) * u). All three matrices of type `quant`
@@ -43,9 +46,14 @@ hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* w, int64_t rows, 
 // Batch 2..8 of Q4_K or Q5_K rows on int8 MFMA (exact integer
 // activations, staged in LDS 4096 columns at a time); `cu` is the device's
 // CU count.
+// With `ws` (gemv_mfma_workspace_bytes(rows, cols), 256-byte aligned, no
+// initialisation needed) the activations are converted once per call into
+// it (one extra launch) instead of by every workgroup, and rows wider than
+// one 4096-column window run split-K over the windows.
 bool gemv_mfma_ok(uint32_t quant, int64_t rows, int64_t cols, int batch);
+size_t gemv_mfma_workspace_bytes(int64_t rows, int64_t cols);
 hipError_t launch_gemv_mfma(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x, float* y,
-                            int batch, int cu, hipStream_t stream);
+                            int batch, int cu, hipStream_t stream, void* ws = nullptr);
 
 // y[c] = sum_i x[i] * W[i][c] for one expert matrix W[rows = in][cols = out]
 // (reference orientation). `workspace` holds expert_workspace_bytes().

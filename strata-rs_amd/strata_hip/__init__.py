@@ -65,6 +65,7 @@ EXPORTS = (
     "sh_gguf_meta_int", "sh_gguf_meta_float", "sh_gguf_meta_str", "sh_upload_gguf_tensor", "sh_gguf_model_open",
     "sh_gguf_model_close", "sh_gguf_model_shards", "sh_gguf_model_shard", "sh_gguf_model_find", "sh_weight_upload",
     "sh_ffn_workspace_bytes", "sh_ffn_dev", "sh_ffn", "sh_ffn_dev_noalloc", "sh_stream_read_dev",
+    "sh_gemv_workspace_bytes", "sh_gemv_dev_ws",
 )
 
 
@@ -222,6 +223,8 @@ def load_library() -> C.CDLL:
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
     L.sh_stream_read_dev.argtypes = [vp, u64, vp, vp]
+    L.sh_gemv_workspace_bytes.argtypes = [u32, u64, u64, u32, C.POINTER(C.c_uint64)]
+    L.sh_gemv_dev_ws.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp, u64, vp]
     dbl, ropep = C.c_double, C.POINTER(_RopeCfgC)
     L.sh_rms_norm.argtypes = [vp, f32p, f32p, u64, dbl]
     L.sh_rope_neox.argtypes = [vp, f32p, u64, ropep]
@@ -713,6 +716,20 @@ def gemv_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, y_ptr: in
              stream: int = 0, flags: int = 0) -> None:
     check(load_library().sh_gemv_dev(int(quant), flags, w_ptr, rows, cols, x_ptr, y_ptr, batch,
                                      stream or None))
+
+
+def gemv_workspace_bytes(quant: int, rows: int, cols: int, batch: int) -> int:
+    v = C.c_uint64()
+    check(load_library().sh_gemv_workspace_bytes(int(quant), rows, cols, batch, C.byref(v)))
+    return v.value
+
+
+def gemv_dev_ws(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, y_ptr: int, batch: int,
+                ws_ptr: int, ws_bytes: int, stream: int = 0, flags: int = 0) -> None:
+    """sh_gemv_dev_ws: batches of 2..8 convert their activations once per
+    call into the workspace."""
+    check(load_library().sh_gemv_dev_ws(int(quant), flags, w_ptr, rows, cols, x_ptr, y_ptr, batch,
+                                        ws_ptr or None, ws_bytes, stream or None))
 
 
 def moe_workspace_bytes(n_tok: int, top_k: int, n_expert: int, n_embd: int, n_ff: int,

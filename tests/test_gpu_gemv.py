@@ -260,3 +260,45 @@ def test_gemv_random_shapes(backend, oracle, seed):
             check(y[b], oracle.gemv(quant, rows, cols, w, x[b], threads=8))
         backend.evict(f"rand{seed}_{case}")
 
+
+
+@pytest.mark.parametrize("quant,rows,cols,batch", [(12, 4096, 12288, 8), (13, 4096, 12288, 3), (12, 4096, 8192, 2),
+                                                   (12, 33, 8192 + 256, 7), (13, 1000, 20480, 8)])
+def test_gemv_dev_ws_batches(oracle, quant, rows, cols, batch):
+    """sh_gemv_dev_ws: batches of rows wider than one 4096-column window
+    convert their activations once per call into the workspace and run
+    split-K (the windows' sums added in window order by the last workgroup
+    of each row block): the same call twice gives the same bits (no
+    dependence on which workgroup finished last), against the oracle at the
+    parity bars; two activation sets on one workspace."""
+    import torch
+    say("gemv_dev_ws", quant, rows, cols, batch)
+    w = S.matrix(quant, 91 + rows + cols, rows, cols)
+    nb = H.gemv_workspace_bytes(quant, rows, cols, batch)
+    assert nb > 0
+    wd = torch.from_numpy(w).cuda()
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    for seed in (92, 93):
+        x = S.normal_f32(seed + cols, batch * cols).reshape(batch, cols)
+        xd = torch.from_numpy(x).cuda()
+        y1 = torch.empty(batch * rows, dtype=torch.float32, device="cuda")
+        y2 = torch.empty_like(y1)
+        H.gemv_dev_ws(quant, wd.data_ptr(), rows, cols, xd.data_ptr(), y1.data_ptr(), batch, ws.data_ptr(), nb, s)
+        H.gemv_dev_ws(quant, wd.data_ptr(), rows, cols, xd.data_ptr(), y2.data_ptr(), batch, ws.data_ptr(), nb, s)
+        torch.cuda.synchronize()
+        a, b = y1.cpu().numpy(), y2.cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        a = a.reshape(batch, rows)
+        for i in sorted({0, batch - 1}):
+            check(a[i], oracle.gemv(quant, rows, cols, w, x[i], threads=8), f"dev_ws b{i}")
+
+
+def test_gemv_workspace_sizes():
+    say("gemv workspace sizes")
+    assert H.gemv_workspace_bytes(12, 4096, 12288, 1) == 0      # batch 1: none
+    assert H.gemv_workspace_bytes(14, 4096, 12288, 8) == 0      # no batched MFMA kernel for Q6_K
+    assert H.gemv_workspace_bytes(12, 4096, 12288, 8) > 0
+    assert H.gemv_workspace_bytes(12, 12288, 4096, 8) == 0      # one window: no split-K
+    with pytest.raises(H.BackendError):
+        H.gemv_dev_ws(12, 1 << 20, 4096, 12288, 1 << 20, 1 << 20, 8, 1 << 20, 16)  # workspace too small
