@@ -4,8 +4,8 @@
  *
  * The library replaces the matvec/matmul half of strata-core's
  * `trait ComputeBackend` (crates/strata-core/src/backend.rs:20-51) for the
- * GGUF types Q8_0, Q4_K and Q6_K (and, for the matvec and dequant only,
- * Q5_K and F32 / F16 / BF16, the types router and gate tensors use).
+ * GGUF types Q8_0, Q4_K, Q5_K and Q6_K (and, for the matvec and dequant
+ * only, IQ4_XS and F32 / F16 / BF16, the types router and gate tensors use).
  * Weights stay packed in device memory in their GGUF block layout; kernels
  * dequantize in registers.
  *
@@ -66,8 +66,9 @@ extern "C" {
 #define SH_QUANT_F16 1u
 #define SH_QUANT_Q8_0 8u
 #define SH_QUANT_Q4_K 12u
-#define SH_QUANT_Q5_K 13u /* matvec and dequant only */
+#define SH_QUANT_Q5_K 13u
 #define SH_QUANT_Q6_K 14u
+#define SH_QUANT_IQ4_XS 23u /* matvec and dequant only */
 #define SH_QUANT_BF16 30u
 
 /* ---- tensor flags ------------------------------------------------------ */
@@ -80,6 +81,11 @@ extern "C" {
  * cols, y_len = rows) with the matvec kernels. The reference's in-major
  * orientation (weights.rs:14-34) is the default. sh_expert_gemv only. */
 #define SH_FLAG_EXPERT_OUT_MAJOR 2u
+/* IQ4_XS in ggml's layout, sub-block ib reading qs[16 ib .. 16 ib + 16).
+ * strata-gguf reads qs[0..16] for every sub-block (its qs slice is never
+ * advanced, crates/strata-gguf/src/dequant.rs:189-206); that reading is the
+ * default. */
+#define SH_FLAG_IQ4XS_GGML 4u
 
 /* ---- matmul modes ------------------------------------------------------ */
 #define SH_MATMUL_BF16 0u /* bf16 activations, dequant-to-bf16 LDS tiles, bf16 MFMA */
@@ -159,8 +165,8 @@ int sh_evict(sh_context* ctx, uint64_t key);
 
 /* ComputeBackend::gemv (backend.rs:25), semantics of ops::gemv
  * (crates/strata-core/src/ops.rs:14-28): y[r] = sum_c W[r][c] * x[c].
- * x_len must equal cols and y_len rows. Q8_0 / Q4_K / Q5_K / Q6_K, and F32 /
- * F16 / BF16 (products and sums in f64, as ops::gemv does). */
+ * x_len must equal cols and y_len rows. Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS,
+ * and F32 / F16 / BF16 (products and sums in f64, as ops::gemv does). */
 int sh_gemv(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint64_t x_len, float* y,
             uint64_t y_len);
 
@@ -236,7 +242,7 @@ int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view
  * out += sigmoid(gate_inp_shexp . x) * down_shexp . (silu(gate_shexp . x) *
  * (up_shexp . x)) (moe.rs:129-142). router [n_expert][n_embd], gate/up_shexp
  * [n_ff_shexp][n_embd], down_shexp [n_embd][n_ff_shexp], gate_inp_shexp
- * [1][n_embd] are ops::gemv matrices of any matvec type (Q5_K and F32 /
+ * [1][n_embd] are ops::gemv matrices of any matvec type (IQ4_XS and F32 /
  * F16 / BF16 included); the expert views as in sh_moe_ffn. n_ff_shexp must be a
  * multiple of 4. The weight budget must hold the eight tensors at once. */
 int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert_view* gate,
@@ -251,10 +257,10 @@ int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert
  * 116-117); the result equals m calls of ops::gemv (ops.rs:14-28) up to the
  * activation rounding of `mode`:
  *   SH_MATMUL_BF16  x rounded to bf16, weights dequantized to bf16, f32
- *                   accumulation (Q8_0, Q4_K, Q6_K);
+ *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K);
  *   SH_MATMUL_Q8    x quantized to 32-element blocks (scale max|x| / 127,
  *                   int8 codes rounded to nearest even), int8 products
- *                   (Q8_0, Q4_K).
+ *                   (Q8_0, Q4_K, Q5_K).
  * cols must be a multiple of 64. */
 int sh_matmul(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint32_t m, float* y,
               uint32_t mode);

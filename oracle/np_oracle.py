@@ -6,13 +6,17 @@ than from the block loops, so a slip in one of the two (a swapped nibble, a
 wrong scale index, a fused multiply-add) shows up as a mismatch.
 
 References: crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :208-234 (Q6_K),
-:237-270 (Q4_K), :272-302 (Q5_K); crates/strata-core/src/ops.rs:14-28 (gemv).
+:237-270 (Q4_K), :272-302 (Q5_K), :189-206 (IQ4_XS);
+crates/strata-core/src/ops.rs:14-28 (gemv).
 """
 from __future__ import annotations
 
 import numpy as np
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 23, 30
+
+# ggml's kvalues_iq4nl (crates/strata-gguf/src/tables.rs:2052-2054)
+IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
 
 
 def _f16(b: np.ndarray) -> np.ndarray:
@@ -107,8 +111,29 @@ def q6_k(data: np.ndarray, signed_scales: bool = False) -> np.ndarray:
     return (ds * q.astype(np.float32)).astype(np.float32).reshape(n * 256)
 
 
+def iq4_xs(data: np.ndarray, ggml: bool = False) -> np.ndarray:
+    """Element i of a super-block: sub-block ib = i // 32, position k = i % 32;
+    code byte k % 16 of the first 16 qs bytes (the reference's reading) or of
+    qs bytes [16 ib, +16) (ggml's), low nibble for k < 16, high otherwise;
+    dl = d * (ls - 32) with the 6-bit ls split over scales_l (4 bits) and
+    scales_h (2 bits)."""
+    b = data.reshape(-1, 136)
+    n = b.shape[0]
+    d = _f16(b[:, 0:2])
+    sh = b[:, 2].astype(np.uint32) | (b[:, 3].astype(np.uint32) << 8)
+    ib = np.arange(8)
+    lo4 = (b[:, 4 + ib // 2] >> (4 * (ib % 2))) & 0x0F
+    ls = lo4.astype(np.int32) | (((sh[:, None] >> (2 * ib)) & 3).astype(np.int32) << 4)
+    dl = (d[:, None] * (ls.astype(np.float32) - np.float32(32))).astype(np.float32)
+    i = np.arange(256)
+    k = i % 32
+    byte = 8 + (16 * (i // 32) if ggml else 0) + k % 16
+    nib = np.where(k[None, :] >= 16, b[:, byte] >> 4, b[:, byte] & 0x0F)
+    return (dl[:, i // 32] * IQ4NL[nib]).astype(np.float32).reshape(n * 256)
+
+
 def dequantize(quant: int, data: np.ndarray, rows: int, cols: int,
-               signed_q6k_scales: bool = False) -> np.ndarray:
+               signed_q6k_scales: bool = False, iq4xs_ggml: bool = False) -> np.ndarray:
     data = np.ascontiguousarray(data, dtype=np.uint8)
     if quant == Q8_0:
         flat = q8_0(data)
@@ -118,6 +143,8 @@ def dequantize(quant: int, data: np.ndarray, rows: int, cols: int,
         flat = q5_k(data)
     elif quant == Q6_K:
         flat = q6_k(data, signed_q6k_scales)
+    elif quant == IQ4_XS:
+        flat = iq4_xs(data, iq4xs_ggml)
     elif quant == F32:
         flat = data.view(np.float32).copy()
     elif quant == F16:

@@ -103,6 +103,7 @@ int64_t sho_block_size(uint32_t quant) {
     case SHO_Q4_K:
     case SHO_Q5_K:
     case SHO_Q6_K:
+    case SHO_IQ4_XS:
       return 256;
     default:
       return -1;
@@ -124,6 +125,8 @@ int64_t sho_type_size(uint32_t quant) {
       return 176;
     case SHO_Q6_K:
       return 210;
+    case SHO_IQ4_XS:
+      return 136;
     default:
       return -1;
   }
@@ -251,7 +254,34 @@ static void dq_q6_k(const uint8_t* b, float* out, int scale_mode) {
   }
 }
 
-static int dq_block(uint32_t quant, const uint8_t* b, float* out, int q6_mode) {
+/* The IQ4_NL / IQ4_XS code book (a format table: ggml's kvalues_iq4nl,
+ * crates/strata-gguf/src/tables.rs:2052-2054). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
+/* dequant.rs:189-206. [d: f16][scales_h: u16][scales_l: 4 B][qs: 128 B];
+ * sub-block ib (32 elements) has the 6-bit scale ls = low nibble ib % 2 of
+ * scales_l[ib / 2] | bits 2ib..2ib+1 of scales_h << 4, dl = d * (ls - 32)
+ * rounded once, and out = dl * code for the code book's value of each
+ * nibble (low nibbles first, then high). Code bytes: the first 16 for every
+ * sub-block (SHO_IQ4XS_REFERENCE) or bytes 16ib.. (SHO_IQ4XS_GGML). */
+static void dq_iq4_xs(const uint8_t* b, float* out, int mode) {
+  float d = sho_f16_to_f32(rd16(b));
+  uint32_t sh = rd16(b + 2);
+  const uint8_t* sl = b + 4;
+  const uint8_t* qs = b + 8;
+  for (int ib = 0; ib < 8; ++ib) {
+    uint32_t ls = ((uint32_t)(sl[ib / 2] >> (4 * (ib % 2))) & 0x0Fu) | (((sh >> (2 * ib)) & 3u) << 4);
+    float dl = d * ((float)ls - 32.0f);
+    const uint8_t* q = mode == SHO_IQ4XS_GGML ? qs + 16 * ib : qs;
+    for (int j = 0; j < 16; ++j) {
+      out[32 * ib + j] = dl * (float)kIq4nl[q[j] & 0x0F];
+      out[32 * ib + j + 16] = dl * (float)kIq4nl[q[j] >> 4];
+    }
+  }
+}
+
+static int dq_block(uint32_t quant, const uint8_t* b, float* out, int mode) {  /* mode: the Q6_K or IQ4_XS reading */
   switch (quant) {
     case SHO_F32:
       memcpy(out, b, 4);
@@ -274,7 +304,10 @@ static int dq_block(uint32_t quant, const uint8_t* b, float* out, int q6_mode) {
       dq_q5_k(b, out);
       return SHO_OK;
     case SHO_Q6_K:
-      dq_q6_k(b, out, q6_mode);
+      dq_q6_k(b, out, mode);
+      return SHO_OK;
+    case SHO_IQ4_XS:
+      dq_iq4_xs(b, out, mode);
       return SHO_OK;
     default:
       return SHO_UNSUPPORTED;
@@ -284,13 +317,13 @@ static int dq_block(uint32_t quant, const uint8_t* b, float* out, int q6_mode) {
 /* dequant.rs:45-61: Truncated when n is not a whole number of blocks or the
  * buffer is short; otherwise block by block. */
 static int dequant_row_mode(uint32_t quant, const uint8_t* block, size_t nbytes,
-                            float* out, size_t n, int q6_mode) {
+                            float* out, size_t n, int mode) {
   int64_t bs = sho_block_size(quant), ts = sho_type_size(quant);
   if (bs <= 0) return SHO_UNSUPPORTED;
   size_t n_blocks = (n + (size_t)bs - 1) / (size_t)bs;
   if (n % (size_t)bs != 0 || nbytes < n_blocks * (size_t)ts) return SHO_TRUNCATED;
   for (size_t i = 0; i < n_blocks; ++i) {
-    int rc = dq_block(quant, block + i * (size_t)ts, out + i * (size_t)bs, q6_mode);
+    int rc = dq_block(quant, block + i * (size_t)ts, out + i * (size_t)bs, mode);
     if (rc) return rc;
   }
   return SHO_OK;
@@ -306,12 +339,17 @@ int sho_dequantize_row_q6k_mode(const uint8_t* block, size_t nbytes, float* out,
   return dequant_row_mode(SHO_Q6_K, block, nbytes, out, n, scale_mode);
 }
 
+int sho_dequantize_row_mode(uint32_t quant, const uint8_t* block, size_t nbytes,
+                            float* out, size_t n, int mode) {
+  return dequant_row_mode(quant, block, nbytes, out, n, mode);
+}
+
 /* ---- gemv (ops.rs:14-28) -----------------------------------------------
  * For each row: dequantize into scratch, then a sequential f64 dot, cast to
  * f32 at the end. Rows [r0, r1) only, so the threaded variant reuses it. */
 static int gemv_rows(uint32_t quant, int64_t r0, int64_t r1, int64_t cols,
                      const uint8_t* data, size_t nbytes, const float* x,
-                     float* y, int q6_mode) {
+                     float* y, int mode) {
   int64_t rb = sho_byte_size(quant, cols);
   if (rb < 0) return SHO_UNSUPPORTED;
   float* row = (float*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(float));
@@ -323,7 +361,7 @@ static int gemv_rows(uint32_t quant, int64_t r0, int64_t r1, int64_t cols,
       rc = SHO_TRUNCATED;
       break;
     }
-    rc = dequant_row_mode(quant, data + off, (size_t)rb, row, (size_t)cols, q6_mode);
+    rc = dequant_row_mode(quant, data + off, (size_t)rb, row, (size_t)cols, mode);
     if (rc) break;
     double acc = 0.0;
     for (int64_t c = 0; c < cols; ++c) acc += (double)row[c] * (double)x[c];
@@ -336,6 +374,11 @@ static int gemv_rows(uint32_t quant, int64_t r0, int64_t r1, int64_t cols,
 int sho_gemv(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
              size_t nbytes, const float* x, float* y) {
   return gemv_rows(quant, 0, rows, cols, data, nbytes, x, y, SHO_Q6K_SCALE_U8);
+}
+
+int sho_gemv_mode(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+                  size_t nbytes, const float* x, float* y, int mode) {
+  return gemv_rows(quant, 0, rows, cols, data, nbytes, x, y, mode);
 }
 
 int sho_gemv_q6k_mode(int64_t rows, int64_t cols, const uint8_t* data,

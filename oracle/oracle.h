@@ -7,7 +7,7 @@
  *
  * It restates, in plain C, the reference's scalar CPU path:
  *   - block geometry          crates/strata-gguf/src/quant.rs:125-181
- *   - f16 -> f32, row dequant crates/strata-gguf/src/dequant.rs:28-61,123-128,208-302
+ *   - f16 -> f32, row dequant crates/strata-gguf/src/dequant.rs:28-61,123-128,189-206,208-302
  *   - gemv / expert_gemv      crates/strata-core/src/ops.rs:14-28,169-195
  *   - silu                    crates/strata-core/src/ops.rs:85-87
  *   - MoE route / combine     crates/strata-core/src/moe.rs:48-127
@@ -44,6 +44,7 @@ enum {
   SHO_Q4_K = 12,
   SHO_Q5_K = 13,
   SHO_Q6_K = 14,
+  SHO_IQ4_XS = 23,
   SHO_BF16 = 30,
 };
 
@@ -57,6 +58,11 @@ enum {
 /* Q6_K sub-block scale semantics: the reference reads the 16 scale bytes as
  * u8 (dequant.rs:211,224-227); ggml declares them int8_t. */
 enum { SHO_Q6K_SCALE_U8 = 0, SHO_Q6K_SCALE_I8 = 1 };
+
+/* IQ4_XS code bytes: the reference reads the first 16 qs bytes for every
+ * 32-element sub-block (dequant.rs:194-204, `qs` is never advanced); ggml's
+ * dequantize_row_iq4_xs advances 16 bytes per sub-block. */
+enum { SHO_IQ4XS_REFERENCE = 0, SHO_IQ4XS_GGML = 1 };
 
 float sho_f16_to_f32(uint16_t h);
 uint16_t sho_f32_to_f16(float f);
@@ -72,6 +78,13 @@ int sho_dequantize_row(uint32_t quant, const uint8_t* block, size_t nbytes,
                        float* out, size_t n);
 int sho_dequantize_row_q6k_mode(const uint8_t* block, size_t nbytes, float* out,
                                 size_t n, int scale_mode);
+
+/* Either reading where the format has two (mode: the Q6_K scale reading
+ * for Q6_K, the IQ4_XS code-byte reading for IQ4_XS; ignored otherwise). */
+int sho_dequantize_row_mode(uint32_t quant, const uint8_t* block, size_t nbytes,
+                            float* out, size_t n, int mode);
+int sho_gemv_mode(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+                  size_t nbytes, const float* x, float* y, int mode);
 
 int sho_gemv(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
              size_t nbytes, const float* x, float* y);

@@ -15,8 +15,13 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 23, 30
+# the two readings of formats that have them (the `scale_mode` arguments):
+# Q6_K sub-block scales as u8 (the reference) or i8 (ggml); IQ4_XS code
+# bytes the first 16 for every sub-block (the reference) or 16 per sub-block
+# (ggml)
 SCALE_U8, SCALE_I8 = 0, 1
+IQ4XS_REFERENCE, IQ4XS_GGML = 0, 1
 OK, TRUNCATED, UNSUPPORTED = 0, -1, -2
 
 _lib = None
@@ -47,6 +52,8 @@ def lib() -> C.CDLL:
         L.sho_get_scale_min_k4.argtypes = [C.c_int, u8p, C.POINTER(C.c_uint8), C.POINTER(C.c_uint8)]
         L.sho_dequantize_row.argtypes = [C.c_uint32, u8p, C.c_size_t, f32p, C.c_size_t]
         L.sho_dequantize_row_q6k_mode.argtypes = [u8p, C.c_size_t, f32p, C.c_size_t, C.c_int]
+        L.sho_dequantize_row_mode.argtypes = [C.c_uint32, u8p, C.c_size_t, f32p, C.c_size_t, C.c_int]
+        L.sho_gemv_mode.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p, C.c_int]
         L.sho_gemv.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p]
         L.sho_gemv_q6k_mode.argtypes = [C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p, C.c_int]
         L.sho_gemv_threads.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, f32p,
@@ -137,8 +144,8 @@ def get_scale_min_k4(j: int, scales) -> tuple[int, int]:
 def dequantize_row(quant: int, block, n: int, scale_mode: int = SCALE_U8) -> np.ndarray:
     b = _u8(block)
     out = np.zeros(n, dtype=np.float32)
-    if quant == Q6_K:
-        rc = lib().sho_dequantize_row_q6k_mode(_ptr(b), b.nbytes, _ptr(out), n, scale_mode)
+    if scale_mode != 0:
+        rc = lib().sho_dequantize_row_mode(quant, _ptr(b), b.nbytes, _ptr(out), n, scale_mode)
     else:
         rc = lib().sho_dequantize_row(quant, _ptr(b), b.nbytes, _ptr(out), n)
     _check(rc, "dequantize_row")
@@ -160,8 +167,8 @@ def gemv(quant: int, rows: int, cols: int, data, x, scale_mode: int = SCALE_U8,
     b, xv = _u8(data), _f32(x)
     assert xv.size == cols
     y = np.empty(rows, dtype=np.float32)
-    if quant == Q6_K and scale_mode != SCALE_U8:
-        rc = lib().sho_gemv_q6k_mode(rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y), scale_mode)
+    if scale_mode != 0:
+        rc = lib().sho_gemv_mode(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y), scale_mode)
     elif threads > 1:
         rc = lib().sho_gemv_threads(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), _ptr(y), threads)
     else:

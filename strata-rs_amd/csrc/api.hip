@@ -293,6 +293,14 @@ int check_matrix(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t n_expert
   return SH_OK;
 }
 
+// The alternate reading a kernel applies to a tensor's blocks (each type has
+// at most one): Q6_K's int8 sub-block scales, or IQ4_XS's ggml qs layout.
+static int reading(uint32_t quant, uint32_t flags) {
+  if (quant == SH_QUANT_Q6_K) return (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0;
+  if (quant == SH_QUANT_IQ4_XS) return (flags & SH_FLAG_IQ4XS_GGML) ? 1 : 0;
+  return 0;
+}
+
 // Holds the context lock for one call and numbers the call, so the weights
 // it admits are pinned until it returns.
 struct Guard {
@@ -421,7 +429,7 @@ static int run_gemv(sh_context* c, const sh_quant_tensor* w, const float* x, flo
   HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
   HIP_TRY(sh::launch_gemv(w->quant, r->dev, int64_t(rows), int64_t(cols),
                           static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
-                          int(batch), (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream,
+                          int(batch), reading(w->quant, w->flags), c->stream,
                           wsb ? c->d_blk.p : nullptr),
           "gemv launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
@@ -489,7 +497,7 @@ int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const flo
     memcpy(c->h_in.p, x, xb);
     HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
     HIP_TRY(sh::launch_gemv(w->quant, we, int64_t(rows), int64_t(cols), static_cast<const float*>(c->d_in.p),
-                            static_cast<float*>(c->d_out.p), 1, (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                            static_cast<float*>(c->d_out.p), 1, reading(w->quant, w->flags),
                             c->stream),
             "expert_gemv launch");
     HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
@@ -533,7 +541,7 @@ int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const flo
   HIP_TRY(sh::launch_expert_gemv(w->quant, we, int64_t(rows), int64_t(cols),
                                  static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
                                  static_cast<float*>(c->d_blk.p),
-                                 (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+                                 reading(w->quant, w->flags), c->stream),
           "expert_gemv launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
   HIP_TRY(hipStreamSynchronize(c->stream), "expert_gemv");
@@ -628,9 +636,9 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
   HIP_TRY(hipMemcpyAsync(c->d_in.p, hi, lb_al + xb, hipMemcpyHostToDevice, c->stream), "input upload");
   const uint8_t* di = static_cast<const uint8_t*>(c->d_in.p);
   HIP_TRY(sh::launch_moe(plan, gate->quant, up->quant, down->quant, rg->dev, ru->dev, rd->dev,
-                         (gate->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
-                         (up->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
-                         (down->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                         reading(gate->quant, gate->flags),
+                         reading(up->quant, up->flags),
+                         reading(down->quant, down->flags),
                          reinterpret_cast<const float*>(di), reinterpret_cast<const float*>(di + lb_al),
                          static_cast<float*>(c->d_out.p), c->d_blk.p, c->stream),
           "moe launch");
@@ -729,11 +737,11 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
     return rc;
   memcpy(c->h_in.p, x, xb);
   HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
-  auto q6 = [](uint32_t flags) { return (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  auto q6 = [](const auto* t) { return reading(t->quant, t->flags); };
   const sh::MoeLayerTensors w{dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], dev[6], dev[7],
-                              q6(router->flags), q6(gate->flags), q6(up->flags), q6(down->flags),
-                              q6(gate_shexp->flags), q6(up_shexp->flags), q6(down_shexp->flags),
-                              q6(gate_inp_shexp->flags)};
+                              q6(router), q6(gate), q6(up), q6(down),
+                              q6(gate_shexp), q6(up_shexp), q6(down_shexp),
+                              q6(gate_inp_shexp)};
   HIP_TRY(sh::launch_moe_layer(plan, q, w, static_cast<const float*>(c->d_in.p), static_cast<float*>(c->d_out.p),
                                c->d_blk.p, c->stream),
           "moe layer launch");
@@ -781,7 +789,7 @@ int sh_matmul(sh_context* c, const sh_quant_tensor* w, const float* x, uint32_t 
   HIP_TRY(hipMemcpyAsync(c->d_in.p, c->h_in.p, xb, hipMemcpyHostToDevice, c->stream), "x upload");
   HIP_TRY(sh::launch_matmul(w->quant, r->dev, int64_t(rows), int64_t(cols),
                             static_cast<const float*>(c->d_in.p), int64_t(m), static_cast<float*>(c->d_out.p),
-                            mode, c->d_blk.p, (w->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+                            mode, c->d_blk.p, reading(w->quant, w->flags), c->stream),
           "matmul launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, yb, hipMemcpyDeviceToHost, c->stream), "y readback");
   HIP_TRY(hipStreamSynchronize(c->stream), "matmul");
@@ -808,7 +816,7 @@ int sh_dequantize_row(sh_context* c, uint32_t quant, uint32_t flags, const uint8
     return rc;
   HIP_TRY(hipMemcpyAsync(c->d_blk.p, block, in_b, hipMemcpyHostToDevice, c->stream), "block upload");
   HIP_TRY(sh::launch_dequant(quant, c->d_blk.p, 1, int64_t(n), static_cast<float*>(c->d_out.p),
-                             (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, c->stream),
+                             reading(quant, flags), c->stream),
           "dequant launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, c->d_out.p, out_b, hipMemcpyDeviceToHost, c->stream), "readback");
   HIP_TRY(hipStreamSynchronize(c->stream), "dequant");
@@ -824,7 +832,7 @@ int sh_dequant_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
     return fail(SH_ERR_TRUNCATED, "cols %llu is not a whole number of blocks", (unsigned long long)cols);
   if (rows && cols && (!w || !out)) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
   HIP_TRY(sh::launch_dequant(quant, w, int64_t(rows), int64_t(cols), out,
-                             (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
+                             reading(quant, flags),
                              static_cast<hipStream_t>(stream)),
           "dequant launch");
   return SH_OK;
@@ -850,10 +858,11 @@ int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, ui
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "gemv %llux%llu of type %u (batch %u) is not supported",
                 (unsigned long long)rows, (unsigned long long)cols, quant, batch);
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
-      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(w) & 3u)))
+      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32 || quant == SH_QUANT_IQ4_XS) &&
+       (reinterpret_cast<uintptr_t>(w) & 3u)))
     return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0 and F32; x 16)");
   HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
-                          (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
+                          reading(quant, flags), static_cast<hipStream_t>(stream)),
           "gemv launch");
   return SH_OK;
 }
@@ -883,10 +892,11 @@ int sh_gemv_dev_ws(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
   if (rows == 0 || cols == 0) return fail(SH_ERR_UNSUPPORTED_SHAPE, "empty matrix on the device path");
   if (!w || !x || !y) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 1u) ||
-      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(w) & 3u)))
+      ((quant == SH_QUANT_Q8_0 || quant == SH_QUANT_F32 || quant == SH_QUANT_IQ4_XS) &&
+       (reinterpret_cast<uintptr_t>(w) & 3u)))
     return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 2 bytes, 4 for Q8_0 and F32; x 16)");
   HIP_TRY(sh::launch_gemv(quant, w, int64_t(rows), int64_t(cols), x, y, int(batch),
-                          (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream),
+                          reading(quant, flags), static_cast<hipStream_t>(stream),
                           need ? workspace : nullptr),
           "gemv launch");
   return SH_OK;
@@ -926,9 +936,9 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
         (t->quant == SH_QUANT_Q8_0 && (reinterpret_cast<uintptr_t>(t->data) & 3u)))
       return fail(SH_ERR_INVALID_ARGUMENT, "misaligned expert tensor");
   HIP_TRY(sh::launch_moe(plan, gate->quant, up->quant, down->quant, gate->data, up->data, down->data,
-                         (gate->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
-                         (up->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0,
-                         (down->flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, logits, x, out, workspace,
+                         reading(gate->quant, gate->flags),
+                         reading(up->quant, up->flags),
+                         reading(down->quant, down->flags), logits, x, out, workspace,
                          static_cast<hipStream_t>(stream)),
           "moe launch");
   return SH_OK;
@@ -954,7 +964,8 @@ int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd,
   for (int i = 0; i < 8; ++i) {
     if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
     if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
-        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
+        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32 || t[i].quant == SH_QUANT_IQ4_XS) &&
+         (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
       return fail(SH_ERR_INVALID_ARGUMENT, "misaligned tensor %d", i);
   }
   if (reinterpret_cast<uintptr_t>(x) & 15u) return fail(SH_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
@@ -972,10 +983,10 @@ int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd,
                 (unsigned long long)workspace_bytes, (unsigned long long)plan.bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255u)
     return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
-  auto q6 = [](uint32_t flags) { return (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
+  auto q6 = [](const sh_expert_dev& d) { return reading(d.quant, d.flags); };
   const sh::MoeLayerTensors w{t[0].data, t[1].data, t[2].data, t[3].data, t[4].data, t[5].data, t[6].data,
-                              t[7].data, q6(t[0].flags), q6(t[1].flags), q6(t[2].flags), q6(t[3].flags),
-                              q6(t[4].flags), q6(t[5].flags), q6(t[6].flags), q6(t[7].flags)};
+                              t[7].data, q6(t[0]), q6(t[1]), q6(t[2]), q6(t[3]),
+                              q6(t[4]), q6(t[5]), q6(t[6]), q6(t[7])};
   HIP_TRY(sh::launch_moe_layer(plan, q, w, x, out, workspace, static_cast<hipStream_t>(stream)),
           "moe layer launch");
   return SH_OK;
@@ -1006,7 +1017,7 @@ int sh_matmul_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, 
       (reinterpret_cast<uintptr_t>(workspace) & 255u))
     return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (w needs 4 bytes, x 16, workspace 256)");
   HIP_TRY(sh::launch_matmul(quant, w, int64_t(rows), int64_t(cols), x, int64_t(m), y, mode, workspace,
-                            (flags & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0, static_cast<hipStream_t>(stream)),
+                            reading(quant, flags), static_cast<hipStream_t>(stream)),
           "matmul launch");
   return SH_OK;
 }
@@ -1420,7 +1431,8 @@ static int ffn_dev_check(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff,
       return fail(SH_ERR_UNSUPPORTED_SHAPE, "ffn tensor %d: %llux%llu of type %u", i,
                   (unsigned long long)dims[i][0], (unsigned long long)dims[i][1], t[i].quant);
     if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
-        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32) && (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
+        ((t[i].quant == SH_QUANT_Q8_0 || t[i].quant == SH_QUANT_F32 || t[i].quant == SH_QUANT_IQ4_XS) &&
+         (reinterpret_cast<uintptr_t>(t[i].data) & 3u)))
       return fail(SH_ERR_INVALID_ARGUMENT, "misaligned tensor %d", i);
   }
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(out) & 15u) || n_embd % 4 != 0 ||
@@ -1432,9 +1444,9 @@ static int ffn_dev_check(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff,
 static hipError_t ffn_dev_launch(const sh_expert_dev* t, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
                                  const float* x, const float* post_norm, double eps, float* out, void* workspace,
                                  void* stream) {
-  auto q6 = [](uint32_t f) { return (f & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
-  return sh::launch_ffn(t[0].quant, t[1].quant, t[2].quant, t[0].data, t[1].data, t[2].data, q6(t[0].flags),
-                        q6(t[1].flags), q6(t[2].flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), x, post_norm, eps,
+  auto q6 = [](const sh_expert_dev& d) { return reading(d.quant, d.flags); };
+  return sh::launch_ffn(t[0].quant, t[1].quant, t[2].quant, t[0].data, t[1].data, t[2].data, q6(t[0]),
+                        q6(t[1]), q6(t[2]), int64_t(n_embd), int64_t(n_ff), int(n_tok), x, post_norm, eps,
                         out, workspace, static_cast<hipStream_t>(stream));
 }
 
@@ -1528,9 +1540,9 @@ int sh_ffn(sh_context* c, const sh_quant_tensor* gate, const sh_quant_tensor* up
   HIP_TRY(hipMemcpyAsync(c->d_in.p, hi, x_al + nb, hipMemcpyHostToDevice, c->stream), "x upload");
   float* dx = static_cast<float*>(c->d_in.p);
   const float* dn = reinterpret_cast<const float*>(static_cast<uint8_t*>(c->d_in.p) + x_al);
-  auto q6 = [](uint32_t f) { return (f & SH_FLAG_Q6K_SIGNED_SCALES) ? 1 : 0; };
-  HIP_TRY(sh::launch_ffn(gate->quant, up->quant, down->quant, dev[0], dev[1], dev[2], q6(gate->flags), q6(up->flags),
-                         q6(down->flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), dx, dn, eps, dx, c->d_blk.p,
+  HIP_TRY(sh::launch_ffn(gate->quant, up->quant, down->quant, dev[0], dev[1], dev[2],
+                         reading(gate->quant, gate->flags), reading(up->quant, up->flags),
+                         reading(down->quant, down->flags), int64_t(n_embd), int64_t(n_ff), int(n_tok), dx, dn, eps, dx, c->d_blk.p,
                          c->stream),
           "ffn launch");
   HIP_TRY(hipMemcpyAsync(c->h_out.p, dx, xb, hipMemcpyDeviceToHost, c->stream), "x readback");

@@ -1,6 +1,6 @@
 // Per-unit "axpy" of one packed row into column sums, for the expert
 // (in-major) matvec and the MoE FFN: a thread owns one 64-column unit (one
-// Q4_K group, one Q6_K quarter, or a pair of Q8_0 blocks -- the units of the
+// Q4_K / Q5_K group, one Q6_K quarter, or a pair of Q8_0 blocks -- the units of the
 // matvec kernels) and adds x[i] * W[i][unit columns] for a row i into 64
 // f32 accumulators per token. Block scales are folded into one coefficient
 // per sub-block and token (x[i] * d * sc); the constant parts of the codes
@@ -70,6 +70,64 @@ struct AxQ4K {
     }
   }
   // column e of the unit belongs to sub-block e / 32
+  __device__ static __forceinline__ int off_index(int e) { return e >> 5; }
+};
+
+// Q5_K: unit u is group g = u & 3 of super-block u >> 2 (176 bytes), as
+// AxQ4K, with each code's fifth bit from the super-block's 32 qh bytes
+// (q5k_codes; codes 0..31, dequant.rs:272-302).
+struct AxQ5K {
+  static constexpr int kOff = 2;
+  struct Raw {
+    u32x4 h, h0, h1, a, b;  // header, qh, the group's 32 code bytes
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int u) {
+    const uint8_t* sb = row + (u >> 2) * 176;
+    const int g = u & 3;
+    return {ld16u(sb), ld16u(sb + 16), ld16u(sb + 32), ld16u(sb + 48 + 32 * g), ld16u(sb + 64 + 32 * g)};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
+                                              float (*acc)[64], float (*off)[kOff], int q6s) {
+    apply<NT>(load(row, u), u, xi, acc, off, q6s);
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int u, const float* xi, float (*acc)[64],
+                                               float (*off)[kOff], int) {
+    const int g = u & 3;
+    uint32_t scp, mp;
+    k4_pair(r.h, g, scp, mp);
+    const float d = h2f(r.h.x), dm = h2f(r.h.x >> 16);
+    const float dsc0 = d * ubyte<0>(scp), dsc1 = d * ubyte<1>(scp);
+    const float dmm0 = dm * ubyte<0>(mp), dmm1 = dm * ubyte<1>(mp);
+    const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    float wv[64];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t lo, hi;
+      q5k_codes(q[k], qh[k], uint32_t(g), lo, hi);
+      wv[4 * k + 0] = ubyte<0>(lo);
+      wv[4 * k + 1] = ubyte<1>(lo);
+      wv[4 * k + 2] = ubyte<2>(lo);
+      wv[4 * k + 3] = ubyte<3>(lo);
+      wv[32 + 4 * k + 0] = ubyte<0>(hi);
+      wv[32 + 4 * k + 1] = ubyte<1>(hi);
+      wv[32 + 4 * k + 2] = ubyte<2>(hi);
+      wv[32 + 4 * k + 3] = ubyte<3>(hi);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (xi[t] == 0.f) continue;  // ops.rs:182-184
+      const float c0 = xi[t] * dsc0, c1 = xi[t] * dsc1;
+      off[t][0] += xi[t] * dmm0;
+      off[t][1] += xi[t] * dmm1;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) acc[t][e] = __builtin_fmaf(c0, wv[e], acc[t][e]);
+#pragma unroll
+      for (int e = 32; e < 64; ++e) acc[t][e] = __builtin_fmaf(c1, wv[e], acc[t][e]);
+    }
+  }
   __device__ static __forceinline__ int off_index(int e) { return e >> 5; }
 };
 
@@ -259,6 +317,54 @@ struct HxQ4K {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint32_t v = q[k] & mask;
+      const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][4 * k + 0] = __builtin_fmaf(c[t], w0, acc[t][4 * k + 0]);
+        acc[t][4 * k + 1] = __builtin_fmaf(c[t], w1, acc[t][4 * k + 1]);
+        acc[t][4 * k + 2] = __builtin_fmaf(c[t], w2, acc[t][4 * k + 2]);
+        acc[t][4 * k + 3] = __builtin_fmaf(c[t], w3, acc[t][4 * k + 3]);
+      }
+    }
+  }
+  __device__ static __forceinline__ int off_index(int) { return 0; }
+};
+
+// Q5_K: half unit hu is sub-block 2g + (hu & 1) of group g = (hu >> 1) & 3
+// of super-block hu >> 3, as HxQ4K; its 32 codes take the nibble (hu & 1)
+// of the group's code bytes and bit 2g + (hu & 1) of qh[l] as 16.
+struct HxQ5K {
+  static constexpr int kOff = 1;
+  struct Raw {
+    u32x4 h, h0, h1, a, b;  // header, qh, the group's 32 code bytes
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int hu) {
+    const int u = hu >> 1;
+    const uint8_t* sb = row + (u >> 2) * 176;
+    const int g = u & 3;
+    return {ld16u(sb), ld16u(sb + 16), ld16u(sb + 32), ld16u(sb + 48 + 32 * g), ld16u(sb + 64 + 32 * g)};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int hu, const float* xi, float (*acc)[32],
+                                               float (*off)[kOff], int) {
+    const int u = hu >> 1, g = u & 3;
+    const uint32_t hi = uint32_t(hu & 1);
+    uint32_t scp, mp;
+    k4_pair(r.h, g, scp, mp);
+    const float d = h2f(r.h.x), dm = h2f(r.h.x >> 16);
+    const float dsc = d * float((scp >> (8 * hi)) & 0xFFu), dmm = dm * float((mp >> (8 * hi)) & 0xFFu);
+    const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    const uint32_t bit = 2u * uint32_t(g) + hi;
+    float c[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      c[t] = xi[t] == 0.f ? 0.f : xi[t] * dsc;  // ops.rs:182-184
+      off[t][0] += xi[t] == 0.f ? 0.f : xi[t] * dmm;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t v = ((q[k] >> (4 * hi)) & 0x0F0F0F0Fu) | (((qh[k] >> bit) & 0x01010101u) << 4);
       const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {

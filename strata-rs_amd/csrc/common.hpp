@@ -6,6 +6,7 @@
 //   Q4_K 256 elements / 144 B: [d: f16][dmin: f16][scales: 12 B][qs: 128 B]
 //   Q5_K 256 elements / 176 B: [d: f16][dmin: f16][scales: 12 B][qh: 32 B][qs: 128 B]
 //   Q6_K 256 elements / 210 B: [ql: 128 B][qh: 64 B][sc: 16 B][d: f16]
+//   IQ4_XS 256 elements / 136 B: [d: f16][scales_h: u16][scales_l: 4 B][qs: 128 B]
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,6 +21,7 @@ enum QuantId : uint32_t {
   kQ4_K = 12,
   kQ5_K = 13,
   kQ6_K = 14,
+  kIQ4_XS = 23,
   kBF16 = 30,
 };
 
@@ -38,6 +40,7 @@ inline Geometry geometry(uint32_t q) {
     case kQ4_K: return {256, 144};
     case kQ5_K: return {256, 176};
     case kQ6_K: return {256, 210};
+    case kIQ4_XS: return {256, 136};
     default: return {0, 0};
   }
 }
@@ -49,13 +52,18 @@ inline int64_t byte_size(uint32_t q, int64_t n) {
   return (n + g.block - 1) / g.block * g.bytes;
 }
 
-// The quantized matvec kernels accept these.
-inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ6_K; }
+// The quantized types every kernel family takes (matvec, expert, MoE, matmul).
+inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ5_K || q == kQ6_K; }
 // Plain-float element types: matvec (f64 sums) and dequant only.
 inline bool plain_quant(uint32_t q) { return q == kF32 || q == kF16 || q == kBF16; }
-// Types the matvec (and dequant) kernels take beyond device_quant: Q5_K has
-// a matvec of its own but no expert, MoE or matmul kernel.
-inline bool gemv_quant(uint32_t q) { return device_quant(q) || q == kQ5_K; }
+// Types the matvec (and dequant) kernels take beyond device_quant: IQ4_XS
+// has a matvec of its own but no expert, MoE or matmul kernel.
+inline bool gemv_quant(uint32_t q) { return device_quant(q) || q == kIQ4_XS; }
+
+// The IQ4_NL / IQ4_XS code book: 4-bit index -> int8 value (a format
+// table: ggml's kvalues_iq4nl, crates/strata-gguf/src/tables.rs:2052-2054),
+// packed little-endian four to a word.
+constexpr uint32_t kIq4Tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
 
 constexpr int kWave = 64;
 
@@ -187,6 +195,26 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 template <int K>
 __device__ __forceinline__ float ubyte(uint32_t w) {
   return static_cast<float>((w >> (8 * K)) & 0xFFu);
+}
+
+// Q5_K codes of group g (dequant.rs:285-297): four code bytes q and the
+// four qh bytes of the same element positions l (l = element % 32); the low
+// nibbles (sub-block 2g) take bit 2g of qh[l] as 16, the high nibbles
+// (sub-block 2g + 1) bit 2g + 1, so codes run 0..31.
+__device__ __forceinline__ void q5k_codes(uint32_t q, uint32_t qh, uint32_t g, uint32_t& lo, uint32_t& hi) {
+  const uint32_t t = qh >> (2u * g);  // bit 2g of byte j at bit 8j, bit 2g+1 at 8j+1
+  lo = (q & 0x0F0F0F0Fu) | ((t << 4) & 0x10101010u);
+  hi = ((q >> 4) & 0x0F0F0F0Fu) | ((t << 3) & 0x10101010u);
+}
+
+// Q4_K / Q5_K (scale, min) of sub-blocks 2g and 2g+1 in the two low bytes of
+// scp / mp, from the 12 packed bytes in words h.y, h.z, h.w of the header
+// (get_scale_min_k4, dequant.rs:237-245).
+__device__ __forceinline__ void k4_pair(u32x4 h, int g, uint32_t& scp, uint32_t& mp) {
+  const uint32_t sh = (g & 1) << 4;
+  const uint32_t t1 = h.y >> sh, t2 = h.z >> sh, t3 = h.w >> sh;
+  scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
+  mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
 }
 
 // Sum over the 64 lanes of a wave; every lane gets the total.

@@ -1,7 +1,8 @@
 // Bit-exact device dequantization: packed GGUF rows -> f32.
 //
-// Follows crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :208-234 (Q6_K),
-// :237-270 (Q4_K) and :272-302 (Q5_K) element for element, with the same rounding: every
+// Follows crates/strata-gguf/src/dequant.rs:123-128 (Q8_0), :189-206
+// (IQ4_XS), :208-234 (Q6_K), :237-270 (Q4_K) and :272-302 (Q5_K) element for
+// element, with the same rounding: every
 // product and difference is a separate f32 operation (contraction is off for
 // this file's arithmetic), f16 scales widen exactly.
 //
@@ -84,9 +85,30 @@ __device__ __forceinline__ float dq_q6_k(const uint8_t* blk, int j, int signed_s
   return a * static_cast<float>(q);
 }
 
+// IQ4_XS element j (dequant.rs:189-206): sub-block ib = j / 32 has the 6-bit
+// scale ls from scales_l (nibble ib % 2 of byte ib / 2) and scales_h (bits
+// 2 ib, 2 ib + 1), dl = d * (ls - 32) (the difference exact, one rounding
+// for the product), and element 32 ib + i takes code-book entry
+// kvalues_iq4nl[q & 15] of byte i % 16 of its 16 qs bytes (low nibble for
+// i < 16, high for i >= 16), then one more rounding for dl * value. The
+// reference reads the same 16 qs bytes, qs[0..16], for every sub-block (its
+// qs slice is never advanced); `ggml` selects ggml's layout, qs[16 ib ..].
+__device__ __forceinline__ float dq_iq4_xs(const uint8_t* blk, int j, int ggml) {
+#pragma clang fp contract(off)
+  const float d = h2f(rd16(blk));
+  const uint32_t sh = rd16(blk + 2);
+  const int ib = j >> 5, i = j & 31;
+  const uint32_t ls = ((uint32_t(blk[4 + (ib >> 1)]) >> (4 * (ib & 1))) & 0x0Fu) | (((sh >> (2 * ib)) & 3u) << 4);
+  const float dl = d * (static_cast<float>(ls) - 32.0f);
+  const uint32_t byte = blk[8 + (ggml ? 16 * ib : 0) + (i & 15)];
+  const uint32_t n = i < 16 ? (byte & 0x0Fu) : (byte >> 4);
+  const int v = int8_t((kIq4Tab[n >> 2] >> (8 * (n & 3))) & 0xFFu);
+  return dl * static_cast<float>(v);
+}
+
 __global__ void dequant_kernel(uint32_t quant, const uint8_t* __restrict__ w, int64_t rows,
                                int64_t cols, int64_t row_bytes, float* __restrict__ out,
-                               int q6_signed) {
+                               int q6_signed) {  // the type's alternate reading (Q6_K i8 scales, IQ4_XS ggml qs)
   int64_t total = rows * cols;
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * blockDim.x) {
@@ -98,6 +120,7 @@ __global__ void dequant_kernel(uint32_t quant, const uint8_t* __restrict__ w, in
       case kQ4_K: v = dq_q4_k(row + (c >> 8) * 144, int(c & 255)); break;
       case kQ5_K: v = dq_q5_k(row + (c >> 8) * 176, int(c & 255)); break;
       case kQ6_K: v = dq_q6_k(row + (c >> 8) * 210, int(c & 255), q6_signed); break;
+      case kIQ4_XS: v = dq_iq4_xs(row + (c >> 8) * 136, int(c & 255), q6_signed); break;
       case kF16: v = h2f(rd16(row + 2 * c)); break;
       case kBF16: v = __builtin_bit_cast(float, rd16(row + 2 * c) << 16); break;
       default: v = __builtin_bit_cast(float, uint32_t(row[4 * c]) | (uint32_t(row[4 * c + 1]) << 8) |

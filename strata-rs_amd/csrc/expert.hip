@@ -113,11 +113,15 @@ hipError_t launch_expert_gemv(uint32_t quant, const void* wv, int64_t rows, int6
       hipLaunchKernelGGL(expert_partial_kernel<AxQ4K>, dim3(n_chunks), dim3(kExpertThreads), lds,
                          stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
       break;
+    case kQ5_K:
+      hipLaunchKernelGGL(expert_partial_kernel<AxQ5K>, dim3(n_chunks), dim3(kExpertThreads), lds,
+                         stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
+      break;
     case kQ8_0:
       hipLaunchKernelGGL(expert_partial_kernel<AxQ8>, dim3(n_chunks), dim3(kExpertThreads), lds,
                          stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
       break;
-    default:
+    default:  // kQ6_K
       hipLaunchKernelGGL(expert_partial_kernel<AxQ6K>, dim3(n_chunks), dim3(kExpertThreads), lds,
                          stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
   }

@@ -119,26 +119,9 @@ struct FmtQ4K {
 };
 
 // ------------------------------------------------------------------ Q5_K --
-// Unit u of a row: super-block u/4, group g = u%4, as FmtQ4K; each code also
-// takes a fifth bit from qh[l] (l = element % 32): bit 2g for the low-nibble
-// sub-block 2g, bit 2g+1 for the high-nibble sub-block 2g+1 (dequant.rs:
-// 285-297), so codes run 0..31. Every lane of a super-block reads its 16
-// header and 32 qh bytes.
-__device__ __forceinline__ void q5k_codes(uint32_t q, uint32_t qh, uint32_t g, uint32_t& lo, uint32_t& hi) {
-  const uint32_t t = qh >> (2u * g);  // bit 2g of byte j at bit 8j, bit 2g+1 at 8j+1
-  lo = (q & 0x0F0F0F0Fu) | ((t << 4) & 0x10101010u);
-  hi = ((q >> 4) & 0x0F0F0F0Fu) | ((t << 3) & 0x10101010u);
-}
-
-// (scale, min) of sub-blocks 2g and 2g+1 in the two low bytes of scp / mp,
-// from the 12 packed bytes in words h.y, h.z, h.w (dequant.rs:237-245).
-__device__ __forceinline__ void k4_pair(u32x4 h, int g, uint32_t& scp, uint32_t& mp) {
-  const uint32_t sh = (g & 1) << 4;
-  const uint32_t t1 = h.y >> sh, t2 = h.z >> sh, t3 = h.w >> sh;
-  scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
-  mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
-}
-
+// Unit u of a row: super-block u/4, group g = u%4, as FmtQ4K, with the fifth
+// code bit of q5k_codes. Every lane of a super-block reads its 16 header and
+// 32 qh bytes.
 struct FmtQ5K {
   static constexpr int kR = 2;
   static constexpr int kRing = 4;
@@ -833,6 +816,69 @@ struct LimbQ8 {
   }
 };
 
+// IQ4_XS with integer dots: unit u = (super-block u/4, group g = u%4), the
+// two 32-element sub-blocks 2g and 2g + 1 (elements 64g..64g+63). Each
+// sub-block's codes are code-book values kvalues_iq4nl[nibble] in
+// [-127, 113] (signed, so the dots are LimbQ8's: the top limb signed, the
+// low limbs against codes biased by 128), its scale dl = d * (ls - 32) from
+// the 6-bit ls. GGML: ggml's layout (sub-block ib reads qs[16 ib ..]); the
+// default follows the reference, whose every sub-block reads qs[0..16]
+// (dequant.rs:189-206).
+__device__ __forceinline__ uint32_t iq4_lut(uint32_t idx) {  // four nibble indices -> four int8 codes
+  const uint32_t i7 = idx & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIq4Tab[1], kIq4Tab[0], i7);
+  const uint32_t hi = __builtin_amdgcn_perm(kIq4Tab[3], kIq4Tab[2], i7);
+  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
+
+template <bool GGML>
+struct LimbIQ4XS {
+  static constexpr uint32_t kQuant = kIQ4_XS;
+  struct Load {
+    uint32_t h0, h1;  // d | scales_h, scales_l
+    u32x4 a, b;       // the qs bytes of sub-blocks 2g and 2g + 1
+  };
+  static constexpr int kWinBytes = 16 * 136;
+  struct Off {
+    int h, q;
+  };
+  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 136, GGML ? 8 + 32 * (u & 3) : 8}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    L.h0 = ld4(row + o.h);
+    L.h1 = ld4(row + o.h + 4);
+    L.a = ld16u(row + o.h + o.q);
+    L.b = ld16u(row + o.h + o.q + (GGML ? 16 : 0));
+  }
+  __device__ static __forceinline__ float block(const u32x4 q, const u32x4* xa, const u32x4* xb, const u32x4* xc,
+                                                int j0, u32x4 info) {
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    int sa = 0;
+    uint32_t sb = 0, sc = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {  // elements 4k..4k+3: low nibbles of bytes 4k.. (k < 4), high nibbles after
+      const uint32_t idx = k < 4 ? (qw[k] & 0x0F0F0F0Fu) : ((qw[k - 4] >> 4) & 0x0F0F0F0Fu);
+      const uint32_t v = iq4_lut(idx);
+      const uint32_t vb = v ^ 0x80808080u;  // v + 128
+      sa = __builtin_amdgcn_sdot4(int(v), int(limb_word(xa, j0 + k)), sa, false);
+      sb = __builtin_amdgcn_udot4(vb, limb_word(xb, j0 + k), sb, false);
+      sc = __builtin_amdgcn_udot4(vb, limb_word(xc, j0 + k), sc, false);
+    }
+    const int bc = int(sb * 256u + sc) - 128 * int(info.w);
+    return __builtin_fmaf(float(sa), 65536.f, float(bc)) * fw(info.z);
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
+    const uint32_t g = uint32_t(lane) & 3u;
+    const float d = h2f(L.h0);
+    const uint32_t shb = L.h0 >> 16;                     // scales_h
+    const uint32_t slb = (L.h1 >> (8 * g)) & 0xFFu;      // scales_l[g]: ls of sub-blocks 2g (low) and 2g + 1
+    const uint32_t ls0 = (slb & 0x0Fu) | (((shb >> (4 * g)) & 3u) << 4);
+    const uint32_t ls1 = (slb >> 4) | (((shb >> (4 * g + 2)) & 3u) << 4);
+    const float dl0 = d * (float(ls0) - 32.f), dl1 = d * (float(ls1) - 32.f);
+    return dl0 * block(L.a, x.a, x.b, x.c, 0, x.i0) + dl1 * block(L.b, x.a, x.b, x.c, 8, x.i1);
+  }
+};
+
 // Q6_K with integer dots: unit u = (super-block u/4, quarter j = u%4) as in
 // FmtQ6K; the 6-bit codes 0..63 go straight into the dots and the -32
 // offset is taken off with the per-16 sums of x.
@@ -911,7 +957,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
                                                         const float* __restrict__ xu,
                                                         const float* xres) {  // xres may be y (in place)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
-  constexpr bool kLow = F::kQuant == kQ8_0;
+  constexpr bool kLow = F::kQuant == kQ8_0 || F::kQuant == kIQ4_XS;  // signed codes: the low-limb sums
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
   const int units = cols >> 6;
@@ -1346,7 +1392,7 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   }
   // Q8_0 reads 68-byte block pairs with dword loads: rows must start on a
   // dword boundary (row_bytes is 68 * cols/64, so only the base matters).
-  if (quant == kQ8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
+  if ((quant == kQ8_0 || quant == kIQ4_XS) && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(w) & 1u) || (reinterpret_cast<uintptr_t>(x) & 15u))
     return hipErrorInvalidValue;
   if (batch >= 2 && gemv_mfma_ok(quant, rows, cols, batch))
@@ -1376,6 +1422,15 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
       case kQ5_K:
         e = nb == 1 ? launch_limb<LimbQ5K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
                     : launch_nb<FmtQ5K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
+        break;
+      case kIQ4_XS:  // batch-1 launches, one vector each
+        e = hipSuccess;
+        for (int b = 0; b < nb && e == hipSuccess; ++b)
+          e = q6_signed ? launch_limb<LimbIQ4XS<true>, 1, 4>(w, int(rows), int(cols), row_bytes, xb + int64_t(b) * cols,
+                                                             yb + int64_t(b) * rows, stream, 512, wpc)
+                        : launch_limb<LimbIQ4XS<false>, 1, 4>(w, int(rows), int(cols), row_bytes,
+                                                              xb + int64_t(b) * cols, yb + int64_t(b) * rows, stream,
+                                                              512, wpc);
         break;
       default:
         e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,

@@ -1,5 +1,5 @@
 // Batched prefill matmul on MFMA: Y[t][r] = sum_c W[r][c] * X[t][c] for m
-// tokens, W packed Q4_K / Q8_0 / Q6_K [rows][cols], X and Y f32 row-major.
+// tokens, W packed Q4_K / Q5_K / Q8_0 / Q6_K [rows][cols], X and Y f32 row-major.
 //
 // The reference has no matmul: prefill runs one forward per token
 // (crates/strata-core/src/generate.rs:116-117), so the op is defined as m
@@ -129,6 +129,58 @@ struct StQ4K {
       run0[k] = q[k] & 0x0F0F0F0Fu;
       run1[k] = (q[k] >> 4) & 0x0F0F0F0Fu;
     }
+    o0 = 16 * hb;
+    o1 = 32 + 16 * hb;
+  }
+};
+
+// Q5_K: chunk c and piece hb as StQ4K (176-byte super-blocks, codes at byte
+// 48); each code takes its fifth bit from the qh bytes of the same element
+// positions [16hb, +16): bit 2g for the low nibbles, 2g + 1 for the high
+// (q5k_codes; dequant.rs:272-302), so codes run 0..31.
+struct StQ5K {
+  static constexpr int kPieces = 2;
+  static constexpr bool kQ8 = true;
+  static constexpr bool kMin = true;  // value d * q - m
+  struct Raw {
+    u32x4 h, q, qh;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int c, int hb) {
+    const uint8_t* sb = row + (c >> 2) * 176;
+    return {ld16(sb), ld16(sb + 48 + 32 * (c & 3) + 16 * hb), ld16(sb + 16 + 16 * hb)};
+  }
+  __device__ static __forceinline__ void codes(const Raw& r, int c, uint32_t* lo, uint32_t* hi) {
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q5k_codes(q[k], qh[k], uint32_t(c & 3), lo[k], hi[k]);
+  }
+  __device__ static __forceinline__ void emit_bf16(const Raw& r, int c, int hb, uint32_t* run0,
+                                                   uint32_t* run1, int& o0, int& o1, int) {
+    float d0, m0, d1, m1;
+    StQ4K::scales(r.h, c & 3, d0, m0, d1, m1);
+    uint32_t lo[4], hi[4];
+    codes(r, c, lo, hi);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      run0[2 * k] = pack_bf16(__builtin_fmaf(d0, ubyte<0>(lo[k]), -m0), __builtin_fmaf(d0, ubyte<1>(lo[k]), -m0));
+      run0[2 * k + 1] =
+          pack_bf16(__builtin_fmaf(d0, ubyte<2>(lo[k]), -m0), __builtin_fmaf(d0, ubyte<3>(lo[k]), -m0));
+      run1[2 * k] = pack_bf16(__builtin_fmaf(d1, ubyte<0>(hi[k]), -m1), __builtin_fmaf(d1, ubyte<1>(hi[k]), -m1));
+      run1[2 * k + 1] =
+          pack_bf16(__builtin_fmaf(d1, ubyte<2>(hi[k]), -m1), __builtin_fmaf(d1, ubyte<3>(hi[k]), -m1));
+    }
+    o0 = 16 * hb;
+    o1 = 32 + 16 * hb;
+  }
+  // int8 codes 0..31, blocks as StQ4K::emit_q8
+  __device__ static __forceinline__ void emit_q8(const Raw& r, int c, int hb, uint32_t* run0,
+                                                 uint32_t* run1, int& o0, int& o1, int& jb0, int& jb1,
+                                                 float* dj, float* mj) {
+    StQ4K::scales(r.h, c & 3, dj[0], mj[0], dj[1], mj[1]);
+    jb0 = 0;
+    jb1 = 1;
+    codes(r, c, run0, run1);
     o0 = 16 * hb;
     o1 = 32 + 16 * hb;
   }
@@ -919,6 +971,7 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
   if (e != hipSuccess) return e;
   switch (quant) {
     case kQ4_K: launch_mm<StQ4K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
+    case kQ5_K: launch_mm<StQ5K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
     case kQ8_0: launch_mm<StQ8>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
     default: launch_mm<StQ6K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s);
   }

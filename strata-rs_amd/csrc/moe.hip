@@ -813,11 +813,13 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
   }
   switch (qg) {
     case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+    case kQ5_K: launch_gateup<HxQ5K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
     case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
     default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
   }
   switch (qd) {
     case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
+    case kQ5_K: launch_down<HxQ5K>(p, down, ws, q6d, s); break;
     case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
     default: launch_down<HxQ6K>(p, down, ws, q6d, s);
   }

@@ -48,6 +48,7 @@ SH_ERR_NOT_FOUND = -11
 
 FLAG_Q6K_SIGNED_SCALES = 1
 FLAG_EXPERT_OUT_MAJOR = 2
+FLAG_IQ4XS_GGML = 4
 MATMUL_BF16 = 0
 MATMUL_Q8 = 1
 
@@ -77,6 +78,7 @@ class QuantType(enum.IntEnum):
     Q4_K = 12
     Q5_K = 13
     Q6_K = 14
+    IQ4_XS = 23
     BF16 = 30
 
 

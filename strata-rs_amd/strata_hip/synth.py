@@ -18,7 +18,9 @@ and block builders for the three GGUF layouts the path reads
 * Q6_K: 210-byte super-blocks ``[ql: 128][qh: 64][sc: 16][d: f16]`` with
   ql/qh uniform bytes, sc uniform int8 in [-64, 63] and d = f16(|N|*0.001);
 * Q5_K: 176-byte super-blocks ``[d: f16][dmin: f16][scales: 12][qh: 32]
-  [ql: 128]`` with d, dmin = f16(|N|*0.01) and the 172 packed bytes uniform.
+  [ql: 128]`` with d, dmin = f16(|N|*0.01) and the 172 packed bytes uniform;
+* IQ4_XS: 136-byte super-blocks ``[d: f16][scales_h: u16][scales_l: 4]
+  [qs: 128]`` with d = f16(|N|*0.01) and the 134 packed bytes uniform.
 
 f32 -> f16 is numpy's round-to-nearest-even. Generation is chunked so a
 510 MB tensor needs only a few hundred MB of temporaries.
@@ -32,8 +34,8 @@ _M1 = np.uint64(0xBF58476D1CE4E5B9)
 _M2 = np.uint64(0x94D049BB133111EB)
 _CHUNK = 1 << 22
 
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 8, 12, 13, 14, 23
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136)}
 
 
 def _mix(z: np.ndarray) -> np.ndarray:
@@ -130,7 +132,17 @@ def q5_k_blocks(seed: int, n_blocks: int) -> np.ndarray:
     return b.reshape(-1)
 
 
+def iq4_xs_blocks(seed: int, n_blocks: int) -> np.ndarray:
+    """``n_blocks`` IQ4_XS super-blocks as a flat uint8 array."""
+    b = np.empty((n_blocks, 136), dtype=np.uint8)
+    b[:, 0:2] = _f16_bytes(np.abs(normal_f32(sub_seed(seed, 1), n_blocks)) * np.float32(0.01))
+    b[:, 2:136] = random_bytes(sub_seed(seed, 3), n_blocks * 134).reshape(n_blocks, 134)
+    return b.reshape(-1)
+
+
 def blocks(quant: int, seed: int, n_blocks: int) -> np.ndarray:
+    if quant == IQ4_XS:
+        return iq4_xs_blocks(seed, n_blocks)
     if quant == Q5_K:
         return q5_k_blocks(seed, n_blocks)
     if quant == Q8_0:

@@ -38,6 +38,7 @@ def test_abi_version_and_geometry():
     assert H.quant_geometry(H.QuantType.Q4_K) == (256, 144)
     assert H.quant_geometry(H.QuantType.Q5_K) == (256, 176)
     assert H.quant_geometry(H.QuantType.Q6_K) == (256, 210)
+    assert H.quant_geometry(H.QuantType.IQ4_XS) == (256, 136)
     assert H.byte_size(H.QuantType.Q4_K, 12288) == 6912
     with pytest.raises(H.UnsupportedQuantError):
         H.quant_geometry(2)  # Q4_0: not on this path

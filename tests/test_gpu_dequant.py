@@ -3,6 +3,7 @@
 Through the C ABI: sh_dequantize_row (host slices) and sh_dequant_dev
 (device pointers). Covers every binary16 scale pattern, the known-answer
 blocks, random blocks at the configs' row widths, both Q6_K scale readings,
+both IQ4_XS code-byte readings,
 and the Truncated error of dequant.rs:50-55.
 """
 import numpy as np
@@ -44,7 +45,7 @@ def test_every_f16_scale_pattern(backend, oracle):
 
 
 @pytest.mark.parametrize("quant,cols", [(8, 4096), (12, 4096), (12, 12288), (14, 4096), (12, 768),
-                                        (14, 2048), (13, 4096), (13, 768)])
+                                        (14, 2048), (13, 4096), (13, 768), (23, 4096), (23, 768)])
 def test_random_rows_bit_exact(backend, oracle, quant, cols):
     say("dequant random rows", quant, cols)
     rows = 16
@@ -66,6 +67,33 @@ def test_q6_k_signed_scales_bit_exact(backend, oracle):
     got_u8 = np.empty_like(got)
     backend.dequantize_row(14, w, got_u8)
     assert not np.array_equal(got, got_u8)
+
+
+def test_iq4_xs_ggml_reading_bit_exact(backend, oracle):
+    say("dequant IQ4_XS ggml reading")
+    w = S.matrix(23, 6, 8, 4096)
+    got = np.empty(8 * 4096, np.float32)
+    backend.dequantize_row(23, w, got, flags=H.FLAG_IQ4XS_GGML)
+    assert same_bits(got, oracle.dequantize_row(23, w, 8 * 4096, oracle.IQ4XS_GGML))
+    got_ref = np.empty_like(got)
+    backend.dequantize_row(23, w, got_ref)
+    assert same_bits(got_ref, oracle.dequantize_row(23, w, 8 * 4096))
+    assert not np.array_equal(got, got_ref)
+
+
+def test_iq4_xs_known_answer_blocks(backend):
+    say("dequant IQ4_XS KAT blocks")
+    from test_oracle_dequant import IQ4NL, iq4xs_block, iq4xs_kat_block
+    out = np.empty(256, np.float32)
+    backend.dequantize_row(23, iq4xs_kat_block(), out)
+    assert (out[0], out[16], out[32], out[48], out[224], out[240]) == (0.5, -63.5, 15.5, -1968.5, -16.0, 2032.0)
+    backend.dequantize_row(23, iq4xs_kat_block(), out, flags=H.FLAG_IQ4XS_GGML)
+    assert (out[32], out[224], out[240]) == (15.5 * -127, -1808.0, 1040.0)
+    # the code book: d = 1, every ls = 33
+    qs = np.zeros(128, np.uint8)
+    qs[:16] = [j | ((15 - j) << 4) for j in range(16)]
+    backend.dequantize_row(23, iq4xs_block(1.0, 0xAAAA, [0x11] * 4, qs), out)
+    assert out[:16].tolist() == IQ4NL and out[16:32].tolist() == IQ4NL[::-1]
 
 
 def test_known_answer_blocks(backend, oracle):

@@ -22,7 +22,7 @@ def say(*a):
 
 @pytest.mark.parametrize("quant,n_expert,rows,cols", [
     (12, 128, 2048, 768), (14, 128, 768, 2048), (8, 4, 300, 512), (12, 3, 5, 256), (14, 2, 1, 256),
-    (12, 2, 4096, 12288),
+    (12, 2, 4096, 12288), (13, 128, 2048, 768), (13, 3, 5, 256), (13, 2, 1, 256), (13, 4, 300, 1024),
 ])
 def test_expert_gemv(backend, oracle, quant, n_expert, rows, cols):
     say("expert_gemv", quant, n_expert, rows, cols)

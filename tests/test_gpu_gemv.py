@@ -4,7 +4,8 @@ Tolerance (conftest.check_parity): max|y - ref| / max|ref| <= 1e-3 (the
 path's stated bound under f32 accumulation), and per element
 |y_i - ref_i| / max(|ref_i|, 1e-3 rms(ref)) <= 2e-3 (f32 arithmetic itself
 scores about 6e-4 there at 12288 inputs). Covers the reference's own gemv unit test, ragged row counts,
-one- and multi-window rows, batches 1..8 (Q5_K too), the Q6_K scale readings, the
+one- and multi-window rows, batches 1..8 (Q5_K too), the Q6_K scale readings, IQ4_XS in
+both code-byte readings, the
 configs' full shapes (the lm_head on a row sample) and the device-pointer
 entry point.
 """
@@ -165,16 +166,39 @@ def test_gemv_shape_errors(backend):
         backend.gemv(H.QuantTensor("q4_0", 2, 4, 32, q4_0), np.zeros(32, np.float32), np.zeros(4, np.float32))
 
 
-def test_q5_k_is_matvec_only(backend):
-    """Q5_K rows run on the matvec (and dequant) kernels only: the expert,
-    MoE and matmul entry points report the type as unsupported."""
-    say("Q5_K outside the matvec")
-    w = S.matrix(13, 3, 2 * 256, 256)
+def test_iq4_xs_is_matvec_only(backend):
+    """IQ4_XS rows run on the matvec (and dequant) kernels only: the expert
+    and matmul entry points report the type as unsupported."""
+    say("IQ4_XS outside the matvec")
+    w = S.matrix(23, 3, 2 * 256, 256)
     with pytest.raises(H.UnsupportedQuantError):
-        backend.expert_gemv(H.ExpertView("q5e", 13, 2, 256, 256, w), 1, np.zeros(256, np.float32),
+        backend.expert_gemv(H.ExpertView("iq4e", 23, 2, 256, 256, w), 1, np.zeros(256, np.float32),
                             np.zeros(256, np.float32))
     with pytest.raises(H.UnsupportedQuantError):
-        backend.matmul(H.QuantTensor("q5m", 13, 512, 256, w), np.zeros((4, 256), np.float32))
+        backend.matmul(H.QuantTensor("iq4m", 23, 512, 256, w), np.zeros((4, 256), np.float32))
+
+
+@pytest.mark.parametrize("ggml", [False, True])
+@pytest.mark.parametrize("rows,cols,batch", [(37, 256, 1), (129, 4096, 1), (9, 12288, 1), (4096, 4096, 1),
+                                             (33, 8192 + 256, 1), (96, 4096, 3), (64, 12288, 8)])
+def test_gemv_iq4_xs(backend, oracle, ggml, rows, cols, batch):
+    """IQ4_XS in both code-byte readings (strata-gguf's first 16 bytes for
+    every sub-block, ggml's 16 bytes per sub-block): one- and multi-window
+    rows, batches."""
+    say("gemv IQ4_XS", "ggml" if ggml else "reference", rows, cols, batch)
+    w = S.matrix(23, 6100 + rows + cols, rows, cols)
+    x = S.normal_f32(6200 + cols + batch, batch * cols).reshape(batch, cols)
+    flags = H.FLAG_IQ4XS_GGML if ggml else 0
+    t = H.QuantTensor(f"iq4_{int(ggml)}_{rows}_{cols}", 23, rows, cols, w, flags)
+    y = backend.gemv_batch(t, x, batch)
+    mode = oracle.IQ4XS_GGML if ggml else oracle.IQ4XS_REFERENCE
+    for b in range(batch):
+        check(y[b], oracle.gemv(23, rows, cols, w, x[b], scale_mode=mode), f"iq4_xs b{b}")
+    if batch == 1 and rows <= 129:
+        # the two readings differ on random code bytes
+        other = oracle.gemv(23, rows, cols, w, x[0], scale_mode=1 - mode)
+        assert np.abs(y[0] - other).max() > 1e-2 * np.abs(other).max()
+    backend.evict(t.name)
 
 
 def test_gemv_empty_shapes(backend):

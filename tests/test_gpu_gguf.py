@@ -34,7 +34,8 @@ def test_upload_from_gguf_then_matvec(tmp_path, oracle):
     q5 = S.matrix(13, 13, 300, 2048)
     ex = S.matrix(14, 14, 4 * 256, 512)          # 4 experts, 256 inputs, 512 outputs
     router = S.normal_f32(15, 128 * 2048)
-    iq = np.zeros(136 * 2, np.uint8)             # IQ4_XS: no device kernel
+    iq = S.matrix(23, 16, 2, 256)                # IQ4_XS: matvec only
+    nl = np.zeros(18 * 2, np.uint8)              # IQ4_NL: no device kernel
     w = Writer()
     w.kv("general.architecture", STRING, "qwen4exp").kv("general.alignment", U32, 32)
     w.tensor("blk.0.ffn_down.weight", [4096, 1024], 12, q4.tobytes())
@@ -43,6 +44,7 @@ def test_upload_from_gguf_then_matvec(tmp_path, oracle):
     w.tensor("blk.0.ffn_down_exps.weight", [512, 256, 4], 14, ex.tobytes())
     w.tensor("blk.0.ffn_gate_inp.weight", [2048, 128], 0, router.tobytes())
     w.tensor("blk.0.iq.weight", [256, 2], 23, iq.tobytes())
+    w.tensor("blk.0.nl.weight", [32, 2], 20, nl.tobytes())
     w.tensor("blk.0.four_d.weight", [32, 1, 1, 1], 0, b"\0" * 128)
     path = tmp_path / "model.gguf"
     path.write_bytes(w.finish())
@@ -51,15 +53,14 @@ def test_upload_from_gguf_then_matvec(tmp_path, oracle):
     try:
         with H.GgufFile(str(path)) as f:
             before = be.resident_bytes()
-            for name in ("blk.0.ffn_down.weight", "blk.0.attn_q.weight", "blk.0.ffn_up.weight",
-                         "blk.0.ffn_down_exps.weight", "blk.0.ffn_gate_inp.weight"):
+            names = ("blk.0.ffn_down.weight", "blk.0.attn_q.weight", "blk.0.ffn_up.weight",
+                     "blk.0.ffn_down_exps.weight", "blk.0.ffn_gate_inp.weight", "blk.0.iq.weight")
+            for name in names:
                 be.upload_gguf(f, f.find(name), name)
-            total = sum(f.tensor(f.find(n)).nbytes for n in ("blk.0.ffn_down.weight", "blk.0.attn_q.weight",
-                                                             "blk.0.ffn_up.weight", "blk.0.ffn_down_exps.weight",
-                                                             "blk.0.ffn_gate_inp.weight"))
+            total = sum(f.tensor(f.find(n)).nbytes for n in names)
             assert be.resident_bytes() - before == total
             with pytest.raises(H.UnsupportedQuantError):
-                be.upload_gguf(f, f.find("blk.0.iq.weight"), "iq")
+                be.upload_gguf(f, f.find("blk.0.nl.weight"), "nl")
             with pytest.raises(H.BackendError):
                 be.upload_gguf(f, f.find("blk.0.four_d.weight"), "four_d")
 
@@ -67,7 +68,8 @@ def test_upload_from_gguf_then_matvec(tmp_path, oracle):
                                               ("blk.0.attn_q.weight", 8, 4096, 4096, q8),
                                               ("blk.0.ffn_up.weight", 13, 300, 2048, q5),
                                               ("blk.0.ffn_gate_inp.weight", 0, 128, 2048,
-                                               router.view(np.uint8))):
+                                               router.view(np.uint8)),
+                                              ("blk.0.iq.weight", 23, 2, 256, iq)):
             x = S.normal_f32(rows + 3, cols)
             y = np.empty(rows, np.float32)
             be.gemv(H.QuantTensor(name, quant, rows, cols, np.zeros(real.nbytes, np.uint8)), x, y)
@@ -107,6 +109,6 @@ def test_weight_upload_pitched_and_idempotent(oracle):
         with pytest.raises(H.BackendError):
             be.upload("bad", 12, 1, rows, cols, pitched, row_pitch=rb - 1)
         with pytest.raises(H.UnsupportedQuantError):
-            be.upload("iq", 23, 1, 2, 256, np.zeros(272, np.uint8))
+            be.upload("nl", 20, 1, 2, 32, np.zeros(36, np.uint8))  # IQ4_NL: no device kernel
     finally:
         be.close()

@@ -51,7 +51,7 @@ def check_rows(got, want, tol, strict_tol=None):
 
 SHAPES = [(12, 96, 256, 1), (12, 200, 512, 37), (12, 100, 768, 300), (8, 96, 256, 5),
           (8, 130, 320, 70), (14, 97, 512, 33), (14, 96, 256, 256), (12, 192, 1024, 513),
-          (8, 64, 64, 3), (8, 100, 128, 257)]
+          (8, 64, 64, 3), (8, 100, 128, 257), (13, 96, 256, 1), (13, 130, 512, 70), (13, 192, 1024, 513)]
 
 
 @pytest.mark.parametrize("quant,rows,cols,m", SHAPES)

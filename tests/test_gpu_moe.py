@@ -166,7 +166,7 @@ def test_moe_ffn_dev_unaligned_tensors_match(backend, n_tok):
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("qg,qd", [(12, 14), (8, 8), (14, 12), (12, 8), (8, 14)])
+@pytest.mark.parametrize("qg,qd", [(12, 14), (8, 8), (14, 12), (12, 8), (8, 14), (13, 13), (13, 14), (12, 13)])
 def test_moe_ffn_one_token_formats(backend, oracle, qg, qd):
     """One token (routed inside the gate/up launch) over aligned tensors whose
     sizes are multiples of 16 bytes (the global_load_lds copy ring), for each
@@ -419,6 +419,25 @@ def test_moe_ffn_random_configs(backend, oracle, seed):
     for t in range(n_tok):
         check_parity(out[t], ref[t], "moe")
     for name in (f"rg{seed}", f"ru{seed}", f"rd{seed}"):
+        backend.evict(name)
+
+
+@pytest.mark.parametrize("n_tok", [2, 7])
+def test_moe_ffn_q5_k(backend, oracle, n_tok):
+    """Q5_K experts (gate/up and down) over several tokens: the two-token
+    work items and the route launch."""
+    n_expert, n_embd, n_ff, top_k = 16, 1024, 512, 4
+    say("moe ffn q5_k", n_tok)
+    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 13, 13, 7400 + n_tok)
+    logits = S.router_logits(7500 + n_tok, n_tok, n_expert)
+    x = S.normal_f32(7600 + n_tok, n_tok * n_embd).reshape(n_tok, n_embd)
+    out = backend.moe_ffn(H.ExpertView(f"q5g{n_tok}", 13, n_expert, n_embd, n_ff, gate),
+                          H.ExpertView(f"q5u{n_tok}", 13, n_expert, n_embd, n_ff, up),
+                          H.ExpertView(f"q5d{n_tok}", 13, n_expert, n_ff, n_embd, down), logits, x, top_k)
+    ref = oracle_moe(oracle, 13, 13, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
+    for t in range(n_tok):
+        check_parity(out[t], ref[t], "moe q5_k")
+    for name in (f"q5g{n_tok}", f"q5u{n_tok}", f"q5d{n_tok}"):
         backend.evict(name)
 
 

@@ -8,6 +8,10 @@
 * hand-derived Q5_K known answers (none in the reference either) for the
   fifth bit of every sub-block;
 * hand-derived negative Q6_K scales, u8 (reference) vs i8 (ggml) reading;
+* hand-derived IQ4_XS known answers for both code-byte readings (the
+  reference's first-16-bytes reading and ggml's 16 bytes per sub-block), the
+  code book, the 6-bit scale split and the readings' agreement when the code
+  bytes repeat;
 * an encoder round trip for get_scale_min_k4 over every (j, sc, m);
 * the exhaustive binary16 -> binary32 table against numpy;
 * a bit-for-bit comparison with the independent numpy restatement.
@@ -200,6 +204,94 @@ def test_q6_k_known_answers_i8(oracle):
     assert out[32] == -30.0
 
 
+# ---- hand-derived IQ4_XS known answers, both code-byte readings -------------
+
+# ggml's kvalues_iq4nl as crates/strata-gguf/src/tables.rs:2052-2054 lists it
+IQ4NL = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def iq4xs_block(d, scales_h, scales_l, qs):
+    b = np.zeros(136, np.uint8)
+    b[0:2] = f16b(d)
+    b[2:4] = [scales_h & 0xFF, scales_h >> 8]
+    b[4:8] = scales_l
+    b[8:136] = qs
+    return b
+
+
+def test_iq4_xs_code_book(oracle):
+    """d = 1 and every ls = 33 (dl = 1): the outputs are the code book's
+    values. qs[j] = j | (15 - j) << 4 puts index j at element j and index
+    15 - j at element 16 + j of the first sub-block."""
+    qs = np.zeros(128, np.uint8)
+    qs[:16] = [j | ((15 - j) << 4) for j in range(16)]
+    sl = [0x11] * 4                      # low 4 bits of every ls: 1
+    sh = 0xAAAA                          # top 2 bits of every ls: 2 -> ls = 33
+    for mode in (oracle.IQ4XS_REFERENCE, oracle.IQ4XS_GGML):
+        out = oracle.dequantize_row(oracle.IQ4_XS, iq4xs_block(1.0, sh, sl, qs), 256, mode)
+        assert out[:16].tolist() == IQ4NL
+        assert out[16:32].tolist() == IQ4NL[::-1]
+
+
+def iq4xs_kat_block():
+    qs = np.zeros(128, np.uint8)
+    qs[0] = 0x08                 # low nibble 8 (code 1), high nibble 0 (code -127)
+    qs[112] = 0x3F               # sub-block 7 in ggml's reading: low 15 (113), high 3 (-65)
+    sl = [0xF1, 0, 0, 0]         # ls low bits: sub-block 0 -> 1, 1 -> 15, 7 -> 0
+    sh = 0x0002 | (3 << 2)       # ls high bits: sub-block 0 -> 2, 1 -> 3, 7 -> 0
+    return iq4xs_block(0.5, sh, sl, qs)
+
+
+def test_iq4_xs_known_answers_reference_reading(oracle):
+    """Every sub-block reads qs[0..16]: ls0 = 33 (dl 0.5), ls1 = 63 (dl
+    15.5), ls7 = 0 (dl -16)."""
+    out = oracle.dequantize_row(oracle.IQ4_XS, iq4xs_kat_block(), 256)
+    assert out[0] == 0.5         # 0.5 * 1
+    assert out[16] == -63.5      # 0.5 * -127
+    assert out[32] == 15.5       # 15.5 * 1 (qs[0] again)
+    assert out[48] == -1968.5    # 15.5 * -127
+    assert out[224] == -16.0     # -16 * 1
+    assert out[240] == 2032.0    # -16 * -127
+    assert out[1] == 0.5 * -127  # qs[1] = 0: code -127
+
+
+def test_iq4_xs_known_answers_ggml_reading(oracle):
+    """Sub-block ib reads qs[16 ib .. 16 ib + 16]: sub-block 1 sees zero
+    bytes, sub-block 7 the 0x3F at qs[112]."""
+    out = oracle.dequantize_row(oracle.IQ4_XS, iq4xs_kat_block(), 256, oracle.IQ4XS_GGML)
+    assert out[0] == 0.5
+    assert out[16] == -63.5
+    assert out[32] == 15.5 * -127
+    assert out[224] == -1808.0   # -16 * 113
+    assert out[240] == 1040.0    # -16 * -65
+
+
+def test_iq4_xs_readings_agree_when_code_bytes_repeat(oracle):
+    for seed in range(20):
+        blk = S.iq4_xs_blocks(3000 + seed, 1)
+        blk[24:136] = np.tile(blk[8:24], 7)
+        a = oracle.dequantize_row(oracle.IQ4_XS, blk, 256)
+        b = oracle.dequantize_row(oracle.IQ4_XS, blk, 256, oracle.IQ4XS_GGML)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # and differ when they do not
+    blk = S.iq4_xs_blocks(3100, 1)
+    assert not np.array_equal(oracle.dequantize_row(oracle.IQ4_XS, blk, 256),
+                              oracle.dequantize_row(oracle.IQ4_XS, blk, 256, oracle.IQ4XS_GGML))
+
+
+def test_iq4_xs_finite_fill(oracle):
+    """dequant_tests.rs:187-244 for IQ4_XS: the LCG byte fill with an f16
+    scale of 0.125 dequantizes to finite values."""
+    state = 0x12345678
+    blk = np.empty(136, np.uint8)
+    for i in range(136):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        blk[i] = (state >> 16) & 0xFF
+    blk[0:2] = f16b(0.125)
+    out = oracle.dequantize_row(oracle.IQ4_XS, blk, 256)
+    assert np.all(np.isfinite(out))
+
+
 # ---- get_scale_min_k4: round trip through an encoder ------------------------
 
 def encode_scale_min_k4(sc, m):
@@ -279,6 +371,7 @@ def test_geometry_constants(oracle):
     assert (oracle.block_size(12), oracle.type_size(12)) == (256, 144)
     assert (oracle.block_size(13), oracle.type_size(13)) == (256, 176)
     assert (oracle.block_size(14), oracle.type_size(14)) == (256, 210)
+    assert (oracle.block_size(23), oracle.type_size(23)) == (256, 136)
     assert oracle.byte_size(8, 4096 * 4096) == 17_825_792
     assert oracle.byte_size(12, 4096 * 12288) == 28_311_552
     assert oracle.byte_size(14, 151936 * 4096) == 510_504_960
@@ -294,7 +387,7 @@ def test_truncated_rows(oracle):
 
 # ---- the independent numpy restatement --------------------------------------
 
-@pytest.mark.parametrize("quant", [8, 12, 13, 14])
+@pytest.mark.parametrize("quant", [8, 12, 13, 14, 23])
 def test_oracle_matches_numpy_restatement(oracle, quant):
     cols = 1024
     rows = 64
@@ -305,6 +398,10 @@ def test_oracle_matches_numpy_restatement(oracle, quant):
     if quant == 14:
         a = oracle.dequantize(quant, w, rows, cols, oracle.SCALE_I8)
         b = N.dequantize(quant, w, rows, cols, signed_q6k_scales=True)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    if quant == 23:
+        a = oracle.dequantize(quant, w, rows, cols, oracle.IQ4XS_GGML)
+        b = N.dequantize(quant, w, rows, cols, iq4xs_ggml=True)
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
@@ -365,6 +462,26 @@ def test_q6_k_is_one_rounding_of_the_exact_value(oracle, mode):
         raw = blk[192 + 8 * h + l // 16 + 2 * t]
         sc = raw.view(np.int8).astype(np.float64) if mode else raw.astype(np.float64)
         assert np.array_equal(out, (d * sc * q).astype(np.float32))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_iq4_xs_products_are_exact(oracle, mode):
+    """dl = d*(ls - 32) has at most 11 + 6 significant bits and dl*code at
+    most 24, so both are exact in f32: the oracle must equal the exact value
+    (f64) for both code-byte readings."""
+    tab = np.array(IQ4NL, np.float64)
+    for seed in range(30):
+        blk = S.iq4_xs_blocks(3500 + seed, 1)
+        out = oracle.dequantize_row(oracle.IQ4_XS, blk, 256, mode)
+        d = np.float64(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+        sh = int(blk[2]) | (int(blk[3]) << 8)
+        want = np.empty(256)
+        for j in range(256):
+            ib, k = j // 32, j % 32
+            ls = ((int(blk[4 + ib // 2]) >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)
+            byte = int(blk[8 + (16 * ib if mode else 0) + k % 16])
+            want[j] = d * (ls - 32) * tab[(byte >> 4) if k >= 16 else (byte & 0xF)]
+        assert np.array_equal(out, want.astype(np.float32))
 
 
 def test_q8_0_is_one_rounding_of_the_exact_value(oracle):
