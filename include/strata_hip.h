@@ -75,11 +75,15 @@ extern "C" {
 /* Q6_K sub-block scales as ggml's int8_t instead of strata-gguf's u8 reading
  * (crates/strata-gguf/src/dequant.rs:211,224-227 reads them as u8). */
 #define SH_FLAG_Q6K_SIGNED_SCALES 1u
-/* sh_expert_view in ggml's orientation, as llama.cpp GGUF files store
- * expert stacks: [n_expert][rows = out][cols = in] with blocks along the
- * input, so sh_expert_gemv computes y[r] = sum_c W_e[r][c] x[c] (x_len =
- * cols, y_len = rows) with the matvec kernels. The reference's in-major
- * orientation (weights.rs:14-34) is the default. sh_expert_gemv only. */
+/* Expert stacks in ggml's orientation, as llama.cpp GGUF files store them:
+ * [n_expert][rows = out][cols = in] with blocks along the input.
+ * sh_expert_gemv then computes y[r] = sum_c W_e[r][c] x[c] (x_len = cols,
+ * y_len = rows) with the matvec kernels; the fused MoE entry points
+ * (sh_moe_ffn, sh_moe_layer and their _dev forms) take gate / up
+ * [n_expert][n_ff][n_embd] and down [n_expert][n_embd][n_ff], each expert
+ * an ops::gemv of its slice, when all three stacks carry the flag (mixed
+ * orientations are refused). The reference's in-major orientation
+ * (weights.rs:14-34) is the default. */
 #define SH_FLAG_EXPERT_OUT_MAJOR 2u
 /* IQ4_XS in ggml's layout, sub-block ib reading qs[16 ib .. 16 ib + 16).
  * strata-gguf reads qs[0..16] for every sub-block (its qs slice is never
@@ -228,8 +232,9 @@ int sh_moe_route(sh_context* ctx, const float* logits, uint32_t n_tok, uint32_t 
 /* The routed half of MoeLayer::combine (moe.rs:108-127) for n_tok tokens,
  * from router logits: out[t] = sum over t's top_k experts (ascending id) of
  * w * down_e(silu(gate_e x_t) * up_e x_t). gate/up are [n_expert][n_embd]
- * [n_ff], down [n_expert][n_ff][n_embd] (reference orientation); x and out
- * are [n_tok][n_embd]. The shared expert (moe.rs:129-143) is not included.
+ * [n_ff], down [n_expert][n_ff][n_embd] (reference orientation), or with
+ * SH_FLAG_EXPERT_OUT_MAJOR on all three [n_expert][n_ff][n_embd] and
+ * [n_expert][n_embd][n_ff]; x and out are [n_tok][n_embd]. The shared expert (moe.rs:129-143) is not included.
  * gate and up must have the same quant type. */
 int sh_moe_ffn(sh_context* ctx, const sh_expert_view* gate, const sh_expert_view* up,
                const sh_expert_view* down, const float* logits, uint32_t n_tok, uint32_t top_k,
@@ -291,7 +296,8 @@ typedef struct sh_expert_dev {
   const void* data; /* [n_expert][rows][cols] packed, as in sh_expert_view */
 } sh_expert_dev;
 
-/* Bytes of device workspace sh_moe_ffn_dev needs for these shapes. */
+/* Bytes of device workspace sh_moe_ffn_dev needs for these shapes, in
+ * either orientation of the expert stacks. */
 int sh_moe_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
                            uint64_t n_ff, uint32_t quant_gate_up, uint32_t quant_down,
                            uint64_t* bytes);
@@ -304,9 +310,9 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
                    uint32_t n_tok, uint32_t top_k, const float* x, float* out, void* workspace,
                    uint64_t workspace_bytes, void* stream);
 
-/* Bytes of device workspace sh_moe_layer_dev needs; quants[8] are the types
- * of router, gate, up, down, gate_shexp, up_shexp, down_shexp,
- * gate_inp_shexp. */
+/* Bytes of device workspace sh_moe_layer_dev needs (either orientation of
+ * the expert stacks); quants[8] are the types of router, gate, up, down,
+ * gate_shexp, up_shexp, down_shexp, gate_inp_shexp. */
 int sh_moe_layer_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
                                  uint64_t n_ff, uint64_t n_ff_shexp, const uint32_t* quants, uint64_t* bytes);
 

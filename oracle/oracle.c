@@ -532,12 +532,30 @@ int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
  * gate/up: [n_expert][n_embd][n_ff]; down: [n_expert][n_ff][n_embd].
  * out (n_embd) is overwritten. The shared expert (moe.rs:129-143) is not
  * part of this op. */
-int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
-                   int64_t n_expert, int64_t n_embd, int64_t n_ff,
-                   const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
-                   size_t up_bytes, const uint8_t* down, size_t down_bytes,
-                   const int64_t* ids, const float* weights, int64_t k,
-                   const float* x, float* out) {
+/* One expert's matvec in either orientation: in-major [n_expert][in][out]
+ * through ops::expert_gemv (the reference's), or out-major
+ * [n_expert][out][in] (llama.cpp's expert stacks) as ops::gemv of the
+ * expert's [out][in] slice. */
+static int expert_apply(uint32_t quant, int64_t n_expert, int64_t n_in, int64_t n_out, const uint8_t* data,
+                        size_t nbytes, int64_t e, const float* x, float* y, int out_major) {
+  if (!out_major) return sho_expert_gemv(quant, n_expert, n_in, n_out, data, nbytes, e, x, y);
+  int64_t rb = sho_byte_size(quant, n_in);
+  if (rb < 0) return SHO_UNSUPPORTED;
+  if (e < 0 || e >= n_expert) return SHO_TRUNCATED;
+  size_t off = (size_t)(e * n_out * rb);
+  if (off > nbytes) return SHO_TRUNCATED;
+  return gemv_rows(quant, 0, n_out, n_in, data + off, nbytes - off, x, y, 0);
+}
+
+/* moe.rs:108-127 for one token: for each selected expert j with w != 0 (in
+ * the order given, ascending id): h = gate_e . x, p = up_e . x,
+ * h = silu(h) * p, d = down_e . h, out += w * d (f32 product, then sum). */
+int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                     int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                     const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                     size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                     const int64_t* ids, const float* weights, int64_t k,
+                     const float* x, float* out, int out_major) {
   float* h = (float*)malloc((size_t)n_ff * sizeof(float));
   float* part = (float*)malloc((size_t)n_ff * sizeof(float));
   float* d = (float*)malloc((size_t)n_embd * sizeof(float));
@@ -547,12 +565,12 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
     float w = weights[j];
     if (w == 0.0f) continue;
     int64_t e = ids[j];
-    rc = sho_expert_gemv(gate_quant, n_expert, n_embd, n_ff, gate, gate_bytes, e, x, h);
+    rc = expert_apply(gate_quant, n_expert, n_embd, n_ff, gate, gate_bytes, e, x, h, out_major);
     if (rc) break;
-    rc = sho_expert_gemv(up_quant, n_expert, n_embd, n_ff, up, up_bytes, e, x, part);
+    rc = expert_apply(up_quant, n_expert, n_embd, n_ff, up, up_bytes, e, x, part, out_major);
     if (rc) break;
     for (int64_t i = 0; i < n_ff; ++i) h[i] = sho_silu(h[i]) * part[i];
-    rc = sho_expert_gemv(down_quant, n_expert, n_ff, n_embd, down, down_bytes, e, h, d);
+    rc = expert_apply(down_quant, n_expert, n_ff, n_embd, down, down_bytes, e, h, d, out_major);
     if (rc) break;
     for (int64_t i = 0; i < n_embd; ++i) {
       float t = w * d[i];
@@ -563,6 +581,16 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
   free(part);
   free(d);
   return rc;
+}
+
+int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                   int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                   const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                   size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                   const int64_t* ids, const float* weights, int64_t k,
+                   const float* x, float* out) {
+  return sho_moe_routed_o(gate_quant, up_quant, down_quant, n_expert, n_embd, n_ff, gate, gate_bytes, up,
+                          up_bytes, down, down_bytes, ids, weights, k, x, out, 0);
 }
 
 /* ops.rs:90-92 */
@@ -578,9 +606,9 @@ float sho_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
  * [n_embd][n_ff_sh], gate_inp [1][n_embd] (ops::gemv orientation).
  * q[8]: the types of router, gate, up, down, gate_sh, up_sh, down_sh,
  * gate_inp; t[8] / nb[8] their bytes. out (n_embd) is overwritten. */
-int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
-                  int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
-                  float* out) {
+int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                    int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                    float* out, int out_major) {
   float* xb = (float*)malloc((size_t)n_embd * sizeof(float));
   float* logits = (float*)malloc((size_t)n_expert * sizeof(float));
   int64_t* ids = (int64_t*)malloc((size_t)top_k * sizeof(int64_t));
@@ -595,8 +623,8 @@ int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, 
   int64_t k = 0;
   if (rc == SHO_OK) {
     k = sho_moe_route(logits, n_expert, top_k, ids, w);
-    rc = sho_moe_routed(q[1], q[2], q[3], n_expert, n_embd, n_ff, t[1], nb[1], t[2], nb[2], t[3], nb[3], ids,
-                        w, k, x, out);
+    rc = sho_moe_routed_o(q[1], q[2], q[3], n_expert, n_embd, n_ff, t[1], nb[1], t[2], nb[2], t[3], nb[3],
+                          ids, w, k, x, out, out_major);
   }
   if (rc == SHO_OK) rc = sho_gemv(q[4], n_ff_sh, n_embd, t[4], nb[4], x, g);
   if (rc == SHO_OK) rc = sho_gemv(q[5], n_ff_sh, n_embd, t[5], nb[5], x, part);
@@ -620,6 +648,12 @@ int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, 
   free(part);
   free(d);
   return rc;
+}
+
+int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                  int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                  float* out) {
+  return sho_moe_layer_o(q, t, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, x, out, 0);
 }
 
 int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,

@@ -126,6 +126,18 @@ int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
 int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
                   int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
                   float* out);
+/* The same with the routed expert stacks in llama.cpp's out-major
+ * orientation when out_major is set: gate / up [n_expert][n_ff][n_embd],
+ * down [n_expert][n_embd][n_ff], each expert an ops::gemv of its slice. */
+int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                     int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                     const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                     size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                     const int64_t* ids, const float* weights, int64_t k,
+                     const float* x, float* out, int out_major);
+int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                    int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                    float* out, int out_major);
 
 /* y[t][r] = gemv(W, x[t]) for t < m: m independent sho_gemv calls, each
  * row-parallel over n_threads (bit-identical to the sequential loop). */

@@ -66,6 +66,11 @@ def lib() -> C.CDLL:
         L.sho_moe_routed.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
                                      C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
                                      i64p, f32p, C.c_int64, f32p, f32p]
+        L.sho_moe_routed_o.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
+                                       C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
+                                       i64p, f32p, C.c_int64, f32p, f32p, C.c_int]
+        L.sho_moe_layer_o.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
+                                      C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, f32p, f32p, C.c_int]
         L.sho_sigmoid.argtypes = [C.c_float]
         L.sho_sigmoid.restype = C.c_float
         L.sho_moe_layer.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
@@ -199,14 +204,17 @@ def moe_route(logits, top_k: int) -> tuple[np.ndarray, np.ndarray]:
 
 
 def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, n_ff: int,
-               gate, up, down, ids, weights, x) -> np.ndarray:
+               gate, up, down, ids, weights, x, out_major: bool = False) -> np.ndarray:
+    """The routed experts of one token; ``out_major``: the stacks are
+    llama.cpp's [n_expert][out][in] (each expert an ops::gemv of its slice)
+    instead of the reference's [n_expert][in][out]."""
     g, u, d = _u8(gate), _u8(up), _u8(down)
     idv = np.ascontiguousarray(ids, dtype=np.int64)
     wv, xv = _f32(weights), _f32(x)
     out = np.empty(n_embd, dtype=np.float32)
-    _check(lib().sho_moe_routed(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
-                                _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
-                                _ptr(xv), _ptr(out)), "moe_routed")
+    _check(lib().sho_moe_routed_o(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
+                                  _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
+                                  _ptr(xv), _ptr(out), int(out_major)), "moe_routed")
     return out
 
 
@@ -268,7 +276,8 @@ def add(a, b) -> np.ndarray:
     return av.reshape(np.shape(a))
 
 
-def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: int, x, top_k: int) -> np.ndarray:
+def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: int, x, top_k: int,
+              out_major: bool = False) -> np.ndarray:
     """The whole MoE layer for one token (moe.rs:48-143): router matvec on
     bf16(x), route, routed experts, then the shared expert added with its
     sigmoid gate. quants / tensors: router, gate, up, down, gate_sh, up_sh,
@@ -280,8 +289,8 @@ def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: i
     q = (C.c_uint32 * 8)(*[int(v) for v in quants])
     tp = (C.c_void_p * 8)(*[_ptr(b) for b in bufs])
     nb = (C.c_size_t * 8)(*[b.nbytes for b in bufs])
-    _check(lib().sho_moe_layer(q, tp, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, _ptr(xv), _ptr(out)),
-           "moe_layer")
+    _check(lib().sho_moe_layer_o(q, tp, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, _ptr(xv), _ptr(out),
+                                 int(out_major)), "moe_layer")
     return out
 
 

@@ -549,8 +549,22 @@ int sh_expert_gemv(sh_context* c, const sh_expert_view* w, uint64_t e, const flo
   return SH_OK;
 }
 
+// The orientation of a call's three expert stacks: 0 all in-major (the
+// reference's [n_expert][in][out]), 1 all out-major (SH_FLAG_EXPERT_OUT_MAJOR,
+// llama.cpp's [n_expert][out][in]), -1 mixed.
+static int orientation(uint32_t fg, uint32_t fu, uint32_t fd) {
+  const uint32_t a = fg & SH_FLAG_EXPERT_OUT_MAJOR, b = fu & SH_FLAG_EXPERT_OUT_MAJOR,
+                 d = fd & SH_FLAG_EXPERT_OUT_MAJOR;
+  if (a != b || b != d) return -1;
+  return a ? 1 : 0;
+}
+
+static int mixed_orientation() {
+  return fail(SH_ERR_UNSUPPORTED_SHAPE, "gate, up and down must share one orientation (SH_FLAG_EXPERT_OUT_MAJOR)");
+}
+
 static int moe_check(uint64_t n_expert, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
-                     uint32_t top_k, uint32_t qa, uint32_t qb, sh::MoePlan* plan) {
+                     uint32_t top_k, uint32_t qa, uint32_t qb, sh::MoePlan* plan, bool out_major = false) {
   if (n_expert == 0 || n_expert > uint64_t(sh::kMoeMaxExperts))
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_expert %llu outside 1..%d", (unsigned long long)n_expert,
                 sh::kMoeMaxExperts);
@@ -560,9 +574,9 @@ static int moe_check(uint64_t n_expert, uint64_t n_embd, uint64_t n_ff, uint32_t
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "n_tok %u outside 1..%d", n_tok, sh::kMoeMaxTokens);
   if (n_embd > (1u << 20) || n_ff > (1u << 20))
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "MoE widths too large");
-  if (!sh::moe_plan(int(n_tok), int(top_k), int(n_expert), int(n_embd), int(n_ff), qa, qb, plan))
-    return fail(SH_ERR_UNSUPPORTED_SHAPE, "MoE %llu x %llu (types %u, %u) is not supported",
-                (unsigned long long)n_embd, (unsigned long long)n_ff, qa, qb);
+  if (!sh::moe_plan(int(n_tok), int(top_k), int(n_expert), int(n_embd), int(n_ff), qa, qb, plan, out_major))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "MoE %llu x %llu (types %u, %u, %s) is not supported",
+                (unsigned long long)n_embd, (unsigned long long)n_ff, qa, qb, out_major ? "out-major" : "in-major");
   return SH_OK;
 }
 
@@ -598,32 +612,35 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
                const float* x, float* out) {
   if (!c || !gate || !up || !down || !logits || !x || !out)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
-  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
-    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
-  const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols;
-  if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
-      down->rows != n_ff || down->cols != n_embd)
+  const int om = orientation(gate->flags, up->flags, down->flags);
+  if (om < 0) return mixed_orientation();
+  // gate / up [E][gr][gc], down [E][gc][gr] in either orientation:
+  // (gr, gc) = (n_embd, n_ff) in-major, (n_ff, n_embd) out-major
+  const uint64_t E = gate->n_expert, gr = gate->rows, gc = gate->cols;
+  const uint64_t n_embd = om ? gc : gr, n_ff = om ? gr : gc;
+  if (up->n_expert != E || down->n_expert != E || up->rows != gr || up->cols != gc || down->rows != gc ||
+      down->cols != gr)
     return fail(SH_ERR_SHAPE, "MoE views disagree: gate/up [%llu][%llu][%llu], down [%llu][%llu][%llu]",
-                (unsigned long long)E, (unsigned long long)n_embd, (unsigned long long)n_ff,
+                (unsigned long long)E, (unsigned long long)gr, (unsigned long long)gc,
                 (unsigned long long)down->n_expert, (unsigned long long)down->rows,
                 (unsigned long long)down->cols);
   if (gate->quant != up->quant)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", gate->quant, up->quant);
   int rc;
-  if ((rc = check_matrix(gate->quant, n_embd, n_ff, E, gate->nbytes)) ||
-      (rc = check_matrix(up->quant, n_embd, n_ff, E, up->nbytes)) ||
-      (rc = check_matrix(down->quant, n_ff, n_embd, E, down->nbytes)))
+  if ((rc = check_matrix(gate->quant, gr, gc, E, gate->nbytes)) ||
+      (rc = check_matrix(up->quant, gr, gc, E, up->nbytes)) ||
+      (rc = check_matrix(down->quant, gc, gr, E, down->nbytes)))
     return rc;
   sh::MoePlan plan;
-  if ((rc = moe_check(E, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan))) return rc;
+  if ((rc = moe_check(E, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan, om == 1))) return rc;
   Guard g(c);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   Resident *rg = nullptr, *ru = nullptr, *rd = nullptr;
-  const uint64_t ga = E * n_embd * uint64_t(sh::byte_size(gate->quant, int64_t(n_ff)));
-  const uint64_t db = E * n_ff * uint64_t(sh::byte_size(down->quant, int64_t(n_embd)));
-  if ((rc = resident(c, gate->key, gate->quant, E, n_embd, n_ff, gate->data, ga, &rg))) return rc;
-  if ((rc = resident(c, up->key, up->quant, E, n_embd, n_ff, up->data, ga, &ru))) return rc;
-  if ((rc = resident(c, down->key, down->quant, E, n_ff, n_embd, down->data, db, &rd))) return rc;
+  const uint64_t ga = E * gr * uint64_t(sh::byte_size(gate->quant, int64_t(gc)));
+  const uint64_t db = E * gc * uint64_t(sh::byte_size(down->quant, int64_t(gr)));
+  if ((rc = resident(c, gate->key, gate->quant, E, gr, gc, gate->data, ga, &rg))) return rc;
+  if ((rc = resident(c, up->key, up->quant, E, gr, gc, up->data, ga, &ru))) return rc;
+  if ((rc = resident(c, down->key, down->quant, E, gc, gr, down->data, db, &rd))) return rc;
   const size_t lb = sizeof(float) * n_tok * E, xb = sizeof(float) * n_tok * n_embd;
   const size_t lb_al = (lb + 255) & ~size_t(255);
   if ((rc = c->d_in.ensure(lb_al + xb, "inputs")) || (rc = c->d_out.ensure(xb, "out buffer")) ||
@@ -652,14 +669,15 @@ int sh_moe_ffn(sh_context* c, const sh_expert_view* gate, const sh_expert_view* 
 // gate/up_shexp [n_ff_sh][n_embd], down_shexp [n_embd][n_ff_sh],
 // gate_inp_shexp [1][n_embd]; then the plan.
 static int moe_layer_check(uint64_t E, uint64_t n_embd, uint64_t n_ff, uint64_t n_sh, uint32_t n_tok,
-                           uint32_t top_k, const sh::MoeLayerTypes& q, sh::MoeLayerPlan* plan) {
-  int rc = moe_check(E, n_embd, n_ff, n_tok, top_k, q.gate, q.down, &plan->moe);
+                           uint32_t top_k, const sh::MoeLayerTypes& q, sh::MoeLayerPlan* plan,
+                           bool out_major = false) {
+  int rc = moe_check(E, n_embd, n_ff, n_tok, top_k, q.gate, q.down, &plan->moe, out_major);
   if (rc) return rc;
   if (q.up != q.gate)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", q.gate, q.up);
   if (n_sh == 0 || n_sh > (1u << 20)) return fail(SH_ERR_UNSUPPORTED_SHAPE, "shared expert width %llu",
                                                  (unsigned long long)n_sh);
-  if (!sh::moe_layer_plan(int(n_tok), int(top_k), int(E), int(n_embd), int(n_ff), int(n_sh), q, plan))
+  if (!sh::moe_layer_plan(int(n_tok), int(top_k), int(E), int(n_embd), int(n_ff), int(n_sh), q, plan, out_major))
     return fail(SH_ERR_UNSUPPORTED_SHAPE,
                 "MoE layer: router %llux%llu (type %u) or shared expert %llu wide (types %u, %u, %u, gate %u) "
                 "is not a matvec shape the kernels take",
@@ -676,13 +694,14 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
   if (!c || !router || !gate || !up || !down || !gate_shexp || !up_shexp || !down_shexp || !gate_inp_shexp ||
       !x || !out)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
-  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
-    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
-  const uint64_t E = gate->n_expert, n_embd = gate->rows, n_ff = gate->cols, n_sh = gate_shexp->rows;
-  if (up->n_expert != E || down->n_expert != E || up->rows != n_embd || up->cols != n_ff ||
-      down->rows != n_ff || down->cols != n_embd)
+  const int om = orientation(gate->flags, up->flags, down->flags);
+  if (om < 0) return mixed_orientation();
+  const uint64_t E = gate->n_expert, gr = gate->rows, gc = gate->cols, n_sh = gate_shexp->rows;
+  const uint64_t n_embd = om ? gc : gr, n_ff = om ? gr : gc;
+  if (up->n_expert != E || down->n_expert != E || up->rows != gr || up->cols != gc || down->rows != gc ||
+      down->cols != gr)
     return fail(SH_ERR_SHAPE, "MoE views disagree: gate/up [%llu][%llu][%llu], down [%llu][%llu][%llu]",
-                (unsigned long long)E, (unsigned long long)n_embd, (unsigned long long)n_ff,
+                (unsigned long long)E, (unsigned long long)gr, (unsigned long long)gc,
                 (unsigned long long)down->n_expert, (unsigned long long)down->rows,
                 (unsigned long long)down->cols);
   if (router->rows != E || router->cols != n_embd || gate_shexp->cols != n_embd || up_shexp->rows != n_sh ||
@@ -691,9 +710,9 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
     return fail(SH_ERR_SHAPE, "MoE layer: router or shared-expert shapes disagree with the %llu x %llu experts",
                 (unsigned long long)E, (unsigned long long)n_embd);
   int rc;
-  if ((rc = check_matrix(gate->quant, n_embd, n_ff, E, gate->nbytes)) ||
-      (rc = check_matrix(up->quant, n_embd, n_ff, E, up->nbytes)) ||
-      (rc = check_matrix(down->quant, n_ff, n_embd, E, down->nbytes)))
+  if ((rc = check_matrix(gate->quant, gr, gc, E, gate->nbytes)) ||
+      (rc = check_matrix(up->quant, gr, gc, E, up->nbytes)) ||
+      (rc = check_matrix(down->quant, gc, gr, E, down->nbytes)))
     return rc;
   const sh_quant_tensor* dense[5] = {router, gate_shexp, up_shexp, down_shexp, gate_inp_shexp};
   for (const sh_quant_tensor* t : dense)
@@ -701,7 +720,7 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
   const sh::MoeLayerTypes q{router->quant, gate->quant, up->quant, down->quant,
                             gate_shexp->quant, up_shexp->quant, down_shexp->quant, gate_inp_shexp->quant};
   sh::MoeLayerPlan plan;
-  if ((rc = moe_layer_check(E, n_embd, n_ff, n_sh, n_tok, top_k, q, &plan))) return rc;
+  if ((rc = moe_layer_check(E, n_embd, n_ff, n_sh, n_tok, top_k, q, &plan, om == 1))) return rc;
   Guard g(c);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   // all eight tensors resident at once (each admission is pinned to this
@@ -714,9 +733,9 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
   };
   const Want want[8] = {
       {router->key, router->quant, 1, router->rows, router->cols, router->data},
-      {gate->key, gate->quant, E, n_embd, n_ff, gate->data},
-      {up->key, up->quant, E, n_embd, n_ff, up->data},
-      {down->key, down->quant, E, n_ff, n_embd, down->data},
+      {gate->key, gate->quant, E, gr, gc, gate->data},
+      {up->key, up->quant, E, gr, gc, up->data},
+      {down->key, down->quant, E, gc, gr, down->data},
       {gate_shexp->key, gate_shexp->quant, 1, n_sh, n_embd, gate_shexp->data},
       {up_shexp->key, up_shexp->quant, 1, n_sh, n_embd, up_shexp->data},
       {down_shexp->key, down_shexp->quant, 1, n_embd, n_sh, down_shexp->data},
@@ -905,10 +924,14 @@ int sh_gemv_dev_ws(uint32_t quant, uint32_t flags, const void* w, uint64_t rows,
 int sh_moe_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expert, uint64_t n_embd,
                            uint64_t n_ff, uint32_t quant_gate_up, uint32_t quant_down, uint64_t* bytes) {
   if (!bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null bytes");
-  sh::MoePlan plan;
-  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, quant_gate_up, quant_down, &plan);
-  if (rc) return rc;
-  *bytes = plan.bytes;
+  // enough for either orientation of the stacks (whichever the shape allows)
+  sh::MoePlan in_major, out_major;
+  const bool a = sh::moe_plan(int(std::min<uint64_t>(n_tok, 1u << 30)), int(std::min<uint32_t>(top_k, 1u << 30)),
+                              int(std::min<uint64_t>(n_expert, 1u << 30)), int(std::min<uint64_t>(n_embd, 1u << 30)),
+                              int(std::min<uint64_t>(n_ff, 1u << 30)), quant_gate_up, quant_down, &out_major, true);
+  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, quant_gate_up, quant_down, &in_major);
+  if (rc && !a) return rc;
+  *bytes = std::max<uint64_t>(rc ? 0 : in_major.bytes, a ? out_major.bytes : 0);
   return SH_OK;
 }
 
@@ -919,12 +942,12 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
   if (!gate || !up || !down || !gate->data || !up->data || !down->data || !logits || !x || !out ||
       !workspace)
     return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
-  if ((gate->flags | up->flags | down->flags) & SH_FLAG_EXPERT_OUT_MAJOR)
-    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
+  const int om = orientation(gate->flags, up->flags, down->flags);
+  if (om < 0) return mixed_orientation();
   if (gate->quant != up->quant)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "gate (%u) and up (%u) types differ", gate->quant, up->quant);
   sh::MoePlan plan;
-  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan);
+  int rc = moe_check(n_expert, n_embd, n_ff, n_tok, top_k, gate->quant, down->quant, &plan, om == 1);
   if (rc) return rc;
   if (workspace_bytes < plan.bytes)
     return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed",
@@ -948,10 +971,15 @@ int sh_moe_layer_workspace_bytes(uint32_t n_tok, uint32_t top_k, uint64_t n_expe
                                  uint64_t n_ff, uint64_t n_ff_shexp, const uint32_t* quants, uint64_t* bytes) {
   if (!quants || !bytes) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
   const sh::MoeLayerTypes q{quants[0], quants[1], quants[2], quants[3], quants[4], quants[5], quants[6], quants[7]};
-  sh::MoeLayerPlan plan;
-  int rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &plan);
-  if (rc) return rc;
-  *bytes = plan.bytes;
+  // enough for either orientation of the stacks (whichever the shape allows)
+  sh::MoeLayerPlan in_major, out_major;
+  const bool a = n_tok > 0 && top_k > 0 && n_expert <= uint64_t(sh::kMoeMaxExperts) && n_embd <= (1u << 20) &&
+                 n_ff <= (1u << 20) && n_ff_shexp <= (1u << 20) && q.up == q.gate &&
+                 sh::moe_layer_plan(int(std::min<uint32_t>(n_tok, 1u << 30)), int(std::min<uint32_t>(top_k, 1u << 30)),
+                                    int(n_expert), int(n_embd), int(n_ff), int(n_ff_shexp), q, &out_major, true);
+  int rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &in_major);
+  if (rc && !a) return rc;
+  *bytes = std::max<uint64_t>(rc ? 0 : in_major.bytes, a ? out_major.bytes : 0);
   return SH_OK;
 }
 
@@ -959,8 +987,8 @@ int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd,
                      uint64_t n_ff_shexp, uint32_t n_tok, uint32_t top_k, const float* x, float* out,
                      void* workspace, uint64_t workspace_bytes, void* stream) {
   if (!t || !x || !out || !workspace) return fail(SH_ERR_INVALID_ARGUMENT, "null argument");
-  if ((t[1].flags | t[2].flags | t[3].flags) & SH_FLAG_EXPERT_OUT_MAJOR)
-    return fail(SH_ERR_UNSUPPORTED_SHAPE, "the fused MoE path takes in-major expert stacks only");
+  const int om = orientation(t[1].flags, t[2].flags, t[3].flags);
+  if (om < 0) return mixed_orientation();
   for (int i = 0; i < 8; ++i) {
     if (!t[i].data) return fail(SH_ERR_INVALID_ARGUMENT, "null tensor %d", i);
     if ((reinterpret_cast<uintptr_t>(t[i].data) & 1u) ||
@@ -972,12 +1000,14 @@ int sh_moe_layer_dev(const sh_expert_dev* t, uint64_t n_expert, uint64_t n_embd,
   const sh::MoeLayerTypes q{t[0].quant, t[1].quant, t[2].quant, t[3].quant,
                             t[4].quant, t[5].quant, t[6].quant, t[7].quant};
   int rc;
-  const uint64_t dims[8][2] = {{n_expert, n_embd}, {n_embd, n_ff}, {n_embd, n_ff}, {n_ff, n_embd},
+  // gate / up [gr][gc] and down [gc][gr] per expert, by orientation
+  const uint64_t gr = om ? n_ff : n_embd, gc = om ? n_embd : n_ff;
+  const uint64_t dims[8][2] = {{n_expert, n_embd}, {gr, gc}, {gr, gc}, {gc, gr},
                                {n_ff_shexp, n_embd}, {n_ff_shexp, n_embd}, {n_embd, n_ff_shexp}, {1, n_embd}};
   for (int i = 0; i < 8; ++i)
     if ((rc = check_matrix(t[i].quant, dims[i][0], dims[i][1], 1, ~uint64_t(0), i == 0 || i >= 4))) return rc;
   sh::MoeLayerPlan plan;
-  if ((rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &plan))) return rc;
+  if ((rc = moe_layer_check(n_expert, n_embd, n_ff, n_ff_shexp, n_tok, top_k, q, &plan, om == 1))) return rc;
   if (workspace_bytes < plan.bytes)
     return fail(SH_ERR_INVALID_ARGUMENT, "workspace of %llu bytes, %llu needed",
                 (unsigned long long)workspace_bytes, (unsigned long long)plan.bytes);

@@ -27,280 +27,11 @@
 #include <atomic>
 
 #include "common.hpp"
+#include "fmt.hpp"
 #include "kernels.hpp"
+#include "limb.hpp"
 
 namespace sh {
-
-// ---------------------------------------------------------------- x slice --
-struct XSlice {
-  f32x4 v[16];  // the lane's 64 floats, in column order
-  f32x4 s;      // sums of x over its four 16-column groups
-};
-
-// LDS layout of one x vector with `cols` columns: floats at e + 4*(e/64),
-// then cols/16 partial sums.
-__host__ __device__ inline int x_stride(int cols) { return cols + cols / 16 + cols / 16; }
-
-__device__ __forceinline__ void load_xslice(const float* xs, int cols, int unit, XSlice& o) {
-  const f32x4* p = reinterpret_cast<const f32x4*>(xs + 64 * unit + 4 * unit);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o.v[i] = p[i];
-  const float* sums = xs + cols + cols / 16;
-  o.s = *reinterpret_cast<const f32x4*>(sums + 4 * unit);
-}
-
-// Stage nb vectors of x (row-major [nb][cols]) into LDS with per-16 sums.
-__device__ __forceinline__ void stage_x(float* lds, const float* __restrict__ x, int cols, int nb) {
-  const int groups = cols / 16;
-  for (int t = threadIdx.x; t < nb * groups; t += blockDim.x) {
-    int b = t / groups, g = t - b * groups;
-    const f32x4* src = reinterpret_cast<const f32x4*>(x + int64_t(b) * cols + 16 * g);
-    f32x4 a = src[0], c = src[1], e = src[2], f = src[3];
-    float* dst = lds + b * x_stride(cols);
-    int e0 = 16 * g;
-    f32x4* d = reinterpret_cast<f32x4*>(dst + e0 + 4 * (e0 >> 6));
-    d[0] = a;
-    d[1] = c;
-    d[2] = e;
-    d[3] = f;
-    float s = ((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w)) +
-              (((e.x + e.y) + (e.z + e.w)) + ((f.x + f.y) + (f.z + f.w)));
-    dst[cols + cols / 16 + g] = s;
-  }
-}
-
-// ------------------------------------------------------------------ Q4_K --
-// Unit u of a row: super-block u/4, group g = u%4 (elements 64g..64g+63 of
-// the super-block: low nibbles of qs[32g..32g+31] are sub-block 2g, high
-// nibbles sub-block 2g+1).
-struct FmtQ4K {
-  static constexpr int kR = 2;
-  static constexpr int kRing = 4;
-  struct Load {
-    u32x4 h, a, b;
-  };
-  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
-    const uint8_t* sb = row + (u >> 2) * 144;
-    int g = u & 3;
-    o.h = ld16(sb);
-    o.a = ld16(sb + 16 + 32 * g);
-    o.b = ld16(sb + 32 + 32 * g);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int u, int) {
-    const int g = u & 3;
-    // (scale, min) of sub-blocks 2g and 2g+1 in the two low bytes of scp/mp,
-    // from the packed 12 bytes (dequant.rs:237-245).
-    const uint32_t sh = (g & 1) << 4;
-    const uint32_t t1 = L.h.y >> sh, t2 = L.h.z >> sh, t3 = L.h.w >> sh;
-    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
-    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
-    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
-    uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
-    float lo0 = 0.f, lo1 = 0.f, hi0 = 0.f, hi1 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t lo = q[k] & 0x0F0F0F0Fu;  // nibble values
-      const uint32_t hi = q[k] & 0xF0F0F0F0u;  // 16 * nibble values
-      const f32x4 xl = x.v[k], xh = x.v[8 + k];
-      lo0 = __builtin_fmaf(ubyte<0>(lo), xl.x, lo0);
-      lo1 = __builtin_fmaf(ubyte<1>(lo), xl.y, lo1);
-      lo0 = __builtin_fmaf(ubyte<2>(lo), xl.z, lo0);
-      lo1 = __builtin_fmaf(ubyte<3>(lo), xl.w, lo1);
-      hi0 = __builtin_fmaf(ubyte<0>(hi), xh.x, hi0);
-      hi1 = __builtin_fmaf(ubyte<1>(hi), xh.y, hi1);
-      hi0 = __builtin_fmaf(ubyte<2>(hi), xh.z, hi0);
-      hi1 = __builtin_fmaf(ubyte<3>(hi), xh.w, hi1);
-    }
-    const float x0 = x.s.x + x.s.y, x1 = x.s.z + x.s.w;
-    const float qsum = ubyte<0>(scp) * (lo0 + lo1) + (ubyte<1>(scp) * 0.0625f) * (hi0 + hi1);
-    const float msum = ubyte<0>(mp) * x0 + ubyte<1>(mp) * x1;
-    return d * qsum - dm * msum;
-  }
-};
-
-// ------------------------------------------------------------------ Q5_K --
-// Unit u of a row: super-block u/4, group g = u%4, as FmtQ4K, with the fifth
-// code bit of q5k_codes. Every lane of a super-block reads its 16 header and
-// 32 qh bytes.
-struct FmtQ5K {
-  static constexpr int kR = 2;
-  static constexpr int kRing = 4;
-  struct Load {
-    u32x4 h, h0, h1, a, b;
-  };
-  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
-    const uint8_t* sb = row + (u >> 2) * 176;
-    const int g = u & 3;
-    o.h = ld16(sb);
-    o.h0 = ld16(sb + 16);
-    o.h1 = ld16(sb + 32);
-    o.a = ld16(sb + 48 + 32 * g);
-    o.b = ld16(sb + 64 + 32 * g);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int u, int) {
-    const int g = u & 3;
-    uint32_t scp, mp;
-    k4_pair(L.h, g, scp, mp);
-    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
-    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
-    const uint32_t qh[8] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w};
-    float lo0 = 0.f, lo1 = 0.f, hi0 = 0.f, hi1 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      uint32_t lo, hi;
-      q5k_codes(q[k], qh[k], uint32_t(g), lo, hi);
-      const f32x4 xl = x.v[k], xh = x.v[8 + k];
-      lo0 = __builtin_fmaf(ubyte<0>(lo), xl.x, lo0);
-      lo1 = __builtin_fmaf(ubyte<1>(lo), xl.y, lo1);
-      lo0 = __builtin_fmaf(ubyte<2>(lo), xl.z, lo0);
-      lo1 = __builtin_fmaf(ubyte<3>(lo), xl.w, lo1);
-      hi0 = __builtin_fmaf(ubyte<0>(hi), xh.x, hi0);
-      hi1 = __builtin_fmaf(ubyte<1>(hi), xh.y, hi1);
-      hi0 = __builtin_fmaf(ubyte<2>(hi), xh.z, hi0);
-      hi1 = __builtin_fmaf(ubyte<3>(hi), xh.w, hi1);
-    }
-    const float x0 = x.s.x + x.s.y, x1 = x.s.z + x.s.w;
-    const float qsum = ubyte<0>(scp) * (lo0 + lo1) + ubyte<1>(scp) * (hi0 + hi1);
-    const float msum = ubyte<0>(mp) * x0 + ubyte<1>(mp) * x1;
-    return d * qsum - dm * msum;
-  }
-};
-
-// ------------------------------------------------------------------ Q8_0 --
-// Unit u of a row: blocks 2u and 2u+1 (68 bytes, 4-byte aligned when the row
-// start is, which the launcher checks).
-struct FmtQ8 {
-  static constexpr int kR = 2;
-  static constexpr int kRing = 3;
-  struct Load {
-    u32x4 a, b, c, d;
-    uint32_t e;
-  };
-  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
-    const uint8_t* p = row + u * 68;
-    o.a = ld16(p);
-    o.b = ld16(p + 16);
-    o.c = ld16(p + 32);
-    o.d = ld16(p + 48);
-    o.e = ld4(p + 64);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int, int) {
-    const uint32_t D[17] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w, L.c.x,
-                            L.c.y, L.c.z, L.c.w, L.d.x, L.d.y, L.d.z, L.d.w, L.e};
-    const float d0 = h2f(D[0]), d1 = h2f(D[8] >> 16);
-    float s00 = 0.f, s01 = 0.f, s10 = 0.f, s11 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      // signed bytes biased to unsigned: (q + 128)
-      const uint32_t q0 = realign(D[k], D[k + 1], 2) ^ 0x80808080u;
-      const uint32_t q1 = D[9 + k] ^ 0x80808080u;
-      const f32x4 xa = x.v[k], xb = x.v[8 + k];
-      s00 = __builtin_fmaf(ubyte<0>(q0), xa.x, s00);
-      s01 = __builtin_fmaf(ubyte<1>(q0), xa.y, s01);
-      s00 = __builtin_fmaf(ubyte<2>(q0), xa.z, s00);
-      s01 = __builtin_fmaf(ubyte<3>(q0), xa.w, s01);
-      s10 = __builtin_fmaf(ubyte<0>(q1), xb.x, s10);
-      s11 = __builtin_fmaf(ubyte<1>(q1), xb.y, s11);
-      s10 = __builtin_fmaf(ubyte<2>(q1), xb.z, s10);
-      s11 = __builtin_fmaf(ubyte<3>(q1), xb.w, s11);
-    }
-    const float x0 = x.s.x + x.s.y, x1 = x.s.z + x.s.w;
-    return d0 * ((s00 + s01) - 128.f * x0) + d1 * ((s10 + s11) - 128.f * x1);
-  }
-};
-
-// ------------------------------------------------------------------ Q6_K --
-// Unit u of a row: super-block u/4, quarter j = u%4 = (half h, pair tp):
-// quadrants t0 = 2tp and t1 = 2tp+1 of half h (dequant.rs:217-229), i.e.
-// elements 64j..64j+63 of the super-block:
-//   t0, l = 0..31: low bits from ql[64h + l], high bits qh[32h + l] >> 2*t0
-//   t1, l = 0..31: low bits from ql[64h + 32 + l], high bits >> 2*t1
-//   the nibble is the low one for tp = 0 and the high one for tp = 1;
-//   sub-block scales sc[8h + 4tp + {0,1,2,3}] cover 16 elements each.
-// Super-blocks are 210 bytes, so a block starts at a 2-byte boundary: loads
-// go through the dword-aligned address at or below it and are realigned by
-// `shift` (0 or 2) bytes. No load leaves the block's own 210 bytes.
-struct FmtQ6K {
-  static constexpr int kR = 1;
-  static constexpr int kRing = 4;
-  struct Load {
-    u32x4 l0, l1, l2, l3;
-    uint32_t l4;
-    u32x4 h0, h1;
-    uint32_t h2;
-    uint32_t s0, s1;
-    uint32_t d;
-    uint32_t shift;
-  };
-  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
-    const uint8_t* blk = row + (u >> 2) * 210;
-    const int j = u & 3, h = j >> 1, tp = j & 1;
-    const uint32_t shift = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
-    const uint8_t* base = blk - shift;
-    const uint8_t* ql = base + 64 * h;
-    o.l0 = ld16(ql);
-    o.l1 = ld16(ql + 16);
-    o.l2 = ld16(ql + 32);
-    o.l3 = ld16(ql + 48);
-    o.l4 = ld4(ql + 64);  // ends at most at byte 131 of the block
-    const uint8_t* qh = base + 128 + 32 * h;
-    o.h0 = ld16(qh);
-    o.h1 = ld16(qh + 16);
-    o.h2 = ld4(qh + 32);  // ends at most at byte 195
-    const uint8_t* sc = base + 192 + 8 * h + 4 * tp;
-    o.s0 = ld4(sc);
-    // a second dword is needed (and stays inside the block) only when the
-    // block is misaligned; aligned, it could run 2 bytes past the block
-    o.s1 = shift ? ld4(sc + 4) : 0u;
-    o.d = *reinterpret_cast<const uint16_t*>(blk + 208);
-    o.shift = shift;
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int u, int q6_signed) {
-    const uint32_t tp = uint32_t(u) & 1u;
-    const uint32_t s = L.shift;
-    const uint32_t qlr[17] = {L.l0.x, L.l0.y, L.l0.z, L.l0.w, L.l1.x, L.l1.y, L.l1.z, L.l1.w, L.l2.x,
-                              L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
-    const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
-    const uint32_t scw = realign(L.s0, L.s1, s);
-    const uint32_t nib = 4u * tp;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // one per 16-element sub-block
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      // high 2 bits of quadrant t0 moved to bits 4-5 of each byte
-      const uint32_t qs = tp ? qh : (qh << 4);
-      const uint32_t a = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      const uint32_t b =
-          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
-      const f32x4 xa = x.v[k], xb = x.v[8 + k];
-      float& ca = acc[k >> 2];
-      float& cb = acc[2 + (k >> 2)];
-      ca = __builtin_fmaf(ubyte<0>(a), xa.x, ca);
-      ca = __builtin_fmaf(ubyte<1>(a), xa.y, ca);
-      ca = __builtin_fmaf(ubyte<2>(a), xa.z, ca);
-      ca = __builtin_fmaf(ubyte<3>(a), xa.w, ca);
-      cb = __builtin_fmaf(ubyte<0>(b), xb.x, cb);
-      cb = __builtin_fmaf(ubyte<1>(b), xb.y, cb);
-      cb = __builtin_fmaf(ubyte<2>(b), xb.z, cb);
-      cb = __builtin_fmaf(ubyte<3>(b), xb.w, cb);
-    }
-    float sc0, sc1, sc2, sc3;
-    if (q6_signed) {
-      sc0 = float(int8_t(scw & 0xFFu));
-      sc1 = float(int8_t((scw >> 8) & 0xFFu));
-      sc2 = float(int8_t((scw >> 16) & 0xFFu));
-      sc3 = float(int8_t(scw >> 24));
-    } else {
-      sc0 = ubyte<0>(scw);
-      sc1 = ubyte<1>(scw);
-      sc2 = ubyte<2>(scw);
-      sc3 = ubyte<3>(scw);
-    }
-    const float t = sc0 * (acc[0] - 32.f * x.s.x) + sc1 * (acc[1] - 32.f * x.s.y) +
-                    sc2 * (acc[2] - 32.f * x.s.z) + sc3 * (acc[3] - 32.f * x.s.w);
-    return h2f(L.d) * t;
-  }
-};
 
 // ---------------------------------------------------------------- kernel --
 // One launch computes y[b][r] for all rows, b < NB. Each wave walks items
@@ -544,391 +275,6 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
     }
   }
 }
-
-// ================================================== batch-1 integer path ==
-// x as three int8 limbs. Each workgroup converts the f32 activations once:
-// per 32-column block a power-of-two scale 2^-k is chosen so that the block's
-// largest |x| times 2^k is below 2^22, and every element becomes the integer
-//   v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c,  a in [-64, 64], b, c in [0, 255]
-// (a is byte 2 of v, b byte 1, c byte 0, in two's complement). Each element
-// is represented to within 2^-23 of its block's maximum, as close to x as the
-// f32 activations themselves for elements near the maximum. Weight codes are
-// small non-negative integers, so the per-block dot products are exact
-// integer sums on v_dot4_i32_i8 (a) and v_dot4_u32_u8 (b, c), four weights
-// per instruction:
-//   sum_j q_j x_j = 2^-k (2^16 sum q a + (2^8 sum q b + sum q c)) + rounding of v
-// and only the per-block scale epilogue is f32.
-//
-// LDS layout for `cols` columns (bytes): three limb planes, each with a
-// 16-byte pad after every 64 bytes (so lanes reading 64-byte runs hit
-// distinct banks), then per 32-column block 16 bytes:
-//   {sum of x over columns 0-15, sum over 16-31, 2^-k, K}
-// with K = sum of (v & 0xFFFF) = sum 2^8 b + c (an integer, for the bias of
-// signed weights against the unsigned low limbs).
-__host__ __device__ inline int plane_stride(int cols) { return cols + cols / 4; }
-__host__ __device__ inline int limb_lds_bytes(int cols) { return 3 * plane_stride(cols) + (cols / 32) * 16; }
-
-// Converts 8 consecutive columns held in registers (elements 8t .. 8t + 7,
-// t the thread) and writes them to LDS. The four lanes of a 32-column block
-// are t & ~3 .. t | 3, neighbours in one quad of the wave: they exchange the
-// block's maximum and sums with DPP moves, and lane t & ~3 writes the block's
-// record. K (the integer sum of the low limbs) is formed only when LOW is
-// set: signed Q8_0 codes need it; the unsigned codes of the k-quants do not.
-template <bool LOW>
-__device__ __forceinline__ void limb_group8(uint8_t* lds, int cols, int t, bool valid, f32x4 a, f32x4 b) {
-  const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float m = 0.f, s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    m = fmaxf(m, fabsf(xs[i]));
-    s += xs[i];
-  }
-  m = fmaxf(m, dpp_xor1(m));
-  m = fmaxf(m, dpp_xor2(m));
-  const float s16 = s + dpp_xor1(s);  // the lane pair's 16 columns
-  const float s16_other = dpp_xor2(s16);
-  // k with m * 2^k < 2^22; for m == 0 any k works
-  // (clamped so 2^k stays finite for blocks whose maximum is below 2^-104)
-  int e = 0;
-  (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
-  const int k = m > 0.f ? min(22 - e, 126) : 0;
-  const float up = ldexpf(1.f, k);
-  // a NaN or infinite block keeps its NaN through the scale
-  const float down = (m - m == 0.f) ? ldexpf(1.f, -k) : __builtin_nanf("");
-  uint32_t v[8];
-  uint32_t low = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
-    const float tt = __builtin_fmaf(xs[i], up, 12582912.0f);
-    v[i] = __builtin_bit_cast(uint32_t, tt) - 0x4B400000u;
-    if constexpr (LOW) low += v[i] & 0xFFFFu;
-  }
-  if constexpr (LOW) {
-    low += dpp_xor1(low);
-    low += dpp_xor2(low);
-  }
-  if (!valid) return;
-  const int e0 = 8 * t;
-  const int off = e0 + 16 * (e0 >> 6);
-  const int ps = plane_stride(cols);
-  uint32_t pc[2], pb[2], pa[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) transpose_bytes(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], pc[q], pb[q], pa[q]);
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  *reinterpret_cast<u32x2*>(lds + off) = u32x2{pa[0], pa[1]};
-  *reinterpret_cast<u32x2*>(lds + ps + off) = u32x2{pb[0], pb[1]};
-  *reinterpret_cast<u32x2*>(lds + 2 * ps + off) = u32x2{pc[0], pc[1]};
-  if ((t & 3) == 0)
-    *reinterpret_cast<u32x4*>(lds + 3 * ps + 16 * (t >> 2)) =
-        u32x4{__builtin_bit_cast(uint32_t, s16), __builtin_bit_cast(uint32_t, s16_other),
-              __builtin_bit_cast(uint32_t, down), low};
-}
-
-// The lane's 64 columns: limb dwords for elements 4j..4j+3 and the two
-// 32-column blocks' {sum, scale}.
-struct XLimbs {
-  u32x4 a[4], b[4], c[4];
-  u32x4 i0, i1;  // the two 32-column blocks: {sum 0-15, sum 16-31, 2^-k, K} as raw words
-};
-
-__device__ __forceinline__ float fw(uint32_t bits) { return __builtin_bit_cast(float, bits); }
-
-__device__ __forceinline__ void load_limbs(const uint8_t* lds, int cols, int u, XLimbs& o) {
-  const int ps = plane_stride(cols);
-  const int off = 80 * u;  // 64 bytes + 16 pad per unit
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o.a[i] = *reinterpret_cast<const u32x4*>(lds + off + 16 * i);
-    o.b[i] = *reinterpret_cast<const u32x4*>(lds + ps + off + 16 * i);
-    o.c[i] = *reinterpret_cast<const u32x4*>(lds + 2 * ps + off + 16 * i);
-  }
-  o.i0 = *reinterpret_cast<const u32x4*>(lds + 3 * ps + 32 * u);
-  o.i1 = *reinterpret_cast<const u32x4*>(lds + 3 * ps + 32 * u + 16);
-}
-
-__device__ __forceinline__ uint32_t limb_word(const u32x4* p, int j) {
-  const u32x4 v = p[j >> 2];
-  return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
-}
-
-// Exact sum over 4 weights (bytes of `q`, each 0..127) times 4 x elements
-// (limb words a, b, c), accumulated into the three integer sums.
-__device__ __forceinline__ void dot_limbs(uint32_t q, uint32_t a, uint32_t b, uint32_t c, int& sa,
-                                          uint32_t& sb, uint32_t& sc) {
-  sa = __builtin_amdgcn_sdot4(int(q), int(a), sa, false);
-  sb = __builtin_amdgcn_udot4(q, b, sb, false);
-  sc = __builtin_amdgcn_udot4(q, c, sc, false);
-}
-
-// sum q*v = 2^16 sa + 2^8 sb + sc as f32 (2^8 sb + sc < 2^25 is exact in u32)
-__device__ __forceinline__ float limb_value(int sa, uint32_t sb, uint32_t sc) {
-  return __builtin_fmaf(float(sa), 65536.f, float(sb * 256u + sc));
-}
-
-// Sum over the 64 lanes with DPP: quad swaps, half-row and row mirrors,
-// then row broadcasts 15 and 31; lane 63 ends with the total.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false)); // row_bcast15
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false)); // row_bcast31
-  return v;
-}
-
-// Q4_K with integer dots: unit u = (super-block u/4, group g = u%4) as in
-// FmtQ4K; low nibbles are sub-block 2g (x block 2u), high nibbles 2g+1.
-struct LimbQ4K {
-  static constexpr uint32_t kQuant = kQ4_K;
-  struct Load {
-    u32x4 h, a, b;
-  };
-  static constexpr int kWinBytes = 16 * 144;  // one 4096-column window of a row
-  struct Off {
-    int h, q;
-  };
-  // h: the super-block's byte offset (advances by kWinBytes per window);
-  // q: the lane's quant bytes relative to it
-  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 144, 16 + 32 * (u & 3)}; }
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    L.h = ld16(row + o.h);
-    L.a = ld16(row + o.h + o.q);
-    L.b = ld16(row + o.h + o.q + 16);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
-    const int g = lane & 3;
-    const uint32_t sh = (g & 1) << 4;
-    const uint32_t t1 = L.h.y >> sh, t2 = L.h.z >> sh, t3 = L.h.w >> sh;
-    const uint32_t scp = g < 2 ? (t1 & 0x3F3Fu) : ((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u));
-    const uint32_t mp = g < 2 ? (t2 & 0x3F3Fu) : (((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u));
-    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
-    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
-    int a0 = 0, a1 = 0;
-    uint32_t b0 = 0, b1 = 0, c0 = 0, c1 = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t lo = q[k] & 0x0F0F0F0Fu;
-      const uint32_t hi = (q[k] >> 4) & 0x0F0F0F0Fu;
-      dot_limbs(lo, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), a0, b0, c0);
-      dot_limbs(hi, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), a1, b1, c1);
-    }
-    const float s0 = limb_value(a0, b0, c0) * fw(x.i0.z);  // sum over sub-block 2g of q * x
-    const float s1 = limb_value(a1, b1, c1) * fw(x.i1.z);  // sub-block 2g + 1
-    const float qsum = ubyte<0>(scp) * s0 + ubyte<1>(scp) * s1;
-    const float msum = ubyte<0>(mp) * (fw(x.i0.x) + fw(x.i0.y)) + ubyte<1>(mp) * (fw(x.i1.x) + fw(x.i1.y));
-    return d * qsum - dm * msum;
-  }
-};
-
-// Q5_K with integer dots: unit u as LimbQ4K; codes 0..31 (nibble plus the
-// fifth bit, q5k_codes) go into the dots unchanged.
-struct LimbQ5K {
-  static constexpr uint32_t kQuant = kQ5_K;
-  struct Load {
-    u32x4 h, h0, h1, a, b;
-  };
-  static constexpr int kWinBytes = 16 * 176;
-  struct Off {
-    int h, q;
-  };
-  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 176, 48 + 32 * (u & 3)}; }
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    L.h = ld16(row + o.h);
-    L.h0 = ld16(row + o.h + 16);
-    L.h1 = ld16(row + o.h + 32);
-    L.a = ld16(row + o.h + o.q);
-    L.b = ld16(row + o.h + o.q + 16);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
-    const int g = lane & 3;
-    uint32_t scp, mp;
-    k4_pair(L.h, g, scp, mp);
-    const float d = h2f(L.h.x), dm = h2f(L.h.x >> 16);
-    const uint32_t q[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
-    const uint32_t qh[8] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w};
-    int a0 = 0, a1 = 0;
-    uint32_t b0 = 0, b1 = 0, c0 = 0, c1 = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      uint32_t lo, hi;
-      q5k_codes(q[k], qh[k], uint32_t(g), lo, hi);
-      dot_limbs(lo, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), a0, b0, c0);
-      dot_limbs(hi, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), a1, b1, c1);
-    }
-    const float s0 = limb_value(a0, b0, c0) * fw(x.i0.z);
-    const float s1 = limb_value(a1, b1, c1) * fw(x.i1.z);
-    const float qsum = ubyte<0>(scp) * s0 + ubyte<1>(scp) * s1;
-    const float msum = ubyte<0>(mp) * (fw(x.i0.x) + fw(x.i0.y)) + ubyte<1>(mp) * (fw(x.i1.x) + fw(x.i1.y));
-    return d * qsum - dm * msum;
-  }
-};
-
-// Q8_0 with integer dots: unit u = blocks 2u and 2u+1 (68 bytes from a
-// dword-aligned address). Codes are signed: the top limb (signed) takes them
-// as they are; against the unsigned low limbs they are biased to q + 128 and
-// the bias 128 * K is removed in integers before the one f32 conversion.
-struct LimbQ8 {
-  static constexpr uint32_t kQuant = kQ8_0;
-  struct Load {
-    u32x4 a, b, c, d;
-    uint32_t e;
-  };
-  static constexpr int kWinBytes = 64 * 68;
-  struct Off {
-    int h, q;
-  };
-  __device__ static __forceinline__ Off offsets(int u) { return {u * 68, 0}; }
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    const uint8_t* p = row + o.h;
-    L.a = ld16(p);
-    L.b = ld16(p + 16);
-    L.c = ld16(p + 32);
-    L.d = ld16(p + 48);
-    L.e = ld4(p + 64);
-  }
-  __device__ static __forceinline__ float block(const uint32_t* q, const u32x4* xa, const u32x4* xb,
-                                                const u32x4* xc, int j0, u32x4 info) {
-    int sa = 0;
-    uint32_t sb = 0, sc = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t qb = q[k] ^ 0x80808080u;  // q + 128
-      sa = __builtin_amdgcn_sdot4(int(q[k]), int(limb_word(xa, j0 + k)), sa, false);
-      sb = __builtin_amdgcn_udot4(qb, limb_word(xb, j0 + k), sb, false);
-      sc = __builtin_amdgcn_udot4(qb, limb_word(xc, j0 + k), sc, false);
-    }
-    const int bc = int(sb * 256u + sc) - 128 * int(info.w);
-    return __builtin_fmaf(float(sa), 65536.f, float(bc)) * fw(info.z);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int, int) {
-    const uint32_t D[17] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w, L.c.x,
-                            L.c.y, L.c.z, L.c.w, L.d.x, L.d.y, L.d.z, L.d.w, L.e};
-    uint32_t q0[8], q1[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      q0[k] = realign(D[k], D[k + 1], 2);
-      q1[k] = D[9 + k];
-    }
-    const float d0 = h2f(D[0]), d1 = h2f(D[8] >> 16);
-    return d0 * block(q0, x.a, x.b, x.c, 0, x.i0) + d1 * block(q1, x.a, x.b, x.c, 8, x.i1);
-  }
-};
-
-// IQ4_XS with integer dots: unit u = (super-block u/4, group g = u%4), the
-// two 32-element sub-blocks 2g and 2g + 1 (elements 64g..64g+63). Each
-// sub-block's codes are code-book values kvalues_iq4nl[nibble] in
-// [-127, 113] (signed, so the dots are LimbQ8's: the top limb signed, the
-// low limbs against codes biased by 128), its scale dl = d * (ls - 32) from
-// the 6-bit ls. GGML: ggml's layout (sub-block ib reads qs[16 ib ..]); the
-// default follows the reference, whose every sub-block reads qs[0..16]
-// (dequant.rs:189-206).
-__device__ __forceinline__ uint32_t iq4_lut(uint32_t idx) {  // four nibble indices -> four int8 codes
-  const uint32_t i7 = idx & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(kIq4Tab[1], kIq4Tab[0], i7);
-  const uint32_t hi = __builtin_amdgcn_perm(kIq4Tab[3], kIq4Tab[2], i7);
-  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
-  return (hi & m) | (lo & ~m);
-}
-
-template <bool GGML>
-struct LimbIQ4XS {
-  static constexpr uint32_t kQuant = kIQ4_XS;
-  struct Load {
-    uint32_t h0, h1;  // d | scales_h, scales_l
-    u32x4 a, b;       // the qs bytes of sub-blocks 2g and 2g + 1
-  };
-  static constexpr int kWinBytes = 16 * 136;
-  struct Off {
-    int h, q;
-  };
-  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 136, GGML ? 8 + 32 * (u & 3) : 8}; }
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    L.h0 = ld4(row + o.h);
-    L.h1 = ld4(row + o.h + 4);
-    L.a = ld16u(row + o.h + o.q);
-    L.b = ld16u(row + o.h + o.q + (GGML ? 16 : 0));
-  }
-  __device__ static __forceinline__ float block(const u32x4 q, const u32x4* xa, const u32x4* xb, const u32x4* xc,
-                                                int j0, u32x4 info) {
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    int sa = 0;
-    uint32_t sb = 0, sc = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {  // elements 4k..4k+3: low nibbles of bytes 4k.. (k < 4), high nibbles after
-      const uint32_t idx = k < 4 ? (qw[k] & 0x0F0F0F0Fu) : ((qw[k - 4] >> 4) & 0x0F0F0F0Fu);
-      const uint32_t v = iq4_lut(idx);
-      const uint32_t vb = v ^ 0x80808080u;  // v + 128
-      sa = __builtin_amdgcn_sdot4(int(v), int(limb_word(xa, j0 + k)), sa, false);
-      sb = __builtin_amdgcn_udot4(vb, limb_word(xb, j0 + k), sb, false);
-      sc = __builtin_amdgcn_udot4(vb, limb_word(xc, j0 + k), sc, false);
-    }
-    const int bc = int(sb * 256u + sc) - 128 * int(info.w);
-    return __builtin_fmaf(float(sa), 65536.f, float(bc)) * fw(info.z);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
-    const uint32_t g = uint32_t(lane) & 3u;
-    const float d = h2f(L.h0);
-    const uint32_t shb = L.h0 >> 16;                     // scales_h
-    const uint32_t slb = (L.h1 >> (8 * g)) & 0xFFu;      // scales_l[g]: ls of sub-blocks 2g (low) and 2g + 1
-    const uint32_t ls0 = (slb & 0x0Fu) | (((shb >> (4 * g)) & 3u) << 4);
-    const uint32_t ls1 = (slb >> 4) | (((shb >> (4 * g + 2)) & 3u) << 4);
-    const float dl0 = d * (float(ls0) - 32.f), dl1 = d * (float(ls1) - 32.f);
-    return dl0 * block(L.a, x.a, x.b, x.c, 0, x.i0) + dl1 * block(L.b, x.a, x.b, x.c, 8, x.i1);
-  }
-};
-
-// Q6_K with integer dots: unit u = (super-block u/4, quarter j = u%4) as in
-// FmtQ6K; the 6-bit codes 0..63 go straight into the dots and the -32
-// offset is taken off with the per-16 sums of x.
-struct LimbQ6K {
-  static constexpr uint32_t kQuant = kQ6_K;
-  using Load = FmtQ6K::Load;
-  static constexpr int kWinBytes = 16 * 210;
-  struct Off {
-    int h, q;
-  };
-  // h: the super-block's byte offset, q: the quarter 0..3
-  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 210, u & 3}; }
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    FmtQ6K::load(row + o.h, o.q, L);
-  }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int q6_signed) {
-    const uint32_t tp = uint32_t(lane) & 1u;
-    const uint32_t s = L.shift;
-    const uint32_t qlr[17] = {L.l0.x, L.l0.y, L.l0.z, L.l0.w, L.l1.x, L.l1.y, L.l1.z, L.l1.w, L.l2.x,
-                              L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
-    const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
-    const uint32_t scw = realign(L.s0, L.s1, s);
-    const uint32_t nib = 4u * tp;
-    int sa[4] = {0, 0, 0, 0};
-    uint32_t sb[4] = {0, 0, 0, 0}, sc[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      const uint32_t qs = tp ? qh : (qh << 4);
-      const uint32_t va = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      const uint32_t vb =
-          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
-      const int ga = k >> 2, gb = 2 + (k >> 2);
-      dot_limbs(va, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), sa[ga], sb[ga], sc[ga]);
-      dot_limbs(vb, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), sa[gb], sb[gb], sc[gb]);
-    }
-    float scf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t byte = (scw >> (8 * i)) & 0xFFu;
-      scf[i] = q6_signed ? float(int8_t(byte)) : float(byte);
-    }
-    const float xs[4] = {fw(x.i0.x), fw(x.i0.y), fw(x.i1.x), fw(x.i1.y)};
-    const float ks[4] = {fw(x.i0.z), fw(x.i0.z), fw(x.i1.z), fw(x.i1.z)};
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t += scf[i] * (limb_value(sa[i], sb[i], sc[i]) * ks[i] - 32.f * xs[i]);
-    return h2f(L.d) * t;
-  }
-};
 
 // Batch-1 matvec on the integer path.
 //

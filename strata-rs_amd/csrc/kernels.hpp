@@ -87,11 +87,22 @@ struct MoePlan {
   size_t o_part_b;               // [pair][nch_b][n_embd]: chunk sums of down . a
   size_t route_lds, lds_a, lds_b;  // dynamic LDS per kernel
   bool staged;                   // row bytes allow 16-byte tile copies
+  bool out_major;                // expert stacks [n_expert][out][in] (moe_om.hip)
+  int om_rows_a, om_rows_b;      // out-major: rows per workgroup of gate/up and of down
   size_t bytes;
 };
 
+// out_major: gate / up [n_expert][n_ff][n_embd] and down [n_expert][n_embd]
+// [n_ff] (llama.cpp's stacks) instead of [n_expert][in][out].
 bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t q_gateup,
-              uint32_t q_down, MoePlan* plan);
+              uint32_t q_down, MoePlan* plan, bool out_major = false);
+bool moe_plan_out_major(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t q_gateup,
+                        uint32_t q_down, MoePlan* plan);
+// The gate/up and down launches of an out-major plan (route and combine as
+// launch_moe's).
+void launch_moe_out_major(const MoePlan& p, uint32_t qg, uint32_t qd, const void* gate, const void* up,
+                          const void* down, int q6g, int q6u, int q6d, const float* logits, const float* x,
+                          void* workspace, bool fused_route, hipStream_t s);
 // The shared expert's part of the layer's combine: out[t] += sigmoid(s[t])
 // * d[t] after the routed sum, once `join` (if any) has completed.
 struct MoeShared {
@@ -122,7 +133,7 @@ struct MoeLayerPlan {
   size_t bytes;
 };
 bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, int n_ff_sh,
-                    const MoeLayerTypes& q, MoeLayerPlan* plan);
+                    const MoeLayerTypes& q, MoeLayerPlan* plan, bool out_major = false);
 hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const MoeLayerTensors& w,
                             const float* x, float* out, void* workspace, hipStream_t s);
 

@@ -40,6 +40,7 @@
 #include "axpy.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "moe_items.hpp"
 
 namespace sh {
 
@@ -47,131 +48,6 @@ constexpr int kMoeThreads = 256;
 constexpr int kMoeMaxChunks = 32;    // row chunks per matrix (their sums are added in one load round)
 constexpr int kRouteThreads = 1024;  // one thread per expert in the grouping scan
 static_assert(kRouteThreads == kMoeMaxExperts, "the scan gives each thread one expert");
-
-// ------------------------------------------------------------------ route --
-// Wave-wide max / min through DPP (quad swaps, row mirrors, row
-// broadcasts; lane 63 ends with the result), returned to every lane.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  const int id = __builtin_bit_cast(int, -__builtin_inff());
-#define SH_DPP_MAX(ctrl, rm) \
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), ctrl, rm, 0xF, false)))
-  SH_DPP_MAX(0xB1, 0xF);
-  SH_DPP_MAX(0x4E, 0xF);
-  SH_DPP_MAX(0x141, 0xF);
-  SH_DPP_MAX(0x140, 0xF);
-  SH_DPP_MAX(0x142, 0xA);
-  SH_DPP_MAX(0x143, 0xC);
-#undef SH_DPP_MAX
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-__device__ __forceinline__ int wave_min_dpp(int v) {
-#define SH_DPP_MIN(ctrl, rm) v = min(v, __builtin_amdgcn_update_dpp(0x7FFFFFFF, v, ctrl, rm, 0xF, false))
-  SH_DPP_MIN(0xB1, 0xF);
-  SH_DPP_MIN(0x4E, 0xF);
-  SH_DPP_MIN(0x141, 0xF);
-  SH_DPP_MIN(0x140, 0xF);
-  SH_DPP_MIN(0x142, 0xA);
-  SH_DPP_MIN(0x143, 0xC);
-#undef SH_DPP_MIN
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
-// Routes one token with one wave (moe.rs:58-90): max-shifted softmax (f32 exp,
-// f64 sum, inv = f32(1 / sum)), k rounds of (largest probability, then lowest
-// id), ids sorted ascending, weights f32(f64(p) / max(sum_f64(p), 2^-14)).
-// sel_id / sel_p are the wave's LDS scratch (kMoeMaxTopK entries); on return
-// they hold the ids ascending and their probabilities, and lane a < K holds
-// id sel_id[a] and its weight in id_out, w_out. KPER experts per lane, with
-// KPER * 64 >= E (a larger KPER gives the same result: experts past E are
-// skipped everywhere).
-template <int KPER>
-__device__ __forceinline__ void route_token(const float* __restrict__ lg, int E, int K, int lane, int* sel_id,
-                                            float* sel_p, int& id_out, float& w_out) {
-  constexpr int kPer = KPER;
-  float p[KPER];
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = lane + kWave * j;
-    p[j] = e < E ? lg[e] : -__builtin_inff();
-    mx = fmaxf(mx, p[j]);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-  double sum = 0.0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int e = lane + kWave * j;
-    if (e < E) {
-      p[j] = expf(p[j] - mx);
-      sum += double(p[j]);
-    }
-  }
-  sum = wave_sum_f64(sum);
-  const float inv = float(1.0 / sum);
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) p[j] *= inv;
-  // top-k: k rounds of (largest p, then lowest id) over what is left; a
-  // NaN probability ranks below every number, so each round picks a valid
-  // id (k <= n_expert)
-  uint32_t taken = 0;
-  for (int r = 0; r < K; ++r) {
-    // exact: the largest remaining probability, then the lowest id holding it
-    float bp = -2.f;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      const float pj = p[j] == p[j] ? p[j] : -1.f;
-      if (e < E && !(taken >> j & 1u)) bp = fmaxf(bp, pj);
-    }
-    bp = wave_max_dpp(bp);
-    int bi = 0x7FFFFFFF;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      const float pj = p[j] == p[j] ? p[j] : -1.f;
-      if (e < E && !(taken >> j & 1u) && pj == bp) bi = min(bi, e);
-    }
-    bi = wave_min_dpp(bi);
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == 0) {
-      sel_id[r] = bi;
-      sel_p[r] = bp;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  // ids ascending: lane a < K goes to its rank among the selected ids
-  int myid = 0, rank = 0;
-  float myp = 0.f;
-  if (lane < K) {
-    myid = sel_id[lane];
-    myp = sel_p[lane];
-    for (int b = 0; b < K; ++b) rank += sel_id[b] < myid;
-  }
-  __builtin_amdgcn_wave_barrier();
-  if (lane < K) {
-    sel_id[rank] = myid;
-    sel_p[rank] = myp;
-  }
-  __builtin_amdgcn_wave_barrier();
-  // f64 renormalisation in ascending-id order (moe.rs:80-90)
-  double wsum = 0.0;
-  for (int a = 0; a < K; ++a) wsum += double(sel_p[a]);
-  const double sden = wsum > 6.103515625e-05 ? wsum : 6.103515625e-05;  // 2^-14
-  id_out = 0;
-  w_out = 0.f;
-  if (lane < K) {
-    id_out = sel_id[lane];
-    w_out = float(double(sel_p[lane]) / sden);
-  }
-}
 
 // KPER: experts per lane (KPER * 64 >= n_expert)
 template <int KPER>
@@ -478,45 +354,9 @@ __global__ void __launch_bounds__(kMoeThreads)
                       const float* __restrict__ logits) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x, m = blockIdx.y, s = blockIdx.z;
-  int n_items, e, p0, cnt, tok0 = 0, tok1 = 0;
-  if constexpr (ROUTE) {
-    __shared__ int r_id[kMoeMaxTopK];
-    __shared__ float r_p[kMoeMaxTopK];
-    const int K = plan.top_k;
-    if (threadIdx.x < kWave) {
-      const int a = threadIdx.x;
-      int id;
-      float wv;
-      route_token<4>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
-      if (c == 0 && m == 0 && s == 0 && a < K) {
-        reinterpret_cast<int*>(ws + plan.o_ids)[a] = id;
-        reinterpret_cast<float*>(ws + plan.o_wts)[a] = wv;
-        reinterpret_cast<int*>(ws + plan.o_item_e)[a] = id;
-        reinterpret_cast<int*>(ws + plan.o_item_off)[a] = a;
-        reinterpret_cast<int*>(ws + plan.o_item_cnt)[a] = 1;
-        reinterpret_cast<int*>(ws + plan.o_item_tok)[2 * a] = 0;
-        reinterpret_cast<int*>(ws + plan.o_item_tok)[2 * a + 1] = 0;
-        reinterpret_cast<int*>(ws + plan.o_tokpair)[a] = a;
-        if (a == 0) reinterpret_cast<int*>(ws + plan.o_meta)[0] = K;
-      }
-    }
-    __syncthreads();
-    n_items = K;
-    if (s >= n_items) return;
-    e = r_id[s];
-    p0 = s;
-    cnt = 1;
-  } else {
-    // all of the item's fields at once (the tables hold z_max entries, so
-    // an item past the count reads allocated memory before returning)
-    n_items = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
-    e = reinterpret_cast<const int*>(ws + plan.o_item_e)[s];
-    p0 = reinterpret_cast<const int*>(ws + plan.o_item_off)[s];
-    cnt = reinterpret_cast<const int*>(ws + plan.o_item_cnt)[s];
-    tok0 = reinterpret_cast<const int*>(ws + plan.o_item_tok)[2 * s];
-    tok1 = reinterpret_cast<const int*>(ws + plan.o_item_tok)[2 * s + 1];
-    if (s >= n_items) return;
-  }
+  MoeItem it;
+  if (!moe_item<ROUTE>(plan, ws, logits, s, c == 0 && m == 0 && s == 0, it)) return;
+  const int e = it.e, p0 = it.p0, cnt = it.cnt, tok0 = it.tok0, tok1 = it.tok1;
   float* part = reinterpret_cast<float*>(ws + plan.o_part_a);
   const int r0 = c * plan.ca, nrows = min(plan.ca, plan.n_embd - r0);
   const int tile_cap = (plan.sr_a * int(plan.rb_a) + 31) & ~15;
@@ -593,11 +433,9 @@ __global__ void __launch_bounds__(kMoeThreads)
     moe_down_kernel(const uint8_t* __restrict__ down, MoePlan plan, uint8_t* ws, int q6_down) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x, s = blockIdx.y;
-  const int n_items = reinterpret_cast<const int*>(ws + plan.o_meta)[0];
-  const int e = reinterpret_cast<const int*>(ws + plan.o_item_e)[s];
-  const int p0 = reinterpret_cast<const int*>(ws + plan.o_item_off)[s];
-  const int cnt = reinterpret_cast<const int*>(ws + plan.o_item_cnt)[s];
-  if (s >= n_items) return;
+  MoeItem it;
+  if (!moe_item<false>(plan, ws, nullptr, s, false, it)) return;
+  const int e = it.e, p0 = it.p0, cnt = it.cnt;
   const float* pa = reinterpret_cast<const float*>(ws + plan.o_part_a);
   float* part = reinterpret_cast<float*>(ws + plan.o_part_b);
   const int r0 = c * plan.cb, nrows = min(plan.cb, plan.n_ff - r0);
@@ -687,10 +525,11 @@ static int sub_rows(int64_t rb, int cols, int chunk, int tp) {
 }
 
 bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t qa, uint32_t qb,
-              MoePlan* plan) {
+              MoePlan* plan, bool out_major) {
   if (n_tok <= 0 || top_k <= 0 || top_k > kMoeMaxTopK || top_k > n_expert ||
-      n_expert > kMoeMaxExperts || n_embd <= 0 || n_ff <= 0)
+      n_expert > kMoeMaxExperts || n_embd <= 0 || n_ff <= 0 || n_tok > kMoeMaxTokens)
     return false;
+  if (out_major) return moe_plan_out_major(n_tok, top_k, n_expert, n_embd, n_ff, qa, qb, plan);
   if (!expert_shape_ok(qa, n_embd, n_ff) || !expert_shape_ok(qb, n_ff, n_embd)) return false;
   if (n_tok > kMoeMaxTokens || n_embd % 32 != 0) return false;
   // one thread per 32-column half unit of a row at least
@@ -811,17 +650,21 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
     hipError_t e = launch_moe_route(p, logits, workspace, s);
     if (e != hipSuccess) return e;
   }
-  switch (qg) {
-    case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
-    case kQ5_K: launch_gateup<HxQ5K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
-    case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
-    default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
-  }
-  switch (qd) {
-    case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
-    case kQ5_K: launch_down<HxQ5K>(p, down, ws, q6d, s); break;
-    case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
-    default: launch_down<HxQ6K>(p, down, ws, q6d, s);
+  if (p.out_major) {
+    launch_moe_out_major(p, qg, qd, gate, up, down, q6g, q6u, q6d, logits, x, workspace, fused_route, s);
+  } else {
+    switch (qg) {
+      case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+      case kQ5_K: launch_gateup<HxQ5K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+      case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+      default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);  // kQ6_K
+    }
+    switch (qd) {
+      case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
+      case kQ5_K: launch_down<HxQ5K>(p, down, ws, q6d, s); break;
+      case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
+      default: launch_down<HxQ6K>(p, down, ws, q6d, s);  // kQ6_K
+    }
   }
   if (shared && shared->join) {
     const hipError_t e = hipStreamWaitEvent(s, shared->join, 0);

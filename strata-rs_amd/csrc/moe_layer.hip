@@ -47,9 +47,9 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* h, int64_t n, 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, int n_ff_sh,
-                    const MoeLayerTypes& q, MoeLayerPlan* plan) {
+                    const MoeLayerTypes& q, MoeLayerPlan* plan, bool out_major) {
   MoeLayerPlan p{};
-  if (!moe_plan(n_tok, top_k, n_expert, n_embd, n_ff, q.gate, q.down, &p.moe)) return false;
+  if (!moe_plan(n_tok, top_k, n_expert, n_embd, n_ff, q.gate, q.down, &p.moe, out_major)) return false;
   if (q.up != q.gate || n_ff_sh <= 0) return false;
   // the matvecs of the layer, at the shapes the gemv kernels take
   if (!gemv_shape_ok(q.router, n_expert, n_embd, 1) || !gemv_shape_ok(q.gate_sh, n_ff_sh, n_embd, 1) ||

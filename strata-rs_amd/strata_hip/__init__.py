@@ -330,7 +330,8 @@ class QuantTensor:
 
 @dataclass
 class ExpertView:
-    """weights.rs:14-34: expert-major ``[n_expert][rows = in][cols = out]``."""
+    """weights.rs:14-34: expert-major ``[n_expert][rows = in][cols = out]``; with
+    ``FLAG_EXPERT_OUT_MAJOR`` llama.cpp's ``[n_expert][rows = out][cols = in]``."""
     name: str
     quant: int
     n_expert: int
@@ -600,6 +601,10 @@ class HipBackend:
         if xv.ndim == 1:
             xv, lg = xv[None, :], lg.reshape(1, -1)
         n_tok = xv.shape[0]
+        n_embd = gate.cols if gate.flags & FLAG_EXPERT_OUT_MAJOR else gate.rows
+        if xv.ndim != 2 or xv.shape[1] != n_embd or lg.shape != (n_tok, gate.n_expert):
+            raise ShapeError(SH_ERR_SHAPE, f"x {xv.shape} and logits {lg.shape} do not fit "
+                                           f"{gate.n_expert} experts of width {n_embd}")
         out = np.empty_like(xv)
         g, u, d = gate._c(), up._c(), down._c()
         check(self._L.sh_moe_ffn(self._ctx, C.byref(g), C.byref(u), C.byref(d), lg.ctypes.data, n_tok,
@@ -615,6 +620,8 @@ class HipBackend:
         xv = np.ascontiguousarray(x, dtype=np.float32)
         if xv.ndim == 1:
             xv = xv[None, :]
+        if xv.ndim != 2 or xv.shape[1] != router.cols:
+            raise ShapeError(SH_ERR_SHAPE, f"x has shape {xv.shape}, want [n_tok][{router.cols}]")
         out = np.empty_like(xv)
         cs = [t._c() for t in (router, gate, up, down, gate_shexp, up_shexp, down_shexp, gate_inp_shexp)]
         check(self._L.sh_moe_layer(self._ctx, *(C.byref(c) for c in cs), xv.ctypes.data, xv.shape[0], top_k,

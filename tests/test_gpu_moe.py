@@ -471,17 +471,3 @@ def test_moe_ffn_budget_holding_two_of_three_refuses(oracle, moe_config_tensors)
         out = be.moe_ffn(g, u, d, logits, x, top_k)
     ref = oracle_moe(oracle, 12, 14, n_expert, n_embd, n_ff, gate, up, down, logits, x, top_k)
     check_parity(out, ref, "moe")
-
-
-def test_fused_moe_refuses_out_major_views(backend):
-    n_expert, n_embd, n_ff, top_k, n_tok = 8, 256, 256, 2, 1
-    say("moe ffn out-major refused")
-    gate, up, down = expert_tensors(n_expert, n_embd, n_ff, 12, 14, 6300)
-    logits = S.router_logits(6310, n_tok, n_expert)
-    x = S.normal_f32(6320, n_tok * n_embd).reshape(n_tok, n_embd)
-    om = H.FLAG_EXPERT_OUT_MAJOR
-    g = H.ExpertView("om.g", 12, n_expert, n_ff, n_embd, gate, flags=om)
-    u = H.ExpertView("om.u", 12, n_expert, n_ff, n_embd, up, flags=om)
-    d = H.ExpertView("om.d", 14, n_expert, n_embd, n_ff, down, flags=om)
-    with pytest.raises(H.UnsupportedShapeError):
-        backend.moe_ffn(g, u, d, logits, x, top_k)

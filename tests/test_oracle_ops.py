@@ -202,6 +202,50 @@ def test_routed_combine_is_its_composition(oracle):
     assert np.array_equal(out, want)
 
 
+def test_routed_out_major_is_the_transposed_in_major(oracle):
+    """F32 stacks can be transposed exactly: an out-major stack holding
+    W_e^T gives bit for bit the in-major result (both sum x[i] * W_e[i][o]
+    over i in f64 in the same order), which pins the out-major slice and
+    row arithmetic."""
+    n_expert, n_embd, n_ff = 5, 64, 96
+    rng = np.random.default_rng(31)
+    g_in = rng.standard_normal((n_expert, n_embd, n_ff)).astype(np.float32)
+    u_in = rng.standard_normal((n_expert, n_embd, n_ff)).astype(np.float32)
+    d_in = rng.standard_normal((n_expert, n_ff, n_embd)).astype(np.float32)
+    x = rng.standard_normal(n_embd).astype(np.float32)
+    ids, w = oracle.moe_route(rng.standard_normal(n_expert).astype(np.float32), 3)
+    tr = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1))
+    a = oracle.moe_routed(0, 0, 0, n_expert, n_embd, n_ff, g_in.view(np.uint8), u_in.view(np.uint8),
+                          d_in.view(np.uint8), ids, w, x)
+    b = oracle.moe_routed(0, 0, 0, n_expert, n_embd, n_ff, tr(g_in).view(np.uint8), tr(u_in).view(np.uint8),
+                          tr(d_in).view(np.uint8), ids, w, x, out_major=True)
+    assert np.array_equal(a, b)
+    # and the orientation matters for a stack that is not symmetric
+    c = oracle.moe_routed(0, 0, 0, n_expert, n_embd, n_ff, tr(g_in).view(np.uint8), tr(u_in).view(np.uint8),
+                          tr(d_in).view(np.uint8), ids, w, x)
+    assert not np.array_equal(a, c)
+
+
+def test_routed_out_major_quantized_is_gemv_of_slices(oracle):
+    """Quantized out-major experts: gate_e . x is ops::gemv of rows
+    [e * n_ff, (e + 1) * n_ff) of the stack (checked through the oracle's
+    own gemv on the sliced bytes for one expert at weight 1)."""
+    n_expert, n_embd, n_ff = 3, 256, 256
+    gate = S.matrix(12, 41, n_expert * n_ff, n_embd)
+    up = S.matrix(12, 42, n_expert * n_ff, n_embd)
+    down = S.matrix(14, 43, n_expert * n_embd, n_ff)
+    x = S.normal_f32(44, n_embd)
+    rg, rd = S.row_bytes(12, n_embd), S.row_bytes(14, n_ff)
+    e = 2
+    out = oracle.moe_routed(12, 12, 14, n_expert, n_embd, n_ff, gate, up, down, np.array([e]),
+                            np.array([1.0], np.float32), x, out_major=True)
+    h = oracle.gemv(12, n_ff, n_embd, gate[e * n_ff * rg:(e + 1) * n_ff * rg], x)
+    p = oracle.gemv(12, n_ff, n_embd, up[e * n_ff * rg:(e + 1) * n_ff * rg], x)
+    a = np.array([np.float32(oracle.silu(float(v))) * p[i] for i, v in enumerate(h)], np.float32)
+    d = oracle.gemv(14, n_embd, n_ff, down[e * n_embd * rd:(e + 1) * n_embd * rd], a)
+    assert np.array_equal(out, d)
+
+
 def test_silu_closed_form(oracle):
     for v in [-20.0, -1.0, 0.0, 0.5, 3.0, 40.0]:
         ref = v / (1.0 + np.exp(-v))
