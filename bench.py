@@ -190,7 +190,9 @@ def bench_moe(torch, H, S, steps):
         sets.append((tg, tu, td))
     del gate, up, down
     res = {}
-    for n_tok in (1, 16):
+    # the out-major (llama.cpp) stacks have the same byte counts, so the same
+    # buffers serve both orientations
+    for n_tok, om in ((1, 0), (16, 0), (1, H.FLAG_EXPERT_OUT_MAJOR), (16, H.FLAG_EXPERT_OUT_MAJOR)):
         variants = 8
         logits = [S.router_logits(0x5EED0044 + 97 * v + n_tok, n_tok, E) for v in range(variants)]
         uniq = []
@@ -213,12 +215,12 @@ def bench_moe(torch, H, S, steps):
             lgv = tl[v % variants]
             byts += uniq[v % variants] * per_expert
             calls.append(lambda st, tg=tg, tu=tu, td=td, lgv=lgv:
-                         H.moe_ffn_dev((S.Q4_K, 0, tg.data_ptr()), (S.Q4_K, 0, tu.data_ptr()),
-                                       (S.Q6_K, 0, td.data_ptr()), E, n_embd, n_ff, lgv.data_ptr(), n_tok,
+                         H.moe_ffn_dev((S.Q4_K, om, tg.data_ptr()), (S.Q4_K, om, tu.data_ptr()),
+                                       (S.Q6_K, om, td.data_ptr()), E, n_embd, n_ff, lgv.data_ptr(), n_tok,
                                        top_k, x.data_ptr(), out.data_ptr(), ws.data_ptr(), nb, st))
         ms = time_calls(torch, calls, steps, len(calls))
         mean_bytes = byts / len(calls)
-        res[f"moe_128x2048x768_top8_{n_tok}tok"] = {
+        res[f"moe_128x2048x768_top8_{n_tok}tok" + ("_out_major" if om else "")] = {
             "us_per_call": round(ms * 1e3, 2), "mean_unique_experts": round(sum(uniq) / variants, 2),
             "expert_bytes_GBps": round(mean_bytes / (ms * 1e-3) / 1e9, 1),
             "pct_hbm_peak": round(100 * mean_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}

@@ -8,34 +8,6 @@
 namespace sh {
 
 // ------------------------------------------------------------------ route --
-// Wave-wide max / min through DPP (quad swaps, row mirrors, row
-// broadcasts; lane 63 ends with the result), returned to every lane.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  const int id = __builtin_bit_cast(int, -__builtin_inff());
-#define SH_DPP_MAX(ctrl, rm) \
-  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), ctrl, rm, 0xF, false)))
-  SH_DPP_MAX(0xB1, 0xF);
-  SH_DPP_MAX(0x4E, 0xF);
-  SH_DPP_MAX(0x141, 0xF);
-  SH_DPP_MAX(0x140, 0xF);
-  SH_DPP_MAX(0x142, 0xA);
-  SH_DPP_MAX(0x143, 0xC);
-#undef SH_DPP_MAX
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-__device__ __forceinline__ int wave_min_dpp(int v) {
-#define SH_DPP_MIN(ctrl, rm) v = min(v, __builtin_amdgcn_update_dpp(0x7FFFFFFF, v, ctrl, rm, 0xF, false))
-  SH_DPP_MIN(0xB1, 0xF);
-  SH_DPP_MIN(0x4E, 0xF);
-  SH_DPP_MIN(0x141, 0xF);
-  SH_DPP_MIN(0x140, 0xF);
-  SH_DPP_MIN(0x142, 0xA);
-  SH_DPP_MIN(0x143, 0xC);
-#undef SH_DPP_MIN
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -43,13 +15,20 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 }
 
 // Routes one token with one wave (moe.rs:58-90): max-shifted softmax (f32 exp,
-// f64 sum, inv = f32(1 / sum)), k rounds of (largest probability, then lowest
-// id), ids sorted ascending, weights f32(f64(p) / max(sum_f64(p), 2^-14)).
+// f64 sum, inv = f32(1 / sum)), then the top k by descending probability
+// with ties to the lower id (the set the reference's k rounds of "largest
+// probability, then lowest id" pick; a NaN probability ranks below every
+// number), ids ascending, weights f32(f64(p) / max(sum_f64(p), 2^-14)).
+// The k largest are found without k serial rounds: probabilities become
+// order-preserving integer keys (p >= 0, so its bits; NaN and experts past E
+// below them), a 32-step bisection over the key bits finds the k-th largest
+// key T with wave ballots, every key above T is taken and the ties at T go
+// to the lowest ids.
 // sel_id / sel_p are the wave's LDS scratch (kMoeMaxTopK entries); on return
 // they hold the ids ascending and their probabilities, and lane a < K holds
 // id sel_id[a] and its weight in id_out, w_out. KPER experts per lane, with
 // KPER * 64 >= E (a larger KPER gives the same result: experts past E are
-// skipped everywhere).
+// never selected, k <= E).
 template <int KPER>
 __device__ __forceinline__ void route_token(const float* __restrict__ lg, int E, int K, int lane, int* sel_id,
                                             float* sel_p, int& id_out, float& w_out) {
@@ -75,49 +54,49 @@ __device__ __forceinline__ void route_token(const float* __restrict__ lg, int E,
   }
   sum = wave_sum_f64(sum);
   const float inv = float(1.0 / sum);
+  uint32_t key[KPER];
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) p[j] *= inv;
-  // top-k: k rounds of (largest p, then lowest id) over what is left; a
-  // NaN probability ranks below every number, so each round picks a valid
-  // id (k <= n_expert)
-  uint32_t taken = 0;
-  for (int r = 0; r < K; ++r) {
-    // exact: the largest remaining probability, then the lowest id holding it
-    float bp = -2.f;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      const float pj = p[j] == p[j] ? p[j] : -1.f;
-      if (e < E && !(taken >> j & 1u)) bp = fmaxf(bp, pj);
-    }
-    bp = wave_max_dpp(bp);
-    int bi = 0x7FFFFFFF;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int e = lane + kWave * j;
-      const float pj = p[j] == p[j] ? p[j] : -1.f;
-      if (e < E && !(taken >> j & 1u) && pj == bp) bi = min(bi, e);
-    }
-    bi = wave_min_dpp(bi);
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == 0) {
-      sel_id[r] = bi;
-      sel_p[r] = bp;
-    }
+  for (int j = 0; j < kPer; ++j) {
+    p[j] *= inv;
+    const int e = lane + kWave * j;
+    // p >= 0: its bits order like its value; NaN (1) below every number (>= 2)
+    key[j] = e >= E ? 0u : (p[j] == p[j] ? __builtin_bit_cast(uint32_t, p[j]) + 2u : 1u);
   }
-  __builtin_amdgcn_wave_barrier();
-  // ids ascending: lane a < K goes to its rank among the selected ids
-  int myid = 0, rank = 0;
-  float myp = 0.f;
-  if (lane < K) {
-    myid = sel_id[lane];
-    myp = sel_p[lane];
-    for (int b = 0; b < K; ++b) rank += sel_id[b] < myid;
+  // T: the largest key with at least K keys >= T (the K-th largest key)
+  uint32_t T = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = T | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) cnt += __popcll(__ballot(key[j] >= c));
+    if (cnt >= K) T = c;
   }
-  __builtin_amdgcn_wave_barrier();
-  if (lane < K) {
-    sel_id[rank] = myid;
-    sel_p[rank] = myp;
+  // every key above T, then the ties at T in ascending id (id = lane + 64 j)
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));  // lanes under this one
+  uint64_t sel[KPER];
+  int need = K;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    sel[j] = __ballot(key[j] > T);
+    need -= __popcll(sel[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint64_t eq = __ballot(key[j] == T);
+    const int take = min(need, __popcll(eq));
+    sel[j] |= __ballot(key[j] == T && __popcll(eq & below) < take);
+    need -= take;
+  }
+  // the selected ids ascending (j-major, then lane) into the LDS scratch
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if ((sel[j] >> lane) & 1ull) {
+      const int pos = base + __popcll(sel[j] & below);
+      sel_id[pos] = lane + kWave * j;
+      sel_p[pos] = p[j];
+    }
+    base += __popcll(sel[j]);
   }
   __builtin_amdgcn_wave_barrier();
   // f64 renormalisation in ascending-id order (moe.rs:80-90)
@@ -156,7 +135,11 @@ __device__ __forceinline__ bool moe_item(const MoePlan& plan, uint8_t* ws, const
       const int a = threadIdx.x;
       int id;
       float wv;
-      route_token<4>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
+      // as few experts per lane as the expert count needs (the bisection's
+      // ballots run per slot)
+      if (plan.n_expert <= 64) route_token<1>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
+      else if (plan.n_expert <= 128) route_token<2>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
+      else route_token<4>(logits, plan.n_expert, K, a, r_id, r_p, id, wv);
       if (writer && a < K) {
         reinterpret_cast<int*>(ws + plan.o_ids)[a] = id;
         reinterpret_cast<float*>(ws + plan.o_wts)[a] = wv;
