@@ -116,6 +116,10 @@ __device__ __forceinline__ void load_unit(const uint8_t* row, int u, typename F:
 
 // Rows [r0, r1) of one expert slice W (rows of `rb` bytes, `cols` inputs)
 // against nt (<= NT) staged vectors: out_t[row] = W[row] . v_t.
+// Rows at most 64 units wide (every lane one unit): the lane's x runs for
+// all nt vectors stay in VGPRs, and the rows of the next passes are
+// requested before the current one is computed. Wider rows loop over their
+// units.
 template <class F, int NT>
 __device__ __forceinline__ void slice_rows(const uint8_t* __restrict__ W, int64_t rb, int cols, int r0, int r1,
                                            const uint8_t* xs, int nt, float* out0, float* out1, int q6) {
@@ -127,14 +131,52 @@ __device__ __forceinline__ void slice_rows(const uint8_t* __restrict__ W, int64_
   const int L = 1 << lg, RW = kWave >> lg;  // lanes per row, rows per wave pass
   const int ul = lane & (L - 1), rr = lane >> lg;
   const int vb = om_vec_bytes(cols);
-  // one vector whose row fits the lanes: the lane's x run stays in VGPRs
-  const bool hold = NT == 1 && U <= L;
-  typename X::T xv;
-  if (hold && ul < U) X::load(xs, cols, ul, xv);
-  for (int base = r0 + wave * RW; base < r1; base += kOmWaves * RW) {
+  const int step = kOmWaves * RW;
+  auto finish = [&](float* acc, int row) {
+    // the L lanes of a row, added in a fixed butterfly order
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      for (int off = L >> 1; off >= 1; off >>= 1) acc[t] += __shfl_xor(acc[t], off, kWave);
+    if (row < r1 && ul == 0) {
+      out0[row] = acc[0];
+      if (NT > 1 && nt > 1) out1[row] = acc[NT - 1];
+    }
+  };
+  if (U <= L) {
+    // lanes past the row's units read a valid unit and discard it
+    const int uc = min(ul, U - 1);
+    const bool on = ul < U;
+    typename X::T xv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if (t < nt) X::load(xs + t * vb, cols, uc, xv[t]);
+    auto row_ptr = [&](int base) { return W + int64_t(min(base + rr, r1 - 1)) * rb; };
+    // a ring of D passes in flight (D from the size of a format's load, so
+    // that two x runs and the ring stay within the VGPR budget)
+    constexpr int D = sizeof(typename F::Load) <= 64 ? 4 : 2;
+    typename F::Load ring[D];
+    const int first = r0 + wave * RW;
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      if (first + k * step < r1) load_unit<F>(row_ptr(first + k * step), uc, ring[k]);
+    for (int base = first; base < r1; base += D * step) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        const int b = base + k * step;
+        if (b < r1) {  // wave-uniform
+          float acc[NT];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = (t < nt && on) ? F::dot(ring[k], xv[t], uc, q6) : 0.f;
+          finish(acc, b + rr);
+          if (b + D * step < r1) load_unit<F>(row_ptr(b + D * step), uc, ring[k]);
+        }
+      }
+    }
+    return;
+  }
+  for (int base = r0 + wave * RW; base < r1; base += step) {
     const int row = base + rr;
-    const bool live = row < r1;
-    const uint8_t* wr = W + int64_t(live ? row : r0) * rb;
+    const uint8_t* wr = W + int64_t(min(row, r1 - 1)) * rb;
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.f;
@@ -143,27 +185,16 @@ __device__ __forceinline__ void slice_rows(const uint8_t* __restrict__ W, int64_
       load_unit<F>(wr, u, ld);
       // the unit's position in its super-block is u's (the limb formats
       // read it from their `lane` argument)
-      if (hold) {
-        acc[0] += F::dot(ld, xv, u, q6);
-      } else {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if (t < nt) {
-            typename X::T xt;
-            X::load(xs + t * vb, cols, u, xt);
-            acc[t] += F::dot(ld, xt, u, q6);
-          }
+      for (int t = 0; t < NT; ++t) {
+        if (t < nt) {
+          typename X::T xt;
+          X::load(xs + t * vb, cols, u, xt);
+          acc[t] += F::dot(ld, xt, u, q6);
         }
       }
     }
-    // the L lanes of a row, added in a fixed butterfly order
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      for (int off = L >> 1; off >= 1; off >>= 1) acc[t] += __shfl_xor(acc[t], off, kWave);
-    if (live && ul == 0) {
-      out0[row] = acc[0];
-      if (NT > 1 && nt > 1) out1[row] = acc[NT - 1];
-    }
+    finish(acc, row);
   }
 }
 
