@@ -15,20 +15,21 @@
 //         32-element block, which the VALU scales by the weight block's scale
 //         and the activation block's scale (and subtracts the Q4_K min term).
 //
-// Workgroup tile: 256 tokens x 96 weight rows, 4 waves stacked along the
-// tokens (wave w owns tokens [64w, 64w + 64) and all 96 rows: 2 x 3 MFMA
-// tiles of 32 x 32). The weight tile, shared by the 4 waves, goes through
-// LDS (double buffered, one barrier per 64-element chunk of K). In bf16 mode
-// the activation tile does too (mm_bf16_lds_kernel: global_load_lds copies
-// into a three-slot ring); the q8 kernel, and bf16 calls whose activations
-// exceed 32-bit byte offsets, load each wave's activation fragments straight
-// from global memory (L2-resident) into registers (q8: in the fragment order
-// its pre-pass writes, one contiguous 1 KiB wave load each). The MFMA's k order is
-// free as long as A and B agree, so lane half h of k-step s holds chunk
-// elements [32h + 8s, +8) (bf16) or [32s + 16h, +16) (int8) of both operands,
-// which keeps every fragment one 16-byte load. Tiles are numbered so that the
-// 8 XCDs (workgroup i runs on XCD i % 8) each get a contiguous run of weight
-// rows, and the token tiles of one weight tile share that XCD's L2.
+// Workgroup tile: 256 tokens x 96 weight rows, K in 64-element chunks.
+// bf16 (mm_bf16_ws_kernel): 8 waves by role -- 4 consumers (wave w owns
+// tokens [64w, 64w + 64) and all 96 rows: 2 x 3 MFMA tiles of 32 x 32),
+// 3 stagers dequantizing each weight chunk into a double-buffered bf16 LDS
+// tile, one barrier per chunk; each consumer loads its activation fragments
+// from a fragment-ordered bf16 copy written by a pre-pass (1 KiB contiguous
+// a wave load) into registers two chunks ahead. q8 (mm_q8_kernel): 4 waves
+// stacked along the tokens, the weight codes staged through LDS, activation
+// fragments loaded from the pre-pass's tiled int8 copy. The MFMA's k order
+// is free as long as A and B agree, so lane half h of k-step s holds chunk
+// elements [32h + 8s, +8) (bf16) or [32s + 16h, +16) (int8) of both
+// operands, which keeps every fragment one 16-byte load. Tiles are numbered
+// so that the 8 XCDs (workgroup i runs on XCD i % 8) each get a contiguous
+// run of weight rows, and the token tiles of one weight tile share that
+// XCD's L2.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -298,13 +299,24 @@ struct StQ6K {
 
 // ----------------------------------------------------- activation pre-pass --
 // X f32 -> bf16 (round to nearest even), 8 elements per thread.
-__global__ void x_bf16_kernel(const float* __restrict__ x, uint32_t* __restrict__ xb, int64_t n8) {
+// X f32 -> bf16 (round to nearest even) in the order the bf16 kernel's
+// consumer waves load their A fragments: piece i = ((T * nchunks + c) * 4 +
+// s) * 64 + lane holds token 32 T + (lane & 31) (the last token repeated
+// past m), elements c * 64 + 32 (lane >> 5) + 8 s .. + 8, so one wave load
+// of a fragment is 1 KiB of contiguous bytes. One thread per piece.
+__global__ void x_bf16_tiled_kernel(const float* __restrict__ x, u32x4* __restrict__ xt, int m, int cols,
+                                    int64_t pieces) {
   const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= n8) return;
-  const f32x4 a = reinterpret_cast<const f32x4*>(x)[2 * i];
-  const f32x4 b = reinterpret_cast<const f32x4*>(x)[2 * i + 1];
-  reinterpret_cast<u32x4*>(xb)[i] = u32x4{pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y),
-                                          pack_bf16(b.z, b.w)};
+  if (i >= pieces) return;
+  const int lane = int(i & 63), s = int((i >> 6) & 3);
+  const int64_t rest = i >> 8;
+  const int nchunks = cols / kMmKC;
+  const int c = int(rest % nchunks);
+  const int64_t T = rest / nchunks;
+  const int64_t t = min(32 * T + (lane & 31), int64_t(m) - 1);
+  const f32x4* src = reinterpret_cast<const f32x4*>(x + t * cols + c * kMmKC + 32 * (lane >> 5) + 8 * s);
+  const f32x4 a = src[0], b = src[1];
+  xt[i] = u32x4{pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w)};
 }
 
 // X f32 -> Q8 blocks of 32: s = max|x| / 127 (f32 division), q = rne(x / s)
@@ -439,193 +451,41 @@ __device__ __forceinline__ uint32_t block_shift<StQ6K>(const uint8_t* row, int c
   return uint32_t(reinterpret_cast<uintptr_t>(row + (c >> 2) * 210)) & 3u;
 }
 
-// ------------------------------------------------------------- bf16 kernel --
+// ------------------------------------------------- bf16 kernel, 8 waves --
+// The same tile (256 tokens x 96 weight rows, K in 64-element chunks) with
+// the work split by role, so that each SIMD holds a wave that issues MFMAs
+// next to one that stages: waves 0-3 consume (tokens [64 w, 64 w + 64) x
+// all 96 rows), waves 4-6 dequantize the weight chunks (one 32-element run
+// of one row per lane, loads kDepth chunks ahead) into a double-buffered
+// bf16 LDS tile, wave 7 only keeps the barrier count. A consumer's
+// activation rows are its own, so it loads their fragments straight into
+// registers two chunks ahead, from the fragment-ordered copy the pre-pass
+// writes (every row tile re-reads them from L2, 1 KiB contiguous a wave
+// load), and LDS carries only the weight tile the four consumers share. One barrier
+// per chunk: during chunk c the consumers read B buffer c & 1 while B(c + 1)
+// is staged into the other one.
+constexpr int kMmWsThreads = 512;
+constexpr size_t kMmLdsWs = 2 * kMmBN * kMmRowB;
+
 template <class S>
-__global__ void __launch_bounds__(kMmThreads)
-    mm_bf16_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
-                   const uint16_t* __restrict__ xb, int m, float* __restrict__ y, int n_tiles_m, int q6s) {
-  __shared__ __attribute__((aligned(16))) uint8_t wl[2][kMmBN * kMmRowB];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__global__ void __launch_bounds__(kMmWsThreads)
+    mm_bf16_ws_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                      const u32x4* __restrict__ xt, int m, float* __restrict__ y, int n_tiles_m, int q6s) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t wlb[];  // [2][kMmBN * kMmRowB]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   int r0, t0;
   tile_of(n_tiles_m, r0, t0);
   const int nchunks = cols / kMmKC;
+  const bool consumer = wave < 4, stager = wave >= 4 && wave < 7;
 
-  // staging task of this thread: (row, piece); the first kMmBN * kPieces
-  // threads (whole waves) stage, the rest only compute
+  // B staging: lane p = tid - 256 < 192 stages row p / 2, piece p % 2
   constexpr int kTasks = kMmBN * S::kPieces;
-  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
-  const bool stager = tid < kTasks;
-  const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
-  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
-
-  const uint16_t* xr[2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int t = min(t0 + 64 * wave + 32 * mi + l32, m - 1);
-    xr[mi] = xb + int64_t(t) * cols + 32 * half;
-  }
-
-  f32x16 acc[2][3];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
-
-  auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf) {
-    uint32_t run0[8], run1[8];
-    int o0, o1;
-    Bf16Emit<S>::run(raw, c, piece, block_shift<S>(wrow, c), run0, run1, o0, o1, q6s);
-    uint8_t* dst = buf + srow * kMmRowB;
-    *reinterpret_cast<u32x4*>(dst + 2 * o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
-    *reinterpret_cast<u32x4*>(dst + 2 * o0 + 16) = u32x4{run0[4], run0[5], run0[6], run0[7]};
-    *reinterpret_cast<u32x4*>(dst + 2 * o1) = u32x4{run1[0], run1[1], run1[2], run1[3]};
-    *reinterpret_cast<u32x4*>(dst + 2 * o1 + 16) = u32x4{run1[4], run1[5], run1[6], run1[7]};
-  };
-
-  // weight chunks are requested kDepth chunks ahead of their staging: the
-  // ring slot of chunk c is c % kDepth, and the loop is unrolled by kDepth so
-  // every slot index is a constant
-  typename S::Raw raw[kDepth];
-  if (stager) {
-#pragma unroll
-    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
-    stage(raw[0], 0, wl[0]);
-    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
-  }
-  bf16x8 xc[2][4];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) xc[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + 8 * s);
-  __syncthreads();
-
-  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
-#pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      const int c = c0 + j;
-      if (c < nchunks) {  // uniform
-        const bool more = c + 1 < nchunks;
-        bf16x8 xn[2][4];
-        if (more) {
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-              xn[mi][s] = *reinterpret_cast<const bf16x8*>(xr[mi] + int64_t(c + 1) * kMmKC + 8 * s);
-        }
-        const uint8_t* wb = wl[c & 1];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          bf16x8 bfr[3];
-#pragma unroll
-          for (int ni = 0; ni < 3; ++ni)
-            bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 3; ++ni)
-              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xc[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
-        }
-        if (more) {
-          const int slot = (j + 1) % kDepth;  // chunk c + 1 (a constant once unrolled)
-          if (stager) {
-            stage(raw[slot], c + 1, wl[(c + 1) & 1]);
-            raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
-          }
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) xc[mi][s] = xn[mi][s];
-        }
-        __syncthreads();
-      }
-    }
-  }
-
-  // D layout of the 32x32 MFMA: lane l holds column l % 32 (a weight row)
-  // and, in register i, row 8 * (i / 4) + 4 * (l / 32) + i % 4 (a token)
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 3; ++ni) {
-      const int r = r0 + 32 * ni + l32;
-      if (r >= n_rows) continue;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = t0 + 64 * wave + 32 * mi + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (t < m) y[int64_t(t) * n_rows + r] = acc[mi][ni][i];
-      }
-    }
-}
-
-// ------------------------------------------------ bf16 kernel, LDS operands --
-// The same tile and MFMA as mm_bf16_kernel with the activations staged too:
-// chunk c's 256 tokens x 64 bf16 (32 KiB) are copied with global_load_lds
-// (no registers hold them in flight; each wave load covers 8 token rows of
-// 128 contiguous bytes) into a ring of three slots, two chunks ahead. Lane p
-// fetches the logical 16-byte chunk that belongs in physical slot p: row r
-// keeps logical chunk cc at physical cc ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1),
-// so fragment reads of 8 or 16 consecutive rows hit distinct bank groups.
-// Every thread stages weights (threads past the 96 * kPieces tasks repeat one
-// and write the same bytes), as straight-line code in the MFMAs' basic block.
-constexpr int kMmRing = 3;
-constexpr int kMmATile = kMmBM * kMmKC * 2;
-constexpr size_t kMmLdsBf16 = size_t(kMmRing) * kMmATile + 2 * kMmBN * kMmRowB;
-
-__device__ __forceinline__ int a_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
-template <class S>
-__global__ void __launch_bounds__(kMmThreads)
-    mm_bf16_lds_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
-                       const uint16_t* __restrict__ xb, int m, float* __restrict__ y, int n_tiles_m, int q6s) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  uint8_t* at = lds;                              // [kMmRing][kMmBM][128]
-  uint8_t* wlb = lds + kMmRing * kMmATile;        // [2][kMmBN * kMmRowB]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, l32 = lane & 31;
-  int r0, t0;
-  tile_of(n_tiles_m, r0, t0);
-  const int nchunks = cols / kMmKC;
-
-  constexpr int kTasks = kMmBN * S::kPieces;
-  static_assert(kTasks <= kMmThreads, "staging tasks fit the workgroup");
-  const int task = tid % kTasks;
+  static_assert(kTasks == 3 * kWave, "waves 4-6 stage one task a lane");
+  const int task = max(tid - 4 * kWave, 0) % kTasks;
   const int srow = task / S::kPieces, piece = task % S::kPieces;
   const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
-
-  // this wave's 8 wave loads of a chunk: tile rows 64 wave + 8 i + lane / 8,
-  // as byte offsets from the chunk's first column (m * cols * 2 < 2^32 is
-  // checked on the host), added to a wave-uniform base
-  uint32_t aoffs[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 64 * wave + 8 * i + (lane >> 3);
-    const int cc = (lane & 7) ^ a_swz(r);
-    aoffs[i] = uint32_t(min(t0 + r, m - 1)) * uint32_t(cols) * 2u + 16u * uint32_t(cc);
-  }
-  const uint8_t* xbytes = reinterpret_cast<const uint8_t*>(xb);
-  auto issue_a = [&](int c) {
-    uint8_t* slot = at + (c % kMmRing) * kMmATile + 8 * wave * 1024;
-    const uint8_t* base = xbytes + int64_t(c) * kMmKC * 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) copy16_to_lds(base + aoffs[i], slot + 1024 * i);
-  };
-  // fragment offsets in a slot: row 64 wave + 32 mi + l32, logical chunk 4 half + s
-  int aoff[2][4];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int r = 64 * wave + 32 * mi + l32;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) aoff[mi][s] = r * 128 + 16 * ((4 * half + s) ^ a_swz(r));
-  }
-
-  f32x16 acc[2][3];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
-
   auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf) {
     uint32_t run0[8], run1[8];
     int o0, o1;
@@ -637,54 +497,77 @@ __global__ void __launch_bounds__(kMmThreads)
     *reinterpret_cast<u32x4*>(dst + 2 * o1 + 16) = u32x4{run1[4], run1[5], run1[6], run1[7]};
   };
 
-  issue_a(0);
-  if (nchunks > 1) issue_a(1);
-  // weight chunks requested kDepth ahead of their staging (ring slot of
-  // chunk c: c % kDepth; the loop is unrolled by kDepth so it is a constant)
-  typename S::Raw raw[kDepth];
+  // consumer A fragments from the tiled pre-pass (x_bf16_tiled_kernel): lane
+  // half h of k-step s holds chunk elements [32 h + 8 s, +8) of token 32 T +
+  // l32, T the 32-token tile of M-subtile mi (clamped to the last tile)
+  const int n_tt = (m + 31) >> 5;
+  const uint8_t* xtile[2];
 #pragma unroll
-  for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
-  stage(raw[0], 0, wlb);
-  raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
+  for (int mi = 0; mi < 2; ++mi) {
+    const int T = min((t0 + 64 * (wave & 3) + 32 * mi) >> 5, n_tt - 1);
+    xtile[mi] = reinterpret_cast<const uint8_t*>(xt) + int64_t(T) * nchunks * 4096 + 16 * lane;
+  }
+  bf16x8 afr[2][2][4];  // [chunk parity][mi][s]
+  auto load_a = [&](int c, bf16x8 (*dst)[4]) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        dst[mi][s] = *reinterpret_cast<const bf16x8*>(xtile[mi] + int64_t(c) * 4096 + 1024 * s);
+  };
+  f32x16 acc[2][3];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+
+  typename S::Raw raw[kDepth];
+  if (consumer) {
+    load_a(0, afr[0]);
+    load_a(min(1, nchunks - 1), afr[1]);
+  } else if (stager) {
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    stage(raw[0], 0, wlb);
+    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
+  }
+  lds_barrier();
 
   for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) {
       const int c = c0 + j;
       if (c < nchunks) {  // uniform
-        // A(c) has landed once at most 8 later vector memory operations (the
-        // copies of A(c + 1), or weight loads issued after them) remain; the
-        // barrier then covers every wave's copies and the staged B(c)
-        if (c + 1 < nchunks) wait_vmem<8>();
-        else wait_vmem<0>();
-        lds_barrier();
-        if (c + 2 < nchunks) issue_a(c + 2);  // into the slot of chunk c - 1: every wave is past it
-        const uint8_t* as = at + (c % kMmRing) * kMmATile;
-        const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
+        if (consumer) {
+          const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
+          bf16x8 (*a)[4] = afr[j & 1];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          bf16x8 afr[2], bfr[3];
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) afr[mi] = *reinterpret_cast<const bf16x8*>(as + aoff[mi][s]);
-#pragma unroll
-          for (int ni = 0; ni < 3; ++ni)
-            bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
+          for (int s = 0; s < 4; ++s) {
+            bf16x8 bfr[3];
 #pragma unroll
             for (int ni = 0; ni < 3; ++ni)
-              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+              bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+              for (int ni = 0; ni < 3; ++ni)
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
+          }
+          // chunk c + 2 into the registers chunk c used (past the end: the last chunk again)
+          load_a(min(c + 2, nchunks - 1), a);
+        } else if (stager) {
+          // B(c + 1) into the buffer chunk c - 1 used; past the last chunk
+          // this re-stages the last one into the buffer nobody reads
+          const int slot = (j + 1) % kDepth;
+          stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
+          raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
         }
-        // the next weight chunk into the buffer of chunk c - 1 (every wave is
-        // past it); past the last chunk this re-stages the last one into the
-        // buffer nobody reads
-        const int slot = (j + 1) % kDepth;
-        stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
-        raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+        lds_barrier();
       }
     }
   }
 
+  if (!consumer) return;
   // D layout of the 32x32 MFMA: lane l holds column l % 32 (a weight row)
   // and, in register i, row 8 * (i / 4) + 4 * (l / 32) + i % 4 (a token)
 #pragma unroll
@@ -908,7 +791,7 @@ bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint
 }
 
 size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
-  if (mode == 0) return align256(size_t(m) * size_t(cols) * 2);
+  if (mode == 0) return align256(size_t((m + 31) / 32 * 32) * size_t(cols) * 2);  // whole 32-token tiles
   const size_t mp = size_t((m + 31) / 32 * 32);  // tokens padded to whole 32-token tiles
   const size_t blocks = mp * size_t(cols / 32);
   return align256(mp * size_t(cols)) + 2 * align256(blocks * sizeof(float));
@@ -920,13 +803,8 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
   const int ntm = (m + kMmBM - 1) / kMmBM, ntn = (rows + kMmBN - 1) / kMmBN;
   const dim3 grid(unsigned(ntm * ntn));
   if (mode == 0) {
-    // activations staged through LDS when their byte offsets fit 32 bits
-    if (uint64_t(m) * uint64_t(cols) * 2u < (uint64_t(1) << 32))
-      hipLaunchKernelGGL(mm_bf16_lds_kernel<S>, grid, dim3(kMmThreads), kMmLdsBf16, s, w, rows, cols, rb,
-                         reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
-    else
-      hipLaunchKernelGGL(mm_bf16_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
-                         reinterpret_cast<const uint16_t*>(ws), m, y, ntm, q6s);
+    hipLaunchKernelGGL(mm_bf16_ws_kernel<S>, grid, dim3(kMmWsThreads), kMmLdsWs, s, w, rows, cols, rb,
+                       reinterpret_cast<const u32x4*>(ws), m, y, ntm, q6s);
   } else if constexpr (S::kQ8) {
     const size_t mp = size_t((m + 31) / 32 * 32);
     const size_t blocks = mp * size_t(cols / 32);
@@ -956,9 +834,9 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int64_t rb = byte_size(quant, cols);
   if (mode == 0) {
-    const int64_t n8 = m * cols / 8;
-    hipLaunchKernelGGL(x_bf16_kernel, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s, x,
-                       reinterpret_cast<uint32_t*>(ws), n8);
+    const int64_t pieces = (m + 31) / 32 * 32 * cols / 8;  // 16-byte pieces of whole 32-token tiles
+    hipLaunchKernelGGL(x_bf16_tiled_kernel, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s, x,
+                       reinterpret_cast<u32x4*>(ws), int(m), int(cols), pieces);
   } else {
     const size_t mp = size_t((m + 31) / 32 * 32);
     const size_t blocks = mp * size_t(cols / 32);
