@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn"),
+    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn", "blaslt"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
                          "'moe' / 'prefill' / 'rowops' / 'ffn': that extra alone (for profiling; prints its JSON)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -170,6 +170,36 @@ def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):
             "peak_TFLOPs": peak, "frac_of_peak": round(tf / peak, 4)}
         del ws
     del w, x, y
+    return res
+
+
+def bench_blaslt_reference(torch, steps):
+    """The library GEMM the prefill kernel is measured beside: torch's bf16
+    matmul (hipBLASLt, two-dimensional) of the same shape, X [512][4096] x
+    W^T with W [12288][4096] already dequantized to bf16, the faster of two
+    operand layouts, plus a 100 MB bf16 write, the least an unfused dequant
+    pass of W costs. Random operands (the timing does not depend on them)."""
+    dev = torch.device("cuda:0")
+    m, n, k = 512, 12288, 4096
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(m, k, device=dev, dtype=torch.float32, generator=g).to(torch.bfloat16)
+    w = torch.randn(n, k, device=dev, dtype=torch.float32, generator=g).to(torch.bfloat16)
+    wt = w.t().contiguous()
+    out = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    # both operand layouts (W as [n][k], read transposed, or materialised
+    # [k][n]); the faster one is the reference
+    ms = min(time_calls(torch, [lambda st: torch.matmul(x, w.t(), out=out)], steps, 5),
+             time_calls(torch, [lambda st: torch.matmul(x, wt, out=out)], steps, 5))
+    fill = torch.empty(n * k, device=dev, dtype=torch.bfloat16)
+    ms_fill = time_calls(torch, [lambda st: fill.fill_(1.0)], steps, 5)
+    res = {"reference_hipblaslt_bf16_gemm_512x12288x4096": {
+               "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1),
+               "note": "torch.matmul on bf16 operands (hipBLASLt), weights pre-dequantized: no dequant in the time"},
+           "reference_bf16_write_100MB": {
+               "us_per_call": round(ms_fill * 1e3, 2),
+               "note": "a 12288x4096 bf16 fill: the least an unfused dequant of W to bf16 adds"}}
+    del x, w, wt, out, fill
+    torch.cuda.empty_cache()
     return res
 
 
@@ -479,6 +509,9 @@ def main():
     elif args.only == "rowops":
         print(json.dumps(bench_rowops(torch, H, S, args.steps)), flush=True)
         return
+    elif args.only == "blaslt":
+        print(json.dumps(bench_blaslt_reference(torch, args.steps)), flush=True)
+        return
     elif args.only == "prefill":
         wp = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
         print(json.dumps(bench_prefill(torch, H, S, wp, 12288, 4096, 512, args.steps)), flush=True)
@@ -551,6 +584,7 @@ def main():
             del wm
         print("[bench] extra prefill matmul", file=sys.stderr, flush=True)
         extra.update(bench_prefill(torch, H, S, prefill_w, 12288, 4096, 512, 50))
+        extra.update(bench_blaslt_reference(torch, 50))
         del prefill_w
         print("[bench] extra moe", file=sys.stderr, flush=True)
         extra.update(bench_moe(torch, H, S, 240))
