@@ -52,9 +52,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn", "blaslt"),
+    ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn", "blaslt",
+                                                    "batched"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
-                         "'moe' / 'prefill' / 'rowops' / 'ffn': that extra alone (for profiling; prints its JSON)")
+                         "'moe' / 'prefill' / 'rowops' / 'ffn' / 'blaslt': that extra alone, 'batched': the "
+                         "batch-8 decode shapes (for profiling; prints its JSON)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -460,6 +462,38 @@ def host_slice_gemv(H, S, w, x, rows, cols, calls):
         return (time.perf_counter() - t0) / calls * 1e6
 
 
+# type ids: 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K
+DECODE_SHAPES = (("q4k_gate_12288x4096_b1", 12, 12288, 4096, 1),
+                 ("q4k_gate_12288x4096_b8", 12, 12288, 4096, 8),
+                 ("q4k_down_4096x12288_b8", 12, 4096, 12288, 8),
+                 ("q8_0_4096x4096_b1", 8, 4096, 4096, 1),
+                 ("q5k_4096x12288_b1", 13, 4096, 12288, 1),
+                 ("q5k_12288x4096_b8", 13, 12288, 4096, 8),
+                 ("q5k_4096x12288_b8", 13, 4096, 12288, 8),
+                 ("q6k_lm_head_151936x4096_b1", 14, 151936, 4096, 1))
+
+
+def bench_decode_shapes(torch, H, S, steps_max, batched_only=False):
+    """The other decode matvec shapes (Q4_K / Q5_K gate and down at batch 1
+    and 8, Q8_0 attention-sized, the Q6_K head), each over rotating weight
+    copies in one graph; microseconds per launch and GB/s of packed weights."""
+    extra = {}
+    for name, q, r, c, b in DECODE_SHAPES:
+        if batched_only and b == 1:
+            continue
+        wm = S.matrix(q, 0x5EED0000 + q + r, r, c)
+        print(f"[bench] extra {name}", file=sys.stderr, flush=True)
+        steps = max(40, min(steps_max, int(2e9 / wm.nbytes)))
+        t, _, _ = timed_graph(torch, H, q, r, c, wm, b, steps, 10)
+        extra[name] = {"us_per_launch": round(t * 1e3, 3),
+                       "weight_GBps": round(wm.nbytes / (t * 1e-3) / 1e9, 1),
+                       "pct_hbm_peak": round(100 * wm.nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
+        if q == S.Q6_K:
+            extra[name]["scale_reading"] = "u8, as strata-gguf reads the Q6_K sub-block scales (dequant.rs:211)"
+        del wm
+    return extra
+
+
 def load_traffic(name):
     p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
@@ -508,6 +542,9 @@ def main():
         return
     elif args.only == "rowops":
         print(json.dumps(bench_rowops(torch, H, S, args.steps)), flush=True)
+        return
+    elif args.only == "batched":
+        print(json.dumps(bench_decode_shapes(torch, H, S, args.steps, batched_only=True)), flush=True)
         return
     elif args.only == "blaslt":
         print(json.dumps(bench_blaslt_reference(torch, args.steps)), flush=True)
@@ -560,29 +597,9 @@ def main():
 
     if not args.no_extra:
         extra = {}
-        shapes = [("q4k_gate_12288x4096_b1", S.Q4_K, 12288, 4096, 1),
-                  ("q4k_gate_12288x4096_b8", S.Q4_K, 12288, 4096, 8),
-                  ("q4k_down_4096x12288_b8", S.Q4_K, 4096, 12288, 8),
-                  ("q8_0_4096x4096_b1", S.Q8_0, 4096, 4096, 1),
-                  ("q5k_4096x12288_b1", S.Q5_K, 4096, 12288, 1),
-                  ("q5k_12288x4096_b8", S.Q5_K, 12288, 4096, 8),
-                  ("q5k_4096x12288_b8", S.Q5_K, 4096, 12288, 8),
-                  ("q6k_lm_head_151936x4096_b1", S.Q6_K, 151936, 4096, 1)]
-        prefill_w = None
-        for name, q, r, c, b in shapes:
-            wm = S.matrix(q, 0x5EED0000 + q + r, r, c)
-            print(f"[bench] extra {name}", file=sys.stderr, flush=True)
-            steps = max(40, min(args.steps, int(2e9 / wm.nbytes)))
-            t, _, _ = timed_graph(torch, H, q, r, c, wm, b, steps, 10)
-            extra[name] = {"us_per_launch": round(t * 1e3, 3),
-                           "weight_GBps": round(wm.nbytes / (t * 1e-3) / 1e9, 1),
-                           "pct_hbm_peak": round(100 * wm.nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
-            if q == S.Q6_K:
-                extra[name]["scale_reading"] = "u8, as strata-gguf reads the Q6_K sub-block scales (dequant.rs:211)"
-            if name == "q4k_gate_12288x4096_b1":
-                prefill_w = wm
-            del wm
+        extra.update(bench_decode_shapes(torch, H, S, args.steps))
         print("[bench] extra prefill matmul", file=sys.stderr, flush=True)
+        prefill_w = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
         extra.update(bench_prefill(torch, H, S, prefill_w, 12288, 4096, 512, 50))
         extra.update(bench_blaslt_reference(torch, 50))
         del prefill_w

@@ -336,21 +336,20 @@ int sh_gemv_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, ui
                 const float* x, float* y, uint32_t batch, void* stream);
 
 /* Bytes of device workspace sh_gemv_dev_ws uses for this shape and batch:
- * nonzero for batches of 2..8 of rows wider than 4096 columns of the types
- * with a batched int8-MFMA kernel (Q4_K, Q5_K), else 0. No reference
- * counterpart. */
+ * nonzero for batches of 2..8 of the types with a batched int8-MFMA kernel
+ * (Q4_K, Q5_K), else 0. No reference counterpart. */
 int sh_gemv_workspace_bytes(uint32_t quant, uint64_t rows, uint64_t cols, uint32_t batch, uint64_t* bytes);
 
 /* sh_gemv_dev with a workspace (256-byte aligned, at least
  * sh_gemv_workspace_bytes() long, no initialisation needed; unused, and may
- * be NULL, when that is 0): batches of 2..8 of rows wider than one
- * 4096-column window convert their activations once per call into it (one
- * small extra launch) and run split-K over the windows, each workgroup
- * holding one window's activations; the last workgroup of a row block adds
- * the windows' sums in window order, so results do not depend on timing
- * (they differ from sh_gemv_dev's by the order of three f32 additions).
- * Calls sharing one workspace must not overlap in time. No reference
- * counterpart. */
+ * be NULL, when that is 0): batches of 2..8 convert their activations once
+ * per call into it (one small extra launch), and every workgroup copies the
+ * window of them it needs instead of converting it; rows wider than one
+ * window (2048 to 4096 columns, chosen per shape) run split-K over the
+ * windows, and the last workgroup of a row block adds the windows' sums in
+ * window order, so results do not depend on timing (they differ from
+ * sh_gemv_dev's by the order of a few f32 additions). Calls sharing one
+ * workspace must not overlap in time. No reference counterpart. */
 int sh_gemv_dev_ws(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, uint64_t cols, const float* x,
                    float* y, uint32_t batch, void* workspace, uint64_t workspace_bytes, void* stream);
 

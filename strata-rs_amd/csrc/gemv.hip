@@ -709,12 +709,11 @@ static hipError_t launch_nb(int nb, const uint8_t* w, int rows, int cols, int64_
   }
 }
 
-// Batches of rows wider than one 4096-column window run split-K over the
-// windows with their activations converted once per call (the workspace);
-// narrower rows gain nothing from the extra launch and take none.
+// Batched Q4_K / Q5_K rows convert their activations once per call into the
+// workspace (each workgroup then copies its window rather than converting
+// it), and rows wider than one window run split-K over the windows.
 size_t gemv_workspace_bytes(uint32_t quant, int64_t rows, int64_t cols, int batch) {
-  return batch >= 2 && cols > 4096 && gemv_mfma_ok(quant, rows, cols, batch) ? gemv_mfma_workspace_bytes(rows, cols)
-                                                                               : 0;
+  return batch >= 2 && gemv_mfma_ok(quant, rows, cols, batch) ? gemv_mfma_workspace_bytes(rows, cols) : 0;
 }
 
 hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,

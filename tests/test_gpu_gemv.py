@@ -287,14 +287,17 @@ def test_gemv_random_shapes(backend, oracle, seed):
 
 
 @pytest.mark.parametrize("quant,rows,cols,batch", [(12, 4096, 12288, 8), (13, 4096, 12288, 3), (12, 4096, 8192, 2),
-                                                   (12, 33, 8192 + 256, 7), (13, 1000, 20480, 8)])
+                                                   (12, 33, 8192 + 256, 7), (13, 1000, 20480, 8),
+                                                   (12, 12288, 4096, 8), (13, 12288, 4096, 8), (12, 500, 2048, 5),
+                                                   (13, 16384, 4096, 2)])
 def test_gemv_dev_ws_batches(oracle, quant, rows, cols, batch):
-    """sh_gemv_dev_ws: batches of rows wider than one 4096-column window
-    convert their activations once per call into the workspace and run
-    split-K (the windows' sums added in window order by the last workgroup
-    of each row block): the same call twice gives the same bits (no
-    dependence on which workgroup finished last), against the oracle at the
-    parity bars; two activation sets on one workspace."""
+    """sh_gemv_dev_ws: batches convert their activations once per call into
+    the workspace, each workgroup copying its window; rows wider than one
+    window (2048 to 4096 columns by shape) run split-K, the windows' sums
+    added in window order by the last workgroup of each row block: the same
+    call twice gives the same bits (no dependence on which workgroup
+    finished last), against the oracle at the parity bars; two activation
+    sets on one workspace."""
     import torch
     say("gemv_dev_ws", quant, rows, cols, batch)
     w = S.matrix(quant, 91 + rows + cols, rows, cols)
@@ -323,6 +326,6 @@ def test_gemv_workspace_sizes():
     assert H.gemv_workspace_bytes(12, 4096, 12288, 1) == 0      # batch 1: none
     assert H.gemv_workspace_bytes(14, 4096, 12288, 8) == 0      # no batched MFMA kernel for Q6_K
     assert H.gemv_workspace_bytes(12, 4096, 12288, 8) > 0
-    assert H.gemv_workspace_bytes(12, 12288, 4096, 8) == 0      # one window: no split-K
+    assert H.gemv_workspace_bytes(12, 12288, 4096, 8) > 0       # one window: converted once, copied
     with pytest.raises(H.BackendError):
         H.gemv_dev_ws(12, 1 << 20, 4096, 12288, 1 << 20, 1 << 20, 8, 1 << 20, 16)  # workspace too small
