@@ -533,14 +533,18 @@ __global__ void __launch_bounds__(kMmWsThreads)
   }
   lds_barrier();
 
-  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+  // One loop per role, each with one barrier per chunk (the barrier counts
+  // match): a loop whose every chunk branched on the role would merge both
+  // roles' loads in flight at each join, and the compiler would then wait
+  // for all of them before each chunk, undoing the prefetch distances.
+  if (consumer) {
+    for (int c0 = 0; c0 < nchunks; c0 += 2) {
 #pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      const int c = c0 + j;
-      if (c < nchunks) {  // uniform
-        if (consumer) {
+      for (int j = 0; j < 2; ++j) {
+        const int c = c0 + j;
+        if (c < nchunks) {  // uniform
           const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
-          bf16x8 (*a)[4] = afr[j & 1];
+          bf16x8 (*a)[4] = afr[j];
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             bf16x8 bfr[3];
@@ -555,16 +559,27 @@ __global__ void __launch_bounds__(kMmWsThreads)
           }
           // chunk c + 2 into the registers chunk c used (past the end: the last chunk again)
           load_a(min(c + 2, nchunks - 1), a);
-        } else if (stager) {
+          lds_barrier();
+        }
+      }
+    }
+  } else if (stager) {
+    for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+#pragma unroll
+      for (int j = 0; j < kDepth; ++j) {
+        const int c = c0 + j;
+        if (c < nchunks) {  // uniform
           // B(c + 1) into the buffer chunk c - 1 used; past the last chunk
           // this re-stages the last one into the buffer nobody reads
           const int slot = (j + 1) % kDepth;
           stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
           raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+          lds_barrier();
         }
-        lds_barrier();
       }
     }
+  } else {
+    for (int c = 0; c < nchunks; ++c) lds_barrier();
   }
 
   if (!consumer) return;
