@@ -155,6 +155,8 @@ extern "C" {
         stream: *mut c_void) -> c_int;
     pub fn sh_quantize_q8_dev(x: *const f32, n: u64, codes: *mut i8, scales: *mut f32, code_sums: *mut f32,
         stream: *mut c_void) -> c_int;
+    pub fn sh_quantize_q8k_dev(x: *const f32, n: u64, codes: *mut i8, scales: *mut f32, sub_sums: *mut i32,
+        stream: *mut c_void) -> c_int;
     pub fn sh_moe_workspace_bytes(n_tok: u32, top_k: u32, n_expert: u64, n_embd: u64, n_ff: u64,
         quant_gate_up: u32, quant_down: u32, bytes: *mut u64) -> c_int;
     pub fn sh_moe_ffn_dev(gate: *const ShExpertDev, up: *const ShExpertDev, down: *const ShExpertDev,

@@ -263,9 +263,10 @@ int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert
  * activation rounding of `mode`:
  *   SH_MATMUL_BF16  x rounded to bf16, weights dequantized to bf16, f32
  *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K);
- *   SH_MATMUL_Q8    x quantized to 32-element blocks (scale max|x| / 127,
- *                   int8 codes rounded to nearest even), int8 products
- *                   (Q8_0, Q4_K, Q5_K).
+ *   SH_MATMUL_Q8    x quantized to blocks of the weight's scale group
+ *                   (scale max|x| / 127 per block, int8 codes rounded to
+ *                   nearest even): 32 elements for Q8_0, 256 (one per
+ *                   super-block) for Q4_K and Q5_K; int8 products.
  * cols must be a multiple of 64. */
 int sh_matmul(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint32_t m, float* y,
               uint32_t mode);
@@ -288,6 +289,14 @@ int sh_matmul_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, 
  * (max|x| / 127 per block) and n / 32 values scale * sum(codes). */
 int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales, float* code_sums,
                        void* stream);
+
+/* The activation rounding of SH_MATMUL_Q8 for Q4_K / Q5_K weights on its
+ * own: n f32 (n a multiple of 256, x 16-byte aligned) -> n int8 codes, n /
+ * 256 scales (max|x| / 127 per 256 elements, one per weight super-block) and
+ * n / 32 integer code sums (one per 32-element sub-block). No counterpart in
+ * the reference (it has no matmul). */
+int sh_quantize_q8k_dev(const float* x, uint64_t n, int8_t* codes, float* scales, int32_t* sub_sums,
+                        void* stream);
 
 /* One expert tensor already in device memory. */
 typedef struct sh_expert_dev {

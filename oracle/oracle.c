@@ -692,6 +692,31 @@ int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,
   return SHO_OK;
 }
 
+int sho_quantize_q8k(const float* x, size_t n, int8_t* q, float* scales,
+                     int32_t* sums) {
+  if (n % 256 != 0) return SHO_TRUNCATED;
+  for (size_t b = 0; b < n / 256; ++b) {
+    const float* v = x + 256 * b;
+    float amax = 0.0f;
+    for (int k = 0; k < 256; ++k) {
+      const float a = fabsf(v[k]);
+      if (a > amax) amax = a;
+    }
+    const float s = amax / 127.0f;
+    for (int j = 0; j < 8; ++j) {
+      int sum = 0;
+      for (int k = 32 * j; k < 32 * j + 32; ++k) {
+        const int c = s > 0.0f ? (int)rintf(v[k] / s) : 0;
+        q[256 * b + k] = (int8_t)c;
+        sum += c;
+      }
+      sums[8 * b + j] = sum;
+    }
+    scales[b] = s;
+  }
+  return SHO_OK;
+}
+
 /* ---- the trait's elementwise methods (backend.rs:38-50, ops.rs:46-165) --
  * f64 where the reference works in f64; the sums run in its sequential
  * order. pow / sin / cos are the C library's, as Rust's f64::powf and

@@ -150,6 +150,14 @@ int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
 int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,
                     float* sums);
 
+/* Activation blocks of 256 (n % 256 == 0), the rounding the q8 matmul
+ * mode applies for Q4_K / Q5_K weights (one scale per weight super-block):
+ * s = max|x| / 127 over the 256 (f32 division), q = rint(x / s) (nearest
+ * even; 0 when s == 0), sums[8b + j] = sum of the codes of elements
+ * [32j, 32j + 32) of block b (exact integers). */
+int sho_quantize_q8k(const float* x, size_t n, int8_t* q, float* scales,
+                     int32_t* sums);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,7 @@ def lib() -> C.CDLL:
         L.sho_matmul.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, C.c_int64, f32p,
                                  C.c_int]
         L.sho_quantize_q8.argtypes = [f32p, C.c_size_t, u8p, f32p, f32p]
+        L.sho_quantize_q8k.argtypes = [f32p, C.c_size_t, u8p, f32p, C.c_void_p]
         L.sho_rms_norm.argtypes = [f32p, f32p, C.c_size_t, C.c_double, f32p]
         L.sho_rms_norm.restype = None
         L.sho_l2_norm.argtypes = [f32p, C.c_size_t, C.c_double]
@@ -319,6 +320,31 @@ def dequantize_q8_activations(x) -> np.ndarray:
     xv = _f32(x)
     q, s, _ = quantize_q8(xv)
     return (np.repeat(s, 32) * q.astype(np.float32)).astype(np.float32).reshape(xv.shape)
+
+
+def quantize_q8k(x) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(codes int8 [n], scales f32 [n/256], code sums int32 [n/32]): blocks of
+    256 with one scale, the q8 matmul mode's rounding for K-quant weights."""
+    xv = _f32(x).reshape(-1)
+    q = np.empty(xv.size, dtype=np.int8)
+    s = np.empty(xv.size // 256, dtype=np.float32)
+    u = np.empty(xv.size // 32, dtype=np.int32)
+    _check(lib().sho_quantize_q8k(_ptr(xv), xv.size, _ptr(q), _ptr(s), _ptr(u)), "quantize_q8k")
+    return q, s, u
+
+
+def dequantize_q8k_activations(x) -> np.ndarray:
+    """x rounded through 256-element Q8 blocks: scale * code per element (f32 product)."""
+    xv = _f32(x)
+    q, s, _ = quantize_q8k(xv)
+    return (np.repeat(s, 256) * q.astype(np.float32)).astype(np.float32).reshape(xv.shape)
+
+
+def q8_activations_for(quant: int, x) -> np.ndarray:
+    """The activation rounding of the q8 matmul mode for weights of `quant`:
+    one scale per weight scale group (32 elements for Q8_0, a 256-element
+    super-block for Q4_K / Q5_K)."""
+    return dequantize_q8k_activations(x) if quant in (Q4_K, Q5_K) else dequantize_q8_activations(x)
 
 
 def bf16_round_array(a) -> np.ndarray:

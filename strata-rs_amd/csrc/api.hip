@@ -1065,6 +1065,20 @@ int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales,
   return SH_OK;
 }
 
+int sh_quantize_q8k_dev(const float* x, uint64_t n, int8_t* codes, float* scales, int32_t* sub_sums,
+                        void* stream) {
+  if (!x || !codes || !scales || !sub_sums) return fail(SH_ERR_INVALID_ARGUMENT, "null pointer");
+  if (n == 0 || n % 256 != 0 || n > (uint64_t(1) << 40))
+    return fail(SH_ERR_UNSUPPORTED_SHAPE, "quantize: %llu values (a positive multiple of 256 needed)",
+                (unsigned long long)n);
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(codes) & 3u) ||
+      (reinterpret_cast<uintptr_t>(scales) & 3u) || (reinterpret_cast<uintptr_t>(sub_sums) & 3u))
+    return fail(SH_ERR_INVALID_ARGUMENT, "misaligned pointer (x needs 16 bytes, the outputs 4)");
+  HIP_TRY(sh::launch_quantize_q8k(x, int64_t(n), codes, scales, sub_sums, static_cast<hipStream_t>(stream)),
+          "quantize launch");
+  return SH_OK;
+}
+
 // ---- the trait's elementwise methods ----------------------------------------
 
 namespace {

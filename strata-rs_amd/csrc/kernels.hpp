@@ -149,6 +149,10 @@ hipError_t launch_matmul(uint32_t quant, const void* w, int64_t rows, int64_t co
 // codes, per-32 scales and per-32 scale * sum of codes.
 hipError_t launch_quantize_q8(const float* x, int64_t n, int8_t* q, float* scales, float* usum,
                               hipStream_t stream);
+// The int8 mode's rounding for Q4_K / Q5_K weights: n f32 (n % 256 == 0)
+// -> int8 codes, one scale per 256 and the integer code sum per 32.
+hipError_t launch_quantize_q8k(const float* x, int64_t n, int8_t* q, float* scales, int32_t* sums,
+                               hipStream_t stream);
 
 // The trait's elementwise methods over `rows` rows of n floats (rope:
 // head_dim floats per row, row r at position pos0 + r / heads_per_pos).

@@ -41,6 +41,21 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Four bytes each times a small factor f (every product < 256, so no byte
+// carries into the next): one v_pk_mul_lo_u16 over the word's two halves.
+__device__ __forceinline__ uint32_t bytes_times(uint32_t w, uint32_t f) {
+  const u16x2 v = __builtin_bit_cast(u16x2, w);
+  const u16x2 k = {static_cast<unsigned short>(f), static_cast<unsigned short>(f)};
+  return __builtin_bit_cast(uint32_t, v * k);
+}
+// Bytes p (0..255) less k (0..127, the same in every byte), each mod 256:
+// with bit 7 set first no byte borrows from the next; the xor restores it.
+__device__ __forceinline__ uint32_t bytes_minus(uint32_t p, uint32_t k4) {
+  return ((p | 0x80808080u) - k4) ^ (~p & 0x80808080u);
+}
 
 constexpr int kMmBM = 256;                  // tokens per workgroup
 constexpr int kMmBN = 96;                   // weight rows per workgroup
@@ -71,6 +86,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 struct StQ4K {
   static constexpr int kPieces = 2;
   static constexpr bool kQ8 = true;
+  static constexpr bool kQ8K = true;  // int8 mode on 256-element activation blocks
   static constexpr bool kMin = true;  // value d * q - m
   struct Raw {
     u32x4 h, q;
@@ -79,16 +95,30 @@ struct StQ4K {
     const uint8_t* sb = row + (c >> 2) * 144;
     return {ld16(sb), ld16(sb + 16 + 32 * (c & 3) + 16 * hb)};
   }
-  // d * sc and dmin * m of sub-blocks 2g and 2g + 1
-  __device__ static __forceinline__ void scales(const u32x4& h, int g, float& d0, float& m0, float& d1,
-                                                float& m1) {
+  // 6-bit scales (scp) and mins (mp) of sub-blocks 2g and 2g + 1 in bytes 0, 1
+  __device__ static __forceinline__ void scale_bytes(const u32x4& h, int g, uint32_t& scp, uint32_t& mp) {
     const uint32_t s = (g & 1) << 4;
     const uint32_t t1 = h.y >> s, t2 = h.z >> s, t3 = h.w >> s;
     // both readings, then a mask select: no branch on the wave-uniform g, so
     // staging stays in the MFMAs' basic block
     const uint32_t hi_sel = 0u - uint32_t(g >> 1);  // all ones for g >= 2
-    const uint32_t scp = ((t1 & 0x3F3Fu) & ~hi_sel) | (((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u)) & hi_sel);
-    const uint32_t mp = ((t2 & 0x3F3Fu) & ~hi_sel) | ((((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u)) & hi_sel);
+    scp = ((t1 & 0x3F3Fu) & ~hi_sel) | (((t3 & 0x0F0Fu) | ((t1 >> 2) & 0x3030u)) & hi_sel);
+    mp = ((t2 & 0x3F3Fu) & ~hi_sel) | ((((t3 >> 4) & 0x0F0Fu) | ((t2 >> 2) & 0x3030u)) & hi_sel);
+  }
+  // all eight 6-bit scales and mins of the super-block, four per word
+  // (get_scale_min_k4, dequant.rs:237-245)
+  __device__ static __forceinline__ void all_scale_bytes(const u32x4& h, uint32_t& sc03, uint32_t& sc47,
+                                                         uint32_t& m03, uint32_t& m47) {
+    sc03 = h.y & 0x3F3F3F3Fu;
+    m03 = h.z & 0x3F3F3F3Fu;
+    sc47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    m47 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+  }
+  // d * sc and dmin * m of sub-blocks 2g and 2g + 1
+  __device__ static __forceinline__ void scales(const u32x4& h, int g, float& d0, float& m0, float& d1,
+                                                float& m1) {
+    uint32_t scp, mp;
+    scale_bytes(h, g, scp, mp);
     const float d = h2f(h.x), dm = h2f(h.x >> 16);
     d0 = d * ubyte<0>(scp);
     d1 = d * ubyte<1>(scp);
@@ -116,6 +146,25 @@ struct StQ4K {
     o0 = 16 * hb;
     o1 = 32 + 16 * hb;
   }
+  // K-quant int8 path: the codes times the two limbs of their sub-block's
+  // scale, sc = 8 sh + sl (sh, sl <= 7: products <= 105 fit int8), for
+  // sub-blocks 2g (h0, l0) and 2g + 1 (h1, l1)
+  static constexpr int kCenter = 0;  // codes enter unshifted
+  __device__ static __forceinline__ void emit_q8k(const Raw& r, int c, uint32_t* h0, uint32_t* l0,
+                                                  uint32_t* h1, uint32_t* l1) {
+    uint32_t scp, mp;
+    scale_bytes(r.h, c & 3, scp, mp);
+    const uint32_t sh0 = (scp >> 3) & 7u, sl0 = scp & 7u, sh1 = (scp >> 11) & 7u, sl1 = (scp >> 8) & 7u;
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t a = q[k] & 0x0F0F0F0Fu, b = (q[k] >> 4) & 0x0F0F0F0Fu;
+      h0[k] = bytes_times(a, sh0);
+      l0[k] = bytes_times(a, sl0);
+      h1[k] = bytes_times(b, sh1);
+      l1[k] = bytes_times(b, sl1);
+    }
+  }
   // int8 codes 0..15; run k lies in block jb_k of the chunk, whose values
   // are dj[k] * q - mj[k]
   __device__ static __forceinline__ void emit_q8(const Raw& r, int c, int hb, uint32_t* run0,
@@ -142,6 +191,7 @@ struct StQ4K {
 struct StQ5K {
   static constexpr int kPieces = 2;
   static constexpr bool kQ8 = true;
+  static constexpr bool kQ8K = true;
   static constexpr bool kMin = true;  // value d * q - m
   struct Raw {
     u32x4 h, q, qh;
@@ -174,6 +224,26 @@ struct StQ5K {
     o0 = 16 * hb;
     o1 = 32 + 16 * hb;
   }
+  // K-quant int8 path as StQ4K::emit_q8k, on the codes less 16 (-16..15,
+  // so that sh * (q - 16) and sl * (q - 16) fit int8); the 16 * sc part
+  // returns through the code sums
+  static constexpr int kCenter = 16;
+  __device__ static __forceinline__ void emit_q8k(const Raw& r, int c, uint32_t* h0, uint32_t* l0,
+                                                  uint32_t* h1, uint32_t* l1) {
+    uint32_t scp, mp;
+    StQ4K::scale_bytes(r.h, c & 3, scp, mp);
+    const uint32_t sh0 = (scp >> 3) & 7u, sl0 = scp & 7u, sh1 = (scp >> 11) & 7u, sl1 = (scp >> 8) & 7u;
+    uint32_t lo[4], hi[4];
+    codes(r, c, lo, hi);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // codes <= 31 times <= 7: products <= 217, one byte each
+      h0[k] = bytes_minus(bytes_times(lo[k], sh0), 0x10101010u * sh0);
+      l0[k] = bytes_minus(bytes_times(lo[k], sl0), 0x10101010u * sl0);
+      h1[k] = bytes_minus(bytes_times(hi[k], sh1), 0x10101010u * sh1);
+      l1[k] = bytes_minus(bytes_times(hi[k], sl1), 0x10101010u * sl1);
+    }
+  }
   // int8 codes 0..31, blocks as StQ4K::emit_q8
   __device__ static __forceinline__ void emit_q8(const Raw& r, int c, int hb, uint32_t* run0,
                                                  uint32_t* run1, int& o0, int& o1, int& jb0, int& jb1,
@@ -193,6 +263,7 @@ struct StQ5K {
 struct StQ8 {
   static constexpr int kPieces = 2;
   static constexpr bool kQ8 = true;
+  static constexpr bool kQ8K = false;  // 32-element activation blocks, as its own scales
   static constexpr bool kMin = false;  // value d * q
   struct Raw {
     u32x4 a, b;
@@ -252,6 +323,7 @@ struct StQ8 {
 struct StQ6K {
   static constexpr int kPieces = 2;
   static constexpr bool kQ8 = false;  // 16-element scales do not fit 32-element int8 blocks
+  static constexpr bool kQ8K = false;
   struct Raw {
     u32x4 l0, l1, qh;
     uint32_t l0e, l1e, qhe, s0, s1;
@@ -392,6 +464,92 @@ __global__ void x_q8_tiled_kernel(const float* __restrict__ x, u32x4* __restrict
   dst[32] = u32x4{w[4], w[5], w[6], w[7]};
   st[i] = sv;
   ut[i] = uv;
+}
+
+// X f32 -> Q8 blocks of 256 (the K-quant int8 path: one scale per weight
+// super-block): s = max|x| / 127 over the 256 (f32 division), q = rne(x / s)
+// (0 where s == 0), and the integer code sum of each 32-element sub-block.
+// One wave per (token, super-block), lane L holding elements 4L .. 4L + 3;
+// the lane's four codes, s (from every lane) and its sub-block's sum (from
+// lanes 8j, zero elsewhere) are returned.
+__device__ __forceinline__ void q8k_wave(const float* __restrict__ x256, bool live, int lane, uint32_t& codes,
+                                         float& s_out, int& sum_out) {
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (live) v = reinterpret_cast<const f32x4*>(x256)[lane];
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  const float s = __fdiv_rn(amax, 127.f);
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  uint32_t word = 0;
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = s > 0.f ? int(__builtin_rintf(__fdiv_rn(e[k], s))) : 0;
+    sum += c;
+    word |= (uint32_t(c) & 0xFFu) << (8 * k);
+  }
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  sum += __shfl_xor(sum, 4, 64);
+  codes = word;
+  s_out = s;
+  sum_out = sum;
+}
+
+// Plain layout (sh_quantize_q8k_dev): codes [n], scales [n / 256], sums [n / 32].
+__global__ void __launch_bounds__(256) x_q8k_kernel(const float* __restrict__ x, uint32_t* __restrict__ q,
+                                                    float* __restrict__ s_out, int* __restrict__ sums,
+                                                    int64_t supers) {
+  const int64_t wv = (blockIdx.x * int64_t(blockDim.x) + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wv >= supers) return;  // whole waves
+  uint32_t codes;
+  float sv;
+  int sum;
+  q8k_wave(x + 256 * wv, true, lane, codes, sv, sum);
+  q[64 * wv + lane] = codes;
+  if (lane == 0) s_out[wv] = sv;
+  if ((lane & 7) == 0) sums[8 * wv + (lane >> 3)] = sum;
+}
+
+// The same blocks for mm_q8k_kernel, in the order its waves load them
+// (tokens padded with zero blocks to a multiple of 32; T = token / 32,
+// l = token % 32, nch = cols / 64, nsb = cols / 256):
+//   codes: as x_q8_tiled_kernel (16-byte piece ((T * nch + c) * 2 + s) * 64
+//          + 32 h + l holds chunk c's elements [32 s + 16 h, +16));
+//   s:     float (T * nsb + sb) * 32 + l;
+//   sums:  16-byte piece (T * nsb + sb) * 64 + 32 h + l, eight f16: h = 0
+//          the high parts b >> 6 of sub-blocks 0..7, h = 1 the low parts
+//          b & 63 (b = 64 * hi + lo exactly; both exact in f16), the B
+//          operand of the min-term MFMA.
+__global__ void __launch_bounds__(256) x_q8k_tiled_kernel(const float* __restrict__ x, uint8_t* __restrict__ qt,
+                                                          float* __restrict__ st, uint8_t* __restrict__ bt, int m,
+                                                          int cols, int64_t waves) {
+  const int64_t wv = (blockIdx.x * int64_t(blockDim.x) + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wv >= waves) return;  // whole waves
+  const int nsb = cols >> 8, nch = cols / kMmKC;
+  const int sb = int(wv % nsb);
+  const int64_t t = wv / nsb;  // padded token
+  const int64_t T = t >> 5;
+  const int l = int(t & 31);
+  uint32_t codes;
+  float sv;
+  int sum;
+  q8k_wave(x + (t < m ? t : 0) * int64_t(cols) + 256 * sb, t < m, lane, codes, sv, sum);
+  // element 4 lane of the super-block: chunk 4 sb + lane / 16, step (lane / 8) & 1,
+  // half (lane / 4) & 1, bytes 4 (lane & 3) of the piece
+  const int c = 4 * sb + (lane >> 4), st_ = (lane >> 3) & 1, h = (lane >> 2) & 1;
+  const int64_t piece = ((T * nch + c) * 2 + st_) * 64 + 32 * h + l;
+  *reinterpret_cast<uint32_t*>(qt + piece * 16 + 4 * (lane & 3)) = codes;
+  if (lane == 0) st[(T * nsb + sb) * 32 + l] = sv;
+  if ((lane & 7) == 0) {
+    const int j = lane >> 3;
+    _Float16* b = reinterpret_cast<_Float16*>(bt + ((T * nsb + sb) * 64 + l) * 16);
+    b[j] = _Float16(float(sum >> 6));          // h = 0 piece
+    b[32 * 8 + j] = _Float16(float(sum & 63));  // h = 1 piece (32 pieces on)
+  }
 }
 
 // --------------------------------------------------------------- tile order --
@@ -792,6 +950,233 @@ __global__ void __launch_bounds__(kMmThreads)
   }
 }
 
+// ------------------------------------------------------ q8 kernel, K-quants --
+// Q4_K / Q5_K weights against activations in 256-element Q8 blocks (one scale
+// s_t per token and super-block, codes c, sub-block code sums b_tj). One
+// super-block of row r holds values d * sc_j * q_k - dmin * m_j for element k
+// of sub-block j; with q_k = z + p_k (z = 0 for Q4_K, 16 for Q5_K, so p fits
+// a signed byte) and sc_j = 8 sh_j + sl_j:
+//   sum_k value_k * x_k = s_t * (d * (8 H + L + z * sum_j sc_j b_tj)
+//                                - dmin * sum_j m_j b_tj)
+// H = sum_k sh_j p_k c_k and L = sum_k sl_j p_k c_k run on
+// v_mfma_i32_32x32x32_i8 (weight operands sh * p and sl * p, int8) with the
+// int32 sums carried through all 8 sub-blocks of the super-block; the two
+// sub-block sums over b_tj are exact integers on one v_mfma_f32_32x32x16_f16
+// each (b = 64 hi + lo, the weight side 64 m | m, both halves exact in f16);
+// the VALU rescales once per super-block and output (5 ops, 6 for Q5_K),
+// not once per 32-element block.
+//
+// Same tile and staging as mm_q8_kernel (4 waves along the tokens, each 2 x 3
+// output tiles of 32 x 32; waves 0-2 also stage, two chunks of loads in
+// flight: the 288 accumulator registers leave little room); LDS holds the two limb planes of the chunk (double-buffered) and,
+// per super-block (double-buffered), the rows' f16 operands of the sum MFMAs
+// and d, dmin.
+template <class S>
+__global__ void __launch_bounds__(kMmThreads)
+    mm_q8k_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                  const int8_t* __restrict__ xq, const float* __restrict__ xs, const u32x4* __restrict__ xb,
+                  int m, float* __restrict__ y, int n_tiles_m) {
+  constexpr bool kZ = S::kCenter != 0;
+  constexpr int kA = kZ ? 32 : 16;  // f16 per row and super-block: 64 m | m (| 1024 sc | 16 sc)
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][2][kMmBN * kMmRowQ];  // [buf][sh * p | sl * p]
+  __shared__ __attribute__((aligned(16))) _Float16 ma[2][kMmBN * kA];         // [super-block buf]
+  __shared__ __attribute__((aligned(16))) float dsc[2][2][kMmBN];             // [super-block buf][d | dmin]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  int r0, t0;
+  tile_of(n_tiles_m, r0, t0);
+  const int nchunks = cols / kMmKC;
+  const int nsb = cols >> 8;
+
+  constexpr int kTasks = kMmBN * S::kPieces;
+  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
+  const bool stager = tid < kTasks;
+  const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
+  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
+
+  const int n_tt = (m + 31) >> 5;
+  const int8_t* xr[2];
+  const float* sr[2];
+  const u32x4* br[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int T = min((t0 + 64 * wave + 32 * mi) >> 5, n_tt - 1);
+    xr[mi] = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
+    sr[mi] = xs + int64_t(T) * nsb * 32 + l32;
+    br[mi] = xb + int64_t(T) * nsb * 64 + lane;
+  }
+
+  f32x16 acc[2][3];
+  i32x16 ah[2][3], al[2][3];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+
+  // one piece of chunk c: its codes times both limbs into LDS buffer buf
+  auto stage = [&](const typename S::Raw& raw, int c, int buf) {
+    uint32_t h0[4], l0[4], h1[4], l1[4];
+    S::emit_q8k(raw, c, h0, l0, h1, l1);
+    const int o0 = srow * kMmRowQ + 16 * piece, o1 = o0 + 32;
+    *reinterpret_cast<u32x4*>(wl[buf][0] + o0) = u32x4{h0[0], h0[1], h0[2], h0[3]};
+    *reinterpret_cast<u32x4*>(wl[buf][1] + o0) = u32x4{l0[0], l0[1], l0[2], l0[3]};
+    *reinterpret_cast<u32x4*>(wl[buf][0] + o1) = u32x4{h1[0], h1[1], h1[2], h1[3]};
+    *reinterpret_cast<u32x4*>(wl[buf][1] + o1) = u32x4{l1[0], l1[1], l1[2], l1[3]};
+  };
+  // the row's super-block operands (piece 0 of the super-block's first chunk)
+  auto header = [&](const typename S::Raw& raw, int sbuf) {
+    uint32_t sc03, sc47, m03, m47;
+    StQ4K::all_scale_bytes(raw.h, sc03, sc47, m03, m47);
+    _Float16* dst = ma[sbuf] + srow * kA;
+    f16x8 a0, a1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float mj = float(((j < 4 ? m03 : m47) >> (8 * (j & 3))) & 0xFFu);
+      a0[j] = _Float16(64.f * mj);
+      a1[j] = _Float16(mj);
+    }
+    *reinterpret_cast<f16x8*>(dst) = a0;
+    *reinterpret_cast<f16x8*>(dst + 8) = a1;
+    if constexpr (kZ) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sj = float(S::kCenter) * float(((j < 4 ? sc03 : sc47) >> (8 * (j & 3))) & 0xFFu);
+        a0[j] = _Float16(64.f * sj);
+        a1[j] = _Float16(sj);
+      }
+      *reinterpret_cast<f16x8*>(dst + 16) = a0;
+      *reinterpret_cast<f16x8*>(dst + 24) = a1;
+    }
+    dsc[sbuf][0][srow] = h2f(raw.h.x);
+    dsc[sbuf][1][srow] = h2f(raw.h.x >> 16);
+  };
+
+  constexpr int kRing = 2;  // weight chunks in flight ahead of staging (registers are short here)
+  typename S::Raw raw[kRing];
+  if (stager) {
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    stage(raw[0], 0, 0);
+    if (piece == 0) header(raw[0], 0);
+    raw[0] = S::load(wrow, min(kRing, nchunks - 1), piece);
+  }
+  i32x4 xc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 1024 * s);
+  lds_barrier();
+
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int sbuf = sb & 1;
+    float sx[2];
+    u32x4 bs[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      sx[mi] = sr[mi][32 * sb];
+      bs[mi] = br[mi][64 * sb];
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {  // chunks of the super-block
+      const int c = 4 * sb + cc;
+      const bool more = c + 1 < nchunks;  // uniform
+      i32x4 xn[2][2];
+      if (more) {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+          for (int s = 0; s < 2; ++s)
+            xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * 2048 + 1024 * s);
+      }
+      const uint8_t* wh = wl[cc & 1][0];
+      const uint8_t* wo = wl[cc & 1][1];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {  // sub-block 2 (c % 4) + s
+#pragma unroll
+        for (int ni = 0; ni < 3; ++ni) {
+          const int ro = (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half;
+          const i32x4 a_h = *reinterpret_cast<const i32x4*>(wh + ro);
+          const i32x4 a_l = *reinterpret_cast<const i32x4*>(wo + ro);
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+            const bool first = cc == 0 && s == 0;  // a new super-block: the int32 sums start at zero
+            ah[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_h, xc[mi][s], first ? i32x16{} : ah[mi][ni], 0,
+                                                               0, 0);
+            al[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_l, xc[mi][s], first ? i32x16{} : al[mi][ni], 0,
+                                                               0, 0);
+          }
+        }
+      }
+      if (more) {
+        if (stager) {
+          const int slot = (cc + 1) % kRing;  // where chunk c + 1 was loaded (c % 4 == cc)
+          stage(raw[slot], c + 1, (cc + 1) & 1);
+          if (cc == 3 && piece == 0) header(raw[slot], sbuf ^ 1);
+          raw[slot] = S::load(wrow, min(c + 1 + kRing, nchunks - 1), piece);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+          for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
+      }
+      if (cc == 3) {
+        // rescale: acc += s_t * (d * (8 H + L [+ z sc.b]) - dmin * m.b)
+#pragma unroll
+        for (int ni = 0; ni < 3; ++ni) {
+          const _Float16* mrow = ma[sbuf] + (32 * ni + l32) * kA;
+          const f16x8 am = *reinterpret_cast<const f16x8*>(mrow + 8 * half);
+          f16x8 az;
+          if constexpr (kZ) az = *reinterpret_cast<const f16x8*>(mrow + 16 + 8 * half);
+          f32x4 dv[4], mv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            dv[q] = *reinterpret_cast<const f32x4*>(&dsc[sbuf][0][32 * ni + 8 * q + 4 * half]);
+            mv[q] = *reinterpret_cast<const f32x4*>(&dsc[sbuf][1][32 * ni + 8 * q + 4 * half]);
+          }
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+            const f16x8 b = __builtin_bit_cast(f16x8, bs[mi]);
+            const f32x16 mb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b, f32x16{}, 0, 0, 0);
+            f32x16 zb = f32x16{};
+            if constexpr (kZ) zb = __builtin_amdgcn_mfma_f32_32x32x16_f16(az, b, f32x16{}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              float f = float((ah[mi][ni][i] << 3) + al[mi][ni][i]);
+              if constexpr (kZ) f += zb[i];
+              const float t = __builtin_fmaf(f, dv[i >> 2][i & 3], -(mb[i] * mv[i >> 2][i & 3]));
+              acc[mi][ni][i] = __builtin_fmaf(t, sx[mi], acc[mi][ni][i]);
+            }
+          }
+        }
+      }
+      lds_barrier();
+    }
+  }
+
+  // D: lane l holds column l % 32 (a token), register i the weight row
+  // 8 * (i / 4) + 4 * (l / 32) + i % 4 -> four runs of 4 consecutive rows
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int t = t0 + 64 * wave + 32 * mi + l32;
+    if (t >= m) continue;
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 32 * ni + 8 * q + 4 * half;
+        float* dst = y + int64_t(t) * n_rows + r;
+        if (r + 3 < n_rows && (n_rows & 3) == 0) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (r + e < n_rows) dst[e] = acc[mi][ni][4 * q + e];
+        }
+      }
+  }
+}
+
 // -------------------------------------------------------------------- host --
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -809,7 +1194,26 @@ size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
   if (mode == 0) return align256(size_t((m + 31) / 32 * 32) * size_t(cols) * 2);  // whole 32-token tiles
   const size_t mp = size_t((m + 31) / 32 * 32);  // tokens padded to whole 32-token tiles
   const size_t blocks = mp * size_t(cols / 32);
+  // 32-element blocks: codes, scales, scaled sums; 256-element blocks
+  // (K-quant weights) need less: codes, a scale per 256 and 16 bytes of f16
+  // sums per 256
   return align256(mp * size_t(cols)) + 2 * align256(blocks * sizeof(float));
+}
+
+// Workspace carve-up of the 256-element int8 path: codes, scales, sums.
+struct Q8kWs {
+  uint8_t* codes;
+  float* scales;
+  uint8_t* sums;
+};
+static Q8kWs q8k_ws(uint8_t* ws, int64_t cols, int64_t m) {
+  const size_t mp = size_t((m + 31) / 32 * 32);
+  const size_t nsb = size_t(cols / 256);
+  Q8kWs r;
+  r.codes = ws;
+  r.scales = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)));
+  r.sums = ws + align256(mp * size_t(cols)) + align256(mp * nsb * sizeof(float));
+  return r;
 }
 
 template <class S>
@@ -820,6 +1224,11 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
   if (mode == 0) {
     hipLaunchKernelGGL(mm_bf16_ws_kernel<S>, grid, dim3(kMmWsThreads), kMmLdsWs, s, w, rows, cols, rb,
                        reinterpret_cast<const u32x4*>(ws), m, y, ntm, q6s);
+  } else if constexpr (S::kQ8K) {
+    const Q8kWs q = q8k_ws(ws, cols, m);
+    hipLaunchKernelGGL(mm_q8k_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
+                       reinterpret_cast<const int8_t*>(q.codes), q.scales, reinterpret_cast<const u32x4*>(q.sums),
+                       m, y, ntm);
   } else if constexpr (S::kQ8) {
     const size_t mp = size_t((m + 31) / 32 * 32);
     const size_t blocks = mp * size_t(cols / 32);
@@ -841,6 +1250,15 @@ hipError_t launch_quantize_q8(const float* x, int64_t n, int8_t* q, float* scale
   return hipGetLastError();
 }
 
+hipError_t launch_quantize_q8k(const float* x, int64_t n, int8_t* q, float* scales, int32_t* sums,
+                               hipStream_t s) {
+  if (n <= 0 || n % 256 != 0) return hipErrorInvalidValue;
+  const int64_t supers = n / 256;  // a wave each
+  hipLaunchKernelGGL(x_q8k_kernel, dim3(unsigned((supers + 3) / 4)), dim3(256), 0, s, x,
+                     reinterpret_cast<uint32_t*>(q), scales, sums, supers);
+  return hipGetLastError();
+}
+
 hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t cols, const float* x,
                          int64_t m, float* y, uint32_t mode, void* workspace, int q6_signed,
                          hipStream_t s) {
@@ -852,6 +1270,11 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
     const int64_t pieces = (m + 31) / 32 * 32 * cols / 8;  // 16-byte pieces of whole 32-token tiles
     hipLaunchKernelGGL(x_bf16_tiled_kernel, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s, x,
                        reinterpret_cast<u32x4*>(ws), int(m), int(cols), pieces);
+  } else if (quant == kQ4_K || quant == kQ5_K) {
+    const Q8kWs q = q8k_ws(ws, cols, m);
+    const int64_t waves = (m + 31) / 32 * 32 * (cols / 256);  // one per (padded token, super-block)
+    hipLaunchKernelGGL(x_q8k_tiled_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s, x, q.codes,
+                       q.scales, q.sums, int(m), int(cols), waves);
   } else {
     const size_t mp = size_t((m + 31) / 32 * 32);
     const size_t blocks = mp * size_t(cols / 32);

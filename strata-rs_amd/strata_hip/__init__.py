@@ -59,7 +59,7 @@ EXPORTS = (
     "sh_gemv", "sh_gemv_batch", "sh_expert_gemv", "sh_dequantize_row",
     "sh_moe_route", "sh_moe_ffn", "sh_moe_layer", "sh_matmul",
     "sh_moe_workspace_bytes", "sh_moe_ffn_dev", "sh_matmul_workspace_bytes", "sh_matmul_dev",
-    "sh_quantize_q8_dev", "sh_moe_layer_workspace_bytes", "sh_moe_layer_dev", "sh_dequant_dev",
+    "sh_quantize_q8_dev", "sh_quantize_q8k_dev", "sh_moe_layer_workspace_bytes", "sh_moe_layer_dev", "sh_dequant_dev",
     "sh_gemv_dev", "sh_rms_norm", "sh_rope_neox", "sh_softmax", "sh_l2_norm", "sh_add", "sh_rms_norm_dev",
     "sh_l2_norm_dev", "sh_softmax_dev", "sh_rope_neox_dev", "sh_add_dev", "sh_gguf_open", "sh_gguf_close",
     "sh_gguf_header", "sh_gguf_tensor", "sh_gguf_find", "sh_gguf_tensor_data", "sh_gguf_meta_type",
@@ -222,6 +222,7 @@ def load_library() -> C.CDLL:
     L.sh_matmul_workspace_bytes.argtypes = [u32, u64, u64, u32, u32, C.POINTER(C.c_uint64)]
     L.sh_matmul_dev.argtypes = [u32, u32, vp, u64, u64, vp, u32, vp, u32, vp, u64, vp]
     L.sh_quantize_q8_dev.argtypes = [vp, u64, vp, vp, vp, vp]
+    L.sh_quantize_q8k_dev.argtypes = [vp, u64, vp, vp, vp, vp]
     L.sh_dequant_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp]
     L.sh_gemv_dev.argtypes = [u32, u32, vp, u64, u64, vp, vp, u32, vp]
     L.sh_stream_read_dev.argtypes = [vp, u64, vp, vp]
@@ -792,6 +793,11 @@ def matmul_dev(quant: int, w_ptr: int, rows: int, cols: int, x_ptr: int, m: int,
 def quantize_q8_dev(x_ptr: int, n: int, codes_ptr: int, scales_ptr: int, sums_ptr: int,
                     stream: int = 0) -> None:
     check(load_library().sh_quantize_q8_dev(x_ptr, n, codes_ptr, scales_ptr, sums_ptr, stream or None))
+
+
+def quantize_q8k_dev(x_ptr: int, n: int, codes_ptr: int, scales_ptr: int, sums_ptr: int,
+                     stream: int = 0) -> None:
+    check(load_library().sh_quantize_q8k_dev(x_ptr, n, codes_ptr, scales_ptr, sums_ptr, stream or None))
 
 
 def rms_norm_dev(x_ptr: int, w_ptr: int, out_ptr: int, rows: int, n: int, eps: float, stream: int = 0) -> None:

@@ -8,10 +8,14 @@ Metric: max|y - r| / max|r| per token row.
   the same gemvs on bf16-rounded operands (W dequantized exactly then rounded
   to bf16, x rounded to bf16, f64 sums): <= 1e-3 -- this isolates the
   kernel's indexing and accumulation from the rounding the mode defines.
-* q8 mode against the oracle gemv of x rounded through Q8 blocks
-  (scale * code): <= 1e-3 (the int8 products are exact); against the f32
-  oracle: <= 2e-2.
-* the device Q8 quantizer is bit-exact with the oracle's.
+* q8 mode against the oracle gemv of x rounded through Q8 blocks of the
+  weight's scale group (scale * code; 32 elements for Q8_0, 256 for Q4_K
+  and Q5_K): <= 1e-3 (the int8 products are exact); against the f32
+  oracle: <= 2e-2 with 32-element blocks, <= 3e-2 with 256-element ones (the
+  code step is max|x| / 127 over 256 elements instead of 32: about 1.3x the
+  rounding; measured worst rows 1.3-2.1%).
+* the device Q8 quantizers (32- and 256-element blocks) are bit-exact with
+  the oracle's.
 """
 import numpy as np
 import pytest
@@ -23,6 +27,7 @@ from strata_hip import synth as S
 pytestmark = pytest.mark.gpu
 
 TOL_F32 = 2e-2
+TOL_F32_Q8K = 3e-2  # the activation rounding of one scale per 256 elements
 TOL_EXACT_OPERANDS = 1e-3
 
 
@@ -80,9 +85,9 @@ def test_matmul_q8(backend, oracle, quant, rows, cols, m):
     w = S.matrix(quant, 920 + rows, rows, cols)
     x = S.normal_f32(921 + m, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor(f"mq{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_Q8)
-    xq = oracle.dequantize_q8_activations(x)
+    xq = oracle.q8_activations_for(quant, x)
     check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
-    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32_Q8K if quant in (12, 13) else TOL_F32)
 
 
 @pytest.fixture(scope="module")
@@ -99,10 +104,10 @@ def test_matmul_prefill_config(backend, oracle, prefill_weight, mode):
     x = S.normal_f32(0x5EED0006, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor("prefill.w", 12, rows, cols, w), x, mode)
     ref = oracle.matmul(12, rows, cols, w, x, threads=16)
-    worst = check_rows(y, ref, TOL_F32)
+    worst = check_rows(y, ref, TOL_F32_Q8K if mode == 1 else TOL_F32)
     print(f"[case] mode {mode}: worst row rel err vs f32 oracle {worst:.3g}", flush=True)
     if mode == 1:
-        exact = oracle.matmul(12, rows, cols, w, oracle.dequantize_q8_activations(x), threads=16)
+        exact = oracle.matmul(12, rows, cols, w, oracle.q8_activations_for(12, x), threads=16)
     else:
         exact = bf16_operand_ref(oracle, 12, rows, cols, w, x)
     check_rows(y, exact, TOL_EXACT_OPERANDS, STRICT_TOL)
@@ -128,6 +133,44 @@ def test_quantize_q8_dev_bit_exact(backend, oracle):
     assert np.array_equal(q.cpu().numpy(), oq)
     assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
     assert np.array_equal(u.cpu().numpy().view(np.uint32), ou.view(np.uint32))
+
+
+def test_quantize_q8k_dev_bit_exact(backend, oracle):
+    import torch
+    say("quantize q8k dev")
+    x = S.normal_f32(931, 256 * 300) * np.float32(5.0)
+    x[:256] = 0.0                     # s = 0: codes 0
+    x[256:262] = [2.5, 3.5, -2.5, 0.5, 1.5, -0.49]
+    x[256 + 200] = -127.0             # s = 1 exactly: ties to even visible
+    x[512:768] *= np.float32(1e-30)   # tiny but normal values
+    x[768 + 32:768 + 64] *= np.float32(1e4)  # one sub-block far above the rest
+    dev = torch.device("cuda:0")
+    tx = torch.from_numpy(x).to(dev)
+    q = torch.empty(x.size, dtype=torch.int8, device=dev)
+    s = torch.empty(x.size // 256, dtype=torch.float32, device=dev)
+    u = torch.empty(x.size // 32, dtype=torch.int32, device=dev)
+    H.quantize_q8k_dev(tx.data_ptr(), x.size, q.data_ptr(), s.data_ptr(), u.data_ptr(),
+                       torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    oq, os_, ou = oracle.quantize_q8k(x)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(u.cpu().numpy(), ou)
+
+
+@pytest.mark.parametrize("quant", [12, 13])
+def test_matmul_q8k_wide_sub_block_spread(backend, oracle, quant):
+    # one sub-block of each super-block 1e3 above the others: the 256-element
+    # scale leaves the small ones few code steps, which the oracle's rounding
+    # reproduces exactly; rows of both halves of the code range
+    rows, cols, m = 96, 1024, 40
+    say("matmul q8k spread", quant)
+    w = S.matrix(quant, 950, rows, cols)
+    x = S.normal_f32(951, m * cols).reshape(m, cols)
+    x.reshape(m, -1, 256)[:, :, 64:96] *= np.float32(1e3)
+    y = backend.matmul(H.QuantTensor(f"mqs{quant}", quant, rows, cols, w), x, H.MATMUL_Q8)
+    xq = oracle.q8_activations_for(quant, x)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
 @pytest.mark.parametrize("mode", [0, 1])

@@ -294,6 +294,54 @@ def test_quantize_q8_closed_form(oracle):
     assert np.array_equal(u, (s * q.reshape(-1, 32).astype(np.int64).sum(axis=1).astype(np.float32)))
 
 
+def test_quantize_q8k_known_answers(oracle):
+    # block 0: max|x| = 127 anywhere in the 256 -> s = 1 exactly, codes are x
+    # rounded to nearest even, sums per 32 elements; block 1: all zero
+    x = np.zeros(512, np.float32)
+    x[:6] = [2.5, 3.5, -2.5, 0.5, 1.5, -0.49]
+    x[200] = -127.0
+    x[33] = 7.0
+    q, s, u = oracle.quantize_q8k(x)
+    assert s.tolist() == [1.0, 0.0]
+    assert q[:6].tolist() == [2, 4, -2, 0, 2, 0] and q[200] == -127 and q[33] == 7
+    assert np.count_nonzero(q) == 6  # 0.5 and -0.49 round to 0
+    assert u.tolist() == [6, 7, 0, 0, 0, 0, -127, 0] + [0] * 8
+
+
+def test_quantize_q8k_is_q8_when_every_sub_block_holds_the_max(oracle):
+    # with +-max|x| of the 256 in each of its 32-element sub-blocks, the one
+    # super-block scale equals every block scale of the 32-element quantizer:
+    # the codes agree and the integer sums are its u / s
+    rng = np.random.default_rng(75)
+    x = S.normal_f32(75, 256 * 40)
+    xb = x.reshape(-1, 8, 32)
+    amax = np.abs(xb).max(axis=(1, 2))
+    for b in range(xb.shape[0]):
+        for j in range(8):
+            xb[b, j, rng.integers(32)] = amax[b] * (1 if rng.integers(2) else -1)
+    q, s, u = oracle.quantize_q8k(x)
+    q8, s8, u8 = oracle.quantize_q8(x)
+    assert np.array_equal(q, q8)
+    assert np.array_equal(np.repeat(s, 8), s8)
+    assert np.array_equal(s8 * u.astype(np.float32), u8)
+
+
+def test_quantize_q8k_closed_form(oracle):
+    # one scale per 256 (not per 32): numpy restatement with f32 division and
+    # rint, the max maps to +-127, sums over each 32-element sub-block
+    x = S.normal_f32(76, 256 * 300) * np.float32(3.0)
+    x[256 * 7: 256 * 8] = 0.0
+    q, s, u = oracle.quantize_q8k(x)
+    xb = x.reshape(-1, 256)
+    sref = (np.abs(xb).max(axis=1) / np.float32(127.0)).astype(np.float32)
+    assert np.array_equal(s, sref)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ref = np.where(sref[:, None] > 0, np.rint(xb / sref[:, None]), 0).astype(np.int8)
+    assert np.array_equal(q.reshape(-1, 256), ref)
+    assert np.all(np.abs(ref).max(axis=1)[sref > 0] == 127)
+    assert np.array_equal(u, ref.reshape(-1, 32).astype(np.int64).sum(axis=1))
+
+
 def test_bf16_round_matches_torch_and_scalar(oracle):
     import torch
     x = np.concatenate([S.normal_f32(74, 4096) * np.float32(100.0),
