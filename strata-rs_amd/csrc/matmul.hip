@@ -514,15 +514,15 @@ __global__ void __launch_bounds__(256) x_q8k_kernel(const float* __restrict__ x,
 }
 
 // The same blocks for mm_q8k_kernel, in the order its waves load them
-// (tokens padded with zero blocks to a multiple of 32; T = token / 32,
-// l = token % 32, nch = cols / 64, nsb = cols / 256):
-//   codes: as x_q8_tiled_kernel (16-byte piece ((T * nch + c) * 2 + s) * 64
-//          + 32 h + l holds chunk c's elements [32 s + 16 h, +16));
-//   s:     float (T * nsb + sb) * 32 + l;
-//   sums:  16-byte piece (T * nsb + sb) * 64 + 32 h + l, eight f16: h = 0
-//          the high parts b >> 6 of sub-blocks 0..7, h = 1 the low parts
-//          b & 63 (b = 64 * hi + lo exactly; both exact in f16), the B
-//          operand of the min-term MFMA.
+// (tokens padded with zero blocks to a multiple of 32; T = token / 16,
+// j = token % 16, nch = cols / 64, nsb = cols / 256):
+//   codes: 16-byte piece (T * nch + c) * 64 + 16 g + j holds chunk c's
+//          elements [16 g, 16 g + 16) (one 1 KiB wave load per 16-token tile);
+//   s:     float (T * nsb + sb) * 16 + j;
+//   sums:  8-byte piece (T * nsb + sb) * 64 + 16 g + j, four f16: g = 0, 1
+//          the high parts b >> 6 of sub-blocks 4g .. 4g + 3, g = 2, 3 the low
+//          parts b & 63 of sub-blocks 4(g - 2) .. +3 (b = 64 hi + lo exactly;
+//          both exact in f16): the B operand of the min-term MFMA.
 __global__ void __launch_bounds__(256) x_q8k_tiled_kernel(const float* __restrict__ x, uint8_t* __restrict__ qt,
                                                           float* __restrict__ st, uint8_t* __restrict__ bt, int m,
                                                           int cols, int64_t waves) {
@@ -532,23 +532,23 @@ __global__ void __launch_bounds__(256) x_q8k_tiled_kernel(const float* __restric
   const int nsb = cols >> 8, nch = cols / kMmKC;
   const int sb = int(wv % nsb);
   const int64_t t = wv / nsb;  // padded token
-  const int64_t T = t >> 5;
-  const int l = int(t & 31);
+  const int64_t T = t >> 4;
+  const int j = int(t & 15);
   uint32_t codes;
   float sv;
   int sum;
   q8k_wave(x + (t < m ? t : 0) * int64_t(cols) + 256 * sb, t < m, lane, codes, sv, sum);
-  // element 4 lane of the super-block: chunk 4 sb + lane / 16, step (lane / 8) & 1,
-  // half (lane / 4) & 1, bytes 4 (lane & 3) of the piece
-  const int c = 4 * sb + (lane >> 4), st_ = (lane >> 3) & 1, h = (lane >> 2) & 1;
-  const int64_t piece = ((T * nch + c) * 2 + st_) * 64 + 32 * h + l;
+  // element 4 lane of the super-block: chunk 4 sb + lane / 16, group
+  // (lane / 4) & 3, bytes 4 (lane & 3) of the piece
+  const int c = 4 * sb + (lane >> 4), g = (lane >> 2) & 3;
+  const int64_t piece = (T * nch + c) * 64 + 16 * g + j;
   *reinterpret_cast<uint32_t*>(qt + piece * 16 + 4 * (lane & 3)) = codes;
-  if (lane == 0) st[(T * nsb + sb) * 32 + l] = sv;
+  if (lane == 0) st[(T * nsb + sb) * 16 + j] = sv;
   if ((lane & 7) == 0) {
-    const int j = lane >> 3;
-    _Float16* b = reinterpret_cast<_Float16*>(bt + ((T * nsb + sb) * 64 + l) * 16);
-    b[j] = _Float16(float(sum >> 6));          // h = 0 piece
-    b[32 * 8 + j] = _Float16(float(sum & 63));  // h = 1 piece (32 pieces on)
+    const int sj = lane >> 3;  // sub-block
+    _Float16* b = reinterpret_cast<_Float16*>(bt + ((T * nsb + sb) * 64 + j) * 8);
+    b[16 * 4 * (sj >> 2) + (sj & 3)] = _Float16(float(sum >> 6));            // group sj / 4
+    b[16 * 4 * (2 + (sj >> 2)) + (sj & 3)] = _Float16(float(sum & 63));      // group 2 + sj / 4
   }
 }
 
@@ -959,59 +959,70 @@ __global__ void __launch_bounds__(kMmThreads)
 //   sum_k value_k * x_k = s_t * (d * (8 H + L + z * sum_j sc_j b_tj)
 //                                - dmin * sum_j m_j b_tj)
 // H = sum_k sh_j p_k c_k and L = sum_k sl_j p_k c_k run on
-// v_mfma_i32_32x32x32_i8 (weight operands sh * p and sl * p, int8) with the
-// int32 sums carried through all 8 sub-blocks of the super-block; the two
-// sub-block sums over b_tj are exact integers on one v_mfma_f32_32x32x16_f16
-// each (b = 64 hi + lo, the weight side 64 m | m, both halves exact in f16);
-// the VALU rescales once per super-block and output (5 ops, 6 for Q5_K),
-// not once per 32-element block.
+// v_mfma_i32_16x16x64_i8 (weight operands sh * p and sl * p, int8; one
+// instruction covers a 64-element chunk) with the int32 sums carried
+// through the super-block's 4 chunks; the two sums over b_tj are exact
+// integers on one v_mfma_f32_16x16x16_f16 each (b = 64 hi + lo, the weight
+// side 64 m | m, every value exact in f16); the VALU rescales once per
+// super-block and output (5 ops, 6 for Q5_K), not once per 32-element block.
 //
-// Same tile and staging as mm_q8_kernel (4 waves along the tokens, each 2 x 3
-// output tiles of 32 x 32; waves 0-2 also stage, two chunks of loads in
-// flight: the 288 accumulator registers leave little room); LDS holds the two limb planes of the chunk (double-buffered) and,
-// per super-block (double-buffered), the rows' f16 operands of the sum MFMAs
-// and d, dmin.
+// Workgroup tile 256 tokens x 96 rows (as the other prefill kernels), 8
+// waves: wave w owns tokens [64 (w % 4), +64) x rows [48 (w / 4), +48), 4 x 3
+// output tiles of 16 x 16 (144 accumulator registers, so two waves fit each
+// SIMD and cover each other's LDS, load and barrier waits). Waves 0-2 also
+// stage: the codes times both limbs into a double-buffered LDS tile, the
+// next chunk's weight loads in flight, and per super-block (double-buffered)
+// the rows' f16 operands of the sum MFMAs and d, dmin.
+constexpr int kMqThreads = 512;
+
 template <class S>
-__global__ void __launch_bounds__(kMmThreads)
+__global__ void __launch_bounds__(kMqThreads)
     mm_q8k_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
-                  const int8_t* __restrict__ xq, const float* __restrict__ xs, const u32x4* __restrict__ xb,
+                  const int8_t* __restrict__ xq, const float* __restrict__ xs, const uint8_t* __restrict__ xb,
                   int m, float* __restrict__ y, int n_tiles_m) {
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
   constexpr bool kZ = S::kCenter != 0;
   constexpr int kA = kZ ? 32 : 16;  // f16 per row and super-block: 64 m | m (| 1024 sc | 16 sc)
   __shared__ __attribute__((aligned(16))) uint8_t wl[2][2][kMmBN * kMmRowQ];  // [buf][sh * p | sl * p]
   __shared__ __attribute__((aligned(16))) _Float16 ma[2][kMmBN * kA];         // [super-block buf]
   __shared__ __attribute__((aligned(16))) float dsc[2][2][kMmBN];             // [super-block buf][d | dmin]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int tg = wave & 3, rg = wave >> 2;
   int r0, t0;
   tile_of(n_tiles_m, r0, t0);
   const int nchunks = cols / kMmKC;
   const int nsb = cols >> 8;
 
   constexpr int kTasks = kMmBN * S::kPieces;
-  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
+  static_assert(kTasks % kWave == 0 && kTasks <= kMqThreads, "staging tasks fill whole waves");
   const bool stager = tid < kTasks;
   const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
   const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
 
-  const int n_tt = (m + 31) >> 5;
-  const int8_t* xr[2];
-  const float* sr[2];
-  const u32x4* br[2];
+  // the wave's 4 token tiles of 16 (clamped to the padded tokens; rows past m
+  // are computed on zero codes and not stored): wave-uniform bases, so the
+  // loads take a scalar base and the lane's 32-bit offset
+  const int n_t16 = ((m + 31) >> 5) * 2;
+  const int8_t* xr[4];
+  const float* sr[4];
+  const uint8_t* br[4];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int T = min((t0 + 64 * wave + 32 * mi) >> 5, n_tt - 1);
-    xr[mi] = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
-    sr[mi] = xs + int64_t(T) * nsb * 32 + l32;
-    br[mi] = xb + int64_t(T) * nsb * 64 + lane;
+  for (int mt = 0; mt < 4; ++mt) {
+    const int T = min((t0 + 64 * tg + 16 * mt) >> 4, n_t16 - 1);
+    xr[mt] = xq + int64_t(T) * nchunks * 1024;
+    sr[mt] = xs + int64_t(T) * nsb * 16;
+    br[mt] = xb + int64_t(T) * nsb * 512;
   }
+  const uint32_t xo = 16u * uint32_t(lane), so = uint32_t(l16), bo = 8u * uint32_t(lane);
 
-  f32x16 acc[2][3];
-  i32x16 ah[2][3], al[2][3];
+  f32x4 acc[4][3];
+  i32x4 ah[4][3], al[4][3];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+    for (int nt = 0; nt < 3; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // one piece of chunk c: its codes times both limbs into LDS buffer buf
   auto stage = [&](const typename S::Raw& raw, int c, int buf) {
@@ -1051,7 +1062,7 @@ __global__ void __launch_bounds__(kMmThreads)
     dsc[sbuf][1][srow] = h2f(raw.h.x >> 16);
   };
 
-  constexpr int kRing = 2;  // weight chunks in flight ahead of staging (registers are short here)
+  constexpr int kRing = 1;  // weight chunks in flight ahead of staging (a second costs spills: slower)
   typename S::Raw raw[kRing];
   if (stager) {
 #pragma unroll
@@ -1060,91 +1071,73 @@ __global__ void __launch_bounds__(kMmThreads)
     if (piece == 0) header(raw[0], 0);
     raw[0] = S::load(wrow, min(kRing, nchunks - 1), piece);
   }
-  i32x4 xc[2][2];
+  i32x4 xc[4];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 1024 * s);
+  for (int mt = 0; mt < 4; ++mt) xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + xo);
   lds_barrier();
 
   for (int sb = 0; sb < nsb; ++sb) {
     const int sbuf = sb & 1;
-    float sx[2];
-    u32x4 bs[2];
+    float sx[4];
+    f16x4 bs[4];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-      sx[mi] = sr[mi][32 * sb];
-      bs[mi] = br[mi][64 * sb];
+    for (int mt = 0; mt < 4; ++mt) {
+      sx[mt] = (sr[mt] + 16 * sb)[so];
+      bs[mt] = *reinterpret_cast<const f16x4*>(br[mt] + 512 * sb + bo);
     }
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {  // chunks of the super-block
       const int c = 4 * sb + cc;
       const bool more = c + 1 < nchunks;  // uniform
-      i32x4 xn[2][2];
-      if (more) {
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-          for (int s = 0; s < 2; ++s)
-            xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * 2048 + 1024 * s);
-      }
       const uint8_t* wh = wl[cc & 1][0];
       const uint8_t* wo = wl[cc & 1][1];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {  // sub-block 2 (c % 4) + s
+      for (int nt = 0; nt < 3; ++nt) {
+        const int ro = (48 * rg + 16 * nt + l16) * kMmRowQ + 16 * g;
+        const i32x4 a_h = *reinterpret_cast<const i32x4*>(wh + ro);
+        const i32x4 a_l = *reinterpret_cast<const i32x4*>(wo + ro);
 #pragma unroll
-        for (int ni = 0; ni < 3; ++ni) {
-          const int ro = (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half;
-          const i32x4 a_h = *reinterpret_cast<const i32x4*>(wh + ro);
-          const i32x4 a_l = *reinterpret_cast<const i32x4*>(wo + ro);
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            const bool first = cc == 0 && s == 0;  // a new super-block: the int32 sums start at zero
-            ah[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_h, xc[mi][s], first ? i32x16{} : ah[mi][ni], 0,
-                                                               0, 0);
-            al[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_l, xc[mi][s], first ? i32x16{} : al[mi][ni], 0,
-                                                               0, 0);
-          }
+        for (int mt = 0; mt < 4; ++mt) {
+          // a new super-block: the int32 sums start at zero
+          ah[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_h, xc[mt], cc == 0 ? i32x4{0, 0, 0, 0} : ah[mt][nt],
+                                                             0, 0, 0);
+          al[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_l, xc[mt], cc == 0 ? i32x4{0, 0, 0, 0} : al[mt][nt],
+                                                             0, 0, 0);
         }
       }
       if (more) {
+        // the next chunk's activation fragments (the MFMAs above have read xc)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + int64_t(c + 1) * 1024 + xo);
         if (stager) {
           const int slot = (cc + 1) % kRing;  // where chunk c + 1 was loaded (c % 4 == cc)
           stage(raw[slot], c + 1, (cc + 1) & 1);
           if (cc == 3 && piece == 0) header(raw[slot], sbuf ^ 1);
           raw[slot] = S::load(wrow, min(c + 1 + kRing, nchunks - 1), piece);
         }
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-          for (int s = 0; s < 2; ++s) xc[mi][s] = xn[mi][s];
       }
       if (cc == 3) {
         // rescale: acc += s_t * (d * (8 H + L [+ z sc.b]) - dmin * m.b)
 #pragma unroll
-        for (int ni = 0; ni < 3; ++ni) {
-          const _Float16* mrow = ma[sbuf] + (32 * ni + l32) * kA;
-          const f16x8 am = *reinterpret_cast<const f16x8*>(mrow + 8 * half);
-          f16x8 az;
-          if constexpr (kZ) az = *reinterpret_cast<const f16x8*>(mrow + 16 + 8 * half);
-          f32x4 dv[4], mv[4];
+        for (int nt = 0; nt < 3; ++nt) {
+          const int row = 48 * rg + 16 * nt;
+          const _Float16* mrow = ma[sbuf] + (row + l16) * kA;
+          const f16x4 am = *reinterpret_cast<const f16x4*>(mrow + 4 * g);
+          f16x4 az;
+          if constexpr (kZ) az = *reinterpret_cast<const f16x4*>(mrow + 16 + 4 * g);
+          const f32x4 dv = *reinterpret_cast<const f32x4*>(&dsc[sbuf][0][row + 4 * g]);
+          const f32x4 mv = *reinterpret_cast<const f32x4*>(&dsc[sbuf][1][row + 4 * g]);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            dv[q] = *reinterpret_cast<const f32x4*>(&dsc[sbuf][0][32 * ni + 8 * q + 4 * half]);
-            mv[q] = *reinterpret_cast<const f32x4*>(&dsc[sbuf][1][32 * ni + 8 * q + 4 * half]);
-          }
+          for (int mt = 0; mt < 4; ++mt) {
+            const f32x4 mb = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bs[mt], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            f32x4 zb = f32x4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (kZ) zb = __builtin_amdgcn_mfma_f32_16x16x16f16(az, bs[mt], zb, 0, 0, 0);
 #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            const f16x8 b = __builtin_bit_cast(f16x8, bs[mi]);
-            const f32x16 mb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b, f32x16{}, 0, 0, 0);
-            f32x16 zb = f32x16{};
-            if constexpr (kZ) zb = __builtin_amdgcn_mfma_f32_32x32x16_f16(az, b, f32x16{}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              float f = float((ah[mi][ni][i] << 3) + al[mi][ni][i]);
+            for (int i = 0; i < 4; ++i) {
+              float f = float((ah[mt][nt][i] << 3) + al[mt][nt][i]);
               if constexpr (kZ) f += zb[i];
-              const float t = __builtin_fmaf(f, dv[i >> 2][i & 3], -(mb[i] * mv[i >> 2][i & 3]));
-              acc[mi][ni][i] = __builtin_fmaf(t, sx[mi], acc[mi][ni][i]);
+              const float t = __builtin_fmaf(f, dv[i], -(mb[i] * mv[i]));
+              acc[mt][nt][i] = __builtin_fmaf(t, sx[mt], acc[mt][nt][i]);
             }
           }
         }
@@ -1153,27 +1146,24 @@ __global__ void __launch_bounds__(kMmThreads)
     }
   }
 
-  // D: lane l holds column l % 32 (a token), register i the weight row
-  // 8 * (i / 4) + 4 * (l / 32) + i % 4 -> four runs of 4 consecutive rows
+  // D of a 16 x 16 tile: lane l holds column l % 16 (a token) and rows
+  // 4 (l / 16) .. + 3
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int t = t0 + 64 * wave + 32 * mi + l32;
+  for (int mt = 0; mt < 4; ++mt) {
+    const int t = t0 + 64 * tg + 16 * mt + l16;
     if (t >= m) continue;
 #pragma unroll
-    for (int ni = 0; ni < 3; ++ni)
+    for (int nt = 0; nt < 3; ++nt) {
+      const int r = r0 + 48 * rg + 16 * nt + 4 * g;
+      float* dst = y + int64_t(t) * n_rows + r;
+      if (r + 3 < n_rows && (n_rows & 3) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = acc[mt][nt];
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = r0 + 32 * ni + 8 * q + 4 * half;
-        float* dst = y + int64_t(t) * n_rows + r;
-        if (r + 3 < n_rows && (n_rows & 3) == 0) {
-          *reinterpret_cast<f32x4*>(dst) =
-              f32x4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (r + e < n_rows) dst[e] = acc[mi][ni][4 * q + e];
-        }
+        for (int e = 0; e < 4; ++e)
+          if (r + e < n_rows) dst[e] = acc[mt][nt][e];
       }
+    }
   }
 }
 
@@ -1226,9 +1216,8 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
                        reinterpret_cast<const u32x4*>(ws), m, y, ntm, q6s);
   } else if constexpr (S::kQ8K) {
     const Q8kWs q = q8k_ws(ws, cols, m);
-    hipLaunchKernelGGL(mm_q8k_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb,
-                       reinterpret_cast<const int8_t*>(q.codes), q.scales, reinterpret_cast<const u32x4*>(q.sums),
-                       m, y, ntm);
+    hipLaunchKernelGGL(mm_q8k_kernel<S>, grid, dim3(kMqThreads), 0, s, w, rows, cols, rb,
+                       reinterpret_cast<const int8_t*>(q.codes), q.scales, q.sums, m, y, ntm);
   } else if constexpr (S::kQ8) {
     const size_t mp = size_t((m + 31) / 32 * 32);
     const size_t blocks = mp * size_t(cols / 32);
