@@ -969,10 +969,11 @@ __global__ void __launch_bounds__(kMmThreads)
 // Workgroup tile 256 tokens x 96 rows (as the other prefill kernels), 8
 // waves: wave w owns tokens [64 (w % 4), +64) x rows [48 (w / 4), +48), 4 x 3
 // output tiles of 16 x 16 (144 accumulator registers, so two waves fit each
-// SIMD and cover each other's LDS, load and barrier waits). Waves 0-2 also
-// stage: the codes times both limbs into a double-buffered LDS tile, the
-// next chunk's weight loads in flight, and per super-block (double-buffered)
-// the rows' f16 operands of the sum MFMAs and d, dmin.
+// SIMD and cover each other's LDS, load and barrier waits; the f32 sums live
+// in LDS, which leaves the registers to the int32 sums and the load ring).
+// Waves 0-2 also stage: the codes times both limbs into a double-buffered
+// LDS tile, two chunks of weight loads in flight, and per super-block
+// (double-buffered) the rows' f16 operands of the sum MFMAs and d, dmin.
 constexpr int kMqThreads = 512;
 
 template <class S>
@@ -986,6 +987,9 @@ __global__ void __launch_bounds__(kMqThreads)
   __shared__ __attribute__((aligned(16))) uint8_t wl[2][2][kMmBN * kMmRowQ];  // [buf][sh * p | sl * p]
   __shared__ __attribute__((aligned(16))) _Float16 ma[2][kMmBN * kA];         // [super-block buf]
   __shared__ __attribute__((aligned(16))) float dsc[2][2][kMmBN];             // [super-block buf][d | dmin]
+  // the f32 sums, touched once per super-block by the lane that owns them
+  // (in LDS, the registers carry the int32 sums and a deeper load ring)
+  __shared__ f32x4 accl[kMqThreads / kWave][12][kWave];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
@@ -1017,12 +1021,10 @@ __global__ void __launch_bounds__(kMqThreads)
   }
   const uint32_t xo = 16u * uint32_t(lane), so = uint32_t(l16), bo = 8u * uint32_t(lane);
 
-  f32x4 acc[4][3];
   i32x4 ah[4][3], al[4][3];
+  f32x4(&acc)[12][kWave] = accl[wave];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 3; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < 12; ++k) acc[k][lane] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // one piece of chunk c: its codes times both limbs into LDS buffer buf
   auto stage = [&](const typename S::Raw& raw, int c, int buf) {
@@ -1062,29 +1064,31 @@ __global__ void __launch_bounds__(kMqThreads)
     dsc[sbuf][1][srow] = h2f(raw.h.x >> 16);
   };
 
-  constexpr int kRing = 1;  // weight chunks in flight ahead of staging (a second costs spills: slower)
+  constexpr int kRing = 2;  // weight chunks in flight ahead of staging
+  static_assert(4 % kRing == 0, "ring slots are constants of the unrolled super-block loop");
+  // Every wave issues the weight loads (the other waves' lanes read row r0,
+  // one cache line a wave): with loads on one path only, the compiler's
+  // wait for the next chunk's activation fragments would also wait for
+  // these, a whole memory latency each chunk.
   typename S::Raw raw[kRing];
-  if (stager) {
 #pragma unroll
-    for (int k = 0; k < kRing; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+  for (int k = 0; k < kRing; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+  if (stager) {
     stage(raw[0], 0, 0);
     if (piece == 0) header(raw[0], 0);
-    raw[0] = S::load(wrow, min(kRing, nchunks - 1), piece);
   }
+  // activation fragments, then the next weight loads: the order of the
+  // chunk loop, so its waits count the same loads on entry as around it
   i32x4 xc[4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + xo);
+  raw[0] = S::load(wrow, min(kRing, nchunks - 1), piece);
   lds_barrier();
 
   for (int sb = 0; sb < nsb; ++sb) {
     const int sbuf = sb & 1;
     float sx[4];
     f16x4 bs[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      sx[mt] = (sr[mt] + 16 * sb)[so];
-      bs[mt] = *reinterpret_cast<const f16x4*>(br[mt] + 512 * sb + bo);
-    }
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {  // chunks of the super-block
       const int c = 4 * sb + cc;
@@ -1109,11 +1113,20 @@ __global__ void __launch_bounds__(kMqThreads)
         // the next chunk's activation fragments (the MFMAs above have read xc)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + int64_t(c + 1) * 1024 + xo);
+        const int slot = (cc + 1) % kRing;  // where chunk c + 1 was loaded (c % 4 == cc)
         if (stager) {
-          const int slot = (cc + 1) % kRing;  // where chunk c + 1 was loaded (c % 4 == cc)
           stage(raw[slot], c + 1, (cc + 1) & 1);
           if (cc == 3 && piece == 0) header(raw[slot], sbuf ^ 1);
-          raw[slot] = S::load(wrow, min(c + 1 + kRing, nchunks - 1), piece);
+        }
+        raw[slot] = S::load(wrow, min(c + 1 + kRing, nchunks - 1), piece);
+      }
+      if (cc == 2) {
+        // the tokens' scales and sums of this super-block, a chunk before the
+        // rescale needs them (not held through the whole super-block)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          sx[mt] = (sr[mt] + 16 * sb)[so];
+          bs[mt] = *reinterpret_cast<const f16x4*>(br[mt] + 512 * sb + bo);
         }
       }
       if (cc == 3) {
@@ -1132,13 +1145,15 @@ __global__ void __launch_bounds__(kMqThreads)
             const f32x4 mb = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bs[mt], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             f32x4 zb = f32x4{0.f, 0.f, 0.f, 0.f};
             if constexpr (kZ) zb = __builtin_amdgcn_mfma_f32_16x16x16f16(az, bs[mt], zb, 0, 0, 0);
+            f32x4 av = acc[3 * mt + nt][lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float f = float((ah[mt][nt][i] << 3) + al[mt][nt][i]);
               if constexpr (kZ) f += zb[i];
               const float t = __builtin_fmaf(f, dv[i], -(mb[i] * mv[i]));
-              acc[mt][nt][i] = __builtin_fmaf(t, sx[mt], acc[mt][nt][i]);
+              av[i] = __builtin_fmaf(t, sx[mt], av[i]);
             }
+            acc[3 * mt + nt][lane] = av;
           }
         }
       }
@@ -1156,12 +1171,13 @@ __global__ void __launch_bounds__(kMqThreads)
     for (int nt = 0; nt < 3; ++nt) {
       const int r = r0 + 48 * rg + 16 * nt + 4 * g;
       float* dst = y + int64_t(t) * n_rows + r;
+      const f32x4 av = acc[3 * mt + nt][lane];
       if (r + 3 < n_rows && (n_rows & 3) == 0) {
-        *reinterpret_cast<f32x4*>(dst) = acc[mt][nt];
+        *reinterpret_cast<f32x4*>(dst) = av;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (r + e < n_rows) dst[e] = acc[mt][nt][e];
+          if (r + e < n_rows) dst[e] = av[e];
       }
     }
   }
