@@ -465,11 +465,17 @@ constexpr int kPlainThreads = 256, kPlainUnroll = 8;
 template <int Q, int NB, bool XB>
 __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t* __restrict__ w, int rows, int cols,
                                                                   int64_t row_bytes, const float* __restrict__ x,
-                                                                  float* __restrict__ y) {
+                                                                  float* __restrict__ y, const uint8_t* __restrict__ w2,
+                                                                  int rows2, float* __restrict__ y2) {
   __shared__ double part[kPlainThreads / kWave][NB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = blockIdx.x;
-  const uint8_t* row = w + int64_t(r) * row_bytes;
+  // workgroups past `rows` take the rows of a second matrix of the same type
+  // and width (the MoE layer's gate-input row beside its router), against x
+  // as given (XB rounds only the first matrix's x) and into y2 [b][rows2]
+  const bool tail = int(blockIdx.x) >= rows;
+  const int r = tail ? int(blockIdx.x) - rows : int(blockIdx.x);
+  const uint8_t* row = (tail ? w2 : w) + int64_t(r) * row_bytes;
+  const bool round_x = XB && !tail;
   double acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = 0.0;
@@ -483,7 +489,7 @@ __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const float v = x[int64_t(b) * cols + c];
-        xv[k][b] = XB ? bf16_rne(v) : v;  // XB: the matvec of bf16(x)
+        xv[k][b] = round_x ? bf16_rne(v) : v;  // XB: the matvec of bf16(x)
       }
     }
 #pragma unroll
@@ -506,24 +512,32 @@ __global__ void __launch_bounds__(kPlainThreads) gemv_plain_kernel(const uint8_t
     double v = part[0][tid];
 #pragma unroll
     for (int k = 1; k < kPlainThreads / kWave; ++k) v += part[k][tid];
-    y[int64_t(tid) * rows + r] = float(v);
+    if (tail)
+      y2[int64_t(tid) * rows2 + r] = float(v);
+    else
+      y[int64_t(tid) * rows + r] = float(v);
   }
 }
 
 template <int Q, bool XB>
 static hipError_t launch_plain(int nb, const uint8_t* w, int rows, int cols, int64_t row_bytes, const float* x,
-                               float* y, hipStream_t s) {
-  const dim3 grid = dim3(unsigned(rows)), block = dim3(kPlainThreads);
+                               float* y, hipStream_t s, const uint8_t* w2 = nullptr, int rows2 = 0,
+                               float* y2 = nullptr) {
+  const dim3 grid = dim3(unsigned(rows + rows2)), block = dim3(kPlainThreads);
+#define SH_PLAIN(N)                                                                                           \
+  hipLaunchKernelGGL((gemv_plain_kernel<Q, N, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y, w2, rows2, \
+                     y2)
   switch (nb) {
-    case 1: hipLaunchKernelGGL((gemv_plain_kernel<Q, 1, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 2: hipLaunchKernelGGL((gemv_plain_kernel<Q, 2, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 3: hipLaunchKernelGGL((gemv_plain_kernel<Q, 3, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 4: hipLaunchKernelGGL((gemv_plain_kernel<Q, 4, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 5: hipLaunchKernelGGL((gemv_plain_kernel<Q, 5, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 6: hipLaunchKernelGGL((gemv_plain_kernel<Q, 6, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    case 7: hipLaunchKernelGGL((gemv_plain_kernel<Q, 7, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y); break;
-    default: hipLaunchKernelGGL((gemv_plain_kernel<Q, 8, XB>), grid, block, 0, s, w, rows, cols, row_bytes, x, y);
+    case 1: SH_PLAIN(1); break;
+    case 2: SH_PLAIN(2); break;
+    case 3: SH_PLAIN(3); break;
+    case 4: SH_PLAIN(4); break;
+    case 5: SH_PLAIN(5); break;
+    case 6: SH_PLAIN(6); break;
+    case 7: SH_PLAIN(7); break;
+    default: SH_PLAIN(8);
   }
+#undef SH_PLAIN
   return hipGetLastError();
 }
 
@@ -797,6 +811,60 @@ hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* wv, int64_t rows,
     case kF32: return launch_plain<kF32, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     case kF16: return launch_plain<kF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
     default: return launch_plain<kBF16, true>(batch, w, int(rows), int(cols), row_bytes, x, y, stream);
+  }
+}
+
+hipError_t launch_gemv_plain_pair(uint32_t quant, const void* w1, int64_t rows1, const void* w2, int64_t rows2,
+                                  int64_t cols, const float* x, float* y1, float* y2, int batch, hipStream_t stream) {
+  if (!plain_quant(quant) || !gemv_shape_ok(quant, rows1 + rows2, cols, batch) || rows2 < 0)
+    return hipErrorInvalidValue;
+  const uint8_t* a = static_cast<const uint8_t*>(w1);
+  const uint8_t* b = static_cast<const uint8_t*>(w2);
+  const uintptr_t al = uintptr_t(quant == kF32 ? 3 : 1);
+  if ((reinterpret_cast<uintptr_t>(a) & al) || (reinterpret_cast<uintptr_t>(b) & al)) return hipErrorInvalidValue;
+  const int64_t row_bytes = byte_size(quant, cols);
+  switch (quant) {
+    case kF32:
+      return launch_plain<kF32, true>(batch, a, int(rows1), int(cols), row_bytes, x, y1, stream, b, int(rows2), y2);
+    case kF16:
+      return launch_plain<kF16, true>(batch, a, int(rows1), int(cols), row_bytes, x, y1, stream, b, int(rows2), y2);
+    default:
+      return launch_plain<kBF16, true>(batch, a, int(rows1), int(cols), row_bytes, x, y1, stream, b, int(rows2), y2);
+  }
+}
+
+// The shared expert of a MoE layer for one token in two limb launches: [g; u]
+// = [gate; up] . x (one launch, x staged once), then d = down . (silu(g) * u)
+// with silu(g) * u formed as the down launch stages its x.
+bool shexp_fused_ok(uint32_t q_gu, uint32_t q_d, int64_t n_embd, int64_t n_ff) {
+  auto limb = [](uint32_t q) { return q == kQ4_K || q == kQ8_0 || q == kQ5_K || q == kQ6_K; };
+  return limb(q_gu) && limb(q_d) && n_embd % 64 == 0 && n_ff % 64 == 0 &&
+         gemv_shape_ok(q_gu, 2 * n_ff, n_embd, 1) && gemv_shape_ok(q_d, n_embd, n_ff, 1) &&
+         2 * n_ff <= (int64_t(1) << 30);
+}
+
+hipError_t launch_shexp_one(uint32_t q_gu, uint32_t q_d, const void* gate, const void* up, const void* down,
+                            int64_t n_embd, int64_t n_ff, const float* x, float* gu, float* d, int q6gu, int q6d,
+                            hipStream_t s) {
+  if (!shexp_fused_ok(q_gu, q_d, n_embd, n_ff)) return hipErrorInvalidValue;
+  const auto* g = static_cast<const uint8_t*>(gate);
+  const auto* u = static_cast<const uint8_t*>(up);
+  const auto* w = static_cast<const uint8_t*>(down);
+  const int64_t rb1 = byte_size(q_gu, n_embd), rb2 = byte_size(q_d, n_ff);
+  const int E = int(n_embd), N = int(n_ff);
+  hipError_t e;
+  switch (q_gu) {
+    case kQ4_K: e = launch_limb<LimbQ4K, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+    case kQ8_0: e = launch_limb<LimbQ8, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+    case kQ5_K: e = launch_limb<LimbQ5K, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+    default: e = launch_limb<LimbQ6K, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N);
+  }
+  if (e != hipSuccess) return e;
+  switch (q_d) {
+    case kQ4_K: return launch_limb<LimbQ4K, 1, 4, kLimbSiluX>(w, E, N, rb2, gu, d, s, 512, 8, q6d, nullptr, 0, gu + N);
+    case kQ8_0: return launch_limb<LimbQ8, 1, 4, kLimbSiluX>(w, E, N, rb2, gu, d, s, 512, 8, q6d, nullptr, 0, gu + N);
+    case kQ5_K: return launch_limb<LimbQ5K, 1, 4, kLimbSiluX>(w, E, N, rb2, gu, d, s, 512, 8, q6d, nullptr, 0, gu + N);
+    default: return launch_limb<LimbQ6K, 1, 4, kLimbSiluX>(w, E, N, rb2, gu, d, s, 512, 8, q6d, nullptr, 0, gu + N);
   }
 }
 

@@ -42,6 +42,16 @@ hipError_t launch_ffn(uint32_t q_gate, uint32_t q_up, uint32_t q_down, const voi
 // The same for F32 / F16 / BF16 rows against bf16(x) (rounded as loaded).
 hipError_t launch_gemv_plain_bf16x(uint32_t quant, const void* w, int64_t rows, int64_t cols, const float* x,
                                    float* y, int batch, hipStream_t stream);
+// Both in one launch: y1 = W1 . bf16(x) (rows1 rows) and y2 = W2 . x (rows2
+// rows of the same type and width), e.g. a MoE layer's router and gate input.
+hipError_t launch_gemv_plain_pair(uint32_t quant, const void* w1, int64_t rows1, const void* w2, int64_t rows2,
+                                  int64_t cols, const float* x, float* y1, float* y2, int batch, hipStream_t stream);
+// A MoE layer's shared expert for one token in two limb launches: gu = [gate;
+// up] . x (2 n_ff floats, g then u), d = down . (silu(g) * u).
+bool shexp_fused_ok(uint32_t q_gu, uint32_t q_d, int64_t n_embd, int64_t n_ff);
+hipError_t launch_shexp_one(uint32_t q_gu, uint32_t q_d, const void* gate, const void* up, const void* down,
+                            int64_t n_embd, int64_t n_ff, const float* x, float* gu, float* d, int q6gu, int q6d,
+                            hipStream_t s);
 
 // Batch 2..8 of Q4_K or Q5_K rows on int8 MFMA (exact integer
 // activations, staged in LDS 4096 columns at a time); `cu` is the device's

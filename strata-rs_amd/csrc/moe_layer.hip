@@ -10,12 +10,15 @@
 //            moe.rs:129-138);
 //   combine  out += sigmoid(s) * d, after the routed sum (moe.rs:139-142),
 //            inside the routed combine kernel.
-// The shared expert runs on a second stream, forked from and joined back to
-// the caller's (just before the combine), beside the route and the routed
-// experts. A plain-float router rounds x to bf16 as its matvec loads it.
-// The matvecs are the library's gemv kernels (F32 / F16 / BF16 rows sum in
-// f64 as ops::gemv does; Q8_0 / Q4_K / Q6_K on the integer-limb path), up
-// to 8 tokens per launch.
+// For several tokens the shared expert runs on a second stream, forked from
+// and joined back to the caller's (just before the combine), beside the route
+// and the routed experts; for one token it is two launches on the caller's
+// stream (gate and up as one matvec, silu(g) * u formed inside the down
+// launch). A plain-float router rounds x to bf16 as its matvec loads it, and
+// a gate-input row of the same plain type shares its launch. The matvecs are
+// the library's gemv kernels (F32 / F16 / BF16 rows sum in f64 as ops::gemv
+// does; Q8_0 / Q4_K / Q6_K on the integer-limb path), up to 8 tokens per
+// launch.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -66,7 +69,7 @@ bool moe_layer_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, in
   const size_t T = size_t(n_tok);
   p.o_logits = take(sizeof(float) * T * n_expert);
   p.o_xb = take(sizeof(float) * T * n_embd);
-  p.o_g = take(sizeof(float) * T * n_ff_sh);
+  p.o_g = take(sizeof(float) * 2 * T * n_ff_sh);  // g, or [g | u] from one two-matrix launch
   p.o_u = take(sizeof(float) * T * n_ff_sh);
   p.o_h = take(sizeof(float) * T * n_ff_sh);
   p.o_d = take(sizeof(float) * T * n_embd);
@@ -143,9 +146,17 @@ hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const
   const int64_t nx = int64_t(T) * n_embd, nh = int64_t(T) * n_sh;
   auto blocks = [](int64_t n) { return dim3(unsigned((n + 255) / 256)); };
   hipError_t e;
-  // the shared expert on the side stream (on `s` itself without one)
+  // fewer launches where the types allow: one token's shared expert in two
+  // launches, the router and the gate-input row in one
+  const bool fuse_sh = T == 1 && q.gate_sh == q.up_sh && w.q6_gate_sh == w.q6_up_sh &&
+                       shexp_fused_ok(q.gate_sh, q.down_sh, n_embd, n_sh);
+  const bool pair_rg = plain_quant(q.router) && q.gate_inp == q.router;
+  // the shared expert on the side stream (on `s` itself without one); its
+  // two-launch form costs less on `s` than a fork and join (one token, in a
+  // captured graph: 41.8 against 47.0 us), the many-token form runs faster
+  // beside the routed experts (16 tokens: 155 against 182 us)
   hipStream_t side = nullptr;
-  if ((e = side_stream(&side)) != hipSuccess) return e;
+  if (!fuse_sh && (e = side_stream(&side)) != hipSuccess) return e;
   hipEvent_t fork = nullptr, join = nullptr;
   if (side) {
     if ((e = hipEventCreateWithFlags(&fork, hipEventDisableTiming)) != hipSuccess) return e;
@@ -162,15 +173,32 @@ hipError_t launch_moe_layer(const MoeLayerPlan& p, const MoeLayerTypes& q, const
       if ((r = hipStreamWaitEvent(side, fork, 0)) != hipSuccess) return r;
       ss = side;
     }
-    if ((r = gemv_tokens(q.gate_sh, w.gate_sh, n_sh, n_embd, x, g, T, w.q6_gate_sh, ss)) != hipSuccess) return r;
-    if ((r = gemv_tokens(q.up_sh, w.up_sh, n_sh, n_embd, x, u, T, w.q6_up_sh, ss)) != hipSuccess) return r;
-    hipLaunchKernelGGL(silu_mul_kernel, blocks(nh), dim3(256), 0, ss, g, u, h, nh);
-    if ((r = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, ss)) != hipSuccess) return r;
-    if ((r = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, ss)) != hipSuccess) return r;
+    if (fuse_sh) {
+      // one token: [g | u] in one launch, then down with silu(g) * u staged
+      if ((r = launch_shexp_one(q.gate_sh, q.down_sh, w.gate_sh, w.up_sh, w.down_sh, n_embd, n_sh, x, g, d,
+                                w.q6_gate_sh, w.q6_down_sh, ss)) != hipSuccess)
+        return r;
+    } else {
+      if ((r = gemv_tokens(q.gate_sh, w.gate_sh, n_sh, n_embd, x, g, T, w.q6_gate_sh, ss)) != hipSuccess) return r;
+      if ((r = gemv_tokens(q.up_sh, w.up_sh, n_sh, n_embd, x, u, T, w.q6_up_sh, ss)) != hipSuccess) return r;
+      hipLaunchKernelGGL(silu_mul_kernel, blocks(nh), dim3(256), 0, ss, g, u, h, nh);
+      if ((r = gemv_tokens(q.down_sh, w.down_sh, n_embd, n_sh, h, d, T, w.q6_down_sh, ss)) != hipSuccess) return r;
+    }
+    if (!pair_rg &&
+        (r = gemv_tokens(q.gate_inp, w.gate_inp, 1, n_embd, x, sg, T, w.q6_gate_inp, ss)) != hipSuccess)
+      return r;
     if (side && (r = hipEventRecord(join, side)) != hipSuccess) return r;
     // route: router . bf16(x), then the routed experts into out; the combine
     // waits for the shared expert and adds sigmoid(s) * d after the routed sum
-    if (plain_quant(q.router)) {
+    if (pair_rg) {
+      // the router on bf16(x) and the gate-input row on x in one launch
+      for (int t0 = 0; t0 < T; t0 += 8) {
+        const int nb = T - t0 < 8 ? T - t0 : 8;
+        if ((r = launch_gemv_plain_pair(q.router, w.router, E, w.gate_inp, 1, n_embd, x + int64_t(t0) * n_embd,
+                                        logits + int64_t(t0) * E, sg + t0, nb, s)) != hipSuccess)
+          return r;
+      }
+    } else if (plain_quant(q.router)) {
       if ((r = gemv_tokens(q.router, w.router, E, n_embd, x, logits, T, 0, s, true)) != hipSuccess) return r;
     } else {
       hipLaunchKernelGGL(bf16_round_kernel, blocks(nx), dim3(256), 0, s, x, xb, nx);

@@ -278,13 +278,17 @@ def layer_views(name, quants, tensors, n_expert, n_embd, n_ff, n_sh):
 
 @pytest.mark.parametrize("n_tok,q_router,q_inp,q_sh", [(1, 0, 0, (12, 12, 14)), (3, 30, 0, (8, 8, 8)),
                                                        (9, 0, 30, (14, 14, 12)), (2, 8, 13, (13, 13, 14)),
-                                                       (1, 12, 0, (12, 12, 14))])
+                                                       (1, 12, 0, (12, 12, 14)), (1, 30, 30, (14, 14, 12)),
+                                                       (1, 0, 30, (13, 13, 8)), (1, 0, 0, (8, 8, 13))])
 def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh):
     """The whole layer (moe.rs:48-143): router matvec on bf16(x) (F32 or
     BF16 rows with f64 sums, rounding x as they load it; or quantized rows
     after a rounding pass), routing, the routed experts and the shared
     expert with its sigmoid gate, against the oracle token by token; 9
-    tokens take two 8-token matvec launches."""
+    tokens take two 8-token matvec launches. One token with gate and up of
+    one type runs the shared expert in two launches (gate and up as one
+    matvec, silu(g) * u formed inside the down launch), and a router and
+    gate input of one plain type share a launch."""
     n_expert, n_embd, n_ff, n_sh, top_k = 32, 512, 256, 256, 6
     say("moe layer", n_tok, q_router, q_inp, q_sh)
     q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8400 + n_tok, q_router, q_inp, q_sh)
@@ -335,13 +339,15 @@ def test_moe_layer_dev_matches_host_path(backend):
     assert np.array_equal(out.cpu().numpy(), host)
 
 
-def test_moe_layer_graph_replays(backend):
+@pytest.mark.parametrize("n_tok", [3, 1])
+def test_moe_layer_graph_replays(backend, n_tok):
     """The layer forks its shared expert onto a second stream and joins it
     back: captured in a HIP graph (two parallel branches), every replay, with
-    eager calls of other inputs between replays, equals the eager result."""
+    eager calls of other inputs between replays, equals the eager result
+    (1 token: the shared expert's two-launch form)."""
     import torch
-    n_expert, n_embd, n_ff, n_sh, top_k, n_tok = 32, 512, 256, 256, 8, 3
-    say("moe layer graph")
+    n_expert, n_embd, n_ff, n_sh, top_k = 32, 512, 256, 256, 8
+    say("moe layer graph", n_tok)
     q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 9000)
     dev = torch.device("cuda:0")
     td = [torch.from_numpy(a).to(dev) for a in t]
