@@ -157,6 +157,52 @@ def test_moe_ffn_dev_out_major_matches_host_path(backend):
     assert np.array_equal(out.cpu().numpy(), host)
 
 
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_moe_ffn_out_major_graph_replays(backend, n_tok):
+    """Captured in a HIP graph (route, gate/up, down, combine), every replay,
+    with eager calls of other inputs between replays, equals the eager
+    result."""
+    import torch
+    n_expert, n_embd, n_ff, top_k = 32, 512, 256, 8
+    say("moe ffn out-major graph", n_tok)
+    gate, up, down = om_tensors(n_expert, n_embd, n_ff, 12, 14, 9850 + n_tok)
+    dev = torch.device("cuda:0")
+    tg, tu, td = (torch.from_numpy(a).to(dev) for a in (gate, up, down))
+    tls = [torch.from_numpy(S.router_logits(9860 + i, n_tok, n_expert)).to(dev) for i in range(2)]
+    txs = [torch.from_numpy(S.normal_f32(9870 + i, n_tok * n_embd)).to(dev) for i in range(2)]
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+    nb = H.moe_workspace_bytes(n_tok, top_k, n_expert, n_embd, n_ff, 12, 14)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+
+    def call(i, stream):
+        H.moe_ffn_dev((12, OM, tg.data_ptr()), (12, OM, tu.data_ptr()), (14, OM, td.data_ptr()), n_expert, n_embd,
+                      n_ff, tls[i].data_ptr(), n_tok, top_k, txs[i].data_ptr(), out.data_ptr(), ws.data_ptr(), nb,
+                      stream)
+
+    eager = []
+    for i in range(2):
+        call(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        eager.append(out.cpu().numpy().copy())
+    assert not np.array_equal(eager[0], eager[1])
+    s = torch.cuda.Stream(dev)
+    with torch.cuda.stream(s):
+        call(0, s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call(0, torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[0]), rep
+        call(1, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[1]), rep
+
+
 def test_moe_layer_dev_out_major_matches_host_path(backend):
     import torch
     n_expert, n_embd, n_ff, n_sh, top_k, n_tok = 32, 512, 256, 256, 6, 2
