@@ -323,7 +323,14 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
 #pragma unroll
       for (int g = 0; g < 4; ++g) qq[i][g] = *reinterpret_cast<const uint64_t*>(p + kCodes + 32 * g + 8 * kg);
     };
-    constexpr int kPre = PREP ? 0 : kRing;  // issued before the staging completes
+    // issued before the staging completes; with the image copy, the first
+    // super-block's loads go behind the copies (in-order completion: waiting
+    // until only they are outstanding means the copies have landed)
+    constexpr int kPre = PREP ? 1 : kRing;
+    // vector loads of issue_sb: the 16-byte header, the lane's 8 qh bytes
+    // (Q5_K) and its four 8-byte code runs, at lane-dependent offsets that
+    // the compiler cannot merge (the ISA shows exactly these, then the wait)
+    constexpr int kSbLoads = Q == kQ5_K ? 6 : 5;
 #pragma unroll
     for (int i = 0; i < kPre; ++i) issue_sb(i);
     __builtin_amdgcn_sched_barrier(0);
@@ -332,7 +339,7 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
     // outstanding), or the conversion's LDS stores
     if (!SPLIT && c0 > 0) lds_barrier();  // every wave is done with the previous window's limbs
     if constexpr (PREP) {
-      wait_vmem<0>();
+      wait_vmem<kSbLoads * kPre>();
     } else {
       // one (vector, block) pair per thread per round; the 8 blocks of a
       // super-block are 8 adjacent lanes (nblk_w and the workgroup size are
