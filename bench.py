@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn", "blaslt",
-                                                    "batched"),
+                                                    "batched", "decode"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
                          "'moe' / 'prefill' / 'rowops' / 'ffn' / 'blaslt': that extra alone, 'batched': the "
                          "batch-8 decode shapes (for profiling; prints its JSON)")
@@ -545,6 +545,9 @@ def main():
         return
     elif args.only == "batched":
         print(json.dumps(bench_decode_shapes(torch, H, S, args.steps, batched_only=True)), flush=True)
+        return
+    elif args.only == "decode":
+        print(json.dumps(bench_decode_shapes(torch, H, S, args.steps)), flush=True)
         return
     elif args.only == "blaslt":
         print(json.dumps(bench_blaslt_reference(torch, args.steps)), flush=True)

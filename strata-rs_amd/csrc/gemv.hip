@@ -281,7 +281,9 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // Wave w owns row groups [w*per, w*per + per) of R rows. Items are
 // (row group, window) pairs taken window-major, so each wave reads its x
 // limbs from LDS once per window and keeps `per` (<= MAXQ) row sums per
-// row in registers. All item control is wave-uniform (scalar registers);
+// row in registers; rows of a single window are final after their one item
+// and are stored at once (then `per` may exceed MAXQ: a wave streams its
+// whole share of a tall matrix and x is staged once per workgroup). All item control is wave-uniform (scalar registers);
 // per-lane byte offsets within a row are computed once. Loads are
 // double-buffered (A/B ping-pong, both refills unconditional so the loop
 // latch never drains the load queue), and the first item is requested
@@ -293,6 +295,7 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // silu(x) * xu, with silu(v) = v / (1 + exp(-v)) in f32 (qwen35.rs:120-124),
 // instead of x; kLimbResid writes y = xres + sum (one f32 add, qwen35.rs:127-129).
 constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4;
+constexpr int kLimbMaxRowsOneWin = 64;  // row groups a wave may take when rows are one window
 
 template <class F, int R, int MAXQ, int MODE = 0, int NPRE = 1>
 __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restrict__ w, int rows,
@@ -409,13 +412,25 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
       load_limbs(lds8, cols, u, xl);
     }
     const bool ok = cw < nwin - 1 || lane_valid_last;
+    if (nwin == 1) {
+      // a single window: each item is whole rows, final at once (so a wave
+      // may take any number of them, and fewer workgroups stage x)
 #pragma unroll
-    for (int q = 0; q < MAXQ; ++q) {
-      if (q == cq) {
+      for (int r = 0; r < R; ++r) {
+        const float t = F::dot(L[r], xl, lane, flags);
+        const float v = wave_sum_dpp(ok ? t : 0.f);
+        const int row = (rg0 + cq) * R + r;
+        if (lane == 63 && row < rows) y[row] = (MODE & kLimbResid) != 0 ? __fadd_rn(xres[row], v) : v;
+      }
+    } else {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float t = F::dot(L[r], xl, lane, flags);
-          acc[q][r] += ok ? t : 0.f;
+      for (int q = 0; q < MAXQ; ++q) {
+        if (q == cq) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const float t = F::dot(L[r], xl, lane, flags);
+            acc[q][r] += ok ? t : 0.f;
+          }
         }
       }
     }
@@ -430,6 +445,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     issue(A);
     if (i + 1 < n_items) step(B);
   }
+  if (nwin == 1) return;  // stored as computed
 #pragma unroll
   for (int q = 0; q < MAXQ; ++q) {
     if (q < my) {
@@ -672,8 +688,11 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   const int units = cols >> 6, nwin = (units + 63) >> 6;
   const int min_waves = cu_count() * waves_per_cu;
   int per = (n_rg + min_waves - 1) / min_waves;
+  // row sums in registers across windows: at most MAXQ row groups a wave;
+  // single-window rows are stored as they complete, so a wave takes its
+  // share of the rows in one pass of resident waves
   if (nwin > 1 && per > MAXQ) per = MAXQ;
-  if (nwin == 1 && per > MAXQ) per = MAXQ;
+  if (nwin == 1 && per > kLimbMaxRowsOneWin) per = kLimbMaxRowsOneWin;
   const int waves = (n_rg + per - 1) / per;
   const int blocks = (waves + wpg - 1) / wpg;
   // x rounds (threads * 8 columns each) whose loads go ahead of the weights
