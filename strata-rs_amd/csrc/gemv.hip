@@ -894,7 +894,9 @@ template <class F>
 static hipError_t launch_ffn1(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_embd, int n_ff,
                               const float* x, float* gu, const float* xres, float* out, int q6s, hipStream_t s) {
   const int64_t rb1 = byte_size(F::kQuant, n_embd), rb2 = byte_size(F::kQuant, n_ff);
-  hipError_t e = launch_limb<F, 1, 4, kLimbTwoMat>(gate, 2 * n_ff, n_embd, rb1, x, gu, s, 512, 8, q6s, up, n_ff);
+  // gate and up: 2 n_ff rows, one window when n_embd <= 4096: 16 waves per CU
+  // as for other tall single-window matrices
+  hipError_t e = launch_limb<F, 1, 4, kLimbTwoMat>(gate, 2 * n_ff, n_embd, rb1, x, gu, s, 512, 16, q6s, up, n_ff);
   if (e != hipSuccess) return e;
   return launch_limb<F, 1, 4, kLimbSiluX | kLimbResid>(down, n_embd, n_ff, rb2, gu, out, s, 512, 8, q6s, nullptr,
                                                        0, gu + n_ff, xres);
