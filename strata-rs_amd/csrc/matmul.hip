@@ -694,33 +694,44 @@ __global__ void __launch_bounds__(kMmWsThreads)
   // One loop per role, each with one barrier per chunk (the barrier counts
   // match): a loop whose every chunk branched on the role would merge both
   // roles' loads in flight at each join, and the compiler would then wait
-  // for all of them before each chunk, undoing the prefetch distances.
+  // for all of them before each chunk, undoing the prefetch distances. For
+  // the same reason each role's main loop runs whole groups of chunks with
+  // no exit inside (a group cut short at the last chunk would reach the loop
+  // head with fewer loads in flight, and the head's waits would have to
+  // assume that path); the chunks past the last whole group run after it.
   if (consumer) {
-    for (int c0 = 0; c0 < nchunks; c0 += 2) {
+    auto consume = [&](int c, bf16x8 (*a)[4]) {
+      const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
+      const int cnext = min(c + 2, nchunks - 1);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int c = c0 + j;
-        if (c < nchunks) {  // uniform
-          const uint8_t* wb = wlb + (c & 1) * (kMmBN * kMmRowB);
-          bf16x8 (*a)[4] = afr[j];
+      for (int s = 0; s < 4; ++s) {
+        bf16x8 bfr[3];
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            bf16x8 bfr[3];
+        for (int ni = 0; ni < 3; ++ni)
+          bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
 #pragma unroll
-            for (int ni = 0; ni < 3; ++ni)
-              bfr[ni] = *reinterpret_cast<const bf16x8*>(wb + (32 * ni + l32) * kMmRowB + 2 * (32 * half + 8 * s));
+        for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+          for (int ni = 0; ni < 3; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
+        // k-step s of chunk c + 2 into the registers this step used (past
+        // the end: the last chunk again), spread over the chunk: the four
+        // consumers' loads would otherwise reach the CU's memory pipe in one
+        // burst at the chunk's end and stall at issue
 #pragma unroll
-              for (int ni = 0; ni < 3; ++ni)
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi][s], bfr[ni], acc[mi][ni], 0, 0, 0);
-          }
-          // chunk c + 2 into the registers chunk c used (past the end: the last chunk again)
-          load_a(min(c + 2, nchunks - 1), a);
-          lds_barrier();
-        }
+        for (int mi = 0; mi < 2; ++mi)
+          a[mi][s] = *reinterpret_cast<const bf16x8*>(xtile[mi] + int64_t(cnext) * 4096 + 1024 * s);
+        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);  // the step's 6 MFMAs,
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // then its 2 loads
       }
+      lds_barrier();
+    };
+    int c0 = 0;
+    for (; c0 + 2 <= nchunks; c0 += 2) {
+      consume(c0, afr[0]);
+      consume(c0 + 1, afr[1]);
     }
+    if (c0 < nchunks) consume(c0, afr[0]);
   } else if (stager) {
     for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
 #pragma unroll
