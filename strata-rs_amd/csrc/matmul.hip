@@ -612,9 +612,11 @@ __device__ __forceinline__ uint32_t block_shift<StQ6K>(const uint8_t* row, int c
 // ------------------------------------------------- bf16 kernel, 8 waves --
 // The same tile (256 tokens x 96 weight rows, K in 64-element chunks) with
 // the work split by role, so that each SIMD holds a wave that issues MFMAs
-// next to one that stages: waves 0-3 consume (tokens [64 w, 64 w + 64) x
+// next to one that stages (waves w and w + 4 share a SIMD; an MFMA wave
+// slows the other wave's VALU issue by about a tenth, so the two overlap):
+// waves 0-3 consume (tokens [64 w, 64 w + 64) x
 // all 96 rows), waves 4-6 dequantize the weight chunks (one 32-element run
-// of one row per lane, loads kDepth chunks ahead) into a double-buffered
+// of one row per lane, loads kBfDepth chunks ahead) into a double-buffered
 // bf16 LDS tile, wave 7 only keeps the barrier count. A consumer's
 // activation rows are its own, so it loads their fragments straight into
 // registers two chunks ahead, from the fragment-ordered copy the pre-pass
@@ -624,6 +626,7 @@ __device__ __forceinline__ uint32_t block_shift<StQ6K>(const uint8_t* row, int c
 // is staged into the other one.
 constexpr int kMmWsThreads = 512;
 constexpr size_t kMmLdsWs = 2 * kMmBN * kMmRowB;
+constexpr int kBfDepth = 3;  // weight chunks a stager's loads run ahead (4: about 2% slower)
 
 template <class S>
 __global__ void __launch_bounds__(kMmWsThreads)
@@ -679,15 +682,15 @@ __global__ void __launch_bounds__(kMmWsThreads)
 #pragma unroll
     for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
 
-  typename S::Raw raw[kDepth];
+  typename S::Raw raw[kBfDepth];
   if (consumer) {
     load_a(0, afr[0]);
     load_a(min(1, nchunks - 1), afr[1]);
   } else if (stager) {
 #pragma unroll
-    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    for (int k = 0; k < kBfDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
     stage(raw[0], 0, wlb);
-    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
+    raw[0] = S::load(wrow, min(kBfDepth, nchunks - 1), piece);
   }
   lds_barrier();
 
@@ -733,16 +736,16 @@ __global__ void __launch_bounds__(kMmWsThreads)
     }
     if (c0 < nchunks) consume(c0, afr[0]);
   } else if (stager) {
-    for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+    for (int c0 = 0; c0 < nchunks; c0 += kBfDepth) {
 #pragma unroll
-      for (int j = 0; j < kDepth; ++j) {
+      for (int j = 0; j < kBfDepth; ++j) {
         const int c = c0 + j;
         if (c < nchunks) {  // uniform
           // B(c + 1) into the buffer chunk c - 1 used; past the last chunk
           // this re-stages the last one into the buffer nobody reads
-          const int slot = (j + 1) % kDepth;
+          const int slot = (j + 1) % kBfDepth;
           stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
-          raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
+          raw[slot] = S::load(wrow, min(c + 1 + kBfDepth, nchunks - 1), piece);
           lds_barrier();
         }
       }
