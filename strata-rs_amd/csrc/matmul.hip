@@ -125,10 +125,26 @@ struct StQ4K {
     m0 = dm * ubyte<0>(mp);
     m1 = dm * ubyte<1>(mp);
   }
+  // d * sc_j and dmin * m_j of all eight sub-blocks: the products scales()
+  // forms, for a stager that decodes them once per super-block
+  __device__ static __forceinline__ void sb_scales(const u32x4& h, float* d8, float* m8) {
+    uint32_t sc03, sc47, m03, m47;
+    all_scale_bytes(h, sc03, sc47, m03, m47);
+    const float d = h2f(h.x), dm = h2f(h.x >> 16);
+    d8[0] = d * ubyte<0>(sc03); d8[1] = d * ubyte<1>(sc03); d8[2] = d * ubyte<2>(sc03); d8[3] = d * ubyte<3>(sc03);
+    d8[4] = d * ubyte<0>(sc47); d8[5] = d * ubyte<1>(sc47); d8[6] = d * ubyte<2>(sc47); d8[7] = d * ubyte<3>(sc47);
+    m8[0] = dm * ubyte<0>(m03); m8[1] = dm * ubyte<1>(m03); m8[2] = dm * ubyte<2>(m03); m8[3] = dm * ubyte<3>(m03);
+    m8[4] = dm * ubyte<0>(m47); m8[5] = dm * ubyte<1>(m47); m8[6] = dm * ubyte<2>(m47); m8[7] = dm * ubyte<3>(m47);
+  }
   __device__ static __forceinline__ void emit_bf16(const Raw& r, int c, int hb, uint32_t* run0,
                                                    uint32_t* run1, int& o0, int& o1, int) {
     float d0, m0, d1, m1;
     scales(r.h, c & 3, d0, m0, d1, m1);
+    emit_bf16_sc(r, c, hb, d0, m0, d1, m1, run0, run1, o0, o1);
+  }
+  __device__ static __forceinline__ void emit_bf16_sc(const Raw& r, int, int hb, float d0, float m0, float d1,
+                                                      float m1, uint32_t* run0, uint32_t* run1, int& o0,
+                                                      int& o1) {
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -206,10 +222,18 @@ struct StQ5K {
 #pragma unroll
     for (int k = 0; k < 4; ++k) q5k_codes(q[k], qh[k], uint32_t(c & 3), lo[k], hi[k]);
   }
+  __device__ static __forceinline__ void sb_scales(const u32x4& h, float* d8, float* m8) {
+    StQ4K::sb_scales(h, d8, m8);
+  }
   __device__ static __forceinline__ void emit_bf16(const Raw& r, int c, int hb, uint32_t* run0,
                                                    uint32_t* run1, int& o0, int& o1, int) {
     float d0, m0, d1, m1;
     StQ4K::scales(r.h, c & 3, d0, m0, d1, m1);
+    emit_bf16_sc(r, c, hb, d0, m0, d1, m1, run0, run1, o0, o1);
+  }
+  __device__ static __forceinline__ void emit_bf16_sc(const Raw& r, int c, int hb, float d0, float m0, float d1,
+                                                      float m1, uint32_t* run0, uint32_t* run1, int& o0,
+                                                      int& o1) {
     uint32_t lo[4], hi[4];
     codes(r, c, lo, hi);
 #pragma unroll
@@ -599,6 +623,21 @@ struct Bf16Emit<StQ6K> {
   }
 };
 
+// K-quants with 8 sub-block scales per 256-element super-block (4 chunks):
+// the bf16 stagers decode them once per super-block (sb_scales).
+template <class S>
+struct SbScales {
+  static constexpr bool value = false;
+};
+template <>
+struct SbScales<StQ4K> {
+  static constexpr bool value = true;
+};
+template <>
+struct SbScales<StQ5K> {
+  static constexpr bool value = true;
+};
+
 // Alignment shift of the block a Q6_K piece reads (0 for the other formats).
 template <class S>
 __device__ __forceinline__ uint32_t block_shift(const uint8_t*, int) {
@@ -626,7 +665,7 @@ __device__ __forceinline__ uint32_t block_shift<StQ6K>(const uint8_t* row, int c
 // is staged into the other one.
 constexpr int kMmWsThreads = 512;
 constexpr size_t kMmLdsWs = 2 * kMmBN * kMmRowB;
-constexpr int kBfDepth = 3;  // weight chunks a stager's loads run ahead (4: about 2% slower)
+constexpr int kBfDepth = 3;  // weight chunks a stager's loads run ahead (4: about 2% slower), Q8_0 / Q6_K
 
 template <class S>
 __global__ void __launch_bounds__(kMmWsThreads)
@@ -647,10 +686,20 @@ __global__ void __launch_bounds__(kMmWsThreads)
   const int task = max(tid - 4 * kWave, 0) % kTasks;
   const int srow = task / S::kPieces, piece = task % S::kPieces;
   const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
-  auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf) {
+  // K-quant stagers decode the 8 sub-block scales once per super-block into
+  // sd / sm and run a ring of 4 aligned to super-blocks, so a chunk's
+  // sub-block pair g is known at compile time; the other formats run a
+  // ring of kBfDepth
+  constexpr bool kSb = SbScales<S>::value;
+  constexpr int kRingB = kSb ? 4 : kBfDepth;
+  float sd[8], sm[8];
+  auto stage = [&](const typename S::Raw& raw, int c, uint8_t* buf, int g) {
     uint32_t run0[8], run1[8];
     int o0, o1;
-    Bf16Emit<S>::run(raw, c, piece, block_shift<S>(wrow, c), run0, run1, o0, o1, q6s);
+    if constexpr (kSb)
+      S::emit_bf16_sc(raw, c, piece, sd[2 * g], sm[2 * g], sd[2 * g + 1], sm[2 * g + 1], run0, run1, o0, o1);
+    else
+      Bf16Emit<S>::run(raw, c, piece, block_shift<S>(wrow, c), run0, run1, o0, o1, q6s);
     uint8_t* dst = buf + srow * kMmRowB;
     *reinterpret_cast<u32x4*>(dst + 2 * o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
     *reinterpret_cast<u32x4*>(dst + 2 * o0 + 16) = u32x4{run0[4], run0[5], run0[6], run0[7]};
@@ -682,15 +731,16 @@ __global__ void __launch_bounds__(kMmWsThreads)
 #pragma unroll
     for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
 
-  typename S::Raw raw[kBfDepth];
+  typename S::Raw raw[kRingB];
   if (consumer) {
     load_a(0, afr[0]);
     load_a(min(1, nchunks - 1), afr[1]);
   } else if (stager) {
 #pragma unroll
-    for (int k = 0; k < kBfDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
-    stage(raw[0], 0, wlb);
-    raw[0] = S::load(wrow, min(kBfDepth, nchunks - 1), piece);
+    for (int k = 0; k < kRingB; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+    if constexpr (kSb) S::sb_scales(raw[0].h, sd, sm);
+    stage(raw[0], 0, wlb, 0);
+    raw[0] = S::load(wrow, min(kRingB, nchunks - 1), piece);
   }
   lds_barrier();
 
@@ -736,16 +786,21 @@ __global__ void __launch_bounds__(kMmWsThreads)
     }
     if (c0 < nchunks) consume(c0, afr[0]);
   } else if (stager) {
-    for (int c0 = 0; c0 < nchunks; c0 += kBfDepth) {
+    for (int c0 = 0; c0 < nchunks; c0 += kRingB) {
 #pragma unroll
-      for (int j = 0; j < kBfDepth; ++j) {
+      for (int j = 0; j < kRingB; ++j) {
         const int c = c0 + j;
         if (c < nchunks) {  // uniform
           // B(c + 1) into the buffer chunk c - 1 used; past the last chunk
-          // this re-stages the last one into the buffer nobody reads
-          const int slot = (j + 1) % kBfDepth;
-          stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB));
-          raw[slot] = S::load(wrow, min(c + 1 + kBfDepth, nchunks - 1), piece);
+          // this re-stages the last one into the buffer nobody reads (for
+          // the K-quants with the next super-block's scales: harmless)
+          const int slot = (j + 1) % kRingB;
+          // K-quants: c0 is a multiple of 4 (cols % 256 == 0), chunk c + 1
+          // is pair (j + 1) & 3 of its super-block, and j = 3 starts the next
+          if constexpr (kSb)
+            if (j == kRingB - 1) S::sb_scales(raw[slot].h, sd, sm);
+          stage(raw[slot], min(c + 1, nchunks - 1), wlb + ((c + 1) & 1) * (kMmBN * kMmRowB), (j + 1) & 3);
+          raw[slot] = S::load(wrow, min(c + 1 + kRingB, nchunks - 1), piece);
           lds_barrier();
         }
       }
