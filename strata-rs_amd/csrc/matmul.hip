@@ -1164,24 +1164,33 @@ __global__ void __launch_bounds__(kMqThreads)
       const bool more = c + 1 < nchunks;  // uniform
       const uint8_t* wh = wl[cc & 1][0];
       const uint8_t* wo = wl[cc & 1][1];
+      i32x4 a_h[3], a_l[3];
 #pragma unroll
       for (int nt = 0; nt < 3; ++nt) {
         const int ro = (48 * rg + 16 * nt + l16) * kMmRowQ + 16 * g;
-        const i32x4 a_h = *reinterpret_cast<const i32x4*>(wh + ro);
-        const i32x4 a_l = *reinterpret_cast<const i32x4*>(wo + ro);
+        a_h[nt] = *reinterpret_cast<const i32x4*>(wh + ro);
+        a_l[nt] = *reinterpret_cast<const i32x4*>(wo + ro);
+      }
+      // token tile mt's six MFMAs, then its fragments of the next chunk (past
+      // the end: the last chunk again) into the registers they read: the
+      // eight waves' loads spread over the chunk instead of reaching the
+      // CU's memory pipe in one burst after all the MFMAs
+      const int cx = min(c + 1, nchunks - 1);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 3; ++nt) {
           // a new super-block: the int32 sums start at zero
-          ah[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_h, xc[mt], cc == 0 ? i32x4{0, 0, 0, 0} : ah[mt][nt],
-                                                             0, 0, 0);
-          al[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_l, xc[mt], cc == 0 ? i32x4{0, 0, 0, 0} : al[mt][nt],
-                                                             0, 0, 0);
+          ah[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_h[nt], xc[mt],
+                                                             cc == 0 ? i32x4{0, 0, 0, 0} : ah[mt][nt], 0, 0, 0);
+          al[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_l[nt], xc[mt],
+                                                             cc == 0 ? i32x4{0, 0, 0, 0} : al[mt][nt], 0, 0, 0);
         }
+        xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + int64_t(cx) * 1024 + xo);
+        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
       if (more) {
-        // the next chunk's activation fragments (the MFMAs above have read xc)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) xc[mt] = *reinterpret_cast<const i32x4*>(xr[mt] + int64_t(c + 1) * 1024 + xo);
         const int slot = (cc + 1) % kRing;  // where chunk c + 1 was loaded (c % 4 == cc)
         if (stager) {
           stage(raw[slot], c + 1, (cc + 1) & 1);
