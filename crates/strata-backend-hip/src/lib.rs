@@ -9,9 +9,11 @@
 //! for: several tokens against one weight read, the fused MoE FFN and layer,
 //! the dense FFN half of a layer, and the prefill matmul.
 //!
-//! Types or shapes the device path does not take, and any device failure,
-//! run on the CPU backend instead, as the wgpu backend does for what it does
-//! not accelerate (crates/strata-backend-wgpu/src/gpu.rs:306-325).
+//! Types or shapes the device path does not take run on the CPU backend
+//! instead, as the wgpu backend does for what it does not accelerate
+//! (crates/strata-backend-wgpu/src/gpu.rs:306-325). Device failures are
+//! returned as `Error::Backend`, as the wgpu backend propagates its own
+//! (gpu.rs:331-365); they are never retried on the CPU.
 
 pub mod ffi;
 
@@ -105,6 +107,39 @@ fn check(rc: c_int) -> Result<()> {
         Ok(())
     } else {
         Err(Error::Backend { message: format!("hip ({rc}): {}", last_error()) })
+    }
+}
+
+/// Where a trait call goes after the library returned `rc`.
+#[derive(Debug, Clone, Copy, PartialEq, Eq)]
+enum Route {
+    /// The device computed the result.
+    Done,
+    /// The CPU backend computes it (or reports the caller's error its way).
+    Cpu,
+}
+
+/// The status of a trait call, mapped as the reference's backends behave:
+/// - `SH_OK`: the device result stands;
+/// - `SH_ERR_UNSUPPORTED_QUANT`, `SH_ERR_UNSUPPORTED_SHAPE`: a type or shape
+///   the kernels do not take; the CPU backend computes it, as the wgpu
+///   backend does for what it does not accelerate (gpu.rs:306-325);
+/// - `SH_ERR_SHAPE`, `SH_ERR_TRUNCATED`: the caller's arguments are wrong;
+///   the CPU body reports them the reference's way (the length asserts of
+///   crates/strata-core/src/ops.rs:15-17, `Error::Truncated` of
+///   crates/strata-gguf/src/dequant.rs:50-55), so the caller sees the same
+///   failure as with the CPU backend;
+/// - anything else (`SH_ERR_DEVICE`, `SH_ERR_OUT_OF_MEMORY`,
+///   `SH_ERR_INVALID_ARGUMENT`, ...): `Error::Backend`, as the wgpu backend
+///   propagates its device errors (gpu.rs:331-365); no CPU retry.
+fn route(rc: c_int, what: &str) -> Result<Route> {
+    match rc {
+        ffi::SH_OK => Ok(Route::Done),
+        ffi::SH_ERR_UNSUPPORTED_QUANT | ffi::SH_ERR_UNSUPPORTED_SHAPE | ffi::SH_ERR_SHAPE | ffi::SH_ERR_TRUNCATED => {
+            tracing::debug!("{what} ({rc}): {}; on the CPU", last_error());
+            Ok(Route::Cpu)
+        }
+        _ => Err(Error::Backend { message: format!("hip {what} ({rc}): {}", last_error()) }),
     }
 }
 
@@ -381,14 +416,9 @@ impl ComputeBackend for HipBackend {
         let t = self.tensor(w);
         // SAFETY: the library checks x_len / y_len against the tensor.
         let rc = unsafe { ffi::sh_gemv(self.ctx, &t, x.as_ptr(), x.len() as u64, y.as_mut_ptr(), y.len() as u64) };
-        match check(rc) {
-            Ok(()) => Ok(()),
-            // callers expect every result (moe.rs:115-123, qwen35.rs:116-126): a
-            // device problem runs the CPU path instead of failing the generation
-            Err(e) => {
-                tracing::warn!("{e}; gemv on the CPU");
-                self.cpu.gemv(w, x, y, scratch)
-            }
+        match route(rc, "gemv")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.gemv(w, x, y, scratch),
         }
     }
 
@@ -409,20 +439,17 @@ impl ComputeBackend for HipBackend {
         let rc = unsafe {
             ffi::sh_expert_gemv(self.ctx, &v, e as u64, x.as_ptr(), x.len() as u64, y.as_mut_ptr(), y.len() as u64)
         };
-        match check(rc) {
-            Ok(()) => Ok(()),
-            Err(err) => {
-                tracing::warn!("{err}; expert_gemv on the CPU");
-                self.cpu_expert_gemv(w, e, x, y, scratch)
-            }
+        match route(rc, "expert_gemv")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu_expert_gemv(w, e, x, y, scratch),
         }
     }
 
     // The elementwise methods run on the device; a host-slice call is one
     // upload, one launch and one readback, so they pay off once a layer's
     // activations stay on the device (the library's *_dev forms). The slices
-    // are written only when a call succeeds, so a failed call runs the CPU
-    // body on the untouched input.
+    // are written only when a call succeeds, so a call routed to the CPU runs
+    // its body on the untouched input.
     fn rms_norm(&self, x: &mut [f32], w: &[f32], eps: f64) -> Result<()> {
         let rc = if w.len() == x.len() {
             // SAFETY: equal lengths, checked above.
@@ -430,7 +457,10 @@ impl ComputeBackend for HipBackend {
         } else {
             ffi::SH_ERR_SHAPE
         };
-        if check(rc).is_ok() { Ok(()) } else { self.cpu.rms_norm(x, w, eps) }
+        match route(rc, "rms_norm")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.rms_norm(x, w, eps),
+        }
     }
 
     fn rope_neox(&self, head: &mut [f32], cfg: &RopeCfg) -> Result<()> {
@@ -442,19 +472,28 @@ impl ComputeBackend for HipBackend {
         };
         // SAFETY: the library checks n against the rope shape.
         let rc = unsafe { ffi::sh_rope_neox(self.ctx, head.as_mut_ptr(), head.len() as u64, &c) };
-        if check(rc).is_ok() { Ok(()) } else { self.cpu.rope_neox(head, cfg) }
+        match route(rc, "rope_neox")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.rope_neox(head, cfg),
+        }
     }
 
     fn softmax(&self, xs: &mut [f32]) -> Result<()> {
         // SAFETY: one slice of its own length.
         let rc = unsafe { ffi::sh_softmax(self.ctx, xs.as_mut_ptr(), xs.len() as u64) };
-        if check(rc).is_ok() { Ok(()) } else { self.cpu.softmax(xs) }
+        match route(rc, "softmax")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.softmax(xs),
+        }
     }
 
     fn l2_norm(&self, head: &mut [f32], eps: f64) -> Result<()> {
         // SAFETY: one slice of its own length.
         let rc = unsafe { ffi::sh_l2_norm(self.ctx, head.as_mut_ptr(), head.len() as u64, eps) };
-        if check(rc).is_ok() { Ok(()) } else { self.cpu.l2_norm(head, eps) }
+        match route(rc, "l2_norm")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.l2_norm(head, eps),
+        }
     }
 
     fn add(&self, a: &mut [f32], b: &[f32]) -> Result<()> {
@@ -464,7 +503,10 @@ impl ComputeBackend for HipBackend {
         } else {
             ffi::SH_ERR_SHAPE
         };
-        if check(rc).is_ok() { Ok(()) } else { self.cpu.add(a, b) }
+        match route(rc, "add")? {
+            Route::Done => Ok(()),
+            Route::Cpu => self.cpu.add(a, b),
+        }
     }
 }
 

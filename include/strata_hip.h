@@ -440,9 +440,12 @@ int sh_ffn_dev(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uin
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Shapes whose sh_ffn_workspace_bytes exceed 4 MiB are refused with
  * SH_ERR_UNSUPPORTED_SHAPE (at n_embd 4096, n_ff 12288: up to 23 tokens).
- * Every call on one GPU shares that array: calls that overlap in time on one
- * GPU (other streams, other threads) race and must not be issued. Same
- * results as sh_ffn_dev, bit for bit. */
+ * WARNING: every call on one GPU shares that array. Calls that overlap in
+ * time on one GPU (on other streams, from other threads or processes, or
+ * graphs holding this call replayed concurrently) race on it and corrupt each
+ * other's results without an error; the caller must serialise them (one
+ * stream, or an event between them). Same results as sh_ffn_dev, bit for
+ * bit. */
 int sh_ffn_dev_noalloc(const sh_expert_dev* tensors, uint64_t n_embd, uint64_t n_ff, uint32_t n_tok,
                        const float* x, const float* post_norm, double eps, float* out, void* stream);
 

@@ -468,10 +468,14 @@ __global__ void __launch_bounds__(64 * kMbMaxWaves)
     __shared__ uint32_t s_last;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial sums are in memory
     __syncthreads();
+    // release: the workgroup's partial sums (ordered before the barrier) are
+    // visible at agent scope before the count; acquire: the last workgroup
+    // sees every other workgroup's sums released with their counts
     if (tid == 0)
-      s_last = __hip_atomic_fetch_add(count + rtb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = __hip_atomic_fetch_add(count + rtb, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (s_last != uint32_t(nwin - 1)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every wave of the last workgroup
     // the last workgroup of the row block: the windows' sums in window order
     const int r0 = rtb * (16 * T), nr = min(16 * T, rows - r0);
     for (int i = tid; i < nb * nr; i += nthreads) {

@@ -137,3 +137,27 @@ def test_build_script_links_the_library():
     assert "cargo:rustc-link-lib=dylib=strata_hip" in b
     cargo = open(os.path.join(CRATE, "Cargo.toml")).read()
     assert 'name = "strata-backend-hip"' in cargo and 'links = "strata_hip"' in cargo
+
+
+def test_device_errors_propagate_and_only_unsupported_or_caller_errors_go_to_the_cpu():
+    """The status mapping of the trait methods (the wgpu backend returns its
+    device errors, crates/strata-backend-wgpu/src/gpu.rs:331-365): every
+    trait method goes through `route`, whose CPU arm names exactly the
+    unsupported-type/shape and caller-argument codes, and whose catch-all is
+    `Error::Backend`; no trait method retries a device failure on the CPU."""
+    lib = open(os.path.join(CRATE, "src", "lib.rs")).read()
+    m = re.search(r"fn route\(rc: c_int, what: &str\) -> Result<Route> \{(.*?)\n\}", lib, flags=re.S)
+    assert m, "route() not found"
+    body = m.group(1)
+    cpu_arm = re.search(r"\n\s*((?:ffi::SH_ERR_\w+\s*\|?\s*)+)=> \{", body)
+    assert cpu_arm, body
+    codes = sorted(c.strip() for c in cpu_arm.group(1).split("|"))
+    assert codes == ["ffi::SH_ERR_SHAPE", "ffi::SH_ERR_TRUNCATED", "ffi::SH_ERR_UNSUPPORTED_QUANT",
+                     "ffi::SH_ERR_UNSUPPORTED_SHAPE"], codes
+    assert "ffi::SH_OK => Ok(Route::Done)" in body
+    assert re.search(r"_ => Err\(Error::Backend", body)
+    impl = lib[lib.index("impl ComputeBackend for HipBackend"):lib.index("#[cfg(test)]")]
+    # no status check that swallows an error into a CPU retry
+    assert "check(rc)" not in impl and "tracing::warn!" not in impl
+    for method in ("gemv", "expert_gemv", "rms_norm", "rope_neox", "softmax", "l2_norm", "add"):
+        assert f'route(rc, "{method}")?' in impl, method
