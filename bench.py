@@ -63,20 +63,38 @@ def parse():
     return ap.parse_args()
 
 
-def _graph_of(torch, stream, calls, n):
-    """A HIP graph of exactly n calls, cycling through `calls`."""
+def _graph_of(torch, stream, calls, n, first=0):
+    """A HIP graph of exactly n calls, cycling through `calls` from index
+    `first`."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         h = torch.cuda.current_stream().cuda_stream
         for i in range(n):
-            calls[i % len(calls)](h)
+            calls[(first + i) % len(calls)](h)
     return g
 
 
+_FLUSH = {}
+
+
+def _flush_caches(torch, stream):
+    """Writes 512 MiB (twice the 256 MB Infinity Cache, far beyond the L2s)
+    on `stream`, so nothing the timed calls read is still cached."""
+    buf = _FLUSH.get("buf")
+    if buf is None:
+        buf = _FLUSH["buf"] = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
+    with torch.cuda.stream(stream):
+        buf.fill_(1)
+
+
 def _time_graph_calls(torch, stream, calls, steps, warmup):
-    """Runs `warmup` calls untimed, then times exactly `steps` calls, each
-    set captured as one HIP graph and replayed once; events on `stream`.
-    Returns ms per call."""
+    """Runs `warmup` calls untimed, then times exactly `steps` calls; events
+    on `stream`. Each set is one captured HIP graph. The timed graph takes the
+    calls that follow the warmed ones (its first call is calls[warmup %
+    len(calls)], so a rotation over weight copies continues instead of
+    re-reading the copies just warmed), is replayed once untimed (the first
+    replay of a graph also uploads it), then the caches are flushed and the
+    second replay is timed. Returns ms per call."""
     with torch.cuda.stream(stream):  # eager pass: the calls are accepted
         for f in calls:
             f(stream.cuda_stream)
@@ -87,7 +105,10 @@ def _time_graph_calls(torch, stream, calls, steps, warmup):
             gw.replay()
         torch.cuda.synchronize()
         del gw
-    g = _graph_of(torch, stream, calls, steps)
+    g = _graph_of(torch, stream, calls, steps, first=warmup % len(calls))
+    with torch.cuda.stream(stream):  # untimed: the graph's first replay
+        g.replay()
+    _flush_caches(torch, stream)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -142,8 +163,8 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
 
 def time_calls(torch, calls, steps, warmup):
     """Mean ms per call of a list of enqueue functions f(stream_handle):
-    exactly `steps` calls, cycled in order, captured in one HIP graph and
-    replayed once after `warmup` untimed calls."""
+    exactly `steps` timed calls, cycled in order, after `warmup` untimed ones
+    (the harness of _time_graph_calls)."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
