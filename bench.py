@@ -172,15 +172,18 @@ def time_calls(torch, calls, steps, warmup):
 
 
 def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):
-    """Prefill matmul W[rows][cols] (Q4_K) x X[m][cols] -> Y[m][rows], both
-    activation modes; TFLOP/s of 2 * m * rows * cols per call."""
+    """Prefill matmul W[rows][cols] (Q4_K) x X[m][cols] -> Y[m][rows] in the
+    bf16 mode and the int8 mode on 32-element Q8 activation blocks (the two
+    variants of the prefill workload), plus the opt-in int8 mode on
+    256-element blocks; TFLOP/s of 2 * m * rows * cols per call."""
     dev = torch.device("cuda:0")
     w = torch.from_numpy(w_host).to(dev)
     x = torch.from_numpy(S.normal_f32(0x5EED0006, m * cols)).to(dev)
     y = torch.empty(m * rows, dtype=torch.float32, device=dev)
     res = {}
     flops = 2.0 * m * rows * cols
-    for mode, name, peak in ((H.MATMUL_BF16, "bf16", 2500.0), (H.MATMUL_Q8, "q8_int8", 5000.0)):
+    for mode, name, peak in ((H.MATMUL_BF16, "bf16", 2500.0), (H.MATMUL_Q8, "q8_int8", 5000.0),
+                             (H.MATMUL_Q8K, "q8k_int8_256blocks", 5000.0)):
         nb = H.matmul_workspace_bytes(S.Q4_K, rows, cols, m, mode)
         ws = torch.empty(nb, dtype=torch.uint8, device=dev)
         call = (lambda st, mode=mode, ws=ws, nb=nb:

@@ -40,6 +40,7 @@ pub const SH_FLAG_IQ4XS_GGML: u32 = 4;
 // ---- matmul modes
 pub const SH_MATMUL_BF16: u32 = 0;
 pub const SH_MATMUL_Q8: u32 = 1;
+pub const SH_MATMUL_Q8K: u32 = 2;
 
 /// Opaque: one device, its stream, pinned staging and resident weights.
 #[repr(C)]

@@ -381,7 +381,8 @@ impl HipBackend {
     }
 
     /// Prefill: `y[t] = W x[t]` for `m` tokens (x `[m][cols]`, y `[m][rows]`);
-    /// `mode` is `ffi::SH_MATMUL_BF16` or `ffi::SH_MATMUL_Q8`.
+    /// `mode` is `ffi::SH_MATMUL_BF16`, `ffi::SH_MATMUL_Q8` (32-element Q8
+    /// activation blocks) or `ffi::SH_MATMUL_Q8K` (256-element blocks, K-quants).
     pub fn matmul(&self, w: &QuantTensor<'_>, x: &[f32], m: usize, y: &mut [f32], mode: u32) -> Result<()> {
         if x.len() != m * w.cols || y.len() != m * w.rows {
             return Err(Error::Backend { message: format!("matmul: {m} x {} shape mismatch", w.name) });

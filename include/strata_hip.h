@@ -93,7 +93,8 @@ extern "C" {
 
 /* ---- matmul modes ------------------------------------------------------ */
 #define SH_MATMUL_BF16 0u /* bf16 activations, dequant-to-bf16 LDS tiles, bf16 MFMA */
-#define SH_MATMUL_Q8 1u   /* activations quantized to Q8 blocks, int8 MFMA */
+#define SH_MATMUL_Q8 1u   /* activations in 32-element Q8 blocks, int8 MFMA */
+#define SH_MATMUL_Q8K 2u  /* activations in 256-element Q8 blocks, int8 MFMA (K-quants) */
 
 typedef struct sh_context sh_context;
 
@@ -263,10 +264,13 @@ int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert
  * activation rounding of `mode`:
  *   SH_MATMUL_BF16  x rounded to bf16, weights dequantized to bf16, f32
  *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K);
- *   SH_MATMUL_Q8    x quantized to blocks of the weight's scale group
- *                   (scale max|x| / 127 per block, int8 codes rounded to
- *                   nearest even): 32 elements for Q8_0, 256 (one per
- *                   super-block) for Q4_K and Q5_K; int8 products.
+ *   SH_MATMUL_Q8    x quantized to Q8 blocks of 32 elements (f32 scale
+ *                   max|x| / 127 per block, int8 codes rounded to nearest
+ *                   even), int8 products (Q8_0, Q4_K, Q5_K);
+ *   SH_MATMUL_Q8K   x quantized to blocks of 256 elements, one scale per
+ *                   weight super-block (Q4_K, Q5_K): a coarser activation
+ *                   rounding than SH_MATMUL_Q8 (the step is max|x| over 256
+ *                   elements), an opt-in alternative.
  * cols must be a multiple of 64. */
 int sh_matmul(sh_context* ctx, const sh_quant_tensor* w, const float* x, uint32_t m, float* y,
               uint32_t mode);
@@ -290,7 +294,7 @@ int sh_matmul_dev(uint32_t quant, uint32_t flags, const void* w, uint64_t rows, 
 int sh_quantize_q8_dev(const float* x, uint64_t n, int8_t* codes, float* scales, float* code_sums,
                        void* stream);
 
-/* The activation rounding of SH_MATMUL_Q8 for Q4_K / Q5_K weights on its
+/* The activation rounding of SH_MATMUL_Q8K (Q4_K / Q5_K weights) on its
  * own: n f32 (n a multiple of 256, x 16-byte aligned) -> n int8 codes, n /
  * 256 scales (max|x| / 127 per 256 elements, one per weight super-block) and
  * n / 32 integer code sums (one per 32-element sub-block). No counterpart in

@@ -340,11 +340,11 @@ def dequantize_q8k_activations(x) -> np.ndarray:
     return (np.repeat(s, 256) * q.astype(np.float32)).astype(np.float32).reshape(xv.shape)
 
 
-def q8_activations_for(quant: int, x) -> np.ndarray:
-    """The activation rounding of the q8 matmul mode for weights of `quant`:
-    one scale per weight scale group (32 elements for Q8_0, a 256-element
-    super-block for Q4_K / Q5_K)."""
-    return dequantize_q8k_activations(x) if quant in (Q4_K, Q5_K) else dequantize_q8_activations(x)
+def q8_activations_for(mode: int, x) -> np.ndarray:
+    """The activation rounding of an int8 matmul mode: Q8 blocks of 32
+    elements (mode 1, every weight type) or of 256 elements (mode 2, one
+    scale per K-quant super-block)."""
+    return dequantize_q8k_activations(x) if mode == 2 else dequantize_q8_activations(x)
 
 
 def bf16_round_array(a) -> np.ndarray:

@@ -771,11 +771,13 @@ int sh_moe_layer(sh_context* c, const sh_quant_tensor* router, const sh_expert_v
 }
 
 static int matmul_check(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t m, uint32_t mode) {
-  if (mode > SH_MATMUL_Q8) return fail(SH_ERR_INVALID_ARGUMENT, "matmul mode %u", mode);
+  if (mode > SH_MATMUL_Q8K) return fail(SH_ERR_INVALID_ARGUMENT, "matmul mode %u", mode);
   if (!sh::device_quant(quant))
     return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: type %u has no device kernel", quant);
   if (mode == SH_MATMUL_Q8 && quant == SH_QUANT_Q6_K)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: Q6_K weights take SH_MATMUL_BF16 only");
+  if (mode == SH_MATMUL_Q8K && quant != SH_QUANT_Q4_K && quant != SH_QUANT_Q5_K)
+    return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: SH_MATMUL_Q8K takes Q4_K / Q5_K weights only");
   if (!sh::matmul_shape_ok(quant, int64_t(rows), int64_t(cols), int64_t(m), mode))
     return fail(SH_ERR_UNSUPPORTED_SHAPE, "matmul %llux%llu (m %llu) of type %u is not supported",
                 (unsigned long long)rows, (unsigned long long)cols, (unsigned long long)m, quant);

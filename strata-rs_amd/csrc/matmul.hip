@@ -465,15 +465,19 @@ __global__ void x_q8_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
 
 // The same blocks for the q8 matmul, in the order its waves load them
 // (tokens padded with zero blocks to a multiple of 32; T = token / 32,
-// l = token % 32, block j = 2c + s of chunk c):
+// l = token % 32, block j = 2c + s of chunk c, nsb = ceil(blocks / 8)):
 //   codes: 16-byte piece ((T * nch + c) * 2 + s) * 64 + 32 h + l holds codes
 //          [16h, 16h + 16) of the block (one 1 KiB wave load per fragment);
-//   s, u:  float (T * nblk + j) * 32 + l (one 128-byte run per block).
+//   s:     float (T * nblk + j) * 32 + l (one 128-byte run per block);
+//   u:     u = s * sum(codes) split into bf16 halves hi = bf16(u), lo =
+//          bf16(u - hi) (u to about 2^-17), as the B operand of the min-term
+//          MFMA: 16-byte piece (T * nsb + j / 8) * 64 + 32 ((j % 8) / 4) + l,
+//          word j % 4 = hi | lo << 16.
 __global__ void x_q8_tiled_kernel(const float* __restrict__ x, u32x4* __restrict__ qt, float* __restrict__ st,
-                                  float* __restrict__ ut, int m, int cols, int64_t blocks) {
+                                  uint32_t* __restrict__ ut, int m, int cols, int64_t blocks) {
   const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;  // (T, j, l)
   if (i >= blocks) return;
-  const int nblk = cols / 32, nch = cols / kMmKC;
+  const int nblk = cols / 32, nch = cols / kMmKC, nsb = (nblk + 7) >> 3;
   const int l = int(i & 31);
   const int64_t tj = i >> 5;
   const int j = int(tj % nblk);
@@ -487,7 +491,9 @@ __global__ void x_q8_tiled_kernel(const float* __restrict__ x, u32x4* __restrict
   dst[0] = u32x4{w[0], w[1], w[2], w[3]};
   dst[32] = u32x4{w[4], w[5], w[6], w[7]};
   st[i] = sv;
-  ut[i] = uv;
+  const uint32_t hi = __builtin_bit_cast(unsigned short, __bf16(uv));
+  const uint32_t lo = __builtin_bit_cast(unsigned short, __bf16(uv - float(__builtin_bit_cast(__bf16, (unsigned short)hi))));
+  ut[((T * nsb + (j >> 3)) * 64 + 32 * ((j & 7) >> 2) + l) * 4 + (j & 3)] = hi | (lo << 16);
 }
 
 // X f32 -> Q8 blocks of 256 (the K-quant int8 path: one scale per weight
@@ -826,53 +832,82 @@ __global__ void __launch_bounds__(kMmWsThreads)
     }
 }
 
-// --------------------------------------------------------------- q8 kernel --
-// A = weight codes (rows r), B = activation codes (tokens t), so the D
-// layout puts one token per lane and the activation block scale is a
-// per-lane scalar; the weight block scales come from LDS per row.
-// Per 32-element block j:  y += d_rj * s_tj * I - m_rj * u_tj, with I the
-// exact int32 dot of the codes and u_tj = s_tj * sum(q_x); the second term
-// is a K = 2 f32 MFMA per chunk, the first three VALU ops per output.
+// ------------------------------------------------------- q8 kernel (int8) --
+// Activations in Q8 blocks of 32 (scale s_tj = max|x| / 127, int8 codes c),
+// weights Q8_0 / Q4_K / Q5_K, whose 32-element blocks carry one scale
+// d_rj = d * sc_j (Q4_K / Q5_K also a min dmin * m_j). Per block j:
+//   y_tr += d_rj * s_tj * I_trj - dmin_r * m_rj * u_tj,
+// I_trj = sum_k q_rk c_tk (exact int32) and u_tj = s_tj * sum_k c_tk.
+// Work per (tile of 32 rows x 32 tokens, block):
+//   v_mfma_i32_32x32x32_i8      I (A = weight codes, B = activation codes);
+//   v_mfma_f32_32x32x1_2b_f32   S = d_rj * s_tj, the outer products of the
+//                               rows' and tokens' scales, both blocks of a
+//                               64-element chunk in one instruction;
+//   VALU                        acc += float(I) * S (a convert and an fma),
+// so the per-output scale products run on the matrix pipe (which the int8
+// dots leave idle most of the time) and the VALU keeps two instructions per
+// output and block. The min term is one v_mfma_f32_32x32x16_bf16 per tile
+// and super-block (K = 8 blocks x the high and low bf16 halves of u; the
+// 6-bit m exact in bf16), scaled by -dmin_r on the VALU. I, S and the min
+// sums share the D layout (lane l: token l % 32, rows 8 (i / 4) + 4 (l / 32)
+// + i % 4), so the VALU works register by register.
+//
+// Workgroup tile 256 tokens x 96 rows, 8 waves: wave w owns tokens
+// [32 w, +32) x all 96 rows (3 tiles), two waves per SIMD. A chunk's six
+// (row tile, block) steps are software pipelined, across chunks too: step
+// k's VALU runs while step k + 1's MFMAs execute and step k + 2's LDS
+// operands load. The chunk tiles rotate through three LDS buffers, so the
+// one barrier per chunk (before step 4) lets a wave read chunk c + 1 while
+// others still finish chunk c. Waves 0-2 also stage: at the start of chunk c
+// the codes of chunk c + 1 with d_rj per block, and per super-block
+// (double-buffered) the rows' m_j as bf16 and dmin.
+constexpr int kMiThreads = 512;
+constexpr int kI8Depth = 4;  // chunks per unrolled loop body
+constexpr int kI8Ring = 2;   // weight chunks in flight ahead of staging (register slots)
+constexpr int kI8Bufs = 3;   // chunk tiles in LDS
+
 template <class S>
-__global__ void __launch_bounds__(kMmThreads)
-    mm_q8_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
-                 const int8_t* __restrict__ xq, const float* __restrict__ xs, const float* __restrict__ xu,
+__global__ void __launch_bounds__(kMiThreads)
+    mm_i8_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                 const int8_t* __restrict__ xq, const float* __restrict__ xs, const u32x4* __restrict__ xu,
                  int m, float* __restrict__ y, int n_tiles_m) {
-  __shared__ __attribute__((aligned(16))) uint8_t wl[2][kMmBN * kMmRowQ];
-  __shared__ __attribute__((aligned(16))) float wsc[2][2][2][kMmBN];  // [buf][block][d|m][row]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  typedef float f32x32 __attribute__((ext_vector_type(32)));
+  constexpr bool kMin = S::kMin;
+  __shared__ __attribute__((aligned(16))) uint8_t wl[kI8Bufs][kMmBN * kMmRowQ];  // [chunk buf] codes
+  __shared__ __attribute__((aligned(16))) float wsc[kI8Bufs][2][kMmBN];  // [chunk buf][block][row] d_rj
+  __shared__ __attribute__((aligned(16))) u32x4 wm[2][kMmBN][2];                 // [sb buf][row][k half] m, bf16
+  __shared__ __attribute__((aligned(16))) float wdm[2][kMmBN];                   // [sb buf][row] dmin
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   int r0, t0;
   tile_of(n_tiles_m, r0, t0);
   const int nchunks = cols / kMmKC;
-  const int nblk = cols / 32;
+  const int nblk = cols / 32, nsb = cols >> 8;
 
   constexpr int kTasks = kMmBN * S::kPieces;
-  static_assert(kTasks % kWave == 0 && kTasks <= kMmThreads, "staging tasks fill whole waves");
+  static_assert(kTasks % kWave == 0 && kTasks <= kMiThreads, "staging tasks fill whole waves");
   const bool stager = tid < kTasks;
   const int srow = stager ? tid / S::kPieces : 0, piece = tid % S::kPieces;
   const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
 
-  // this lane's token tiles (one per M-subtile): codes of fragment (T, c, s)
-  // at 16-byte piece ((T * nchunks + c) * 2 + s) * 64 + lane, scales and min
-  // sums of (T, block j) at float (T * nblk + j) * 32 + l32
-  const int n_tt = (m + 31) >> 5;
-  const int8_t* xr[2];
-  const float *sr[2], *ur[2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int T = min((t0 + 64 * wave + 32 * mi) >> 5, n_tt - 1);
-    xr[mi] = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
-    sr[mi] = xs + int64_t(T) * nblk * 32 + l32;
-    ur[mi] = xu + int64_t(T) * nblk * 32 + l32;
-  }
+  // the wave's token tile (clamped to the padded tokens; tokens past m are
+  // computed on zero codes and not stored): codes of fragment (T, c, s) at
+  // 16-byte piece ((T * nch + c) * 2 + s) * 64 + lane, scales of (T, j) at
+  // float (T * nblk + j) * 32 + l32, the min operand of (T, sb) at 16-byte
+  // piece (T * nsb + sb) * 64 + lane
+  const int T = min((t0 >> 5) + wave, ((m + 31) >> 5) - 1);
+  const int8_t* xr = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
+  const float* sr = xs + int64_t(T) * nblk * 32 + l32;
+  const u32x4* ur = xu + int64_t(T) * nsb * 64 + lane;
 
-  f32x16 acc[2][3];
+  f32x16 acc[3];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 3; ++ni) acc[mi][ni] = f32x16{};
+  for (int ni = 0; ni < 3; ++ni) acc[ni] = f32x16{};
 
+  // one piece of chunk c into chunk buffer buf (codes and block scales); a
+  // K-quant row's m_j of the chunk's two blocks (and at the super-block's
+  // first chunk its dmin) into super-block buffer (c / 4) % 2
   auto stage = [&](const typename S::Raw& raw, int c, int buf) {
     uint32_t run0[4], run1[4];
     int o0, o1, jb0, jb1;
@@ -881,126 +916,153 @@ __global__ void __launch_bounds__(kMmThreads)
     uint8_t* dst = wl[buf] + srow * kMmRowQ;
     *reinterpret_cast<u32x4*>(dst + o0) = u32x4{run0[0], run0[1], run0[2], run0[3]};
     *reinterpret_cast<u32x4*>(dst + o1) = u32x4{run1[0], run1[1], run1[2], run1[3]};
-    // (two pieces of a Q4_K row write the same scales of both blocks)
-    wsc[buf][jb0][0][srow] = dj[0];
-    wsc[buf][jb0][1][srow] = mj[0];
-    wsc[buf][jb1][0][srow] = dj[1];
-    wsc[buf][jb1][1][srow] = mj[1];
+    // (two pieces of a K-quant row write the same scales of both blocks)
+    wsc[buf][jb0][srow] = dj[0];
+    wsc[buf][jb1][srow] = dj[1];
+    if constexpr (kMin) {
+      if (piece == 0) {
+        const int g = c & 3, sbuf = (c >> 2) & 1;
+        uint32_t scp, mp;
+        StQ4K::scale_bytes(raw.h, g, scp, mp);
+        // k = 8 (j / 4) + 2 (j % 4) + p for block j of the super-block and
+        // half p of u: blocks 2g and 2g + 1 are words 2 (g % 2), +1 of half g / 2
+        const uint32_t b0 = __builtin_bit_cast(uint32_t, float(mp & 0xFFu)) >> 16;
+        const uint32_t b1 = __builtin_bit_cast(uint32_t, float((mp >> 8) & 0xFFu)) >> 16;
+        uint32_t* wd = reinterpret_cast<uint32_t*>(&wm[sbuf][srow][g >> 1]) + 2 * (g & 1);
+        *reinterpret_cast<uint2*>(wd) = uint2{b0 | (b0 << 16), b1 | (b1 << 16)};
+        if (g == 0) wdm[sbuf][srow] = h2f(raw.h.x >> 16);
+      }
+    }
   };
 
-  typename S::Raw raw[kDepth];
-  if (stager) {
+  static_assert(kI8Depth % kI8Ring == 0, "ring slots are constants of the unrolled loop");
+  typename S::Raw raw[kI8Ring];
 #pragma unroll
-    for (int k = 0; k < kDepth; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
-    stage(raw[0], 0, 0);
-    raw[0] = S::load(wrow, min(kDepth, nchunks - 1), piece);
-  }
-  i32x4 xc[2][2];
+  for (int k = 0; k < kI8Ring; ++k) raw[k] = S::load(wrow, min(k, nchunks - 1), piece);
+  if (stager) stage(raw[0], 0, 0);
+  raw[0] = S::load(wrow, min(kI8Ring, nchunks - 1), piece);
+  // chunk c's activation fragments and the lane's token scale of block
+  // `half` (the B operand of the scale products), loaded a chunk ahead; the
+  // min operand a super-block ahead
+  i32x4 xc[2];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) xc[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + 1024 * s);
-  // the lane's tokens' block scales and min sums, a chunk ahead with the codes
-  float sxc[2][2], umc[2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) sxc[mi][s] = sr[mi][32 * s];
-    umc[mi] = S::kMin ? ur[mi][32 * half] : 0.f;
-  }
-  __syncthreads();
+  for (int s = 0; s < 2; ++s) xc[s] = *reinterpret_cast<const i32x4*>(xr + 1024 * s);
+  float sxc = sr[32 * half];
+  u32x4 uc = kMin ? ur[0] : u32x4{0u, 0u, 0u, 0u};
+  lds_barrier();
 
-  for (int c0 = 0; c0 < nchunks; c0 += kDepth) {
+  // step k of a chunk is (row tile k / 2, block k % 2); its weight
+  // fragment, and a row tile's d_rj of block `half` (the A operand of the
+  // scale products: lane half h supplies block h of the two-block MFMA)
+  auto ld_a = [&](int buf, int k) {
+    return *reinterpret_cast<const i32x4*>(wl[buf] + (32 * (k >> 1) + l32) * kMmRowQ + 32 * (k & 1) + 16 * half);
+  };
+  auto ld_d = [&](int buf, int ni) { return wsc[buf][half][32 * ni + l32]; };
+
+  // The pipeline's products live in ping-pong pairs indexed by constants of
+  // the unrolled loops, so that no register copy reads an MFMA result early:
+  // step k's int8 sums in Ib[k % 2] (six steps a chunk), row tile g's scale
+  // products (both blocks: registers 16 b + i) in Sb[g % 2] (g = 3 c + ni,
+  // whose parity repeats every kI8Depth chunks). Entering a chunk: step 0's
+  // int8 products and row tile 0's scale products issued, step 1's fragment
+  // loaded.
+  static_assert(kI8Depth % 4 == 0, "the super-block position repeats every kI8Depth chunks");
+  i32x16 Ib[2];
+  f32x32 Sb[2];
+  i32x4 a_nn = ld_a(0, 1);
+  float d_nn = 0.f;
+  Ib[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ld_a(0, 0), xc[0], i32x16{}, 0, 0, 0);
+  Sb[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(ld_d(0, 0), sxc, f32x32{}, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int c0 = 0; c0 < nchunks; c0 += kI8Depth) {
 #pragma unroll
-    for (int jj = 0; jj < kDepth; ++jj) {
+    for (int jj = 0; jj < kI8Depth; ++jj) {
       const int c = c0 + jj;
       if (c < nchunks) {  // uniform
         const bool more = c + 1 < nchunks;
-        i32x4 xn[2][2];
-        float sxn[2][2], umn[2];
-        if (more) {
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-              xn[mi][s] = *reinterpret_cast<const i32x4*>(xr[mi] + int64_t(c + 1) * 2048 + 1024 * s);
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) sxn[mi][s] = sr[mi][32 * (2 * (c + 1) + s)];
-            umn[mi] = S::kMin ? ur[mi][32 * (2 * (c + 1) + half)] : 0.f;
-          }
+        const int buf = c % kI8Bufs, nbuf = (c + 1) % kI8Bufs;
+        {
+          const int slot = (jj + 1) % kI8Ring;  // chunk c + 1 (a constant once unrolled)
+          if (more && stager) stage(raw[slot], c + 1, nbuf);
+          // every wave issues the weight loads (the other waves' lanes read
+          // row r0, one cache line a wave): with loads on the stagers' path
+          // only, the compiler's counted wait for the activation loads would
+          // also wait for these, a whole memory latency each chunk
+          raw[slot] = S::load(wrow, min(c + 1 + kI8Ring, nchunks - 1), piece);
         }
-        const int buf = c & 1;
-        const uint8_t* wb = wl[buf];
-        // min term of both blocks of the chunk on the f32 MFMA (K = 2 blocks):
-        // A[row][k] = -m of the lane's row and block k = lane half, B[k][token] = u
-        if constexpr (S::kMin) {
-          float um[2];
-    #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) um[mi] = umc[mi];
-    #pragma unroll
-          for (int ni = 0; ni < 3; ++ni) {
-            const float ma = -wsc[buf][half][1][32 * ni + l32];
-    #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-              acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(ma, um[mi], acc[mi][ni], 0, 0, 0);
+        const int cn = more ? c + 1 : c;
+        i32x4 xn[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) xn[s] = *reinterpret_cast<const i32x4*>(xr + int64_t(cn) * 2048 + 1024 * s);
+        const float sxn = sr[32 * (2 * cn + half)];
+        // the super-block's min term runs in its last chunk (c % 4 == jj: c0 is
+        // a multiple of kI8Depth)
+        const bool min_chunk = kMin && jj % 4 == 3;
+        const int sbuf = (c >> 2) & 1;
+        const bf16x8 ub = __builtin_bit_cast(bf16x8, uc);
+        f32x16 D_min = f32x16{};
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          const int ni = k >> 1, s = k & 1;
+          const int tp = (3 * jj + ni) & 1;  // this row tile's scale-product pair
+          if (k == 4) lds_barrier();  // chunk c + 1 staged; nobody reads chunk c - 2's buffer any more
+          // issue step k + 1's products (past the chunk: chunk c + 1's step 0;
+          // after the last chunk they read an unstaged buffer and go unused)
+          {
+            const i32x4 xb = k < 5 ? xc[(k + 1) & 1] : xn[0];
+            Ib[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_nn, xb, i32x16{}, 0, 0, 0);
+            if (s == 1)  // the next row tile's scale products
+              Sb[tp ^ 1] = __builtin_amdgcn_mfma_f32_32x32x1f32(d_nn, k < 5 ? sxc : sxn, f32x32{}, 0, 0, 0);
           }
-        }
-    #pragma unroll
-        for (int s = 0; s < 2; ++s) {  // one 32-element block per step
-          float sx[2];
-    #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) sx[mi] = sxc[mi][s];
-    #pragma unroll
-          for (int ni = 0; ni < 3; ++ni) {
-            const i32x4 a = *reinterpret_cast<const i32x4*>(wb + (32 * ni + l32) * kMmRowQ + 32 * s + 16 * half);
-            // weight rows of this lane's registers: 32 ni + 8 (i / 4) + 4 half + i % 4
-            f32x4 dw[4];
-    #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              dw[q] = *reinterpret_cast<const f32x4*>(&wsc[buf][s][0][32 * ni + 8 * q + 4 * half]);
-    #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-              // volatile fences keep each integer MFMA next to its scaling, so
-              // at most one 16-register integer result is live at a time
-              i32x4 av = a;
-              asm volatile("" : "+v"(av));
-              const i32x16 I = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, xc[mi][s], i32x16{}, 0, 0, 0);
-    #pragma unroll
-              for (int i = 0; i < 16; ++i)
-                acc[mi][ni][i] = __builtin_fmaf(float(I[i]), dw[i >> 2][i & 3] * sx[mi], acc[mi][ni][i]);
-              asm volatile("" : "+v"(acc[mi][ni]));
+          // (LDS reads complete in order: issued before these MFMAs, step k + 2's
+          // loads would make the MFMAs' wait for step k + 1's operands wait for them)
+          __builtin_amdgcn_sched_barrier(0);
+          // load step k + 2's operands (past the chunk: chunk c + 1's)
+          {
+            const int k2 = k + 2;
+            const int b2 = k2 < 6 ? buf : nbuf, kk = k2 < 6 ? k2 : k2 - 6;
+            a_nn = ld_a(b2, kk);
+            if ((kk & 1) == 0) d_nn = ld_d(b2, kk >> 1);
+          }
+          if (min_chunk && s == 0) {  // this tile's min sums, used at its block 1 step
+            const bf16x8 ma = __builtin_bit_cast(bf16x8, wm[sbuf][32 * ni + l32][half]);
+            D_min = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ma, ub, f32x16{}, 0, 0, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          // step k's scaling
+          const i32x16& I = Ib[k & 1];
+          const f32x32& Sc = Sb[tp];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[ni][i] = __builtin_fmaf(float(I[i]), Sc[16 * s + i], acc[ni][i]);
+          if (min_chunk && s == 1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 dm = *reinterpret_cast<const f32x4*>(&wdm[sbuf][32 * ni + 8 * q + 4 * half]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                acc[ni][4 * q + e] = __builtin_fmaf(-dm[e], D_min[4 * q + e], acc[ni][4 * q + e]);
             }
           }
+          // step k's sums are formed here: without this the compiler sinks the
+          // scaling below later steps' MFMAs and holds all their products
+          asm volatile("" : "+v"(acc[ni]));
+          __builtin_amdgcn_sched_barrier(0);
         }
-        if (more) {
-          const int slot = (jj + 1) % kDepth;  // chunk c + 1 (a constant once unrolled)
-          if (stager) {
-            stage(raw[slot], c + 1, (c + 1) & 1);
-            raw[slot] = S::load(wrow, min(c + 1 + kDepth, nchunks - 1), piece);
-          }
+        if (min_chunk) uc = ur[64 * min((c >> 2) + 1, nsb - 1)];
 #pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-              xc[mi][s] = xn[mi][s];
-              sxc[mi][s] = sxn[mi][s];
-            }
-            umc[mi] = umn[mi];
-          }
+        for (int s = 0; s < 2; ++s) {
+          xc[s] = xn[s];
         }
-        __syncthreads();
+        sxc = sxn;
       }
     }
   }
 
   // D: lane l holds column l % 32 (a token), register i the weight row
   // 8 * (i / 4) + 4 * (l / 32) + i % 4 -> four runs of 4 consecutive rows
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int t = t0 + 64 * wave + 32 * mi + l32;
-    if (t >= m) continue;
+  const int t = t0 + 32 * wave + l32;
+  if (t < m) {
 #pragma unroll
     for (int ni = 0; ni < 3; ++ni)
 #pragma unroll
@@ -1009,11 +1071,11 @@ __global__ void __launch_bounds__(kMmThreads)
         float* dst = y + int64_t(t) * n_rows + r;
         if (r + 3 < n_rows && (n_rows & 3) == 0) {
           *reinterpret_cast<f32x4*>(dst) =
-              f32x4{acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1], acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]};
+              f32x4{acc[ni][4 * q], acc[ni][4 * q + 1], acc[ni][4 * q + 2], acc[ni][4 * q + 3]};
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (r + e < n_rows) dst[e] = acc[mi][ni][4 * q + e];
+            if (r + e < n_rows) dst[e] = acc[ni][4 * q + e];
         }
       }
   }
@@ -1264,24 +1326,39 @@ __global__ void __launch_bounds__(kMqThreads)
 // -------------------------------------------------------------------- host --
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Modes: 0 bf16; 1 q8 (activations in 32-element Q8 blocks, every int8
+// format); 2 q8k (activations in 256-element blocks, one scale per weight
+// super-block: Q4_K / Q5_K only; a coarser rounding than mode 1, kept as an
+// opt-in alternative).
 bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint32_t mode) {
   if (!device_quant(quant) || rows <= 0 || cols <= 0 || m <= 0) return false;
   if (cols % kMmKC != 0 || cols % geometry(quant).block != 0) return false;
   if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 30) || m > (int64_t(1) << 24)) return false;
   if (mode == 1 && quant == kQ6_K) return false;  // 16-element Q6_K scales: bf16 mode only
-  if (mode > 1) return false;
+  if (mode == 2 && quant != kQ4_K && quant != kQ5_K) return false;
+  if (mode > 2) return false;
   const int64_t tiles = ((rows + kMmBN - 1) / kMmBN) * ((m + kMmBM - 1) / kMmBM);
   return tiles <= (int64_t(1) << 31) - 1;
 }
 
-size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
-  if (mode == 0) return align256(size_t((m + 31) / 32 * 32) * size_t(cols) * 2);  // whole 32-token tiles
+// Workspace carve-up of the 32-element int8 path: codes, scales (f32 per
+// block), min-term operands (bf16 halves per block, whole super-blocks).
+struct Q8Ws {
+  int8_t* codes;
+  float* scales;
+  uint32_t* u;
+  size_t bytes;
+};
+static Q8Ws q8_ws(uint8_t* ws, int64_t cols, int64_t m) {
   const size_t mp = size_t((m + 31) / 32 * 32);  // tokens padded to whole 32-token tiles
-  const size_t blocks = mp * size_t(cols / 32);
-  // 32-element blocks: codes, scales, scaled sums; 256-element blocks
-  // (K-quant weights) need less: codes, a scale per 256 and 16 bytes of f16
-  // sums per 256
-  return align256(mp * size_t(cols)) + 2 * align256(blocks * sizeof(float));
+  const size_t nblk = size_t(cols / 32), nsb = (nblk + 7) / 8;
+  Q8Ws r;
+  const size_t o1 = align256(mp * size_t(cols)), o2 = o1 + align256(mp * nblk * sizeof(float));
+  r.codes = reinterpret_cast<int8_t*>(ws);
+  r.scales = reinterpret_cast<float*>(ws + o1);
+  r.u = reinterpret_cast<uint32_t*>(ws + o2);
+  r.bytes = o2 + align256(mp * nsb * 32);
+  return r;
 }
 
 // Workspace carve-up of the 256-element int8 path: codes, scales, sums.
@@ -1289,15 +1366,24 @@ struct Q8kWs {
   uint8_t* codes;
   float* scales;
   uint8_t* sums;
+  size_t bytes;
 };
 static Q8kWs q8k_ws(uint8_t* ws, int64_t cols, int64_t m) {
   const size_t mp = size_t((m + 31) / 32 * 32);
   const size_t nsb = size_t(cols / 256);
   Q8kWs r;
+  const size_t o1 = align256(mp * size_t(cols)), o2 = o1 + align256(mp * nsb * sizeof(float));
   r.codes = ws;
-  r.scales = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)));
-  r.sums = ws + align256(mp * size_t(cols)) + align256(mp * nsb * sizeof(float));
+  r.scales = reinterpret_cast<float*>(ws + o1);
+  r.sums = ws + o2;
+  r.bytes = o2 + align256(mp * nsb * 32);  // 512 bytes per 16 tokens and super-block
   return r;
+}
+
+size_t matmul_workspace_bytes(int64_t cols, int64_t m, uint32_t mode) {
+  if (mode == 0) return align256(size_t((m + 31) / 32 * 32) * size_t(cols) * 2);  // whole 32-token tiles
+  if (mode == 2) return q8k_ws(nullptr, cols, m).bytes;
+  return q8_ws(nullptr, cols, m).bytes;
 }
 
 template <class S>
@@ -1308,19 +1394,18 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
   if (mode == 0) {
     hipLaunchKernelGGL(mm_bf16_ws_kernel<S>, grid, dim3(kMmWsThreads), kMmLdsWs, s, w, rows, cols, rb,
                        reinterpret_cast<const u32x4*>(ws), m, y, ntm, q6s);
-  } else if constexpr (S::kQ8K) {
-    const Q8kWs q = q8k_ws(ws, cols, m);
-    hipLaunchKernelGGL(mm_q8k_kernel<S>, grid, dim3(kMqThreads), 0, s, w, rows, cols, rb,
-                       reinterpret_cast<const int8_t*>(q.codes), q.scales, q.sums, m, y, ntm);
   } else if constexpr (S::kQ8) {
-    const size_t mp = size_t((m + 31) / 32 * 32);
-    const size_t blocks = mp * size_t(cols / 32);
-    const int8_t* xq = reinterpret_cast<const int8_t*>(ws);
-    const float* xs = reinterpret_cast<const float*>(ws + align256(mp * size_t(cols)));
-    const float* xu = reinterpret_cast<const float*>(ws + align256(mp * size_t(cols)) +
-                                                     align256(blocks * sizeof(float)));
-    hipLaunchKernelGGL(mm_q8_kernel<S>, grid, dim3(kMmThreads), 0, s, w, rows, cols, rb, xq, xs, xu, m, y,
-                       ntm);
+    if (mode == 2) {
+      if constexpr (S::kQ8K) {
+        const Q8kWs q = q8k_ws(ws, cols, m);
+        hipLaunchKernelGGL(mm_q8k_kernel<S>, grid, dim3(kMqThreads), 0, s, w, rows, cols, rb,
+                           reinterpret_cast<const int8_t*>(q.codes), q.scales, q.sums, m, y, ntm);
+      }
+    } else {
+      const Q8Ws q = q8_ws(ws, cols, m);
+      hipLaunchKernelGGL(mm_i8_kernel<S>, grid, dim3(kMiThreads), 0, s, w, rows, cols, rb, q.codes, q.scales,
+                         reinterpret_cast<const u32x4*>(q.u), m, y, ntm);
+    }
   }
 }
 
@@ -1353,18 +1438,16 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
     const int64_t pieces = (m + 31) / 32 * 32 * cols / 8;  // 16-byte pieces of whole 32-token tiles
     hipLaunchKernelGGL(x_bf16_tiled_kernel, dim3(unsigned((pieces + 255) / 256)), dim3(256), 0, s, x,
                        reinterpret_cast<u32x4*>(ws), int(m), int(cols), pieces);
-  } else if (quant == kQ4_K || quant == kQ5_K) {
+  } else if (mode == 2) {
     const Q8kWs q = q8k_ws(ws, cols, m);
     const int64_t waves = (m + 31) / 32 * 32 * (cols / 256);  // one per (padded token, super-block)
     hipLaunchKernelGGL(x_q8k_tiled_kernel, dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s, x, q.codes,
                        q.scales, q.sums, int(m), int(cols), waves);
   } else {
-    const size_t mp = size_t((m + 31) / 32 * 32);
-    const size_t blocks = mp * size_t(cols / 32);
-    float* xs = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)));
-    float* xu = reinterpret_cast<float*>(ws + align256(mp * size_t(cols)) + align256(blocks * sizeof(float)));
+    const Q8Ws q = q8_ws(ws, cols, m);
+    const int64_t blocks = (m + 31) / 32 * 32 * (cols / 32);
     hipLaunchKernelGGL(x_q8_tiled_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, x,
-                       reinterpret_cast<u32x4*>(ws), xs, xu, int(m), int(cols), int64_t(blocks));
+                       reinterpret_cast<u32x4*>(q.codes), q.scales, q.u, int(m), int(cols), blocks);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -51,6 +51,7 @@ FLAG_EXPERT_OUT_MAJOR = 2
 FLAG_IQ4XS_GGML = 4
 MATMUL_BF16 = 0
 MATMUL_Q8 = 1
+MATMUL_Q8K = 2
 
 # Every symbol include/strata_hip.h declares (kept in step with the header).
 EXPORTS = (

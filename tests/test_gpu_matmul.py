@@ -8,12 +8,15 @@ Metric: max|y - r| / max|r| per token row.
   the same gemvs on bf16-rounded operands (W dequantized exactly then rounded
   to bf16, x rounded to bf16, f64 sums): <= 1e-3 -- this isolates the
   kernel's indexing and accumulation from the rounding the mode defines.
-* q8 mode against the oracle gemv of x rounded through Q8 blocks of the
-  weight's scale group (scale * code; 32 elements for Q8_0, 256 for Q4_K
-  and Q5_K): <= 1e-3 (the int8 products are exact); against the f32
-  oracle: <= 2e-2 with 32-element blocks, <= 3e-2 with 256-element ones (the
-  code step is max|x| / 127 over 256 elements instead of 32: about 1.3x the
-  rounding; measured worst rows 1.3-2.1%).
+* q8 mode (activations in Q8 blocks of 32 elements, f32 scale, int8 codes;
+  Q8_0, Q4_K and Q5_K weights) against the oracle gemv of x rounded through
+  those blocks (scale * code): <= 1e-3 normwise and the strict per-element
+  bar (the int8 products are exact; the scale products and the min term are
+  f32); against the f32 oracle: <= 2e-2.
+* q8k mode (opt-in: 256-element activation blocks, one scale per K-quant
+  super-block) against the oracle gemv of x rounded through its blocks: <=
+  1e-3 and the strict bar. Its coarser rounding is the mode's definition and
+  is not held to the q8 mode's f32 bar.
 * the device Q8 quantizers (32- and 256-element blocks) are bit-exact with
   the oracle's.
 """
@@ -27,7 +30,6 @@ from strata_hip import synth as S
 pytestmark = pytest.mark.gpu
 
 TOL_F32 = 2e-2
-TOL_F32_Q8K = 3e-2  # the activation rounding of one scale per 256 elements
 TOL_EXACT_OPERANDS = 1e-3
 
 
@@ -85,9 +87,39 @@ def test_matmul_q8(backend, oracle, quant, rows, cols, m):
     w = S.matrix(quant, 920 + rows, rows, cols)
     x = S.normal_f32(921 + m, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor(f"mq{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_Q8)
-    xq = oracle.q8_activations_for(quant, x)
+    xq = oracle.q8_activations_for(H.MATMUL_Q8, x)
     check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
-    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32_Q8K if quant in (12, 13) else TOL_F32)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, x, threads=8), TOL_F32)
+
+
+@pytest.mark.parametrize("quant,rows,cols,m", [s for s in SHAPES if s[0] in (12, 13)])
+def test_matmul_q8k(backend, oracle, quant, rows, cols, m):
+    say("matmul q8k", quant, rows, cols, m)
+    w = S.matrix(quant, 960 + rows, rows, cols)
+    x = S.normal_f32(961 + m, m * cols).reshape(m, cols)
+    y = backend.matmul(H.QuantTensor(f"mk{quant}_{rows}_{cols}", quant, rows, cols, w), x, H.MATMUL_Q8K)
+    xq = oracle.q8_activations_for(H.MATMUL_Q8K, x)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
+
+
+@pytest.mark.parametrize("quant", [8, 12, 13])
+def test_matmul_q8_block_spread_and_signs(backend, oracle, quant):
+    # 32-element blocks far apart in scale (1e-3 .. 1e3 within a super-block),
+    # blocks of one sign (large code sums: the min term's u = s * sum(codes)
+    # at its largest) and an all-zero block (s = 0)
+    rows, cols, m = 96, 1024, 40
+    say("matmul q8 spread", quant)
+    w = S.matrix(quant, 952, rows, cols)
+    x = S.normal_f32(953, m * cols).reshape(m, cols)
+    xb = x.reshape(m, -1, 32)
+    xb[:, 1::8] *= np.float32(1e3)
+    xb[:, 2::8] *= np.float32(1e-3)
+    xb[:, 3::8] = np.abs(xb[:, 3::8])
+    xb[:, 5::8] = -np.abs(xb[:, 5::8])
+    xb[:, 6::8] = 0.0
+    y = backend.matmul(H.QuantTensor(f"mqsp{quant}", quant, rows, cols, w), x, H.MATMUL_Q8)
+    xq = oracle.q8_activations_for(H.MATMUL_Q8, x)
+    check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
 @pytest.fixture(scope="module")
@@ -96,20 +128,21 @@ def prefill_weight():
     return S.matrix(12, 0x5EED0005, 12288, 4096)
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 def test_matmul_prefill_config(backend, oracle, prefill_weight, mode):
     rows, cols, m = 12288, 4096, 512
     say("matmul prefill config, mode", mode)
     w = prefill_weight
     x = S.normal_f32(0x5EED0006, m * cols).reshape(m, cols)
     y = backend.matmul(H.QuantTensor("prefill.w", 12, rows, cols, w), x, mode)
-    ref = oracle.matmul(12, rows, cols, w, x, threads=16)
-    worst = check_rows(y, ref, TOL_F32_Q8K if mode == 1 else TOL_F32)
-    print(f"[case] mode {mode}: worst row rel err vs f32 oracle {worst:.3g}", flush=True)
-    if mode == 1:
-        exact = oracle.matmul(12, rows, cols, w, oracle.q8_activations_for(12, x), threads=16)
-    else:
+    if mode != 2:  # the opt-in 256-element mode's rounding is its own definition
+        ref = oracle.matmul(12, rows, cols, w, x, threads=16)
+        worst = check_rows(y, ref, TOL_F32)
+        print(f"[case] mode {mode}: worst row rel err vs f32 oracle {worst:.3g}", flush=True)
+    if mode == 0:
         exact = bf16_operand_ref(oracle, 12, rows, cols, w, x)
+    else:
+        exact = oracle.matmul(12, rows, cols, w, oracle.q8_activations_for(mode, x), threads=16)
     check_rows(y, exact, TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
@@ -168,12 +201,12 @@ def test_matmul_q8k_wide_sub_block_spread(backend, oracle, quant):
     w = S.matrix(quant, 950, rows, cols)
     x = S.normal_f32(951, m * cols).reshape(m, cols)
     x.reshape(m, -1, 256)[:, :, 64:96] *= np.float32(1e3)
-    y = backend.matmul(H.QuantTensor(f"mqs{quant}", quant, rows, cols, w), x, H.MATMUL_Q8)
-    xq = oracle.q8_activations_for(quant, x)
+    y = backend.matmul(H.QuantTensor(f"mqs{quant}", quant, rows, cols, w), x, H.MATMUL_Q8K)
+    xq = oracle.q8_activations_for(H.MATMUL_Q8K, x)
     check_rows(y, oracle.matmul(quant, rows, cols, w, xq, threads=8), TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 def test_matmul_dev_matches_host_path(backend, mode):
     import torch
     rows, cols, m = 192, 512, 40
@@ -205,3 +238,6 @@ def test_matmul_errors(backend):
         backend.matmul(w4, np.zeros((2, 128), np.float32))
     with pytest.raises(H.BackendError):
         backend.matmul(w4, np.zeros((2, 256), np.float32), 7)
+    w80 = H.QuantTensor("e80", 8, 4, 256, S.matrix(8, 1, 4, 256))
+    with pytest.raises(H.UnsupportedQuantError):  # 256-element blocks: K-quant weights only
+        backend.matmul(w80, np.zeros((2, 256), np.float32), H.MATMUL_Q8K)
