@@ -74,27 +74,17 @@ def _graph_of(torch, stream, calls, n, first=0):
     return g
 
 
-_FLUSH = {}
-
-
-def _flush_caches(torch, stream):
-    """Writes 512 MiB (twice the 256 MB Infinity Cache, far beyond the L2s)
-    on `stream`, so nothing the timed calls read is still cached."""
-    buf = _FLUSH.get("buf")
-    if buf is None:
-        buf = _FLUSH["buf"] = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0")
-    with torch.cuda.stream(stream):
-        buf.fill_(1)
-
-
 def _time_graph_calls(torch, stream, calls, steps, warmup):
     """Runs `warmup` calls untimed, then times exactly `steps` calls; events
     on `stream`. Each set is one captured HIP graph. The timed graph takes the
     calls that follow the warmed ones (its first call is calls[warmup %
     len(calls)], so a rotation over weight copies continues instead of
-    re-reading the copies just warmed), is replayed once untimed (the first
-    replay of a graph also uploads it), then the caches are flushed and the
-    second replay is timed. Returns ms per call."""
+    re-reading the copies just warmed). It is replayed twice back to back on
+    the stream, the first replay untimed (a graph's first replay also uploads
+    it, and the back-to-back order keeps the launch latency of the timed
+    replay out of the timed region: the start event completes as the untimed
+    replay ends, with the timed replay already queued behind it). Returns ms
+    per call."""
     with torch.cuda.stream(stream):  # eager pass: the calls are accepted
         for f in calls:
             f(stream.cuda_stream)
@@ -106,16 +96,14 @@ def _time_graph_calls(torch, stream, calls, steps, warmup):
         torch.cuda.synchronize()
         del gw
     g = _graph_of(torch, stream, calls, steps, first=warmup % len(calls))
-    with torch.cuda.stream(stream):  # untimed: the graph's first replay
-        g.replay()
-    _flush_caches(torch, stream)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
     with torch.cuda.stream(stream):
+        g.replay()  # untimed
+        start.record(stream)
         g.replay()
-    end.record(stream)
+        end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     del g
@@ -519,14 +507,17 @@ def bench_decode_shapes(torch, H, S, steps_max, batched_only=False):
 
 
 def load_traffic(name):
+    """(HBM bytes per launch, the kernel they were counted on) from a counter
+    summary under profiles/, or (None, None)."""
     p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
-        return None
+        return None, None
     try:
         with open(p) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            d = json.load(f)
+        return d.get("traffic_bytes_per_launch"), d.get("kernel")
     except (OSError, ValueError):
-        return None
+        return None, None
 
 
 def main():
@@ -593,6 +584,7 @@ def main():
     alg = wbytes + 4 * cols + 4 * rows
     achieved = alg / (ms * 1e-3) / 1e9
     ceil_gbs = wbytes / (ceiling["ms"] * 1e-3) / 1e9
+    traffic = load_traffic("gemv_q4k_4096x12288_b1.traffic.json")
     out = {
         "metric": "Q4_K fused matvec packed-weight GB/s + % HBM peak (4096x12288, batch 1)",
         "value": round(gbs, 2),
@@ -613,7 +605,7 @@ def main():
                    "rows": rows, "cols": cols, "batch": 1, "weight_bytes": wbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("gemv_q4k_4096x12288_b1.traffic.json"),
+                     "traffic": traffic[0], "traffic_kernel": traffic[1],
                      "measured_ceiling_GBps": round(ceil_gbs, 2),
                      "frac_of_measured_ceiling": round(gbs / ceil_gbs, 4),
                      "ceiling": "plain streaming read of the same 28,311,552 bytes (sh_stream_read_dev: 16-byte "
