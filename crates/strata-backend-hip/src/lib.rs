@@ -87,7 +87,7 @@ fn gemv_quant(q: QuantType) -> bool {
 
 /// Types the expert, MoE and matmul kernels read.
 fn device_quant(q: QuantType) -> bool {
-    matches!(q, QuantType::Q8_0 | QuantType::Q4K | QuantType::Q5K | QuantType::Q6K)
+    matches!(q, QuantType::Q8_0 | QuantType::Q4K | QuantType::Q5K | QuantType::Q6K | QuantType::Iq4Xs)
 }
 
 fn last_error() -> String {

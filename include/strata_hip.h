@@ -4,8 +4,8 @@
  *
  * The library replaces the matvec/matmul half of strata-core's
  * `trait ComputeBackend` (crates/strata-core/src/backend.rs:20-51) for the
- * GGUF types Q8_0, Q4_K, Q5_K and Q6_K (and, for the matvec and dequant
- * only, IQ4_XS and F32 / F16 / BF16, the types router and gate tensors use).
+ * GGUF types Q8_0, Q4_K, Q5_K, Q6_K and IQ4_XS (and, for the matvec and
+ * dequant only, F32 / F16 / BF16, the types router and gate tensors use).
  * Weights stay packed in device memory in their GGUF block layout; kernels
  * dequantize in registers.
  *
@@ -68,7 +68,7 @@ extern "C" {
 #define SH_QUANT_Q4_K 12u
 #define SH_QUANT_Q5_K 13u
 #define SH_QUANT_Q6_K 14u
-#define SH_QUANT_IQ4_XS 23u /* matvec and dequant only */
+#define SH_QUANT_IQ4_XS 23u
 #define SH_QUANT_BF16 30u
 
 /* ---- tensor flags ------------------------------------------------------ */
@@ -263,10 +263,10 @@ int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert
  * 116-117); the result equals m calls of ops::gemv (ops.rs:14-28) up to the
  * activation rounding of `mode`:
  *   SH_MATMUL_BF16  x rounded to bf16, weights dequantized to bf16, f32
- *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K);
+ *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS);
  *   SH_MATMUL_Q8    x quantized to Q8 blocks of 32 elements (f32 scale
  *                   max|x| / 127 per block, int8 codes rounded to nearest
- *                   even), int8 products (Q8_0, Q4_K, Q5_K);
+ *                   even), int8 products (Q8_0, Q4_K, Q5_K, IQ4_XS);
  *   SH_MATMUL_Q8K   x quantized to blocks of 256 elements, one scale per
  *                   weight super-block (Q4_K, Q5_K): a coarser activation
  *                   rounding than SH_MATMUL_Q8 (the step is max|x| over 256

@@ -397,20 +397,21 @@ typedef struct {
   size_t nbytes;
   const float* x;
   float* y;
+  int mode;
   int rc;
 } gemv_job;
 
 static void* gemv_worker(void* p) {
   gemv_job* j = (gemv_job*)p;
   j->rc = gemv_rows(j->quant, j->r0, j->r1, j->cols, j->data, j->nbytes, j->x,
-                    j->y, SHO_Q6K_SCALE_U8);
+                    j->y, j->mode);
   return NULL;
 }
 
-int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
-                     const uint8_t* data, size_t nbytes, const float* x,
-                     float* y, int n_threads) {
-  if (n_threads <= 1 || rows < 2) return sho_gemv(quant, rows, cols, data, nbytes, x, y);
+static int gemv_threads_mode(uint32_t quant, int64_t rows, int64_t cols,
+                             const uint8_t* data, size_t nbytes, const float* x,
+                             float* y, int n_threads, int mode) {
+  if (n_threads <= 1 || rows < 2) return gemv_rows(quant, 0, rows, cols, data, nbytes, x, y, mode);
   if (n_threads > 256) n_threads = 256;
   pthread_t th[256];
   int started[256];
@@ -421,7 +422,7 @@ int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
     int64_t r0 = t * per;
     if (r0 >= rows) break;
     int64_t r1 = r0 + per < rows ? r0 + per : rows;
-    jobs[t] = (gemv_job){quant, r0, r1, cols, data, nbytes, x, y, 0};
+    jobs[t] = (gemv_job){quant, r0, r1, cols, data, nbytes, x, y, mode, 0};
     started[t] = pthread_create(&th[t], NULL, gemv_worker, &jobs[t]) == 0;
     if (!started[t]) gemv_worker(&jobs[t]); /* could not start: run inline */
     ++n_jobs;
@@ -434,13 +435,19 @@ int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
   return rc;
 }
 
+int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
+                     const uint8_t* data, size_t nbytes, const float* x,
+                     float* y, int n_threads) {
+  return gemv_threads_mode(quant, rows, cols, data, nbytes, x, y, n_threads, SHO_Q6K_SCALE_U8);
+}
+
 /* ---- expert_gemv (ops.rs:169-195) --------------------------------------
  * Expert-major [n_expert][rows = in][cols = out] (weights.rs:14-34):
  * acc[c] += x[i] * W_e[i][c] in f64 over input rows i, skipping x[i] == 0,
  * then cast to f32. */
-int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
-                    int64_t cols, const uint8_t* data, size_t nbytes,
-                    int64_t e, const float* x, float* y) {
+int sho_expert_gemv_mode(uint32_t quant, int64_t n_expert, int64_t rows,
+                         int64_t cols, const uint8_t* data, size_t nbytes,
+                         int64_t e, const float* x, float* y, int mode) {
   int64_t rb = sho_byte_size(quant, cols);
   if (rb < 0) return SHO_UNSUPPORTED;
   if (e < 0 || e >= n_expert) return SHO_TRUNCATED;
@@ -461,7 +468,7 @@ int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
       rc = SHO_TRUNCATED;
       break;
     }
-    rc = sho_dequantize_row(quant, data + off, (size_t)rb, row, (size_t)cols);
+    rc = sho_dequantize_row_mode(quant, data + off, (size_t)rb, row, (size_t)cols, mode);
     if (rc) break;
     for (int64_t c = 0; c < cols; ++c) acc[c] += xi * (double)row[c];
   }
@@ -470,6 +477,12 @@ int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
   free(acc);
   free(row);
   return rc;
+}
+
+int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
+                    int64_t cols, const uint8_t* data, size_t nbytes,
+                    int64_t e, const float* x, float* y) {
+  return sho_expert_gemv_mode(quant, n_expert, rows, cols, data, nbytes, e, x, y, 0);
 }
 
 /* ops.rs:85-87 */
@@ -537,25 +550,26 @@ int sho_moe_route(const float* logits, int64_t n_expert, int64_t top_k,
  * [n_expert][out][in] (llama.cpp's expert stacks) as ops::gemv of the
  * expert's [out][in] slice. */
 static int expert_apply(uint32_t quant, int64_t n_expert, int64_t n_in, int64_t n_out, const uint8_t* data,
-                        size_t nbytes, int64_t e, const float* x, float* y, int out_major) {
-  if (!out_major) return sho_expert_gemv(quant, n_expert, n_in, n_out, data, nbytes, e, x, y);
+                        size_t nbytes, int64_t e, const float* x, float* y, int out_major, int mode) {
+  if (!out_major) return sho_expert_gemv_mode(quant, n_expert, n_in, n_out, data, nbytes, e, x, y, mode);
   int64_t rb = sho_byte_size(quant, n_in);
   if (rb < 0) return SHO_UNSUPPORTED;
   if (e < 0 || e >= n_expert) return SHO_TRUNCATED;
   size_t off = (size_t)(e * n_out * rb);
   if (off > nbytes) return SHO_TRUNCATED;
-  return gemv_rows(quant, 0, n_out, n_in, data + off, nbytes - off, x, y, 0);
+  return gemv_rows(quant, 0, n_out, n_in, data + off, nbytes - off, x, y, mode);
 }
 
 /* moe.rs:108-127 for one token: for each selected expert j with w != 0 (in
  * the order given, ascending id): h = gate_e . x, p = up_e . x,
  * h = silu(h) * p, d = down_e . h, out += w * d (f32 product, then sum). */
-int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+int sho_moe_routed_m(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
                      int64_t n_expert, int64_t n_embd, int64_t n_ff,
                      const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
                      size_t up_bytes, const uint8_t* down, size_t down_bytes,
                      const int64_t* ids, const float* weights, int64_t k,
-                     const float* x, float* out, int out_major) {
+                     const float* x, float* out, int out_major, const int* modes) {
+  const int mg = modes ? modes[0] : 0, mu = modes ? modes[1] : 0, md = modes ? modes[2] : 0;
   float* h = (float*)malloc((size_t)n_ff * sizeof(float));
   float* part = (float*)malloc((size_t)n_ff * sizeof(float));
   float* d = (float*)malloc((size_t)n_embd * sizeof(float));
@@ -565,12 +579,12 @@ int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant
     float w = weights[j];
     if (w == 0.0f) continue;
     int64_t e = ids[j];
-    rc = expert_apply(gate_quant, n_expert, n_embd, n_ff, gate, gate_bytes, e, x, h, out_major);
+    rc = expert_apply(gate_quant, n_expert, n_embd, n_ff, gate, gate_bytes, e, x, h, out_major, mg);
     if (rc) break;
-    rc = expert_apply(up_quant, n_expert, n_embd, n_ff, up, up_bytes, e, x, part, out_major);
+    rc = expert_apply(up_quant, n_expert, n_embd, n_ff, up, up_bytes, e, x, part, out_major, mu);
     if (rc) break;
     for (int64_t i = 0; i < n_ff; ++i) h[i] = sho_silu(h[i]) * part[i];
-    rc = expert_apply(down_quant, n_expert, n_ff, n_embd, down, down_bytes, e, h, d, out_major);
+    rc = expert_apply(down_quant, n_expert, n_ff, n_embd, down, down_bytes, e, h, d, out_major, md);
     if (rc) break;
     for (int64_t i = 0; i < n_embd; ++i) {
       float t = w * d[i];
@@ -581,6 +595,16 @@ int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant
   free(part);
   free(d);
   return rc;
+}
+
+int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                     int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                     const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                     size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                     const int64_t* ids, const float* weights, int64_t k,
+                     const float* x, float* out, int out_major) {
+  return sho_moe_routed_m(gate_quant, up_quant, down_quant, n_expert, n_embd, n_ff, gate, gate_bytes, up,
+                          up_bytes, down, down_bytes, ids, weights, k, x, out, out_major, NULL);
 }
 
 int sho_moe_routed(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
@@ -606,9 +630,12 @@ float sho_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
  * [n_embd][n_ff_sh], gate_inp [1][n_embd] (ops::gemv orientation).
  * q[8]: the types of router, gate, up, down, gate_sh, up_sh, down_sh,
  * gate_inp; t[8] / nb[8] their bytes. out (n_embd) is overwritten. */
-int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+int sho_moe_layer_m(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
                     int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
-                    float* out, int out_major) {
+                    float* out, int out_major, const int* modes) {
+  int md[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (modes)
+    for (int i = 0; i < 8; ++i) md[i] = modes[i];
   float* xb = (float*)malloc((size_t)n_embd * sizeof(float));
   float* logits = (float*)malloc((size_t)n_expert * sizeof(float));
   int64_t* ids = (int64_t*)malloc((size_t)top_k * sizeof(int64_t));
@@ -619,20 +646,20 @@ int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb
   float s = 0.0f;
   int rc = SHO_OK;
   for (int64_t i = 0; i < n_embd; ++i) xb[i] = sho_bf16_round(x[i]);
-  rc = sho_gemv(q[0], n_expert, n_embd, t[0], nb[0], xb, logits);
+  rc = sho_gemv_mode(q[0], n_expert, n_embd, t[0], nb[0], xb, logits, md[0]);
   int64_t k = 0;
   if (rc == SHO_OK) {
     k = sho_moe_route(logits, n_expert, top_k, ids, w);
-    rc = sho_moe_routed_o(q[1], q[2], q[3], n_expert, n_embd, n_ff, t[1], nb[1], t[2], nb[2], t[3], nb[3],
-                          ids, w, k, x, out, out_major);
+    rc = sho_moe_routed_m(q[1], q[2], q[3], n_expert, n_embd, n_ff, t[1], nb[1], t[2], nb[2], t[3], nb[3],
+                          ids, w, k, x, out, out_major, md + 1);
   }
-  if (rc == SHO_OK) rc = sho_gemv(q[4], n_ff_sh, n_embd, t[4], nb[4], x, g);
-  if (rc == SHO_OK) rc = sho_gemv(q[5], n_ff_sh, n_embd, t[5], nb[5], x, part);
+  if (rc == SHO_OK) rc = sho_gemv_mode(q[4], n_ff_sh, n_embd, t[4], nb[4], x, g, md[4]);
+  if (rc == SHO_OK) rc = sho_gemv_mode(q[5], n_ff_sh, n_embd, t[5], nb[5], x, part, md[5]);
   if (rc == SHO_OK) {
     for (int64_t i = 0; i < n_ff_sh; ++i) g[i] = sho_silu(g[i]) * part[i];
-    rc = sho_gemv(q[6], n_embd, n_ff_sh, t[6], nb[6], g, d);
+    rc = sho_gemv_mode(q[6], n_embd, n_ff_sh, t[6], nb[6], g, d, md[6]);
   }
-  if (rc == SHO_OK) rc = sho_gemv(q[7], 1, n_embd, t[7], nb[7], x, &s);
+  if (rc == SHO_OK) rc = sho_gemv_mode(q[7], 1, n_embd, t[7], nb[7], x, &s, md[7]);
   if (rc == SHO_OK) {
     const float gate = sho_sigmoid(s);
     for (int64_t i = 0; i < n_embd; ++i) {
@@ -650,23 +677,31 @@ int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb
   return rc;
 }
 
+int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                    int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                    float* out, int out_major) {
+  return sho_moe_layer_m(q, t, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, x, out, out_major, NULL);
+}
+
 int sho_moe_layer(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
                   int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
                   float* out) {
   return sho_moe_layer_o(q, t, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, x, out, 0);
 }
 
-int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
-               size_t nbytes, const float* x, int64_t m, float* y, int n_threads) {
+int sho_matmul_mode(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+                    size_t nbytes, const float* x, int64_t m, float* y, int n_threads, int mode) {
   if (m < 0) return SHO_UNSUPPORTED;
   for (int64_t t = 0; t < m; ++t) {
-    int rc = n_threads > 1
-                 ? sho_gemv_threads(quant, rows, cols, data, nbytes, x + t * cols,
-                                    y + t * rows, n_threads)
-                 : sho_gemv(quant, rows, cols, data, nbytes, x + t * cols, y + t * rows);
+    int rc = gemv_threads_mode(quant, rows, cols, data, nbytes, x + t * cols, y + t * rows, n_threads, mode);
     if (rc != SHO_OK) return rc;
   }
   return SHO_OK;
+}
+
+int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+               size_t nbytes, const float* x, int64_t m, float* y, int n_threads) {
+  return sho_matmul_mode(quant, rows, cols, data, nbytes, x, m, y, n_threads, SHO_Q6K_SCALE_U8);
 }
 
 int sho_quantize_q8(const float* x, size_t n, int8_t* q, float* scales,

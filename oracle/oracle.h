@@ -97,6 +97,11 @@ int sho_gemv_threads(uint32_t quant, int64_t rows, int64_t cols,
 int sho_expert_gemv(uint32_t quant, int64_t n_expert, int64_t rows,
                     int64_t cols, const uint8_t* data, size_t nbytes,
                     int64_t e, const float* x, float* y);
+/* The same under either reading of a two-reading format (as
+ * sho_dequantize_row_mode). */
+int sho_expert_gemv_mode(uint32_t quant, int64_t n_expert, int64_t rows,
+                         int64_t cols, const uint8_t* data, size_t nbytes,
+                         int64_t e, const float* x, float* y, int mode);
 
 float sho_silu(float x);
 float sho_sigmoid(float x);
@@ -138,11 +143,24 @@ int sho_moe_routed_o(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant
 int sho_moe_layer_o(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
                     int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
                     float* out, int out_major);
+/* The same with each tensor's reading (modes[3] for gate, up, down; modes[8]
+ * in the order of q for the layer; NULL: all 0). */
+int sho_moe_routed_m(uint32_t gate_quant, uint32_t up_quant, uint32_t down_quant,
+                     int64_t n_expert, int64_t n_embd, int64_t n_ff,
+                     const uint8_t* gate, size_t gate_bytes, const uint8_t* up,
+                     size_t up_bytes, const uint8_t* down, size_t down_bytes,
+                     const int64_t* ids, const float* weights, int64_t k,
+                     const float* x, float* out, int out_major, const int* modes);
+int sho_moe_layer_m(const uint32_t* q, const uint8_t* const* t, const size_t* nb, int64_t n_expert,
+                    int64_t n_embd, int64_t n_ff, int64_t n_ff_sh, int64_t top_k, const float* x,
+                    float* out, int out_major, const int* modes);
 
 /* y[t][r] = gemv(W, x[t]) for t < m: m independent sho_gemv calls, each
  * row-parallel over n_threads (bit-identical to the sequential loop). */
 int sho_matmul(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
                size_t nbytes, const float* x, int64_t m, float* y, int n_threads);
+int sho_matmul_mode(uint32_t quant, int64_t rows, int64_t cols, const uint8_t* data,
+                    size_t nbytes, const float* x, int64_t m, float* y, int n_threads, int mode);
 
 /* Activation blocks of 32 (n % 32 == 0): s = max|x| / 127 (f32 division),
  * q = rint(x / s) (round to nearest even; 0 when s == 0), sums[b] =

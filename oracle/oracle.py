@@ -60,6 +60,17 @@ def lib() -> C.CDLL:
                                        C.c_int]
         L.sho_expert_gemv.argtypes = [C.c_uint32, C.c_int64, C.c_int64, C.c_int64, u8p, C.c_size_t,
                                       C.c_int64, f32p, f32p]
+        L.sho_expert_gemv_mode.argtypes = [C.c_uint32, C.c_int64, C.c_int64, C.c_int64, u8p, C.c_size_t,
+                                           C.c_int64, f32p, f32p, C.c_int]
+        ip = C.POINTER(C.c_int)
+        L.sho_moe_routed_m.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int64, C.c_int64,
+                                       C.c_int64, u8p, C.c_size_t, u8p, C.c_size_t, u8p, C.c_size_t,
+                                       i64p, f32p, C.c_int64, f32p, f32p, C.c_int, ip]
+        L.sho_moe_layer_m.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t),
+                                      C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, f32p, f32p, C.c_int,
+                                      ip]
+        L.sho_matmul_mode.argtypes = [C.c_uint32, C.c_int64, C.c_int64, u8p, C.c_size_t, f32p, C.c_int64,
+                                      f32p, C.c_int, C.c_int]
         L.sho_silu.argtypes = [C.c_float]
         L.sho_silu.restype = C.c_float
         L.sho_moe_route.argtypes = [f32p, C.c_int64, C.c_int64, i64p, f32p]
@@ -183,12 +194,15 @@ def gemv(quant: int, rows: int, cols: int, data, x, scale_mode: int = SCALE_U8,
     return y
 
 
-def expert_gemv(quant: int, n_expert: int, rows: int, cols: int, data, e: int, x) -> np.ndarray:
+def expert_gemv(quant: int, n_expert: int, rows: int, cols: int, data, e: int, x,
+                mode: int = 0) -> np.ndarray:
+    """``mode``: the reading of a two-reading format (Q6_K scales, IQ4_XS
+    code bytes), as ``dequantize``'s."""
     b, xv = _u8(data), _f32(x)
     assert xv.size == rows
     y = np.empty(cols, dtype=np.float32)
-    _check(lib().sho_expert_gemv(quant, n_expert, rows, cols, _ptr(b), b.nbytes, e, _ptr(xv), _ptr(y)),
-           "expert_gemv")
+    _check(lib().sho_expert_gemv_mode(quant, n_expert, rows, cols, _ptr(b), b.nbytes, e, _ptr(xv), _ptr(y),
+                                      mode), "expert_gemv")
     return y
 
 
@@ -205,17 +219,19 @@ def moe_route(logits, top_k: int) -> tuple[np.ndarray, np.ndarray]:
 
 
 def moe_routed(gate_q: int, up_q: int, down_q: int, n_expert: int, n_embd: int, n_ff: int,
-               gate, up, down, ids, weights, x, out_major: bool = False) -> np.ndarray:
+               gate, up, down, ids, weights, x, out_major: bool = False, modes=(0, 0, 0)) -> np.ndarray:
     """The routed experts of one token; ``out_major``: the stacks are
     llama.cpp's [n_expert][out][in] (each expert an ops::gemv of its slice)
-    instead of the reference's [n_expert][in][out]."""
+    instead of the reference's [n_expert][in][out]; ``modes``: the readings
+    of gate, up and down."""
     g, u, d = _u8(gate), _u8(up), _u8(down)
     idv = np.ascontiguousarray(ids, dtype=np.int64)
     wv, xv = _f32(weights), _f32(x)
     out = np.empty(n_embd, dtype=np.float32)
-    _check(lib().sho_moe_routed_o(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
+    md = (C.c_int * 3)(*[int(v) for v in modes])
+    _check(lib().sho_moe_routed_m(gate_q, up_q, down_q, n_expert, n_embd, n_ff, _ptr(g), g.nbytes,
                                   _ptr(u), u.nbytes, _ptr(d), d.nbytes, _ptr(idv), _ptr(wv), idv.size,
-                                  _ptr(xv), _ptr(out), int(out_major)), "moe_routed")
+                                  _ptr(xv), _ptr(out), int(out_major), md), "moe_routed")
     return out
 
 
@@ -278,11 +294,11 @@ def add(a, b) -> np.ndarray:
 
 
 def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: int, x, top_k: int,
-              out_major: bool = False) -> np.ndarray:
+              out_major: bool = False, modes=(0,) * 8) -> np.ndarray:
     """The whole MoE layer for one token (moe.rs:48-143): router matvec on
     bf16(x), route, routed experts, then the shared expert added with its
-    sigmoid gate. quants / tensors: router, gate, up, down, gate_sh, up_sh,
-    down_sh, gate_inp."""
+    sigmoid gate. quants / tensors / modes (readings): router, gate, up,
+    down, gate_sh, up_sh, down_sh, gate_inp."""
     bufs = [_u8(t) for t in tensors]
     xv = _f32(x)
     assert xv.size == n_embd and len(bufs) == 8
@@ -290,18 +306,21 @@ def moe_layer(quants, tensors, n_expert: int, n_embd: int, n_ff: int, n_ff_sh: i
     q = (C.c_uint32 * 8)(*[int(v) for v in quants])
     tp = (C.c_void_p * 8)(*[_ptr(b) for b in bufs])
     nb = (C.c_size_t * 8)(*[b.nbytes for b in bufs])
-    _check(lib().sho_moe_layer_o(q, tp, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, _ptr(xv), _ptr(out),
-                                 int(out_major)), "moe_layer")
+    md = (C.c_int * 8)(*[int(v) for v in modes])
+    _check(lib().sho_moe_layer_m(q, tp, nb, n_expert, n_embd, n_ff, n_ff_sh, top_k, _ptr(xv), _ptr(out),
+                                 int(out_major), md), "moe_layer")
     return out
 
 
-def matmul(quant: int, rows: int, cols: int, data, x, threads: int = 1) -> np.ndarray:
-    """y[t] = gemv(W, x[t]) for every row t of x ([m][cols] -> [m][rows])."""
+def matmul(quant: int, rows: int, cols: int, data, x, threads: int = 1, mode: int = 0) -> np.ndarray:
+    """y[t] = gemv(W, x[t]) for every row t of x ([m][cols] -> [m][rows])
+    under reading ``mode``."""
     b, xv = _u8(data), _f32(x)
     m = xv.size // cols
     assert xv.size == m * cols
     y = np.empty((m, rows), dtype=np.float32)
-    _check(lib().sho_matmul(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), m, _ptr(y), threads), "matmul")
+    _check(lib().sho_matmul_mode(quant, rows, cols, _ptr(b), b.nbytes, _ptr(xv), m, _ptr(y), threads, mode),
+           "matmul")
     return y
 
 

@@ -958,7 +958,8 @@ int sh_moe_ffn_dev(const sh_expert_dev* gate, const sh_expert_dev* up, const sh_
     return fail(SH_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   for (const sh_expert_dev* t : {gate, up, down})
     if ((reinterpret_cast<uintptr_t>(t->data) & 1u) ||
-        (t->quant == SH_QUANT_Q8_0 && (reinterpret_cast<uintptr_t>(t->data) & 3u)))
+        ((t->quant == SH_QUANT_Q8_0 || t->quant == SH_QUANT_IQ4_XS) &&
+         (reinterpret_cast<uintptr_t>(t->data) & 3u)))
       return fail(SH_ERR_INVALID_ARGUMENT, "misaligned expert tensor");
   HIP_TRY(sh::launch_moe(plan, gate->quant, up->quant, down->quant, gate->data, up->data, down->data,
                          reading(gate->quant, gate->flags),

@@ -1,7 +1,7 @@
 // Per-unit "axpy" of one packed row into column sums, for the expert
 // (in-major) matvec and the MoE FFN: a thread owns one 64-column unit (one
-// Q4_K / Q5_K group, one Q6_K quarter, or a pair of Q8_0 blocks -- the units of the
-// matvec kernels) and adds x[i] * W[i][unit columns] for a row i into 64
+// Q4_K / Q5_K / IQ4_XS group, one Q6_K quarter, or a pair of Q8_0 blocks --
+// the units of the matvec kernels) and adds x[i] * W[i][unit columns] for a row i into 64
 // f32 accumulators per token. Block scales are folded into one coefficient
 // per sub-block and token (x[i] * d * sc); the constant parts of the codes
 // (Q4_K min, Q6_K -32, Q8_0 +128 bias) are summed per sub-block in `off` and
@@ -273,6 +273,67 @@ struct AxQ6K {
   __device__ static __forceinline__ int off_index(int e) { return e >> 4; }
 };
 
+// IQ4_XS: unit u is group g = u & 3 of super-block u >> 2 (136 bytes), the
+// 32-element sub-blocks 2g and 2g + 1. Element i of sub-block ib takes the
+// code-book value of the low (i < 16) or high nibble of qs byte i % 16; the
+// sub-block's 16 qs bytes are qs[0..16] in the reference's reading (its
+// slice is never advanced, dequant.rs:189-206) and qs[16 ib ..] in ggml's
+// (GGML). Scale d * (ls - 32). The signed codes are biased to v + 128 for
+// the unsigned conversion, 128 * coefficient going to the offset (as Q8_0).
+template <bool GGML>
+struct AxIQ4XS {
+  static constexpr int kOff = 2;
+  struct Raw {
+    uint32_t h0, h1;  // d | scales_h, scales_l
+    u32x4 a, b;       // the qs bytes of sub-blocks 2g and 2g + 1
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int u) {
+    const uint8_t* sb = row + (u >> 2) * 136;
+    const int g = u & 3;
+    return {ld4(sb), ld4(sb + 4), ld16u(sb + 8 + (GGML ? 32 * g : 0)), ld16u(sb + 8 + (GGML ? 32 * g + 16 : 0))};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void axpy(const uint8_t* row, int u, const float* xi,
+                                              float (*acc)[64], float (*off)[kOff], int q6s) {
+    apply<NT>(load(row, u), u, xi, acc, off, q6s);
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int u, const float* xi, float (*acc)[64],
+                                               float (*off)[kOff], int) {
+    const int g = u & 3;
+    const float d = h2f(r.h0);
+    const float dl0 = d * iq4xs_scale(r.h0, r.h1, 2 * g), dl1 = d * iq4xs_scale(r.h0, r.h1, 2 * g + 1);
+    const uint32_t qa[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, qb[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    float wv[64];  // v + 128
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t v[4] = {iq4_lut(qa[k] & 0x0F0F0F0Fu) ^ 0x80808080u,
+                             iq4_lut((qa[k] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u,
+                             iq4_lut(qb[k] & 0x0F0F0F0Fu) ^ 0x80808080u,
+                             iq4_lut((qb[k] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // columns 16 q + 4 k ..
+        wv[16 * q + 4 * k + 0] = ubyte<0>(v[q]);
+        wv[16 * q + 4 * k + 1] = ubyte<1>(v[q]);
+        wv[16 * q + 4 * k + 2] = ubyte<2>(v[q]);
+        wv[16 * q + 4 * k + 3] = ubyte<3>(v[q]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (xi[t] == 0.f) continue;  // ops.rs:182-184
+      const float c0 = xi[t] * dl0, c1 = xi[t] * dl1;
+      off[t][0] += 128.f * c0;
+      off[t][1] += 128.f * c1;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) acc[t][e] = __builtin_fmaf(c0, wv[e], acc[t][e]);
+#pragma unroll
+      for (int e = 32; e < 64; ++e) acc[t][e] = __builtin_fmaf(c1, wv[e], acc[t][e]);
+    }
+  }
+  __device__ static __forceinline__ int off_index(int e) { return e >> 5; }
+};
+
 // ------------------------------------------------------- half units --
 // The same axpy for 32-column half units (one Q4_K sub-block, one Q8_0
 // block, half a Q6_K quarter), with the codes decoded four at a time next to
@@ -495,6 +556,47 @@ struct HxQ6K {
     }
   }
   __device__ static __forceinline__ int off_index(int e) { return e >> 4; }
+};
+
+// IQ4_XS: half unit hu is sub-block ib = hu & 7 of super-block hu >> 3, its
+// 16 qs bytes read as AxIQ4XS (columns 0-15 the low nibbles, 16-31 the high).
+template <bool GGML>
+struct HxIQ4XS {
+  static constexpr int kOff = 1;
+  struct Raw {
+    uint32_t h0, h1;
+    u32x4 a;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int hu) {
+    const uint8_t* sb = row + (hu >> 3) * 136;
+    return {ld4(sb), ld4(sb + 4), ld16u(sb + 8 + (GGML ? 16 * (hu & 7) : 0))};
+  }
+  template <int NT>
+  __device__ static __forceinline__ void apply(const Raw& r, int hu, const float* xi, float (*acc)[32],
+                                               float (*off)[kOff], int) {
+    const float dl = h2f(r.h0) * iq4xs_scale(r.h0, r.h1, hu & 7);
+    const uint32_t q[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    float c[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      c[t] = xi[t] == 0.f ? 0.f : xi[t] * dl;  // ops.rs:182-184
+      off[t][0] += 128.f * c[t];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t idx = k < 4 ? (q[k] & 0x0F0F0F0Fu) : ((q[k - 4] >> 4) & 0x0F0F0F0Fu);
+      const uint32_t v = iq4_lut(idx) ^ 0x80808080u;  // v + 128
+      const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][4 * k + 0] = __builtin_fmaf(c[t], w0, acc[t][4 * k + 0]);
+        acc[t][4 * k + 1] = __builtin_fmaf(c[t], w1, acc[t][4 * k + 1]);
+        acc[t][4 * k + 2] = __builtin_fmaf(c[t], w2, acc[t][4 * k + 2]);
+        acc[t][4 * k + 3] = __builtin_fmaf(c[t], w3, acc[t][4 * k + 3]);
+      }
+    }
+  }
+  __device__ static __forceinline__ int off_index(int) { return 0; }
 };
 
 }  // namespace sh

@@ -53,17 +53,37 @@ inline int64_t byte_size(uint32_t q, int64_t n) {
 }
 
 // The quantized types every kernel family takes (matvec, expert, MoE, matmul).
-inline bool device_quant(uint32_t q) { return q == kQ8_0 || q == kQ4_K || q == kQ5_K || q == kQ6_K; }
+inline bool device_quant(uint32_t q) {
+  return q == kQ8_0 || q == kQ4_K || q == kQ5_K || q == kQ6_K || q == kIQ4_XS;
+}
 // Plain-float element types: matvec (f64 sums) and dequant only.
 inline bool plain_quant(uint32_t q) { return q == kF32 || q == kF16 || q == kBF16; }
-// Types the matvec (and dequant) kernels take beyond device_quant: IQ4_XS
-// has a matvec of its own but no expert, MoE or matmul kernel.
-inline bool gemv_quant(uint32_t q) { return device_quant(q) || q == kIQ4_XS; }
+// Types the matvec (and dequant) kernels take: the quantized ones.
+inline bool gemv_quant(uint32_t q) { return device_quant(q); }
 
 // The IQ4_NL / IQ4_XS code book: 4-bit index -> int8 value (a format
 // table: ggml's kvalues_iq4nl, crates/strata-gguf/src/tables.rs:2052-2054),
 // packed little-endian four to a word.
 constexpr uint32_t kIq4Tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+
+// Four nibble indices (one per byte) -> the four int8 code-book values.
+__device__ __forceinline__ uint32_t iq4_lut(uint32_t idx) {
+  const uint32_t i7 = idx & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kIq4Tab[1], kIq4Tab[0], i7);
+  const uint32_t hi = __builtin_amdgcn_perm(kIq4Tab[3], kIq4Tab[2], i7);
+  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
+
+// IQ4_XS super-block header (bytes 0..7: d f16, scales_h u16, scales_l[4]):
+// the 6-bit scale of sub-block ib is the nibble ib % 2 of scales_l[ib / 2]
+// and bits 2 ib, 2 ib + 1 of scales_h (dequant.rs:189-206); h0 holds bytes
+// 0..3, h1 bytes 4..7. Returns ls - 32.
+__device__ __forceinline__ float iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
+  const uint32_t lo = (h1 >> (4 * ib)) & 0x0Fu;  // nibble ib % 2 of byte ib / 2 = nibble ib of h1
+  const uint32_t hi = (h0 >> (16 + 2 * ib)) & 3u;
+  return float(lo | (hi << 4)) - 32.f;
+}
 
 constexpr int kWave = 64;
 

@@ -101,7 +101,7 @@ hipError_t launch_expert_gemv(uint32_t quant, const void* wv, int64_t rows, int6
                               hipStream_t stream) {
   if (!expert_shape_ok(quant, rows, cols)) return hipErrorInvalidValue;
   const uint8_t* w = static_cast<const uint8_t*>(wv);
-  if (quant == kQ8_0 && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
+  if ((quant == kQ8_0 || quant == kIQ4_XS) && (reinterpret_cast<uintptr_t>(w) & 3u)) return hipErrorInvalidValue;
   const int64_t row_bytes = byte_size(quant, cols);
   const int n_chunks = expert_chunks(rows, cols);
   const int chunk = int((rows + n_chunks - 1) / n_chunks);
@@ -121,9 +121,20 @@ hipError_t launch_expert_gemv(uint32_t quant, const void* wv, int64_t rows, int6
       hipLaunchKernelGGL(expert_partial_kernel<AxQ8>, dim3(n_chunks), dim3(kExpertThreads), lds,
                          stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
       break;
-    default:  // kQ6_K
+    case kIQ4_XS:  // the reading (reference or ggml qs bytes) is a template argument
+      if (q6_signed)
+        hipLaunchKernelGGL(expert_partial_kernel<AxIQ4XS<true>>, dim3(n_chunks), dim3(kExpertThreads), lds,
+                           stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
+      else
+        hipLaunchKernelGGL(expert_partial_kernel<AxIQ4XS<false>>, dim3(n_chunks), dim3(kExpertThreads), lds,
+                           stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
+      break;
+    case kQ6_K:
       hipLaunchKernelGGL(expert_partial_kernel<AxQ6K>, dim3(n_chunks), dim3(kExpertThreads), lds,
                          stream, w, int(rows), int(cols), row_bytes, chunk, x, workspace, q6_signed);
+      break;
+    default:
+      return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -279,4 +279,59 @@ struct FmtQ6K {
   }
 };
 
+// ---------------------------------------------------------------- IQ4_XS --
+// Unit u of a row: super-block u/4 (136 bytes), group g = u%4 = sub-blocks
+// 2g and 2g + 1, the qs bytes as AxIQ4XS reads them (the reference's
+// qs[0..16] for every sub-block, or ggml's qs[16 ib ..] with GGML). The
+// signed code-book values are biased to v + 128 (as FmtQ8).
+template <bool GGML>
+struct FmtIQ4XS {
+  static constexpr int kR = 2;
+  static constexpr int kRing = 3;
+  struct Load {
+    uint32_t h0, h1;
+    u32x4 a, b;
+  };
+  __device__ static __forceinline__ void load(const uint8_t* row, int u, Load& o) {
+    const uint8_t* sb = row + (u >> 2) * 136;
+    const int g = u & 3;
+    o.h0 = ld4(sb);
+    o.h1 = ld4(sb + 4);
+    o.a = ld16u(sb + 8 + (GGML ? 32 * g : 0));
+    o.b = ld16u(sb + 8 + (GGML ? 32 * g + 16 : 0));
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XSlice& x, int u, int) {
+    const int g = u & 3;
+    const uint32_t qa[4] = {L.a.x, L.a.y, L.a.z, L.a.w}, qb[4] = {L.b.x, L.b.y, L.b.z, L.b.w};
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;  // columns 0-15, 16-31, 32-47, 48-63
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t v0 = iq4_lut(qa[k] & 0x0F0F0F0Fu) ^ 0x80808080u;
+      const uint32_t v1 = iq4_lut((qa[k] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u;
+      const uint32_t v2 = iq4_lut(qb[k] & 0x0F0F0F0Fu) ^ 0x80808080u;
+      const uint32_t v3 = iq4_lut((qb[k] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u;
+      const f32x4 x0 = x.v[k], x1 = x.v[4 + k], x2 = x.v[8 + k], x3 = x.v[12 + k];
+      s0 = __builtin_fmaf(ubyte<0>(v0), x0.x, s0);
+      s0 = __builtin_fmaf(ubyte<1>(v0), x0.y, s0);
+      s0 = __builtin_fmaf(ubyte<2>(v0), x0.z, s0);
+      s0 = __builtin_fmaf(ubyte<3>(v0), x0.w, s0);
+      s1 = __builtin_fmaf(ubyte<0>(v1), x1.x, s1);
+      s1 = __builtin_fmaf(ubyte<1>(v1), x1.y, s1);
+      s1 = __builtin_fmaf(ubyte<2>(v1), x1.z, s1);
+      s1 = __builtin_fmaf(ubyte<3>(v1), x1.w, s1);
+      s2 = __builtin_fmaf(ubyte<0>(v2), x2.x, s2);
+      s2 = __builtin_fmaf(ubyte<1>(v2), x2.y, s2);
+      s2 = __builtin_fmaf(ubyte<2>(v2), x2.z, s2);
+      s2 = __builtin_fmaf(ubyte<3>(v2), x2.w, s2);
+      s3 = __builtin_fmaf(ubyte<0>(v3), x3.x, s3);
+      s3 = __builtin_fmaf(ubyte<1>(v3), x3.y, s3);
+      s3 = __builtin_fmaf(ubyte<2>(v3), x3.z, s3);
+      s3 = __builtin_fmaf(ubyte<3>(v3), x3.w, s3);
+    }
+    const float d = h2f(L.h0);
+    const float dl0 = d * iq4xs_scale(L.h0, L.h1, 2 * g), dl1 = d * iq4xs_scale(L.h0, L.h1, 2 * g + 1);
+    return dl0 * ((s0 + s1) - 128.f * (x.s.x + x.s.y)) + dl1 * ((s2 + s3) - 128.f * (x.s.z + x.s.w));
+  }
+};
+
 }  // namespace sh

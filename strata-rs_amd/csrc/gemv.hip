@@ -801,16 +801,17 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
         e = nb == 1 ? launch_limb<LimbQ5K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
                     : launch_nb<FmtQ5K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
-      case kIQ4_XS:  // batch-1 launches, one vector each
-        e = hipSuccess;
-        for (int b = 0; b < nb && e == hipSuccess; ++b)
-          e = q6_signed ? launch_limb<LimbIQ4XS<true>, 1, 4>(w, int(rows), int(cols), row_bytes, xb + int64_t(b) * cols,
-                                                             yb + int64_t(b) * rows, stream, 512, wpc)
-                        : launch_limb<LimbIQ4XS<false>, 1, 4>(w, int(rows), int(cols), row_bytes,
-                                                              xb + int64_t(b) * cols, yb + int64_t(b) * rows, stream,
-                                                              512, wpc);
+      case kIQ4_XS:  // the reading (reference or ggml qs bytes) is a template argument
+        if (q6_signed)
+          e = nb == 1 ? launch_limb<LimbIQ4XS<true>, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512,
+                                                            wpc)
+                      : launch_nb<FmtIQ4XS<true>>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
+        else
+          e = nb == 1 ? launch_limb<LimbIQ4XS<false>, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512,
+                                                             wpc)
+                      : launch_nb<FmtIQ4XS<false>>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
-      default:
+      default:  // kQ6_K
         e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,
                                                   q6_signed)
                     : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);

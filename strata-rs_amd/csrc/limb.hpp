@@ -286,14 +286,6 @@ struct LimbQ8 {
 // the 6-bit ls. GGML: ggml's layout (sub-block ib reads qs[16 ib ..]); the
 // default follows the reference, whose every sub-block reads qs[0..16]
 // (dequant.rs:189-206).
-__device__ __forceinline__ uint32_t iq4_lut(uint32_t idx) {  // four nibble indices -> four int8 codes
-  const uint32_t i7 = idx & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(kIq4Tab[1], kIq4Tab[0], i7);
-  const uint32_t hi = __builtin_amdgcn_perm(kIq4Tab[3], kIq4Tab[2], i7);
-  const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
-  return (hi & m) | (lo & ~m);
-}
-
 template <bool GGML>
 struct LimbIQ4XS {
   static constexpr uint32_t kQuant = kIQ4_XS;

@@ -1,5 +1,6 @@
 // Batched prefill matmul on MFMA: Y[t][r] = sum_c W[r][c] * X[t][c] for m
-// tokens, W packed Q4_K / Q5_K / Q8_0 / Q6_K [rows][cols], X and Y f32 row-major.
+// tokens, W packed Q4_K / Q5_K / Q8_0 / Q6_K / IQ4_XS [rows][cols], X and Y
+// f32 row-major.
 //
 // The reference has no matmul: prefill runs one forward per token
 // (crates/strata-core/src/generate.rs:116-117), so the op is defined as m
@@ -333,6 +334,64 @@ struct StQ8 {
     // both runs are block hb
     jb0 = jb1 = hb;
     dj[0] = dj[1] = d;
+    mj[0] = mj[1] = 0.f;
+    o0 = 32 * hb;
+    o1 = 32 * hb + 16;
+  }
+};
+
+// IQ4_XS: chunk c is sub-blocks 2g and 2g + 1 (g = c % 4) of super-block
+// c / 4 (136 bytes); piece hb is sub-block 2g + hb, whose 16 qs bytes (the
+// reference's qs[0..16], or ggml's qs[16 ib ..] with GGML; dequant.rs:189-206)
+// give elements [32 hb, +16) from their low nibbles and [32 hb + 16, +16)
+// from their high ones: code-book values v (int8) scaled by dl = d * (ls - 32).
+template <bool GGML>
+struct StIQ4XS {
+  static constexpr int kPieces = 2;
+  static constexpr bool kQ8 = true;
+  static constexpr bool kQ8K = false;  // 32-element activation blocks, as its own scales
+  static constexpr bool kMin = false;  // value dl * v
+  struct Raw {
+    uint32_t h0, h1;
+    u32x4 q;
+  };
+  __device__ static __forceinline__ Raw load(const uint8_t* row, int c, int hb) {
+    const uint8_t* sb = row + (c >> 2) * 136;
+    const int ib = 2 * (c & 3) + hb;
+    return {ld4(sb), ld4(sb + 4), ld16u(sb + 8 + (GGML ? 16 * ib : 0))};
+  }
+  __device__ static __forceinline__ float scale(const Raw& r, int c, int hb) {
+    return h2f(r.h0) * iq4xs_scale(r.h0, r.h1, 2 * (c & 3) + hb);
+  }
+  __device__ static __forceinline__ void emit_bf16(const Raw& r, int c, int hb, uint32_t* run0,
+                                                   uint32_t* run1, int& o0, int& o1, int) {
+    const float dl = scale(r, c, hb);
+    const float bias = -128.f * dl;  // dl * ((v ^ 0x80) - 128) = dl * v, one rounding
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = iq4_lut(q[k] & 0x0F0F0F0Fu) ^ 0x80808080u;
+      const uint32_t hi = iq4_lut((q[k] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u;
+      run0[2 * k] = pack_bf16(__builtin_fmaf(dl, ubyte<0>(lo), bias), __builtin_fmaf(dl, ubyte<1>(lo), bias));
+      run0[2 * k + 1] = pack_bf16(__builtin_fmaf(dl, ubyte<2>(lo), bias), __builtin_fmaf(dl, ubyte<3>(lo), bias));
+      run1[2 * k] = pack_bf16(__builtin_fmaf(dl, ubyte<0>(hi), bias), __builtin_fmaf(dl, ubyte<1>(hi), bias));
+      run1[2 * k + 1] = pack_bf16(__builtin_fmaf(dl, ubyte<2>(hi), bias), __builtin_fmaf(dl, ubyte<3>(hi), bias));
+    }
+    o0 = 32 * hb;
+    o1 = 32 * hb + 16;
+  }
+  // int8 codes: the code-book values themselves; both runs are block hb
+  __device__ static __forceinline__ void emit_q8(const Raw& r, int c, int hb, uint32_t* run0,
+                                                 uint32_t* run1, int& o0, int& o1, int& jb0, int& jb1,
+                                                 float* dj, float* mj) {
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      run0[k] = iq4_lut(q[k] & 0x0F0F0F0Fu);
+      run1[k] = iq4_lut((q[k] >> 4) & 0x0F0F0F0Fu);
+    }
+    jb0 = jb1 = hb;
+    dj[0] = dj[1] = scale(r, c, hb);
     mj[0] = mj[1] = 0.f;
     o0 = 32 * hb;
     o1 = 32 * hb + 16;
@@ -1455,7 +1514,12 @@ hipError_t launch_matmul(uint32_t quant, const void* wv, int64_t rows, int64_t c
     case kQ4_K: launch_mm<StQ4K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
     case kQ5_K: launch_mm<StQ5K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
     case kQ8_0: launch_mm<StQ8>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
-    default: launch_mm<StQ6K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s);
+    case kQ6_K: launch_mm<StQ6K>(mode, w, int(rows), int(cols), rb, ws, int(m), y, q6_signed, s); break;
+    case kIQ4_XS:  // the reading (reference or ggml qs bytes) is a template argument
+      if (q6_signed) launch_mm<StIQ4XS<true>>(mode, w, int(rows), int(cols), rb, ws, int(m), y, 0, s);
+      else launch_mm<StIQ4XS<false>>(mode, w, int(rows), int(cols), rb, ws, int(m), y, 0, s);
+      break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

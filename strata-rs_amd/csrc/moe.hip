@@ -642,6 +642,7 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       const float* logits, const float* x, float* out, void* workspace,
                       hipStream_t s, const MoeShared* shared) {
   if (qg != qu) return hipErrorInvalidValue;  // gate and up share one kernel
+  if (qg == kIQ4_XS && (q6g != 0) != (q6u != 0)) return hipErrorInvalidValue;  // and one IQ4_XS reading
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   // one token (decode): gate/up routes it itself; otherwise the route kernel
   // groups every token's pairs by expert first
@@ -657,13 +658,19 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
       case kQ4_K: launch_gateup<HxQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
       case kQ5_K: launch_gateup<HxQ5K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
       case kQ8_0: launch_gateup<HxQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
-      default: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);  // kQ6_K
+      case kQ6_K: launch_gateup<HxQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+      default:  // kIQ4_XS: gate and up of one reading (checked by the caller)
+        if (q6g) launch_gateup<HxIQ4XS<true>>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
+        else launch_gateup<HxIQ4XS<false>>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
     }
     switch (qd) {
       case kQ4_K: launch_down<HxQ4K>(p, down, ws, q6d, s); break;
       case kQ5_K: launch_down<HxQ5K>(p, down, ws, q6d, s); break;
       case kQ8_0: launch_down<HxQ8>(p, down, ws, q6d, s); break;
-      default: launch_down<HxQ6K>(p, down, ws, q6d, s);  // kQ6_K
+      case kQ6_K: launch_down<HxQ6K>(p, down, ws, q6d, s); break;
+      default:  // kIQ4_XS
+        if (q6d) launch_down<HxIQ4XS<true>>(p, down, ws, q6d, s);
+        else launch_down<HxIQ4XS<false>>(p, down, ws, q6d, s);
     }
   }
   if (shared && shared->join) {

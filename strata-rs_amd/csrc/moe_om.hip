@@ -44,9 +44,13 @@ namespace sh {
 constexpr int kOmThreads = 256;
 constexpr int kOmWaves = kOmThreads / kWave;
 
-// Q8_0 rows take limb activations; the k-quants f32 ones.
+// Q8_0 and IQ4_XS rows (signed codes) take limb activations; the k-quants
+// f32 ones.
 template <class F>
-constexpr bool limb_x() { return std::is_same<F, LimbQ8>::value; }
+constexpr bool limb_x() {
+  return std::is_same<F, LimbQ8>::value || std::is_same<F, LimbIQ4XS<false>>::value ||
+         std::is_same<F, LimbIQ4XS<true>>::value;
+}
 
 // LDS bytes of one staged vector of `cols` values (either representation).
 __host__ __device__ inline int om_vec_bytes(int cols) {
@@ -98,13 +102,18 @@ struct OmX {
     load_xslice(reinterpret_cast<const float*>(lds), cols, u, o);
   }
 };
-template <>
-struct OmX<LimbQ8> {
+struct OmXLimbs {
   using T = XLimbs;
   __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) {
     load_limbs(lds, cols, u, o);
   }
 };
+template <>
+struct OmX<LimbQ8> : OmXLimbs {};
+template <>
+struct OmX<LimbIQ4XS<false>> : OmXLimbs {};
+template <>
+struct OmX<LimbIQ4XS<true>> : OmXLimbs {};
 
 template <class F>
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, typename F::Load& ld) {
@@ -356,13 +365,19 @@ void launch_moe_out_major(const MoePlan& p, uint32_t qg, uint32_t qd, const void
     case kQ4_K: launch_om_gateup<FmtQ4K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
     case kQ5_K: launch_om_gateup<FmtQ5K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
     case kQ8_0: launch_om_gateup<LimbQ8>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
-    default: launch_om_gateup<FmtQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);  // kQ6_K
+    case kQ6_K: launch_om_gateup<FmtQ6K>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s); break;
+    default:  // kIQ4_XS: gate and up of one reading (checked by the caller)
+      if (q6g) launch_om_gateup<LimbIQ4XS<true>>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
+      else launch_om_gateup<LimbIQ4XS<false>>(p, gate, up, x, ws, q6g, q6u, logits, fused_route, s);
   }
   switch (qd) {
     case kQ4_K: launch_om_down<FmtQ4K>(p, down, ws, q6d, s); break;
     case kQ5_K: launch_om_down<FmtQ5K>(p, down, ws, q6d, s); break;
     case kQ8_0: launch_om_down<LimbQ8>(p, down, ws, q6d, s); break;
-    default: launch_om_down<FmtQ6K>(p, down, ws, q6d, s);  // kQ6_K
+    case kQ6_K: launch_om_down<FmtQ6K>(p, down, ws, q6d, s); break;
+    default:  // kIQ4_XS
+      if (q6d) launch_om_down<LimbIQ4XS<true>>(p, down, ws, q6d, s);
+      else launch_om_down<LimbIQ4XS<false>>(p, down, ws, q6d, s);
   }
 }
 

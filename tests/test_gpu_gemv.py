@@ -166,18 +166,6 @@ def test_gemv_shape_errors(backend):
         backend.gemv(H.QuantTensor("q4_0", 2, 4, 32, q4_0), np.zeros(32, np.float32), np.zeros(4, np.float32))
 
 
-def test_iq4_xs_is_matvec_only(backend):
-    """IQ4_XS rows run on the matvec (and dequant) kernels only: the expert
-    and matmul entry points report the type as unsupported."""
-    say("IQ4_XS outside the matvec")
-    w = S.matrix(23, 3, 2 * 256, 256)
-    with pytest.raises(H.UnsupportedQuantError):
-        backend.expert_gemv(H.ExpertView("iq4e", 23, 2, 256, 256, w), 1, np.zeros(256, np.float32),
-                            np.zeros(256, np.float32))
-    with pytest.raises(H.UnsupportedQuantError):
-        backend.matmul(H.QuantTensor("iq4m", 23, 512, 256, w), np.zeros((4, 256), np.float32))
-
-
 @pytest.mark.parametrize("ggml", [False, True])
 @pytest.mark.parametrize("rows,cols,batch", [(37, 256, 1), (129, 4096, 1), (9, 12288, 1), (4096, 4096, 1),
                                              (33, 8192 + 256, 1), (96, 4096, 3), (64, 12288, 8)])
