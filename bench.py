@@ -53,10 +53,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", choices=("", "headline", "moe", "prefill", "rowops", "ffn", "blaslt",
-                                                    "batched", "decode"),
+                                                    "batched", "decode", "hostslice"),
                     help="'headline': the Q4_K 4096x12288 line only (no extra shapes, no CPU leg); "
                          "'moe' / 'prefill' / 'rowops' / 'ffn' / 'blaslt': that extra alone, 'batched': the "
-                         "batch-8 decode shapes (for profiling; prints its JSON)")
+                         "batch-8 decode shapes (for profiling; prints its JSON), 'hostslice': sh_gemv on host "
+                         "slices")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain elementwise copy of 256 MiB (known bytes) 3 times, "
                          "to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -428,9 +429,12 @@ def cpu_baseline(w, x, rows, cols, seconds):
     t = sorted(times)[2]
     gbs = n_rows * rb / t / 1e9
     nthreads = min(16, os.cpu_count() or 1)  # the box's CPU share per GPU
-    t0 = time.perf_counter()
-    O.gemv(O.Q4_K, rows, cols, w, x, threads=nthreads)
-    t_mt = time.perf_counter() - t0
+    times_mt = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        O.gemv(O.Q4_K, rows, cols, w, x, threads=nthreads)
+        times_mt.append(time.perf_counter() - t0)
+    t_mt = sorted(times_mt)[2]
     return {
         "value": round(gbs, 4),
         "unit": "GB/s",
@@ -440,38 +444,79 @@ def cpu_baseline(w, x, rows, cols, seconds):
                   f"(ops::gemv restated in C: per-row dequant + sequential f64 dot, one thread, "
                   f"as the reference runs)",
         "all_cores": {"value": round(rows * rb / t_mt / 1e9, 4), "cores": nthreads,
-                      "sample": "the whole matrix once, rows split over threads"},
+                      "sample": "the whole matrix, rows split over threads, median of 5"},
         "cpu_model": cpu_model(),
         "nproc": os.cpu_count(),
     }
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it)."""
+    """The host CPU as /proc/cpuinfo names it: model name plus family, model
+    and stepping (the name alone can be as short as "AMD EPYC" under a
+    hypervisor; family 25 is Zen 3/4, 26 Zen 5)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block
+                k, _, v = line.partition(":")
+                info[k.strip()] = v.strip()
     except OSError:
-        pass
-    return None
+        return None
+    name = info.get("model name")
+    if name is None:
+        return None
+    ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(ids)})" if ids else name
+
+
+def launch_sync_floor(torch, H, calls):
+    """One launch of sh_stream_read_dev over 16 bytes (2048 workgroups, one
+    lane of which loads anything) and a synchronisation of its stream, per
+    call: about the round trip any synchronous host-slice call pays on top of
+    its kernels; microseconds."""
+    buf = torch.zeros(4, dtype=torch.int32, device="cuda")
+    out = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream()
+    for _ in range(20):
+        H.stream_read_dev(buf.data_ptr(), 16, out.data_ptr(), st.cuda_stream)
+        st.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        H.stream_read_dev(buf.data_ptr(), 16, out.data_ptr(), st.cuda_stream)
+        st.synchronize()
+    return (time.perf_counter() - t0) / calls * 1e6
 
 
 def host_slice_gemv(H, S, w, x, rows, cols, calls):
-    """The trait drop-in path end to end: sh_gemv on host slices (x copied in
-    through pinned staging, the launch, y read back, a synchronisation) with
-    the weights already resident; microseconds per call."""
+    """The trait drop-in path end to end: sh_gemv on host slices (x copied
+    into mapped pinned staging, a copy kernel to the device, the matvec
+    storing y into the staging, a synchronisation) with the weights already
+    resident; microseconds per call, as (bare C-ABI call with its arguments
+    built once -- what the crate's FFI call pays --, the same through the
+    Python wrapper HipBackend.gemv)."""
+    import ctypes as C
     import numpy as np
     y = np.empty(rows, np.float32)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
     with H.HipBackend(0) as be:
         t = H.QuantTensor("bench.host_slice", S.Q4_K, rows, cols, w)
         for _ in range(10):
-            be.gemv(t, x, y)
+            be.gemv(t, xv, y)
+        wc = t._c()
+        fn, ctx, wp = be._L.sh_gemv, be._ctx, C.byref(wc)
+        xp, yp = xv.ctypes.data, y.ctypes.data
         t0 = time.perf_counter()
         for _ in range(calls):
-            be.gemv(t, x, y)
-        return (time.perf_counter() - t0) / calls * 1e6
+            rc = fn(ctx, wp, xp, cols, yp, rows)
+        bare = (time.perf_counter() - t0) / calls * 1e6
+        H.check(rc)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            be.gemv(t, xv, y)
+        wrapped = (time.perf_counter() - t0) / calls * 1e6
+    return bare, wrapped
 
 
 # type ids: 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K
@@ -567,6 +612,15 @@ def main():
     elif args.only == "blaslt":
         print(json.dumps(bench_blaslt_reference(torch, args.steps)), flush=True)
         return
+    elif args.only == "hostslice":
+        w = S.matrix(S.Q4_K, 0x5EED0002, 4096, 12288)
+        us, wrapped = host_slice_gemv(H, S, w, S.normal_f32(7, 12288), 4096, 12288, args.steps)
+        floor = launch_sync_floor(torch, H, args.steps)
+        print(json.dumps({"host_slice_gemv_q4k_4096x12288_b1": {"us_per_call": round(us, 2),
+                                                                "us_per_call_python_wrapper": round(wrapped, 2),
+                                                                "launch_sync_floor_us": round(floor, 2)}}),
+              flush=True)
+        return
     elif args.only == "prefill":
         wp = S.matrix(S.Q4_K, 0x5EED0000 + S.Q4_K + 12288, 12288, 4096)
         print(json.dumps(bench_prefill(torch, H, S, wp, 12288, 4096, 512, args.steps)), flush=True)
@@ -631,11 +685,17 @@ def main():
         print("[bench] extra elementwise methods", file=sys.stderr, flush=True)
         extra.update(bench_rowops(torch, H, S, 200))
         print("[bench] extra host-slice gemv", file=sys.stderr, flush=True)
-        us = host_slice_gemv(H, S, w, S.normal_f32(7, cols), rows, cols, 200)
+        us, wrapped = host_slice_gemv(H, S, w, S.normal_f32(7, cols), rows, cols, 200)
         extra["host_slice_gemv_q4k_4096x12288_b1"] = {
             "us_per_call": round(us, 2),
-            "note": "sh_gemv on host slices (the ComputeBackend::gemv drop-in): x in through pinned staging, "
-                    "launch, y back, synchronise; weights resident; 200 calls, wall clock"}
+            "us_per_call_python_wrapper": round(wrapped, 2),
+            "launch_sync_floor_us": round(launch_sync_floor(torch, H, 200), 2),
+            "note": "sh_gemv on host slices (the ComputeBackend::gemv drop-in): x copied into mapped pinned "
+                    "staging, a copy kernel in, the matvec storing y into the staging, synchronise; weights "
+                    "resident; 200 calls, wall clock; us_per_call: the bare C-ABI call (arguments built "
+                    "once, as an FFI caller holds them), us_per_call_python_wrapper: through "
+                    "HipBackend.gemv. launch_sync_floor_us: one launch of a near-empty "
+                    "kernel and a stream synchronisation, the round trip under every synchronous call"}
         out["extra"] = extra
 
     if not args.no_cpu:

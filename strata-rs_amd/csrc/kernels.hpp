@@ -182,5 +182,7 @@ hipError_t launch_add_out(float* out, const float* a, const float* b, int64_t n,
 // out[b]; the XOR of out[] is the XOR of all words.
 constexpr int kStreamBlocks = 2048;
 hipError_t launch_stream_read(const void* data, uint64_t nbytes, uint32_t* out, hipStream_t stream);
+// n bytes from src to dst (device memory or mapped pinned host memory).
+hipError_t launch_copy_bytes(const void* src, void* dst, uint64_t n, hipStream_t stream);
 
 }  // namespace sh

@@ -61,10 +61,8 @@ __device__ __forceinline__ uint32_t bytes_minus(uint32_t p, uint32_t k4) {
 constexpr int kMmBM = 256;                  // tokens per workgroup
 constexpr int kMmBN = 96;                   // weight rows per workgroup
 constexpr int kMmKC = 64;                   // K elements per chunk
-constexpr int kMmThreads = 256;
 constexpr int kMmRowB = kMmKC * 2 + 16;     // bytes per bf16 LDS row (padded)
 constexpr int kMmRowQ = kMmKC + 16;         // bytes per int8 LDS row (padded)
-constexpr int kDepth = 4;                   // weight chunks in flight ahead of staging
 
 // Two floats -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {

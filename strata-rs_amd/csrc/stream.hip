@@ -5,6 +5,8 @@
 // pattern measured on MI355X for a 28 MB span), and folds them with XOR so
 // no load is dead; workgroup b writes its fold to out[b]. No reference
 // counterpart.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -30,6 +32,35 @@ hipError_t launch_stream_read(const void* data, uint64_t nbytes, uint32_t* out, 
   if ((reinterpret_cast<uintptr_t>(data) & 15u) || (nbytes & 15u)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(stream_read_kernel, dim3(kStreamBlocks), dim3(256), 0, s, static_cast<const u32x4*>(data),
                      nbytes / 16, out);
+  return hipGetLastError();
+}
+
+// A byte copy for the host-slice entry points: between device memory and
+// the context's mapped pinned staging (device-visible host memory), so a
+// call's small input and output slices move in a kernel's loads and stores
+// instead of a DMA-engine transfer each way. 16-byte accesses when both
+// ends and the length allow, bytes otherwise (unaligned slices are small:
+// routing ids and weights).
+__global__ void __launch_bounds__(256) copy_bytes_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         uint64_t n, int vec) {
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  const uint64_t i0 = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (vec) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src);
+    u32x4* d = reinterpret_cast<u32x4*>(dst);
+    for (uint64_t i = i0; i < n / 16; i += stride) d[i] = s[i];
+  } else {
+    for (uint64_t i = i0; i < n; i += stride) dst[i] = src[i];
+  }
+}
+
+hipError_t launch_copy_bytes(const void* src, void* dst, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | n) & 15u) == 0;
+  const uint64_t items = vec ? n / 16 : n;
+  const uint64_t blocks = std::min<uint64_t>((items + 255) / 256, 1024);
+  hipLaunchKernelGGL(copy_bytes_kernel, dim3(unsigned(blocks)), dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                     static_cast<uint8_t*>(dst), n, int(vec));
   return hipGetLastError();
 }
 
