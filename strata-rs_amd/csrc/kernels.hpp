@@ -79,6 +79,7 @@ hipError_t launch_expert_gemv(uint32_t quant, const void* w, int64_t rows, int64
 constexpr int kMoeMaxExperts = 1024;
 constexpr int kMoeMaxTopK = 32;
 constexpr int kMoeMaxTokens = 256;
+constexpr int kMoeMaxChunks = 32;  // down chunk sums a combine adds per column (in one load round)
 
 struct MoePlan {
   int n_tok, top_k, n_expert, n_embd, n_ff;
@@ -99,6 +100,15 @@ struct MoePlan {
   bool staged;                   // row bytes allow 16-byte tile copies
   bool out_major;                // expert stacks [n_expert][out][in] (moe_om.hip)
   int om_rows_a, om_rows_b;      // out-major: rows per workgroup of gate/up and of down
+  // one token over in-major stacks (moe_one.hip): per phase the 64-column
+  // units of a column block, column blocks, row slots, rows per chunk,
+  // chunks, and threads per column in the row-slot reduction
+  bool one;
+  int a1_cbu, a1_ncb, a1_rs, a1_rc, a1_nrc, a1_tpc;
+  int b1_cbu, b1_ncb, b1_rs, b1_rc, b1_nrc, b1_tpc;
+  size_t o_p1a;                  // [item][2][a1_nrc][n_ff]: gate/up chunk sums
+  size_t o_p1b;                  // [item][b1_nrc][n_embd]: down chunk sums
+  size_t lds1_a, lds1_b;
   size_t bytes;
 };
 
@@ -125,6 +135,18 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
                       const float* logits, const float* x, float* out, void* workspace,
                       hipStream_t s, const MoeShared* shared = nullptr);
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
+// out[t] = sum over t's experts in ascending id with w != 0 of w * (the
+// sum of the pair's nch_b down chunk sums at o_part_b), plus the shared
+// expert's gated output when `shared` is given.
+hipError_t launch_moe_combine(const MoePlan& p, const uint8_t* ws, float* out, const MoeShared* shared,
+                              hipStream_t s);
+// The one-token in-major path (moe_one.hip): fills p's one-token fields
+// and sets p.one when the shape allows it; the launches (gate/up, down,
+// then launch_moe_combine over its sums).
+bool moe_one_plan(MoePlan& p, uint32_t q_gateup, uint32_t q_down);
+hipError_t launch_moe_one(const MoePlan& p, uint32_t qg, uint32_t qd, const void* gate, const void* up,
+                          const void* down, int q6g, int q6u, int q6d, const float* logits, const float* x,
+                          float* out, void* workspace, bool fused_route, hipStream_t s, const MoeShared* shared);
 
 // The whole MoE layer (router matvec on bf16-rounded x, routed experts,
 // shared expert with its sigmoid gate): the routed plan plus the layer's

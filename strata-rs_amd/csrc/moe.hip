@@ -45,7 +45,6 @@
 namespace sh {
 
 constexpr int kMoeThreads = 256;
-constexpr int kMoeMaxChunks = 32;    // row chunks per matrix (their sums are added in one load round)
 constexpr int kRouteThreads = 1024;  // one thread per expert in the grouping scan
 static_assert(kRouteThreads == kMoeMaxExperts, "the scan gives each thread one expert");
 
@@ -599,6 +598,11 @@ bool moe_plan(int n_tok, int top_k, int n_expert, int n_embd, int n_ff, uint32_t
   p.o_tokpair = take(sizeof(int) * pairs);
   p.o_part_a = take(sizeof(float) * size_t(pairs) * 2 * p.nch_a * n_ff);
   p.o_part_b = take(sizeof(float) * size_t(pairs) * p.nch_b * n_embd);
+  // one token: the moe_one.hip launches and their sums instead
+  if (moe_one_plan(p, qa, qb)) {
+    p.o_p1a = take(sizeof(float) * size_t(top_k) * 2 * p.a1_nrc * n_ff);
+    p.o_p1b = take(sizeof(float) * size_t(top_k) * p.b1_nrc * n_embd);
+  }
   p.bytes = o;
   *plan = p;
   return true;
@@ -651,6 +655,11 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
     hipError_t e = launch_moe_route(p, logits, workspace, s);
     if (e != hipSuccess) return e;
   }
+  if (p.one) {
+    // gate/up, down, then the combine (with the shared expert's add)
+    return launch_moe_one(p, qg, qd, gate, up, down, q6g, q6u, q6d, logits, x, out, workspace, fused_route, s,
+                          shared);
+  }
   if (p.out_major) {
     launch_moe_out_major(p, qg, qd, gate, up, down, q6g, q6u, q6d, logits, x, workspace, fused_route, s);
   } else {
@@ -673,6 +682,11 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
         else launch_down<HxIQ4XS<false>>(p, down, ws, q6d, s);
     }
   }
+  return launch_moe_combine(p, ws, out, shared, s);
+}
+
+hipError_t launch_moe_combine(const MoePlan& p, const uint8_t* ws, float* out, const MoeShared* shared,
+                              hipStream_t s) {
   if (shared && shared->join) {
     const hipError_t e = hipStreamWaitEvent(s, shared->join, 0);
     if (e != hipSuccess) return e;
