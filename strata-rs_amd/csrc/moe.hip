@@ -463,35 +463,52 @@ __global__ void __launch_bounds__(kMoeThreads)
 // 32 columns of token t, by 256 threads as 32 columns x 8 expert lanes. Lane
 // (col, a) sums the down chunk sums of the token's a-th expert (pair qa[a]);
 // then the token's experts are added in ascending id order: out += w * d,
-// skipping w == 0 (moe.rs:112-126).
+// skipping w == 0 (moe.rs:112-126). Every load a thread needs is issued
+// before its first use (the pairs, weights and shared-expert values beside
+// the chunk sums), so a workgroup waits for memory about twice.
 __device__ __forceinline__ void combine_cols(const MoePlan& plan, const float* __restrict__ part,
                                              const int* qa, const float* wa, int t, int col0,
-                                             float* __restrict__ out, float (*dsum)[32],
+                                             float* __restrict__ out, float (*dsum)[32], float* wsh,
                                              const float* sh_d = nullptr, const float* sh_s = nullptr) {
   const int cl = threadIdx.x & 31, al = threadIdx.x >> 5;
+  // the weights (one per expert lane) and the shared expert's terms, loaded
+  // with everything else and passed on through LDS
+  if (threadIdx.x < kMoeMaxTopK && int(threadIdx.x) < plan.top_k) wsh[threadIdx.x] = wa[threadIdx.x];
+  float shd = 0.f, shs = 0.f;
+  if (sh_d && al == 0) {
+    shd = sh_d[int64_t(t) * plan.n_embd + col0 + cl];
+    shs = sh_s[t];
+  }
   for (int a = al; a < plan.top_k; a += 8) {
     const float* src = part + int64_t(qa[a]) * plan.nch_b * plan.n_embd + col0 + cl;
+    // batches of 8 chunks (uniform), each batch's loads issued together
+    // (indices clamped into the chunks, the extra values not added)
     float v[kMoeMaxChunks];
 #pragma unroll
-    for (int k = 0; k < kMoeMaxChunks; ++k) v[k] = k < plan.nch_b ? src[int64_t(k) * plan.n_embd] : 0.f;
+    for (int k8 = 0; k8 < kMoeMaxChunks; k8 += 8) {
+      if (k8 < plan.nch_b) {
+#pragma unroll
+        for (int k = k8; k < k8 + 8; ++k) v[k] = src[int64_t(min(k, plan.nch_b - 1)) * plan.n_embd];
+      }
+    }
     float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < kMoeMaxChunks; ++k) sum += v[k];
+    for (int k = 0; k < kMoeMaxChunks; ++k)
+      if (k < plan.nch_b) sum += v[k];
     dsum[a][cl] = sum;
   }
   __syncthreads();
   if (al == 0) {
     float acc = 0.f;
     for (int a = 0; a < plan.top_k; ++a) {
-      const float wv = wa[a];
+      const float wv = wsh[a];
       if (wv != 0.f) acc = __fadd_rn(acc, __fmul_rn(wv, dsum[a][cl]));
     }
     if (sh_d) {
       // the shared expert: sigmoid(v) = 1 / (1 + exp(-v)) (ops.rs:90-92), then
       // one f32 product and one f32 add (moe.rs:139-142)
-      const float sv = sh_s[t];
-      const float gate = 1.f / (1.f + expf(-sv));
-      acc = __fadd_rn(acc, __fmul_rn(gate, sh_d[int64_t(t) * plan.n_embd + col0 + cl]));
+      const float gate = 1.f / (1.f + expf(-shs));
+      acc = __fadd_rn(acc, __fmul_rn(gate, shd));
     }
     out[int64_t(t) * plan.n_embd + col0 + cl] = acc;
   }
@@ -504,11 +521,17 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const ui
                                                           float* __restrict__ out, const float* __restrict__ sh_d,
                                                           const float* __restrict__ sh_s) {
   __shared__ float dsum[kMoeMaxTopK][32];
+  __shared__ float wsh[kMoeMaxTopK];
+  __shared__ int qsh[kMoeMaxTopK];
   const int blocks_per_tok = plan.n_embd / 32;
   const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
-  combine_cols(plan, reinterpret_cast<const float*>(ws + plan.o_part_b),
-               reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k,
-               reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum, sh_d, sh_s);
+  // the token's pairs, once for the workgroup (each expert lane reads its own)
+  const int* tp = reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k;
+  if (int(threadIdx.x) < plan.top_k) qsh[threadIdx.x] = tp[threadIdx.x];
+  __syncthreads();
+  combine_cols(plan, reinterpret_cast<const float*>(ws + plan.o_part_b), qsh,
+               reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum, wsh, sh_d,
+               sh_s);
 }
 
 // ------------------------------------------------------------------- host --
