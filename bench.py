@@ -185,6 +185,24 @@ def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):
             "peak_TFLOPs": peak, "frac_of_peak": round(tf / peak, 4)}
         del ws
     del w, x, y
+    # Q6_K weights of the same shape in both modes (the int8 mode on its
+    # 16-element sub-block kernel)
+    w6 = torch.from_numpy(S.matrix(S.Q6_K, 0x5EED0007, rows, cols)).to(dev)
+    x = torch.from_numpy(S.normal_f32(0x5EED0006, m * cols)).to(dev)
+    y = torch.empty(m * rows, dtype=torch.float32, device=dev)
+    for mode, name, peak in ((H.MATMUL_BF16, "bf16", 2500.0), (H.MATMUL_Q8, "q8_int8", 5000.0)):
+        nb = H.matmul_workspace_bytes(S.Q6_K, rows, cols, m, mode)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        call = (lambda st, mode=mode, ws=ws, nb=nb:
+                H.matmul_dev(S.Q6_K, w6.data_ptr(), rows, cols, x.data_ptr(), m, y.data_ptr(), mode,
+                             ws.data_ptr(), nb, st))
+        ms = time_calls(torch, [call], steps, 3)
+        tf = flops / (ms * 1e-3) / 1e12
+        res[f"prefill_q6k_12288x4096_m{m}_{name}"] = {
+            "us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+            "peak_TFLOPs": peak, "frac_of_peak": round(tf / peak, 4)}
+        del ws
+    del w6, x, y
     return res
 
 

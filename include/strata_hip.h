@@ -266,7 +266,7 @@ int sh_moe_layer(sh_context* ctx, const sh_quant_tensor* router, const sh_expert
  *                   accumulation (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS);
  *   SH_MATMUL_Q8    x quantized to Q8 blocks of 32 elements (f32 scale
  *                   max|x| / 127 per block, int8 codes rounded to nearest
- *                   even), int8 products (Q8_0, Q4_K, Q5_K, IQ4_XS);
+ *                   even), int8 products (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS);
  *   SH_MATMUL_Q8K   x quantized to blocks of 256 elements, one scale per
  *                   weight super-block (Q4_K, Q5_K): a coarser activation
  *                   rounding than SH_MATMUL_Q8 (the step is max|x| over 256

@@ -782,8 +782,6 @@ static int matmul_check(uint32_t quant, uint64_t rows, uint64_t cols, uint64_t m
   if (mode > SH_MATMUL_Q8K) return fail(SH_ERR_INVALID_ARGUMENT, "matmul mode %u", mode);
   if (!sh::device_quant(quant))
     return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: type %u has no device kernel", quant);
-  if (mode == SH_MATMUL_Q8 && quant == SH_QUANT_Q6_K)
-    return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: Q6_K weights take SH_MATMUL_BF16 only");
   if (mode == SH_MATMUL_Q8K && quant != SH_QUANT_Q4_K && quant != SH_QUANT_Q5_K)
     return fail(SH_ERR_UNSUPPORTED_QUANT, "matmul: SH_MATMUL_Q8K takes Q4_K / Q5_K weights only");
   if (!sh::matmul_shape_ok(quant, int64_t(rows), int64_t(cols), int64_t(m), mode))

@@ -31,6 +31,8 @@
 // so that the 8 XCDs (workgroup i runs on XCD i % 8) each get a contiguous
 // run of weight rows, and the token tiles of one weight tile share that
 // XCD's L2.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -403,7 +405,7 @@ struct StIQ4XS {
 // (dequant.rs:211,224-227) or, with the signed-scale flag, as i8.
 struct StQ6K {
   static constexpr int kPieces = 2;
-  static constexpr bool kQ8 = false;  // 16-element scales do not fit 32-element int8 blocks
+  static constexpr bool kQ8 = false;  // 16-element scales: its own int8 kernel (mm_i8q6_kernel)
   static constexpr bool kQ8K = false;
   struct Raw {
     u32x4 l0, l1, qh;
@@ -1138,6 +1140,186 @@ __global__ void __launch_bounds__(kMiThreads)
   }
 }
 
+// ------------------------------------------------------- q8 kernel, Q6_K --
+// Q6_K weights against the same 32-element Q8 activation blocks. Q6_K
+// carries a scale per 16 elements (d * sc_j, values d * sc_j * (q - 32)), so
+// each 32-element activation block j covers two weight sub-blocks and
+//   y_tr += s_tj * sum_{h = 0, 1} d_r * sc_r,2j+h * I_tr,2j+h,
+// I_tr,k = sum over sub-block k of (q - 32) c (exact int32). Per (tile of 32
+// rows x 32 tokens, activation block):
+//   v_mfma_i32_32x32x16_i8 twice    I of the two sub-blocks (K = 16; the
+//                                   block's K = 32 activation fragment is
+//                                   split into its two halves with one
+//                                   exchange between the wave's lane halves);
+//   v_mfma_f32_32x32x1_2b_f32       both sub-blocks' scale products d * sc *
+//                                   s_t as the outer products of its two blocks;
+//   VALU                            acc += float(I) * S, per sub-block.
+// So against the 32-element K-quants it does twice the int8 MFMAs and twice
+// the VALU per element. Tile 256 tokens x 96 rows, 8 waves (wave w owns
+// tokens [32 w, +32) x all 96 rows); waves 0-2 stage chunk c + 1 (codes
+// q - 32 as int8, d * sc per sub-block) while chunk c is computed, with a
+// two-chunk ring of weight loads.
+constexpr int kM6Threads = 512;
+
+// Four 6-bit codes q (one per byte) -> the bytes q - 32 (int8, -32..31)
+// without carries between bytes: q ^ 32 clears bit 5 of q >= 32 (giving
+// q - 32) and sets it for q < 32 (giving q + 32, which bits 6 and 7 then
+// turn into q - 32 + 256).
+__device__ __forceinline__ uint32_t q6_centered(uint32_t q) {
+  const uint32_t t = q ^ 0x20202020u, m = t & 0x20202020u;
+  return t | (m << 1) | (m << 2);
+}
+
+__global__ void __launch_bounds__(kM6Threads)
+    mm_i8q6_kernel(const uint8_t* __restrict__ w, int n_rows, int cols, int64_t row_bytes,
+                   const int8_t* __restrict__ xq, const float* __restrict__ xs, int m, float* __restrict__ y,
+                   int n_tiles_m, int q6s) {
+  typedef float f32x32 __attribute__((ext_vector_type(32)));
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][kMmBN * kMmRowQ];  // [chunk buf] codes q - 32
+  __shared__ __attribute__((aligned(16))) float wsc[2][4][kMmBN];          // [chunk buf][sub-block][row] d * sc
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, l32 = lane & 31;
+  int r0, t0;
+  tile_of(n_tiles_m, r0, t0);
+  const int nchunks = cols / kMmKC;
+  const int nblk = cols / 32;
+
+  constexpr int kTasks = kMmBN * StQ6K::kPieces;
+  static_assert(kTasks % kWave == 0 && kTasks <= kM6Threads, "staging tasks fill whole waves");
+  const bool stager = tid < kTasks;
+  const int srow = stager ? tid / StQ6K::kPieces : 0, piece = tid % StQ6K::kPieces;
+  const uint8_t* wrow = w + int64_t(min(r0 + srow, n_rows - 1)) * row_bytes;
+
+  // the wave's token tile, as mm_i8_kernel: fragment (T, c, s) at 16-byte
+  // piece ((T * nch + c) * 2 + s) * 64 + lane, scale of (T, j) at float
+  // (T * nblk + j) * 32 + l32
+  const int T = min((t0 >> 5) + wave, ((m + 31) >> 5) - 1);
+  const int8_t* xr = xq + int64_t(T) * nchunks * 2048 + 16 * lane;
+  const float* sr = xs + int64_t(T) * nblk * 32 + l32;
+
+  f32x16 acc[3];
+#pragma unroll
+  for (int ni = 0; ni < 3; ++ni) acc[ni] = f32x16{};
+
+  // piece hb of chunk c: elements [16 hb, +16) (sub-block hb) and
+  // [32 + 16 hb, +16) (sub-block 2 + hb) of the row's chunk
+  auto stage = [&](const StQ6K::Raw& raw, int c, int buf) {
+    uint32_t va[4], vb[4], scw;
+    StQ6K::decode(raw, c, block_shift<StQ6K>(wrow, c), va, vb, scw);
+    uint8_t* dst = wl[buf] + srow * kMmRowQ;
+    *reinterpret_cast<u32x4*>(dst + 16 * piece) =
+        u32x4{q6_centered(va[0]), q6_centered(va[1]), q6_centered(va[2]), q6_centered(va[3])};
+    *reinterpret_cast<u32x4*>(dst + 32 + 16 * piece) =
+        u32x4{q6_centered(vb[0]), q6_centered(vb[1]), q6_centered(vb[2]), q6_centered(vb[3])};
+    const uint32_t b0 = (scw >> (8 * piece)) & 0xFFu, b1 = (scw >> (8 * (2 + piece))) & 0xFFu;
+    const float d = h2f(raw.d);
+    wsc[buf][piece][srow] = d * (q6s ? float(int8_t(b0)) : float(b0));
+    wsc[buf][2 + piece][srow] = d * (q6s ? float(int8_t(b1)) : float(b1));
+  };
+
+  // a two-chunk ring of weight loads (slots are constants: two chunks per
+  // loop body); every wave issues them (other lanes read row r0), as in
+  // mm_i8_kernel
+  StQ6K::Raw raw[2];
+  raw[0] = StQ6K::load(wrow, 0, piece);
+  raw[1] = StQ6K::load(wrow, min(1, nchunks - 1), piece);
+  if (stager) stage(raw[0], 0, 0);
+  raw[0] = StQ6K::load(wrow, min(2, nchunks - 1), piece);
+  i32x4 xc[2];
+  float sxc[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    xc[s] = *reinterpret_cast<const i32x4*>(xr + 1024 * s);
+    sxc[s] = sr[32 * s];
+  }
+  lds_barrier();
+
+  for (int c0 = 0; c0 < nchunks; c0 += 2) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int c = c0 + jj;
+      if (c < nchunks) {  // uniform
+        const int buf = c & 1;
+        const bool more = c + 1 < nchunks;
+        // stage chunk c + 1 (slot (jj + 1) % 2) and refill the slot with c + 3
+        if (more && stager) stage(raw[(jj + 1) & 1], c + 1, buf ^ 1);
+        raw[(jj + 1) & 1] = StQ6K::load(wrow, min(c + 3, nchunks - 1), piece);
+        // chunk c + 1's activations, a chunk ahead
+        const int cn = more ? c + 1 : c;
+        i32x4 xn[2];
+        float sxn[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          xn[s] = *reinterpret_cast<const i32x4*>(xr + int64_t(cn) * 2048 + 1024 * s);
+          sxn[s] = sr[32 * (2 * cn + s)];
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          // the block's K = 32 fragment (lane half h: bytes 16 h .. 16 h + 15
+          // of the block) -> the K = 16 fragments of its two sub-blocks (lane
+          // half h: bytes 8 h .. 8 h + 7 of the sub-block)
+          const i32x4 f = xc[s];
+          i32x4 pf;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pf[q] = __shfl_xor(f[q], 32, kWave);
+          const long b_lo = half ? (long(uint32_t(pf[2])) | (long(uint32_t(pf[3])) << 32))
+                                 : (long(uint32_t(f[0])) | (long(uint32_t(f[1])) << 32));
+          const long b_hi = half ? (long(uint32_t(f[2])) | (long(uint32_t(f[3])) << 32))
+                                 : (long(uint32_t(pf[0])) | (long(uint32_t(pf[1])) << 32));
+#pragma unroll
+          for (int ni = 0; ni < 3; ++ni) {
+            const uint8_t* wa = wl[buf] + (32 * ni + l32) * kMmRowQ + 32 * s + 8 * half;
+            const i32x16 I0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(*reinterpret_cast<const long*>(wa), b_lo,
+                                                                    i32x16{}, 0, 0, 0);
+            const i32x16 I1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(*reinterpret_cast<const long*>(wa + 16), b_hi,
+                                                                    i32x16{}, 0, 0, 0);
+            // A: lane half h supplies sub-block 2 s + h's d * sc of row l32;
+            // B: the lane's token scale of block s (both halves)
+            const f32x32 Sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsc[buf][2 * s + half][32 * ni + l32], sxc[s],
+                                                                   f32x32{}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              acc[ni][i] = __builtin_fmaf(float(I0[i]), Sc[i], acc[ni][i]);
+              acc[ni][i] = __builtin_fmaf(float(I1[i]), Sc[16 + i], acc[ni][i]);
+            }
+            // the step's sums are formed here: otherwise the compiler holds
+            // every step's products at once (hundreds of registers)
+            asm volatile("" : "+v"(acc[ni]));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          xc[s] = xn[s];
+          sxc[s] = sxn[s];
+        }
+        lds_barrier();  // chunk c + 1 staged; nobody reads chunk c's buffer any more
+      }
+    }
+  }
+
+  // D layout as mm_i8_kernel's
+  const int t = t0 + 32 * wave + l32;
+  if (t < m) {
+#pragma unroll
+    for (int ni = 0; ni < 3; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 32 * ni + 8 * q + 4 * half;
+        float* dst = y + int64_t(t) * n_rows + r;
+        if (r + 3 < n_rows && (n_rows & 3) == 0) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[ni][4 * q], acc[ni][4 * q + 1], acc[ni][4 * q + 2], acc[ni][4 * q + 3]};
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (r + e < n_rows) dst[e] = acc[ni][4 * q + e];
+        }
+      }
+  }
+}
+
 // ------------------------------------------------------ q8 kernel, K-quants --
 // Q4_K / Q5_K weights against activations in 256-element Q8 blocks (one scale
 // s_t per token and super-block, codes c, sub-block code sums b_tj). One
@@ -1391,7 +1573,6 @@ bool matmul_shape_ok(uint32_t quant, int64_t rows, int64_t cols, int64_t m, uint
   if (!device_quant(quant) || rows <= 0 || cols <= 0 || m <= 0) return false;
   if (cols % kMmKC != 0 || cols % geometry(quant).block != 0) return false;
   if (rows > (int64_t(1) << 31) - 1 || cols > (int64_t(1) << 30) || m > (int64_t(1) << 24)) return false;
-  if (mode == 1 && quant == kQ6_K) return false;  // 16-element Q6_K scales: bf16 mode only
   if (mode == 2 && quant != kQ4_K && quant != kQ5_K) return false;
   if (mode > 2) return false;
   const int64_t tiles = ((rows + kMmBN - 1) / kMmBN) * ((m + kMmBM - 1) / kMmBM);
@@ -1451,6 +1632,12 @@ static void launch_mm(uint32_t mode, const uint8_t* w, int rows, int cols, int64
   if (mode == 0) {
     hipLaunchKernelGGL(mm_bf16_ws_kernel<S>, grid, dim3(kMmWsThreads), kMmLdsWs, s, w, rows, cols, rb,
                        reinterpret_cast<const u32x4*>(ws), m, y, ntm, q6s);
+  } else if constexpr (std::is_same<S, StQ6K>::value) {
+    if (mode == 1) {  // 16-element scales: the Q6_K int8 kernel
+      const Q8Ws q = q8_ws(ws, cols, m);
+      hipLaunchKernelGGL(mm_i8q6_kernel, grid, dim3(kM6Threads), 0, s, w, rows, cols, rb, q.codes, q.scales, m, y,
+                         ntm, q6s);
+    }
   } else if constexpr (S::kQ8) {
     if (mode == 2) {
       if constexpr (S::kQ8K) {

@@ -9,7 +9,8 @@ Metric: max|y - r| / max|r| per token row.
   to bf16, x rounded to bf16, f64 sums): <= 1e-3 -- this isolates the
   kernel's indexing and accumulation from the rounding the mode defines.
 * q8 mode (activations in Q8 blocks of 32 elements, f32 scale, int8 codes;
-  Q8_0, Q4_K and Q5_K weights) against the oracle gemv of x rounded through
+  Q8_0, Q4_K, Q5_K and Q6_K weights -- Q6_K's 16-element sub-blocks on their
+  own kernel, in both scale readings) against the oracle gemv of x rounded through
   those blocks (scale * code): <= 1e-3 normwise and the strict per-element
   bar (the int8 products are exact; the scale products and the min term are
   f32); against the f32 oracle: <= 2e-2.
@@ -81,7 +82,7 @@ def test_matmul_bf16_q6k_signed_scales(backend, oracle):
     check_rows(y, bf16_operand_ref(oracle, 14, rows, cols, w, x, scale_mode=1), TOL_EXACT_OPERANDS, STRICT_TOL)
 
 
-@pytest.mark.parametrize("quant,rows,cols,m", [s for s in SHAPES if s[0] != 14])
+@pytest.mark.parametrize("quant,rows,cols,m", SHAPES)
 def test_matmul_q8(backend, oracle, quant, rows, cols, m):
     say("matmul q8", quant, rows, cols, m)
     w = S.matrix(quant, 920 + rows, rows, cols)
@@ -225,11 +226,29 @@ def test_matmul_dev_matches_host_path(backend, mode):
     assert np.array_equal(ty.cpu().numpy(), host)
 
 
+@pytest.mark.parametrize("rows,cols,m", [(96, 256, 5), (130, 1024, 70), (192, 4096, 257)])
+def test_matmul_q8_q6k_signed_scales(backend, oracle, rows, cols, m):
+    """Q6_K in the int8 mode (16-element weight sub-blocks inside 32-element
+    activation blocks) with ggml's int8 sub-block scales, and the reading
+    shown to matter."""
+    say("matmul q8 q6k signed", rows, cols, m)
+    w = S.matrix(14, 970 + rows, rows, cols)
+    x = S.normal_f32(971 + m, m * cols).reshape(m, cols)
+    t = H.QuantTensor(f"mq6s_{rows}_{cols}", 14, rows, cols, w, flags=H.FLAG_Q6K_SIGNED_SCALES)
+    y = backend.matmul(t, x, H.MATMUL_Q8)
+    xq = oracle.q8_activations_for(H.MATMUL_Q8, x)
+    check_rows(y, oracle.matmul(14, rows, cols, w, xq, threads=8, mode=1), TOL_EXACT_OPERANDS, STRICT_TOL)
+    check_rows(y, oracle.matmul(14, rows, cols, w, x, threads=8, mode=1), TOL_F32)
+    other = oracle.matmul(14, rows, cols, w, xq[:1], threads=8, mode=0)
+    assert rel_err(y[0], other[0]) > 1e-2, "the two scale readings must differ on random scale bytes"
+    backend.evict(t.name)
+
+
 def test_matmul_errors(backend):
     say("matmul errors")
     w6 = H.QuantTensor("e6", 14, 4, 256, S.matrix(14, 1, 4, 256))
-    with pytest.raises(H.UnsupportedQuantError):
-        backend.matmul(w6, np.zeros((2, 256), np.float32), H.MATMUL_Q8)
+    with pytest.raises(H.UnsupportedQuantError):  # 256-element blocks: Q4_K / Q5_K only
+        backend.matmul(w6, np.zeros((2, 256), np.float32), H.MATMUL_Q8K)
     w8 = H.QuantTensor("e8", 8, 4, 96, S.matrix(8, 1, 4, 96))
     with pytest.raises(H.BackendError):
         backend.matmul(w8, np.zeros((2, 96), np.float32), H.MATMUL_BF16)  # cols not a multiple of 64
