@@ -287,7 +287,8 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // per-lane byte offsets within a row are computed once. Loads are
 // double-buffered (A/B ping-pong, both refills unconditional so the loop
 // latch never drains the load queue), and the first item is requested
-// before x is staged, so weight bytes are in flight from the first cycles.
+// before x is staged, so weight bytes are in flight from the first cycles
+// (after every wave's x loads, when x takes more than one round).
 //
 // MODE bits (compile-time; 0 for the plain matvec) let the dense FFN run in
 // two launches: kLimbTwoMat reads rows [0, rows1) from w and [rows1, rows)
@@ -370,6 +371,17 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     }
   }
   typename F::Load A[R], B[R];
+  if constexpr (NPRE > 1) {
+    // A CU returns vector loads about in the order they were issued, so a
+    // weight load issued before another wave's x loads delays that wave's x
+    // (and the barrier below) by a memory latency. An issue-only barrier
+    // puts every x load of the workgroup ahead of its first weight load:
+    // 4096x12288 Q4_K 8.16 -> 7.70 us. Rows of one window (one x round, 16
+    // KiB) lose more to the barrier than they gain, and skip it.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   issue(A);
   auto stage = [&](int t, f32x4 a, f32x4 b, f32x4 ua, f32x4 ub) {
     if constexpr ((MODE & kLimbSiluX) != 0) {
