@@ -408,7 +408,9 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     }
     stage(t0 + tid, src[0], src[1], ua, ub);
   }
-  __syncthreads();
+  // LDS only: __syncthreads() would also wait for the first item's weight
+  // loads, which keeps the second item's loads from issuing until they land
+  lds_barrier();
   if (n_items == 0) return;
 
   float acc[MAXQ][R];
