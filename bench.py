@@ -6,8 +6,9 @@ packed weight matrix (the FFN down projection of a Qwen3.5-9B-like model:
 4096 outputs, 12288 inputs) with an f32 activation vector; weights and x are
 resident in HBM before the timed region starts. The launches rotate over
 enough distinct weight copies (>= 1 GiB) that the 256 MB Infinity Cache cannot
-serve repeats, and run as one captured HIP graph so launch gaps do not bound
-the measurement. Events are recorded on the stream the kernels run on.
+serve repeats, and are all queued behind a spin kernel before the GPU reaches
+them, so host launch costs do not bound the measurement. Events are recorded
+on the stream the kernels run on.
 
 Prints ONE JSON line (rank 0):
   value          packed-weight GB/s (weight bytes / mean time per launch)
@@ -16,7 +17,7 @@ Prints ONE JSON line (rank 0):
                  bytes per launch measured with rocprofv3 counters, when a
                  summary exists under profiles/; `measured_ceiling_GBps` is a
                  plain streaming read of the same bytes over the same rotating
-                 copies in the same graph harness
+                 copies in the same harness
   cpu_baseline   the reference's CPU path (the C restatement of ops::gemv,
                  single thread, sequential f64) timed on this host on a
                  bounded sample of the same workload
@@ -64,55 +65,70 @@ def parse():
     return ap.parse_args()
 
 
-def _graph_of(torch, stream, calls, n, first=0):
-    """A HIP graph of exactly n calls, cycling through `calls` from index
-    `first`."""
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        h = torch.cuda.current_stream().cuda_stream
-        for i in range(n):
-            calls[(first + i) % len(calls)](h)
-    return g
+_SPIN = {}
 
 
-def _time_graph_calls(torch, stream, calls, steps, warmup):
-    """Runs `warmup` calls untimed, then times exactly `steps` calls; events
-    on `stream`. Each set is one captured HIP graph. The timed graph takes the
-    calls that follow the warmed ones (its first call is calls[warmup %
-    len(calls)], so a rotation over weight copies continues instead of
-    re-reading the copies just warmed). It is replayed twice back to back on
-    the stream, the first replay untimed (a graph's first replay also uploads
-    it, and the back-to-back order keeps the launch latency of the timed
-    replay out of the timed region: the start event completes as the untimed
-    replay ends, with the timed replay already queued behind it). Returns ms
+def _spin_cycles_per_us(torch, stream):
+    """The rate of torch.cuda._sleep's cycle counter, measured once."""
+    if "rate" not in _SPIN:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(1000)  # the first launch of the spin kernel loads it
+            a.record(stream)
+            torch.cuda._sleep(1_000_000)
+            b.record(stream)
+        torch.cuda.synchronize()
+        _SPIN["rate"] = 1_000_000 / (a.elapsed_time(b) * 1e3)
+    return _SPIN["rate"]
+
+
+def _time_queued_calls(torch, stream, calls, steps, warmup):
+    """Runs `warmup` calls untimed, then times exactly `steps` calls with
+    events on `stream`, cycling through `calls` (the timed calls continue
+    where the warm-up stopped, so a rotation over weight copies never re-reads
+    the copies just warmed). Every launch is queued before the GPU reaches
+    it: the stream first runs a spin kernel (torch.cuda._sleep) long enough
+    to cover the host's enqueueing, measured on an eager pass, three times
+    over, so the timed region holds exactly the `steps` calls back to back
+    and no host launch cost. A captured HIP graph would also do that, but a
+    replay adds ~8 us of its own per timed region (measured at 20 and 400
+    launches, and with the replays queued behind the same spin), 0.4 us a
+    launch at 20. Raises if the host fell behind the GPU anyway. Returns ms
     per call."""
     with torch.cuda.stream(stream):  # eager pass: the calls are accepted
         for f in calls:
             f(stream.cuda_stream)
     torch.cuda.synchronize()
-    if warmup > 0:
-        gw = _graph_of(torch, stream, calls, warmup)
-        with torch.cuda.stream(stream):
-            gw.replay()
-        torch.cuda.synchronize()
-        del gw
-    g = _graph_of(torch, stream, calls, steps, first=warmup % len(calls))
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for f in calls:
+            f(stream.cuda_stream)
+    host_us = (time.perf_counter() - t0) * 1e6 / len(calls)
     torch.cuda.synchronize()
+    spin_us = 500.0 + 3.0 * host_us * (warmup + steps)
+    cycles = int(spin_us * _spin_cycles_per_us(torch, stream))
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    n = len(calls)
     with torch.cuda.stream(stream):
-        g.replay()  # untimed
+        h = stream.cuda_stream
+        torch.cuda._sleep(cycles)
+        for i in range(warmup):
+            calls[i % n](h)
         start.record(stream)
-        g.replay()
+        for i in range(steps):
+            calls[(warmup + i) % n](h)
         end.record(stream)
+        ahead = not start.query()  # still spinning: everything was queued in time
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    del g
-    return ms
+    if not ahead:
+        raise RuntimeError("the host fell behind the GPU while queueing the timed calls")
+    return start.elapsed_time(end) / steps
 
 
-def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags=0, ceiling=None):
-    """Mean ms per launch over exactly `steps` launches (one graph replay)
+def timed_rotation(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags=0, ceiling=None):
+    """Mean ms per launch over exactly `steps` launches (queued back to back)
     after `warmup` untimed ones, rotating over copies of the weights; returns
     (ms, n_copies, launches_timed). With `ceiling` (a dict), a plain
     streaming read of the same copies (sh_stream_read_dev) is timed the same
@@ -137,14 +153,14 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
                                            ws.data_ptr(), nws, s, flags)
         return lambda s: H.gemv_dev(quant, c.data_ptr(), rows, cols, x.data_ptr(), y.data_ptr(), batch, s, flags)
 
-    ms = _time_graph_calls(torch, stream, [call(c) for c in copies], steps, warmup)
+    ms = _time_queued_calls(torch, stream, [call(c) for c in copies], steps, warmup)
     if ceiling is not None:
         folds = torch.empty(H.STREAM_READ_BLOCKS, dtype=torch.int32, device=dev)
 
         def read(c):
             return lambda s: H.stream_read_dev(c.data_ptr(), nbytes, folds.data_ptr(), s)
 
-        ceiling["ms"] = _time_graph_calls(torch, stream, [read(c) for c in copies], steps, warmup)
+        ceiling["ms"] = _time_queued_calls(torch, stream, [read(c) for c in copies], steps, warmup)
     del copies, base
     torch.cuda.empty_cache()
     return ms, n_copies, steps
@@ -153,11 +169,11 @@ def timed_graph(torch, H, quant, rows, cols, w_host, batch, steps, warmup, flags
 def time_calls(torch, calls, steps, warmup):
     """Mean ms per call of a list of enqueue functions f(stream_handle):
     exactly `steps` timed calls, cycled in order, after `warmup` untimed ones
-    (the harness of _time_graph_calls)."""
+    (the harness of _time_queued_calls)."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
-    return _time_graph_calls(torch, stream, calls, steps, warmup)
+    return _time_queued_calls(torch, stream, calls, steps, warmup)
 
 
 def bench_prefill(torch, H, S, w_host, rows, cols, m, steps):
@@ -359,8 +375,7 @@ def bench_moe_layer(torch, H, S, steps):
 def bench_rowops(torch, H, S, steps):
     """The trait's elementwise methods at a decode step's shapes (hidden 4096,
     32 heads of 128 with 64 rotated dims, a 4096-long attention row per head)
-    and a 16-token prefill's; 64 launches of one method captured in a graph
-    and replayed; us per launch and GB/s of the bytes each launch reads and
+    and a 16-token prefill's; launches of one method back to back; us per launch and GB/s of the bytes each launch reads and
     writes (the data stays in L2 between launches)."""
     import numpy as np
     dev = torch.device("cuda:0")
@@ -391,7 +406,7 @@ def bench_rowops(torch, H, S, steps):
              lambda st, x=x, o=o, n=n_tok: H.add_dev(o.data_ptr(), x.data_ptr(), n * 4096, st)),
         ]
     for name, nbytes, f in cases:
-        ms = time_calls(torch, [f] * 64, steps, 64)  # 64 launches per graph replay
+        ms = time_calls(torch, [f], steps, 64)
         res[name] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     return res
 
@@ -551,7 +566,7 @@ DECODE_SHAPES = (("q4k_gate_12288x4096_b1", 12, 12288, 4096, 1),
 def bench_decode_shapes(torch, H, S, steps_max, batched_only=False):
     """The other decode matvec shapes (Q4_K / Q5_K gate and down at batch 1
     and 8, Q8_0 attention-sized, the Q6_K head), each over rotating weight
-    copies in one graph; microseconds per launch and GB/s of packed weights."""
+    copies; microseconds per launch and GB/s of packed weights."""
     extra = {}
     for name, q, r, c, b in DECODE_SHAPES:
         if batched_only and b == 1:
@@ -559,7 +574,7 @@ def bench_decode_shapes(torch, H, S, steps_max, batched_only=False):
         wm = S.matrix(q, 0x5EED0000 + q + r, r, c)
         print(f"[bench] extra {name}", file=sys.stderr, flush=True)
         steps = max(40, min(steps_max, int(2e9 / wm.nbytes)))
-        t, _, _ = timed_graph(torch, H, q, r, c, wm, b, steps, 10)
+        t, _, _ = timed_rotation(torch, H, q, r, c, wm, b, steps, 10)
         extra[name] = {"us_per_launch": round(t * 1e3, 3),
                        "weight_GBps": round(wm.nbytes / (t * 1e-3) / 1e9, 1),
                        "pct_hbm_peak": round(100 * wm.nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 1)}
@@ -650,7 +665,7 @@ def main():
     print(f"[bench] Q4_K {rows}x{cols} ({wbytes} B) batch 1: warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     ceiling = {}
-    ms, n_copies, launches = timed_graph(torch, H, S.Q4_K, rows, cols, w, 1, args.steps, args.warmup,
+    ms, n_copies, launches = timed_rotation(torch, H, S.Q4_K, rows, cols, w, 1, args.steps, args.warmup,
                                          ceiling=ceiling)
     gbs = wbytes / (ms * 1e-3) / 1e9
     alg = wbytes + 4 * cols + 4 * rows
@@ -672,7 +687,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": f"synthetic (seeded GGUF Q4_K blocks, x ~ N(0,1)); {n_copies} rotating weight copies "
-                f"({n_copies * wbytes / 2**30:.2f} GiB), one HIP graph",
+                f"({n_copies * wbytes / 2**30:.2f} GiB), launches queued behind a spin kernel",
         "config": {"workload": "Q4_K fused dequant-matvec, W 4096x12288 (outputs x inputs), batch 1",
                    "rows": rows, "cols": cols, "batch": 1, "weight_bytes": wbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
@@ -681,7 +696,7 @@ def main():
                      "measured_ceiling_GBps": round(ceil_gbs, 2),
                      "frac_of_measured_ceiling": round(gbs / ceil_gbs, 4),
                      "ceiling": "plain streaming read of the same 28,311,552 bytes (sh_stream_read_dev: 16-byte "
-                                "loads, 2048 x 256 threads) over the same rotating copies, one HIP graph, "
+                                "loads, 2048 x 256 threads) over the same rotating copies, same harness, "
                                 f"{ceiling['ms'] * 1e3:.3f} us per launch"},
     }
     print(f"[bench] {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s", file=sys.stderr, flush=True)
