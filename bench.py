@@ -89,13 +89,15 @@ def _time_queued_calls(torch, stream, calls, steps, warmup):
     where the warm-up stopped, so a rotation over weight copies never re-reads
     the copies just warmed). Every launch is queued before the GPU reaches
     it: the stream first runs a spin kernel (torch.cuda._sleep) long enough
-    to cover the host's enqueueing, measured on an eager pass, three times
-    over, so the timed region holds exactly the `steps` calls back to back
-    and no host launch cost. A captured HIP graph would also do that, but a
+    to cover the host's enqueueing (1 ms plus four times the host cost of
+    the calls, measured on an eager pass; four times longer again on a retry
+    if the host still fell behind, as under a tracer), so the timed region
+    holds exactly the `steps` calls back to back and no host launch cost.
+    A captured HIP graph would also do that, but a
     replay adds ~8 us of its own per timed region (measured at 20 and 400
     launches, and with the replays queued behind the same spin), 0.4 us a
-    launch at 20. Raises if the host fell behind the GPU anyway. Returns ms
-    per call."""
+    launch at 20. Raises if the host still fell behind after three tries.
+    Returns ms per call."""
     with torch.cuda.stream(stream):  # eager pass: the calls are accepted
         for f in calls:
             f(stream.cuda_stream)
@@ -106,22 +108,26 @@ def _time_queued_calls(torch, stream, calls, steps, warmup):
             f(stream.cuda_stream)
     host_us = (time.perf_counter() - t0) * 1e6 / len(calls)
     torch.cuda.synchronize()
-    spin_us = 500.0 + 3.0 * host_us * (warmup + steps)
-    cycles = int(spin_us * _spin_cycles_per_us(torch, stream))
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    spin_us = 1000.0 + 4.0 * host_us * (warmup + steps)
     n = len(calls)
-    with torch.cuda.stream(stream):
-        h = stream.cuda_stream
-        torch.cuda._sleep(cycles)
-        for i in range(warmup):
-            calls[i % n](h)
-        start.record(stream)
-        for i in range(steps):
-            calls[(warmup + i) % n](h)
-        end.record(stream)
-        ahead = not start.query()  # still spinning: everything was queued in time
-    torch.cuda.synchronize()
+    for _attempt in range(3):
+        cycles = int(spin_us * _spin_cycles_per_us(torch, stream))
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            h = stream.cuda_stream
+            torch.cuda._sleep(cycles)
+            for i in range(warmup):
+                calls[i % n](h)
+            start.record(stream)
+            for i in range(steps):
+                calls[(warmup + i) % n](h)
+            end.record(stream)
+            ahead = not start.query()  # still spinning: everything was queued in time
+        torch.cuda.synchronize()
+        if ahead:
+            break
+        spin_us *= 4.0  # the host was slower than measured (a tracer, a busy host): queue again
     if not ahead:
         raise RuntimeError("the host fell behind the GPU while queueing the timed calls")
     return start.elapsed_time(end) / steps
