@@ -94,7 +94,7 @@ def check_parity(got, want, label="", norm_tol=NORM_TOL, strict_tol=STRICT_TOL):
 
 def pytest_terminal_summary(terminalreporter):
     """The worst parity metrics per test file (and a JSON record of every
-    check under gpurun_out/ when that folder exists)."""
+    check in the file STRATA_PARITY_JSON names, when it is set)."""
     if not METRICS:
         return
     worst = {}
@@ -105,8 +105,8 @@ def pytest_terminal_summary(terminalreporter):
     terminalreporter.write_sep("-", "parity metrics (worst per file: normwise, per-element with 1e-3 rms floor)")
     for f, (n, st, c) in sorted(worst.items()):
         terminalreporter.write_line(f"{f}: {c} checks, normwise {n:.2e}, per-element {st:.2e}")
-    out = os.path.join(ROOT, "gpurun_out")
-    if os.path.isdir(out):
+    out = os.environ.get("STRATA_PARITY_JSON")
+    if out:
         import json
-        with open(os.path.join(out, "parity_metrics.json"), "w") as fh:
+        with open(out, "w") as fh:
             json.dump([{"test": t, "label": l, "normwise": n, "per_element": st} for t, l, n, st in METRICS], fh)
