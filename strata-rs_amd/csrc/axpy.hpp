@@ -239,15 +239,11 @@ struct AxQ6K {
     const uint32_t qlr[17] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w, l2.x,
                               l2.y, l2.z, l2.w, l3.x, l3.y, l3.z, l3.w, l4};
     const uint32_t qhr[9] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w, h2};
-    const uint32_t nib = 4u * tp;
     float wv[64];  // 6-bit codes 0..63
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      const uint32_t qs = tp ? qh : (qh << 4);
-      const uint32_t va = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      const uint32_t vb =
-          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+      uint32_t va, vb;
+      q6_code_words(qlr[k], qlr[k + 1], qlr[8 + k], qlr[9 + k], qhr[k], qhr[k + 1], s, tp, va, vb);
       wv[4 * k + 0] = ubyte<0>(va);
       wv[4 * k + 1] = ubyte<1>(va);
       wv[4 * k + 2] = ubyte<2>(va);
@@ -541,9 +537,9 @@ struct HxQ6K {
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t ql = realign(qlr[k], qlr[k + 1], s);
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      const uint32_t v = ((ql >> nib) & 0x0F0F0F0Fu) | (((qh >> hsh) & 0x03030303u) << 4);
+      // realignment and shift in one funnel shift each (s <= 3, so 8 s + 6 < 32)
+      const uint32_t v = (__builtin_amdgcn_alignbit(qlr[k + 1], qlr[k], 8u * s + nib) & 0x0F0F0F0Fu) |
+                         ((__builtin_amdgcn_alignbit(qhr[k + 1], qhr[k], 8u * s + hsh) & 0x03030303u) << 4);
       const float w0 = ubyte<0>(v), w1 = ubyte<1>(v), w2 = ubyte<2>(v), w3 = ubyte<3>(v);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {

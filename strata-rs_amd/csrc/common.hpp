@@ -204,6 +204,22 @@ __device__ __forceinline__ uint32_t realign(uint32_t lo, uint32_t hi, uint32_t s
   return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
+// Q6_K 6-bit codes, four to a word, from a lane's ql and qh words loaded
+// from the 4-byte boundary `s` (0..3) bytes below its bytes: va takes the
+// low nibbles of the ql bytes (high nibbles when `tp`) of words la0:la1
+// under bits 4-5 from bit pair 0 of the qh bytes (pair 2 when `tp`); vb
+// the same of lb0:lb1 with pair 1 (3). The byte realignment and the nibble
+// shift are one funnel shift (v_alignbit), and the pair moves to bits 4-5
+// by one shift of lane-dependent width: 3 instructions fewer per pair of
+// words than realigning, shifting and selecting.
+__device__ __forceinline__ void q6_code_words(uint32_t la0, uint32_t la1, uint32_t lb0, uint32_t lb1, uint32_t h0,
+                                              uint32_t h1, uint32_t s, uint32_t tp, uint32_t& va, uint32_t& vb) {
+  const uint32_t qs = __builtin_amdgcn_alignbyte(h1, h0, s) << (4u - 4u * tp);
+  const uint32_t sh = 8u * s + 4u * tp;
+  va = (__builtin_amdgcn_alignbit(la1, la0, sh) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
+  vb = (__builtin_amdgcn_alignbit(lb1, lb0, sh) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+}
+
 // IEEE binary16 bits -> f32 through the hardware conversion (exact, f16
 // denormals preserved under the default FP16 denorm mode).
 __device__ __forceinline__ float h2f(uint32_t bits16) {

@@ -239,16 +239,11 @@ struct FmtQ6K {
                               L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
     const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
     const uint32_t scw = realign(L.s0, L.s1, s);
-    const uint32_t nib = 4u * tp;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};  // one per 16-element sub-block
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      // high 2 bits of quadrant t0 moved to bits 4-5 of each byte
-      const uint32_t qs = tp ? qh : (qh << 4);
-      const uint32_t a = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      const uint32_t b =
-          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+      uint32_t a, b;
+      q6_code_words(qlr[k], qlr[k + 1], qlr[8 + k], qlr[9 + k], qhr[k], qhr[k + 1], s, tp, a, b);
       const f32x4 xa = x.v[k], xb = x.v[8 + k];
       float& ca = acc[k >> 2];
       float& cb = acc[2 + (k >> 2)];

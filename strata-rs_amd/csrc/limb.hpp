@@ -355,16 +355,12 @@ struct LimbQ6K {
                               L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
     const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
     const uint32_t scw = realign(L.s0, L.s1, s);
-    const uint32_t nib = 4u * tp;
     int sa[4] = {0, 0, 0, 0};
     uint32_t sb[4] = {0, 0, 0, 0}, sc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const uint32_t qh = realign(qhr[k], qhr[k + 1], s);
-      const uint32_t qs = tp ? qh : (qh << 4);
-      const uint32_t va = ((realign(qlr[k], qlr[k + 1], s) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      const uint32_t vb =
-          ((realign(qlr[8 + k], qlr[9 + k], s) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+      uint32_t va, vb;
+      q6_code_words(qlr[k], qlr[k + 1], qlr[8 + k], qlr[9 + k], qhr[k], qhr[k + 1], s, tp, va, vb);
       const int ga = k >> 2, gb = 2 + (k >> 2);
       dot_limbs(va, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), sa[ga], sb[ga], sc[ga]);
       dot_limbs(vb, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), sa[gb], sb[gb], sc[gb]);

@@ -440,13 +440,9 @@ struct StQ6K {
     const uint32_t L0[5] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l0e};
     const uint32_t L1[5] = {r.l1.x, r.l1.y, r.l1.z, r.l1.w, r.l1e};
     const uint32_t QH[5] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w, r.qhe};
-    const uint32_t nib = 4u * tp;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t qh = realign(QH[k], QH[k + 1], shift);
-      const uint32_t qs = tp ? qh : (qh << 4);
-      va[k] = ((realign(L0[k], L0[k + 1], shift) >> nib) & 0x0F0F0F0Fu) | (qs & 0x30303030u);
-      vb[k] = ((realign(L1[k], L1[k + 1], shift) >> nib) & 0x0F0F0F0Fu) | ((qs >> 2) & 0x30303030u);
+      q6_code_words(L0[k], L0[k + 1], L1[k], L1[k + 1], QH[k], QH[k + 1], shift, tp, va[k], vb[k]);
     }
     scw = realign(r.s0, r.s1, shift);
   }
