@@ -294,8 +294,19 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // two launches: kLimbTwoMat reads rows [0, rows1) from w and [rows1, rows)
 // from w2 (gate and up in one launch, x staged once); kLimbSiluX stages
 // silu(x) * xu, with silu(v) = v / (1 + exp(-v)) in f32 (qwen35.rs:120-124),
-// instead of x; kLimbResid writes y = xres + sum (one f32 add, qwen35.rs:127-129).
-constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4;
+// instead of x; kLimbResid writes y = xres + sum (one f32 add, qwen35.rs:127-129);
+// kLimbPairSilu (R = 2, rows of one 4096-column window) takes row group q
+// as row q of w (gate) and row q of w2 (up) and stores y[q] = silu(g) * u,
+// the same f32 expression kLimbSiluX stages, so the down launch stages one
+// vector instead of two.
+constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4, kLimbPairSilu = 8;
+
+// silu(g) * u in f32, g / (1 + exp(-g)) * u without contraction
+// (qwen35.rs:120-124, ops.rs:85-87)
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.f + expf(-g)) * u;
+}
 constexpr int kLimbMaxRowsOneWin = 64;  // row groups a wave may take when rows are one window
 
 template <class F, int R, int MAXQ, int MODE = 0, int NPRE = 1>
@@ -340,6 +351,8 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
       const uint8_t* base = w + int64_t(row) * row_bytes;
       if constexpr ((MODE & kLimbTwoMat) != 0)
         base = row >= rows1 ? w2 + int64_t(row - rows1) * row_bytes : base;
+      if constexpr ((MODE & kLimbPairSilu) != 0)
+        base = (r == 0 ? w : w2) + int64_t(row >> 1) * row_bytes;
       F::load(base, o, L[r]);
     }
     if (++pq == my) {
@@ -429,14 +442,22 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     if (nwin == 1) {
       // a single window: each item is whole rows, final at once (so a wave
       // may take any number of them, and fewer workgroups stage x)
+      if constexpr ((MODE & kLimbPairSilu) != 0) {
+        static_assert(R == 2, "a gate row and an up row per item");
+        const float g = wave_sum_dpp(ok ? F::dot(L[0], xl, lane, flags) : 0.f);
+        const float u = wave_sum_dpp(ok ? F::dot(L[1], xl, lane, flags) : 0.f);
+        const int q = rg0 + cq;
+        if (lane == 63 && q < n_rg) y[q] = silu_mul(g, u);
+      } else {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float t = F::dot(L[r], xl, lane, flags);
-        const float v = wave_sum_dpp(ok ? t : 0.f);
-        const int row = (rg0 + cq) * R + r;
-        if (lane == 63 && row < rows) y[row] = (MODE & kLimbResid) != 0 ? __fadd_rn(xres[row], v) : v;
+        for (int r = 0; r < R; ++r) {
+          const float t = F::dot(L[r], xl, lane, flags);
+          const float v = wave_sum_dpp(ok ? t : 0.f);
+          const int row = (rg0 + cq) * R + r;
+          if (lane == 63 && row < rows) y[row] = (MODE & kLimbResid) != 0 ? __fadd_rn(xres[row], v) : v;
+        }
       }
-    } else {
+    } else if constexpr ((MODE & kLimbPairSilu) == 0) {  // the pair mode takes one window only
 #pragma unroll
       for (int q = 0; q < MAXQ; ++q) {
         if (q == cq) {
@@ -459,7 +480,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     issue(A);
     if (i + 1 < n_items) step(B);
   }
-  if (nwin == 1) return;  // stored as computed
+  if (nwin == 1 || (MODE & kLimbPairSilu) != 0) return;  // stored as computed
 #pragma unroll
   for (int q = 0; q < MAXQ; ++q) {
     if (q < my) {
@@ -887,6 +908,24 @@ hipError_t launch_shexp_one(uint32_t q_gu, uint32_t q_d, const void* gate, const
   const int64_t rb1 = byte_size(q_gu, n_embd), rb2 = byte_size(q_d, n_ff);
   const int E = int(n_embd), N = int(n_ff);
   hipError_t e;
+  if (E <= 4096) {
+    // gate and up in one launch, a gate row and an up row per item, storing
+    // h = silu(g) * u (gu[0, N)); down stages h as its x
+    switch (q_gu) {
+      case kQ4_K: e = launch_limb<LimbQ4K, 2, 4, kLimbPairSilu>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+      case kQ8_0: e = launch_limb<LimbQ8, 2, 4, kLimbPairSilu>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+      case kQ5_K: e = launch_limb<LimbQ5K, 2, 4, kLimbPairSilu>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
+      default: e = launch_limb<LimbQ6K, 2, 4, kLimbPairSilu>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N);
+    }
+    if (e != hipSuccess) return e;
+    switch (q_d) {
+      case kQ4_K: return launch_limb<LimbQ4K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      case kQ8_0: return launch_limb<LimbQ8, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      case kQ5_K: return launch_limb<LimbQ5K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      default: return launch_limb<LimbQ6K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+    }
+  }
+  // wider rows: [g; u] in one launch, silu(g) * u formed as down stages its x
   switch (q_gu) {
     case kQ4_K: e = launch_limb<LimbQ4K, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
     case kQ8_0: e = launch_limb<LimbQ8, 1, 4, kLimbTwoMat>(g, 2 * N, E, rb1, x, gu, s, 512, 8, q6gu, u, N); break;
@@ -903,14 +942,24 @@ hipError_t launch_shexp_one(uint32_t q_gu, uint32_t q_d, const void* gate, const
 }
 
 // One token through the dense FFN's two matvec launches (limb kernels):
-// [g; u] = [gate; up] . x (both n_ff x n_embd, one launch, x staged once),
-// then out = xres + down . (silu(g) * u) (silu and the residual add inside).
+// h = silu(gate . x) * (up . x) (both n_ff x n_embd, one launch, x staged
+// once, each wave taking gate row q and up row q together), then
+// out = xres + down . h (the residual add inside).
 template <class F>
 static hipError_t launch_ffn1(const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_embd, int n_ff,
                               const float* x, float* gu, const float* xres, float* out, int q6s, hipStream_t s) {
   const int64_t rb1 = byte_size(F::kQuant, n_embd), rb2 = byte_size(F::kQuant, n_ff);
-  // gate and up: 2 n_ff rows, one window when n_embd <= 4096: 16 waves per CU
-  // as for other tall single-window matrices
+  // gate and up: n_ff row pairs, one window when n_embd <= 4096: 16 waves
+  // per CU as for other tall single-window matrices
+  // a gate row and an up row per item, storing h = silu(g) * u into gu[0, n_ff);
+  // down stages h as its x
+  if (n_embd <= 4096) {
+    hipError_t e = launch_limb<F, 2, 4, kLimbPairSilu>(gate, 2 * n_ff, n_embd, rb1, x, gu, s, 512, 16, q6s, up, n_ff);
+    if (e != hipSuccess) return e;
+    return launch_limb<F, 1, 4, kLimbResid>(down, n_embd, n_ff, rb2, gu, out, s, 512, 8, q6s, nullptr, 0, nullptr,
+                                            xres);
+  }
+  // wider rows: [g; u] in one launch, silu(g) * u formed as down stages its x
   hipError_t e = launch_limb<F, 1, 4, kLimbTwoMat>(gate, 2 * n_ff, n_embd, rb1, x, gu, s, 512, 16, q6s, up, n_ff);
   if (e != hipSuccess) return e;
   return launch_limb<F, 1, 4, kLimbSiluX | kLimbResid>(down, n_embd, n_ff, rb2, gu, out, s, 512, 8, q6s, nullptr,
