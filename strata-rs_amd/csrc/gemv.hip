@@ -299,7 +299,9 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // as row q of w (gate) and row q of w2 (up) and stores y[q] = silu(g) * u,
 // the same f32 expression kLimbSiluX stages, so the down launch stages one
 // vector instead of two.
-constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4, kLimbPairSilu = 8;
+// kLimbFine stages x in the 23-bit limbs (limb.hpp), as the modes that take
+// a silu(g) * u input (kLimbSiluX, kLimbResid, the shared expert's down) do.
+constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4, kLimbPairSilu = 8, kLimbFine = 16;
 
 // silu(g) * u in f32, g / (1 + exp(-g)) * u without contraction
 // (qwen35.rs:120-124, ops.rs:85-87)
@@ -319,6 +321,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
                                                         const float* xres) {  // xres may be y (in place)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   constexpr bool kLow = F::kQuant == kQ8_0 || F::kQuant == kIQ4_XS;  // signed codes: the low-limb sums
+  constexpr bool kFine = (MODE & (kLimbSiluX | kLimbResid | kLimbFine)) != 0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
   const int units = cols >> 6;
@@ -403,9 +406,9 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
                      a.z / (1.f + expf(-a.z)) * ua.z, a.w / (1.f + expf(-a.w)) * ua.w};
       const f32x4 h1{b.x / (1.f + expf(-b.x)) * ub.x, b.y / (1.f + expf(-b.y)) * ub.y,
                      b.z / (1.f + expf(-b.z)) * ub.z, b.w / (1.f + expf(-b.w)) * ub.w};
-      limb_group8<kLow>(lds8, cols, t, t < n8, h0, h1);
+      limb_group8<kLow, kFine>(lds8, cols, t, t < n8, h0, h1);
     } else {
-      limb_group8<kLow>(lds8, cols, t, t < n8, a, b);
+      limb_group8<kLow, kFine>(lds8, cols, t, t < n8, a, b);
     }
   };
 #pragma unroll
@@ -919,10 +922,10 @@ hipError_t launch_shexp_one(uint32_t q_gu, uint32_t q_d, const void* gate, const
     }
     if (e != hipSuccess) return e;
     switch (q_d) {
-      case kQ4_K: return launch_limb<LimbQ4K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
-      case kQ8_0: return launch_limb<LimbQ8, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
-      case kQ5_K: return launch_limb<LimbQ5K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
-      default: return launch_limb<LimbQ6K, 1, 4>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      case kQ4_K: return launch_limb<LimbQ4K, 1, 4, kLimbFine>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      case kQ8_0: return launch_limb<LimbQ8, 1, 4, kLimbFine>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      case kQ5_K: return launch_limb<LimbQ5K, 1, 4, kLimbFine>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
+      default: return launch_limb<LimbQ6K, 1, 4, kLimbFine>(w, E, N, rb2, gu, d, s, 512, 8, q6d);
     }
   }
   // wider rows: [g; u] in one launch, silu(g) * u formed as down stages its x

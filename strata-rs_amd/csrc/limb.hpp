@@ -10,11 +10,16 @@ namespace sh {
 // ================================================== batch-1 integer path ==
 // x as three int8 limbs. Each workgroup converts the f32 activations once:
 // per 32-column block a power-of-two scale 2^-k is chosen so that the block's
-// largest |x| times 2^k is below 2^22, and every element becomes the integer
-//   v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c,  a in [-64, 64], b, c in [0, 255]
-// (a is byte 2 of v, b byte 1, c byte 0, in two's complement). Each element
-// is represented to within 2^-23 of its block's maximum, as close to x as the
-// f32 activations themselves for elements near the maximum. Weight codes are
+// largest |x| times 2^k is below 2^22 (2^23 with FINE), and every element
+// becomes the integer
+//   v = rne(x * 2^k) = a * 2^16 + b * 2^8 + c,  b, c in [0, 255]
+// (a is byte 2 of v, b byte 1, c byte 0, in two's complement): a in [-64, 64],
+// each element within 2^-23 of its block's maximum; with FINE a in
+// [-128, 127] (a value that rounds up to 2^23 is held at 2^23 - 1), within
+// 2^-24, at two more instructions per element. Near the block maximum either
+// is as close to x as the f32 activations themselves; FINE serves inputs that
+// went through a chain of products (silu(g) * u), whose rounding the next
+// matvec passes on. Weight codes are
 // small non-negative integers, so the per-block dot products are exact
 // integer sums on v_dot4_i32_i8 (a) and v_dot4_u32_u8 (b, c), four weights
 // per instruction:
@@ -36,7 +41,7 @@ __host__ __device__ inline int limb_lds_bytes(int cols) { return 3 * plane_strid
 // block's maximum and sums with DPP moves, and lane t & ~3 writes the block's
 // record. K (the integer sum of the low limbs) is formed only when LOW is
 // set: signed Q8_0 codes need it; the unsigned codes of the k-quants do not.
-template <bool LOW>
+template <bool LOW, bool FINE = false>
 __device__ __forceinline__ void limb_group8(uint8_t* lds, int cols, int t, bool valid, f32x4 a, f32x4 b) {
   const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   float m = 0.f, s = 0.f;
@@ -49,11 +54,11 @@ __device__ __forceinline__ void limb_group8(uint8_t* lds, int cols, int t, bool 
   m = fmaxf(m, dpp_xor2(m));
   const float s16 = s + dpp_xor1(s);  // the lane pair's 16 columns
   const float s16_other = dpp_xor2(s16);
-  // k with m * 2^k < 2^22; for m == 0 any k works
+  // k with m * 2^k < 2^22 (2^23 FINE); for m == 0 any k works
   // (clamped so 2^k stays finite for blocks whose maximum is below 2^-104)
   int e = 0;
   (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
-  const int k = m > 0.f ? min(22 - e, 126) : 0;
+  const int k = m > 0.f ? min((FINE ? 23 : 22) - e, 126) : 0;
   const float up = ldexpf(1.f, k);
   // a NaN or infinite block keeps its NaN through the scale
   const float down = (m - m == 0.f) ? ldexpf(1.f, -k) : __builtin_nanf("");
@@ -61,9 +66,15 @@ __device__ __forceinline__ void limb_group8(uint8_t* lds, int cols, int t, bool 
   uint32_t low = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
-    const float tt = __builtin_fmaf(xs[i], up, 12582912.0f);
-    v[i] = __builtin_bit_cast(uint32_t, tt) - 0x4B400000u;
+    if constexpr (FINE) {
+      // rne(x * 2^k), |x * 2^k| < 2^23 (exact: 2^k is a power of two); the
+      // one value that can round up to 2^23 is held below it
+      v[i] = uint32_t(min(int(__builtin_rintf(xs[i] * up)), 0x7FFFFF));
+    } else {
+      // rne(x * 2^k) through the 1.5 * 2^23 magic constant (|x * 2^k| < 2^22)
+      const float tt = __builtin_fmaf(xs[i], up, 12582912.0f);
+      v[i] = __builtin_bit_cast(uint32_t, tt) - 0x4B400000u;
+    }
     if constexpr (LOW) low += v[i] & 0xFFFFu;
   }
   if constexpr (LOW) {

@@ -52,6 +52,8 @@ def check(got, want, x):
     ((8, 8, 8), 2048, 4096, 1, False),       # fused Q8_0
     ((13, 13, 13), 2048, 4096, 1, False),    # fused Q5_K
     ((14, 14, 14), 2048, 4096, 1, False),    # fused Q6_K
+    ((12, 12, 12), 8192, 1024, 1, False),    # fused, rows of two windows: h formed in down's staging
+    ((14, 14, 14), 8192, 1024, 1, True),
 ])
 def test_ffn_matches_oracle(oracle, quants, n_embd, n_ff, n_tok, in_place):
     say("ffn", quants, n_embd, n_ff, n_tok, in_place)

@@ -286,8 +286,8 @@ def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh)
     after a rounding pass), routing, the routed experts and the shared
     expert with its sigmoid gate, against the oracle token by token; 9
     tokens take two 8-token matvec launches. One token with gate and up of
-    one type runs the shared expert in two launches (gate and up as one
-    matvec, silu(g) * u formed inside the down launch), and a router and
+    one type runs the shared expert in two launches (gate and up rows paired
+    in one matvec that stores silu(g) * u, then down), and a router and
     gate input of one plain type share a launch."""
     n_expert, n_embd, n_ff, n_sh, top_k = 32, 512, 256, 256, 6
     say("moe layer", n_tok, q_router, q_inp, q_sh)
@@ -298,6 +298,20 @@ def test_moe_layer_matches_oracle(backend, oracle, n_tok, q_router, q_inp, q_sh)
     for i in range(n_tok):
         ref = oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[i], top_k)
         check_parity(out[i], ref, "moe")
+
+
+@pytest.mark.parametrize("q_sh", [(12, 12, 14), (13, 13, 8)])
+def test_moe_layer_wide_rows(backend, oracle, q_sh):
+    """One token with rows of more than one 4096-column window: the shared
+    expert's gate and up run as one 2 n_ff-row matvec and down forms
+    silu(g) * u as it stages its x (the paired mode takes one window)."""
+    n_expert, n_embd, n_ff, n_sh, top_k = 8, 8192, 256, 256, 2
+    say("moe layer wide", q_sh)
+    q, t = layer_tensors(n_expert, n_embd, n_ff, n_sh, 8700, 0, 0, q_sh)
+    x = S.normal_f32(8701, n_embd).reshape(1, n_embd)
+    views = layer_views("Lw", q, t, n_expert, n_embd, n_ff, n_sh)
+    out = backend.moe_layer(*views, x, top_k)
+    check_parity(out[0], oracle.moe_layer(q, t, n_expert, n_embd, n_ff, n_sh, x[0], top_k), "moe")
 
 
 @pytest.fixture(scope="module")
