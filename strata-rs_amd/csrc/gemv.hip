@@ -311,7 +311,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 constexpr int kLimbMaxRowsOneWin = 64;  // row groups a wave may take when rows are one window
 
-template <class F, int R, int MAXQ, int MODE = 0, int NPRE = 1>
+template <class F, int R, int MAXQ, int MODE = 0, int NPRE = 1, bool SPREAD = false>
 __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restrict__ w, int rows,
                                                         int cols, int64_t row_bytes,
                                                         const float* __restrict__ x,
@@ -327,8 +327,16 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
   const int units = cols >> 6;
   const int nwin = (units + 63) >> 6;
   const int n_rg = (rows + R - 1) / R;
-  const int rg0 = wave * per;
-  const int my = max(0, min(per, n_rg - rg0));  // row groups of this wave
+  // Row groups of this wave: a run of `per` from wave * per; or, with
+  // SPREAD (rows of one window), every W-th from the wave's index (W the
+  // waves of the launch, per = ceil(n_rg / W)), so that the waves read one
+  // stretch of the matrix at a time (the 151936-row Q6_K head: 111 -> 104
+  // us). No division here: it would delay the first weight loads.
+  static_assert(!SPREAD || NPRE == 1, "spread rows are single-window rows");
+  const int W = int(gridDim.x) * int(blockDim.x >> 6);
+  const int gstep = SPREAD ? W : 1;
+  const int rg0 = SPREAD ? wave : wave * per;
+  const int my = SPREAD ? max(0, per - (wave + (per - 1) * W >= n_rg ? 1 : 0)) : max(0, min(per, n_rg - rg0));
   const int n_items = my * nwin;
 
   // per-lane offsets: window 0, and the clamped unit of a partial last window
@@ -350,7 +358,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     const typename F::Off o = item_off(wn);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min((rg0 + qq) * R + r, rows - 1);
+      const int row = min((rg0 + qq * gstep) * R + r, rows - 1);
       const uint8_t* base = w + int64_t(row) * row_bytes;
       if constexpr ((MODE & kLimbTwoMat) != 0)
         base = row >= rows1 ? w2 + int64_t(row - rows1) * row_bytes : base;
@@ -434,42 +442,41 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
   for (int q = 0; q < MAXQ; ++q)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[q][r] = 0.f;
-  XLimbs xl;
+  typename LimbX<F>::T xl;
   int cw = 0, cq = 0;  // item being computed
   auto step = [&](const typename F::Load* L) {
     if (cq == 0) {
       const int u = cw == nwin - 1 ? ulast : cw * 64 + lane;
-      load_limbs(lds8, cols, u, xl);
+      LimbX<F>::load(lds8, cols, u, xl);
     }
     const bool ok = cw < nwin - 1 || lane_valid_last;
-    if (nwin == 1) {
-      // a single window: each item is whole rows, final at once (so a wave
-      // may take any number of them, and fewer workgroups stage x)
+    if constexpr (NPRE == 1) {
+      // a single window (NPRE == nwin): each item is whole rows, final at
+      // once (so a wave may take any number of them, and fewer workgroups
+      // stage x)
       if constexpr ((MODE & kLimbPairSilu) != 0) {
         static_assert(R == 2, "a gate row and an up row per item");
         const float g = wave_sum_dpp(ok ? F::dot(L[0], xl, lane, flags) : 0.f);
         const float u = wave_sum_dpp(ok ? F::dot(L[1], xl, lane, flags) : 0.f);
-        const int q = rg0 + cq;
+        const int q = rg0 + cq * gstep;
         if (lane == 63 && q < n_rg) y[q] = silu_mul(g, u);
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const float t = F::dot(L[r], xl, lane, flags);
           const float v = wave_sum_dpp(ok ? t : 0.f);
-          const int row = (rg0 + cq) * R + r;
+          const int row = (rg0 + cq * gstep) * R + r;
           if (lane == 63 && row < rows) y[row] = (MODE & kLimbResid) != 0 ? __fadd_rn(xres[row], v) : v;
         }
       }
     } else if constexpr ((MODE & kLimbPairSilu) == 0) {  // the pair mode takes one window only
+      // one copy of the dot, its sum selected into row group cq's accumulator
 #pragma unroll
-      for (int q = 0; q < MAXQ; ++q) {
-        if (q == cq) {
+      for (int r = 0; r < R; ++r) {
+        const float t = F::dot(L[r], xl, lane, flags);
+        const float v = ok ? t : 0.f;
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const float t = F::dot(L[r], xl, lane, flags);
-            acc[q][r] += ok ? t : 0.f;
-          }
-        }
+        for (int q = 0; q < MAXQ; ++q) acc[q][r] = q == cq ? acc[q][r] + v : acc[q][r];
       }
     }
     if (++cq == my) {
@@ -483,7 +490,7 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
     issue(A);
     if (i + 1 < n_items) step(B);
   }
-  if (nwin == 1 || (MODE & kLimbPairSilu) != 0) return;  // stored as computed
+  if constexpr (NPRE == 1 || (MODE & kLimbPairSilu) != 0) return;  // stored as computed
 #pragma unroll
   for (int q = 0; q < MAXQ; ++q) {
     if (q < my) {
@@ -720,10 +727,14 @@ template <class F, int R, int MAXQ, int MODE = 0>
 static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_bytes,
                               const float* x, float* y, hipStream_t stream, int threads,
                               int waves_per_cu, int flags = 0, const uint8_t* w2 = nullptr, int rows1 = 0,
-                              const float* xu = nullptr, const float* xres = nullptr) {
+                              const float* xu = nullptr, const float* xres = nullptr, bool spread = false) {
   const int wpg = threads / 64;
   const int n_rg = (rows + R - 1) / R;
   const int units = cols >> 6, nwin = (units + 63) >> 6;
+  // 512 threads stage 4096 columns a round, so the kernel's x rounds NPRE
+  // equal its windows when there is one (the single-window code is chosen
+  // at compile time); the paired gate/up rows take one window only
+  if (threads != 512 || ((MODE & kLimbPairSilu) != 0 && nwin != 1)) return hipErrorInvalidValue;
   const int min_waves = cu_count() * waves_per_cu;
   int per = (n_rg + min_waves - 1) / min_waves;
   // row sums in registers across windows: at most MAXQ row groups a wave;
@@ -733,11 +744,16 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   if (nwin == 1 && per > kLimbMaxRowsOneWin) per = kLimbMaxRowsOneWin;
   const int waves = (n_rg + per - 1) / per;
   const int blocks = (waves + wpg - 1) / wpg;
+  // spread rows: each of the launch's waves takes every W-th row group
+  if (spread && nwin == 1) per = (n_rg + blocks * wpg - 1) / (blocks * wpg);
   // x rounds (threads * 8 columns each) whose loads go ahead of the weights
   const int rounds = (cols + threads * 8 - 1) / (threads * 8);
   const dim3 grid = dim3(unsigned(blocks)), block = dim3(unsigned(threads));
   const size_t lds = size_t(limb_lds_bytes(cols));
-  if (rounds <= 1)
+  if (rounds <= 1 && spread)
+    hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 1, true>), grid, block, lds, stream, w, rows, cols,
+                       row_bytes, x, y, per, flags, w2, rows1, xu, xres);
+  else if (rounds <= 1)
     hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 1>), grid, block, lds, stream, w, rows, cols, row_bytes, x,
                        y, per, flags, w2, rows1, xu, xres);
   else if (rounds == 2)
@@ -818,6 +834,7 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
   // rows to stream); 8 otherwise (fewer workgroups stage x, and multi-window
   // rows keep the x limbs of every window they visit)
   const int wpc = (cols <= 4096 && rows >= 8192) ? 16 : 8;
+  const bool spread = wpc == 16;  // tall single-window matrices: rows spread over the waves
   // x for all of the batch must fit in LDS; a larger batch runs in slices
   int per = int(kMaxLds / lds_bytes(int(cols), 1));
   if (per > 8) per = 8;
@@ -828,30 +845,33 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
     hipError_t e;
     switch (quant) {
       case kQ4_K:
-        e = nb == 1 ? launch_limb<LimbQ4K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
+        e = nb == 1 ? launch_limb<LimbQ4K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc, 0,
+                                                  nullptr, 0, nullptr, nullptr, spread)
                     : launch_nb<FmtQ4K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       case kQ8_0:
-        e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
+        e = nb == 1 ? launch_limb<LimbQ8, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc, 0,
+                                                 nullptr, 0, nullptr, nullptr, spread)
                     : launch_nb<FmtQ8>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       case kQ5_K:
-        e = nb == 1 ? launch_limb<LimbQ5K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc)
+        e = nb == 1 ? launch_limb<LimbQ5K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc, 0,
+                                                  nullptr, 0, nullptr, nullptr, spread)
                     : launch_nb<FmtQ5K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       case kIQ4_XS:  // the reading (reference or ggml qs bytes) is a template argument
         if (q6_signed)
           e = nb == 1 ? launch_limb<LimbIQ4XS<true>, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512,
-                                                            wpc)
+                                                            wpc, 0, nullptr, 0, nullptr, nullptr, spread)
                       : launch_nb<FmtIQ4XS<true>>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         else
           e = nb == 1 ? launch_limb<LimbIQ4XS<false>, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512,
-                                                             wpc)
+                                                             wpc, 0, nullptr, 0, nullptr, nullptr, spread)
                       : launch_nb<FmtIQ4XS<false>>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
       default:  // kQ6_K
         e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,
-                                                  q6_signed)
+                                                  q6_signed, nullptr, 0, nullptr, nullptr, spread)
                     : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
     }
     if (e != hipSuccess) return e;

@@ -344,50 +344,123 @@ struct LimbIQ4XS {
   }
 };
 
-// Q6_K with integer dots: unit u = (super-block u/4, quarter j = u%4) as in
-// FmtQ6K; the 6-bit codes 0..63 go straight into the dots and the -32
-// offset is taken off with the per-16 sums of x.
+// Q6_K with integer dots. Unit u covers half h = (u >> 1) & 1 of super-block
+// u / 4 split between the lanes of a pair by t = u & 1: the lane takes the
+// 16 positions l in [16 t, 16 t + 16) of the half's four 32-element groups
+// i (elements 128 h + 32 i + l, dequant.rs:208-234), so each of its four
+// 16-element sub-blocks (scale 8 h + 2 i + t) is whole and it reads only its
+// own 16 bytes of ql[l], ql[l + 32] and qh[l] (the quarter-per-lane split
+// has both lanes of a pair read all 96 of them). The codes 0..63 go straight
+// into the dots and the -32 offset is taken off with the per-16 sums of x.
+struct XLimbsQ6 {
+  u32x4 a[4], b[4], c[4];  // limb words of group i's 16 columns
+  uint32_t xs[4], ks[4];   // group i's sum of those 16 x, and its block's 2^-k
+};
+
 struct LimbQ6K {
   static constexpr uint32_t kQuant = kQ6_K;
-  using Load = FmtQ6K::Load;
+  struct Load {
+    u32x4 a;       // ql[l .. l + 16) of the lane, from the dword below
+    uint32_t a4;   // the dword after (bytes past 16 when misaligned)
+    u32x4 b;       // ql[l + 32 ..]
+    uint32_t b4;
+    u32x4 h;       // qh[l ..]
+    uint32_t h4;
+    uint32_t s0, s1, s2;  // scales[8 h .. 8 h + 8) from the dword below
+    uint32_t d;           // d | misalignment << 16
+  };
   static constexpr int kWinBytes = 16 * 210;
   struct Off {
     int h, q;
   };
-  // h: the super-block's byte offset, q: the quarter 0..3
+  // h: the super-block's byte offset, q: 2 * half + lane of the pair
   __device__ static __forceinline__ Off offsets(int u) { return {(u >> 2) * 210, u & 3}; }
+  // Rows start on even bytes (the entry points check it), so a block's
+  // misalignment is 0 or 2 and every dword read below ends inside the block;
+  // s2 is read only when misaligned (aligned, it would run 2 bytes past).
   __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    FmtQ6K::load(row + o.h, o.q, L);
+    const uint8_t* blk = row + o.h;
+    const int h = o.q >> 1, t = o.q & 1;
+    const uint32_t shift = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    const uint8_t* base = blk - shift;
+    const uint8_t* ql = base + 64 * h + 16 * t;
+    L.a = ld16(ql);
+    L.a4 = ld4(ql + 16);
+    L.b = ld16(ql + 32);
+    L.b4 = ld4(ql + 48);  // ends at most at byte 133 of the block
+    const uint8_t* qh = base + 128 + 32 * h + 16 * t;
+    L.h = ld16(qh);
+    L.h4 = ld4(qh + 16);  // ends at most at byte 195
+    const uint8_t* sc = base + 192 + 8 * h;
+    L.s0 = ld4(sc);
+    L.s1 = ld4(sc + 4);
+    L.s2 = shift ? ld4(sc + 8) : 0u;
+    L.d = uint32_t(*reinterpret_cast<const uint16_t*>(blk + 208)) | (shift << 16);
   }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int q6_signed) {
-    const uint32_t tp = uint32_t(lane) & 1u;
-    const uint32_t s = L.shift;
-    const uint32_t qlr[17] = {L.l0.x, L.l0.y, L.l0.z, L.l0.w, L.l1.x, L.l1.y, L.l1.z, L.l1.w, L.l2.x,
-                              L.l2.y, L.l2.z, L.l2.w, L.l3.x, L.l3.y, L.l3.z, L.l3.w, L.l4};
-    const uint32_t qhr[9] = {L.h0.x, L.h0.y, L.h0.z, L.h0.w, L.h1.x, L.h1.y, L.h1.z, L.h1.w, L.h2};
-    const uint32_t scw = realign(L.s0, L.s1, s);
-    int sa[4] = {0, 0, 0, 0};
-    uint32_t sb[4] = {0, 0, 0, 0}, sc[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      uint32_t va, vb;
-      q6_code_words(qlr[k], qlr[k + 1], qlr[8 + k], qlr[9 + k], qhr[k], qhr[k + 1], s, tp, va, vb);
-      const int ga = k >> 2, gb = 2 + (k >> 2);
-      dot_limbs(va, limb_word(x.a, k), limb_word(x.b, k), limb_word(x.c, k), sa[ga], sb[ga], sc[ga]);
-      dot_limbs(vb, limb_word(x.a, 8 + k), limb_word(x.b, 8 + k), limb_word(x.c, 8 + k), sa[gb], sb[gb], sc[gb]);
-    }
-    float scf[4];
+  // Limb words and sums of unit u's columns: group i lies in the 64-column
+  // LDS unit 2 (u >> 1) + (i >> 1), at byte 32 (i & 1) + 16 t of it, and
+  // in x block 4 (u >> 1) + i (half t of its two 16-column sums).
+  __device__ static __forceinline__ void load_x(const uint8_t* lds, int cols, int u, XLimbsQ6& o) {
+    const int ps = plane_stride(cols);
+    const int p = u >> 1, t = u & 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t byte = (scw >> (8 * i)) & 0xFFu;
-      scf[i] = q6_signed ? float(int8_t(byte)) : float(byte);
+      const int off = 80 * (2 * p + (i >> 1)) + 32 * (i & 1) + 16 * t;
+      o.a[i] = *reinterpret_cast<const u32x4*>(lds + off);
+      o.b[i] = *reinterpret_cast<const u32x4*>(lds + ps + off);
+      o.c[i] = *reinterpret_cast<const u32x4*>(lds + 2 * ps + off);
+      const u32x4 rec = *reinterpret_cast<const u32x4*>(lds + 3 * ps + 16 * (4 * p + i));
+      o.xs[i] = t ? rec.y : rec.x;
+      o.ks[i] = rec.z;
     }
-    const float xs[4] = {fw(x.i0.x), fw(x.i0.y), fw(x.i1.x), fw(x.i1.y)};
-    const float ks[4] = {fw(x.i0.z), fw(x.i0.z), fw(x.i1.z), fw(x.i1.z)};
-    float t = 0.f;
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbsQ6& x, int lane, int q6_signed) {
+    const uint32_t t = uint32_t(lane) & 1u;
+    const uint32_t s = L.d >> 16;
+    const uint32_t qa[5] = {L.a.x, L.a.y, L.a.z, L.a.w, L.a4};
+    const uint32_t qb[5] = {L.b.x, L.b.y, L.b.z, L.b.w, L.b4};
+    const uint32_t qh[5] = {L.h.x, L.h.y, L.h.z, L.h.w, L.h4};
+    // scales 8 h + 2 i + t: bytes t and t + 2 of the first realigned word
+    // (groups 0, 1) and of the second (groups 2, 3)
+    const uint32_t sw[2] = {realign(L.s0, L.s1, s), realign(L.s1, L.s2, s)};
+    constexpr uint32_t kLo = 0x0F0F0F0Fu, kHi = 0x30303030u;
+    float t_sum = 0.f;
+    // one group at a time (three live sums): group i's codes are the low
+    // (i < 2) or high nibbles of ql[l] (i even) or ql[l + 32] (i odd) under
+    // bits 4-5 from qh bit pair i; the realignment and the nibble shift are
+    // one funnel shift
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t += scf[i] * (limb_value(sa[i], sb[i], sc[i]) * ks[i] - 32.f * xs[i]);
-    return h2f(L.d) * t;
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t* q = (i & 1) ? qb : qa;
+      int sa = 0;
+      uint32_t sb = 0, sc = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = __builtin_amdgcn_alignbit(q[w + 1], q[w], 8u * s + 4u * uint32_t(i >> 1)) & kLo;
+        const uint32_t hb = __builtin_amdgcn_alignbyte(qh[w + 1], qh[w], s);
+        const uint32_t hi = (i == 0 ? hb << 4 : i == 1 ? hb << 2 : i == 2 ? hb : hb >> 2) & kHi;
+        dot_limbs(lo | hi, limb_word(x.a, 4 * i + w), limb_word(x.b, 4 * i + w), limb_word(x.c, 4 * i + w), sa, sb,
+                  sc);
+      }
+      const uint32_t byte = (sw[i >> 1] >> (8u * t + 16u * uint32_t(i & 1))) & 0xFFu;
+      const float scf = q6_signed ? float(int8_t(byte)) : float(byte);
+      t_sum += scf * (limb_value(sa, sb, sc) * fw(x.ks[i]) - 32.f * fw(x.xs[i]));
+    }
+    return h2f(L.d) * t_sum;
+  }
+};
+
+// The x limbs a unit of F reads, and how it reads them.
+template <class F>
+struct LimbX {
+  using T = XLimbs;
+  __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) { load_limbs(lds, cols, u, o); }
+};
+template <>
+struct LimbX<LimbQ6K> {
+  using T = XLimbsQ6;
+  __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) {
+    LimbQ6K::load_x(lds, cols, u, o);
   }
 };
 
