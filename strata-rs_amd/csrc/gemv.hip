@@ -735,6 +735,8 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   // equal its windows when there is one (the single-window code is chosen
   // at compile time); the paired gate/up rows take one window only
   if (threads != 512 || ((MODE & kLimbPairSilu) != 0 && nwin != 1)) return hipErrorInvalidValue;
+  // units that read whole rows through LDS take rows of one window
+  if (LimbX<F>::kWaveLds > 0 && (nwin != 1 || F::kWinBytes != row_bytes)) return hipErrorInvalidValue;
   const int min_waves = cu_count() * waves_per_cu;
   int per = (n_rg + min_waves - 1) / min_waves;
   // row sums in registers across windows: at most MAXQ row groups a wave;
@@ -749,7 +751,7 @@ static hipError_t launch_limb(const uint8_t* w, int rows, int cols, int64_t row_
   // x rounds (threads * 8 columns each) whose loads go ahead of the weights
   const int rounds = (cols + threads * 8 - 1) / (threads * 8);
   const dim3 grid = dim3(unsigned(blocks)), block = dim3(unsigned(threads));
-  const size_t lds = size_t(limb_lds_bytes(cols));
+  const size_t lds = size_t(limb_lds_bytes(cols)) + size_t(LimbX<F>::kWaveLds) * wpg;
   if (rounds <= 1 && spread)
     hipLaunchKernelGGL((gemv_limb_kernel<F, R, MAXQ, MODE, 1, true>), grid, block, lds, stream, w, rows, cols,
                        row_bytes, x, y, per, flags, w2, rows1, xu, xres);
@@ -869,10 +871,14 @@ hipError_t launch_gemv(uint32_t quant, const void* wv, int64_t rows, int64_t col
                                                              wpc, 0, nullptr, 0, nullptr, nullptr, spread)
                       : launch_nb<FmtIQ4XS<false>>(nb, w, int(rows), int(cols), row_bytes, xb, yb, 0, stream);
         break;
-      default:  // kQ6_K
-        e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,
-                                                  q6_signed, nullptr, 0, nullptr, nullptr, spread)
-                    : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
+      default:  // kQ6_K: rows of 4096 columns on 16-byte boundaries are read whole
+        if (nb == 1 && row_bytes == LimbQ6KRow::kRowBytes && (reinterpret_cast<uintptr_t>(w) & 15u) == 0)
+          e = launch_limb<LimbQ6KRow, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc, q6_signed,
+                                            nullptr, 0, nullptr, nullptr, spread);
+        else
+          e = nb == 1 ? launch_limb<LimbQ6K, 1, 4>(w, int(rows), int(cols), row_bytes, xb, yb, stream, 512, wpc,
+                                                    q6_signed, nullptr, 0, nullptr, nullptr, spread)
+                      : launch_nb<FmtQ6K>(nb, w, int(rows), int(cols), row_bytes, xb, yb, q6_signed, stream);
     }
     if (e != hipSuccess) return e;
   }

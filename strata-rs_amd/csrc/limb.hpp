@@ -378,24 +378,28 @@ struct LimbQ6K {
   // Rows start on even bytes (the entry points check it), so a block's
   // misalignment is 0 or 2 and every dword read below ends inside the block;
   // s2 is read only when misaligned (aligned, it would run 2 bytes past).
-  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
-    const uint8_t* blk = row + o.h;
-    const int h = o.q >> 1, t = o.q & 1;
-    const uint32_t shift = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
-    const uint8_t* base = blk - shift;
+  // `base` is the dword boundary `shift` bytes below the block; LDS sources
+  // take 16-byte reads that promise 4-byte alignment only.
+  template <bool LDS>
+  __device__ static __forceinline__ void load_at(const uint8_t* base, uint32_t shift, int h, int t, Load& L) {
     const uint8_t* ql = base + 64 * h + 16 * t;
-    L.a = ld16(ql);
+    L.a = LDS ? ld16u(ql) : ld16(ql);
     L.a4 = ld4(ql + 16);
-    L.b = ld16(ql + 32);
+    L.b = LDS ? ld16u(ql + 32) : ld16(ql + 32);
     L.b4 = ld4(ql + 48);  // ends at most at byte 133 of the block
     const uint8_t* qh = base + 128 + 32 * h + 16 * t;
-    L.h = ld16(qh);
+    L.h = LDS ? ld16u(qh) : ld16(qh);
     L.h4 = ld4(qh + 16);  // ends at most at byte 195
     const uint8_t* sc = base + 192 + 8 * h;
     L.s0 = ld4(sc);
     L.s1 = ld4(sc + 4);
     L.s2 = shift ? ld4(sc + 8) : 0u;
-    L.d = uint32_t(*reinterpret_cast<const uint16_t*>(blk + 208)) | (shift << 16);
+    L.d = uint32_t(*reinterpret_cast<const uint16_t*>(base + shift + 208)) | (shift << 16);
+  }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    const uint8_t* blk = row + o.h;
+    const uint32_t shift = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
+    load_at<false>(blk - shift, shift, o.q >> 1, o.q & 1, L);
   }
   // Limb words and sums of unit u's columns: group i lies in the 64-column
   // LDS unit 2 (u >> 1) + (i >> 1), at byte 32 (i & 1) + 16 t of it, and
@@ -450,17 +454,71 @@ struct LimbQ6K {
   }
 };
 
-// The x limbs a unit of F reads, and how it reads them.
+// Q6_K rows of 4096 columns (3360 bytes, 16-byte aligned), the unit of
+// LimbQ6K read a whole row at a time: the wave's loads take the row in
+// contiguous 16-byte pieces (lane i: bytes 16 i + 1024 k), which the memory
+// system serves as whole lines, and each lane then gathers its unit's bytes
+// from a per-wave LDS copy of the row. LimbQ6K's own loads are ten partial-
+// line reads a row (151936-row head: 104 -> 97 us).
+struct XLimbsQ6Row : XLimbsQ6 {
+  uint8_t* buf;  // the wave's row buffer in LDS
+};
+
+struct LimbQ6KRow {
+  static constexpr uint32_t kQuant = kQ6_K;
+  static constexpr int kRowBytes = 3360;
+  static constexpr int kPieces = (kRowBytes + 1023) / 1024;
+  struct Load {
+    u32x4 p[kPieces];
+  };
+  static constexpr int kWinBytes = kRowBytes;
+  using Off = LimbQ6K::Off;
+  __device__ static __forceinline__ Off offsets(int u) { return {0, u & 3}; }  // rows of one window
+  __device__ static __forceinline__ void load(const uint8_t* row, Off, Load& L) {
+    const int ln = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) L.p[k] = ld16(row + min(16 * ln + 1024 * k, kRowBytes - 16));
+  }
+  __device__ static __forceinline__ float dot(const Load& L, const XLimbsQ6Row& x, int lane, int q6_signed) {
+    // the row into LDS (a wave's LDS operations run in order, so the reads
+    // below see every lane's piece, and the next row's writes come after
+    // them), then the unit's bytes from it: block lane / 4, 2-byte aligned
+#pragma unroll
+    for (int k = 0; k < kPieces; ++k) {
+      const int off = 16 * lane + 1024 * k;
+      if (off < kRowBytes) *reinterpret_cast<u32x4*>(x.buf + off) = L.p[k];
+    }
+    const int sbo = (lane >> 2) * 210;
+    const uint32_t shift = uint32_t(sbo) & 3u;
+    LimbQ6K::Load q;
+    LimbQ6K::load_at<true>(x.buf + sbo - int(shift), shift, (lane >> 1) & 1, lane & 1, q);
+    return LimbQ6K::dot(q, x, lane, q6_signed);
+  }
+};
+
+// The x limbs a unit of F reads, and how it reads them; LDS bytes per wave
+// that F needs beyond the limbs.
 template <class F>
 struct LimbX {
   using T = XLimbs;
+  static constexpr int kWaveLds = 0;
   __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) { load_limbs(lds, cols, u, o); }
 };
 template <>
 struct LimbX<LimbQ6K> {
   using T = XLimbsQ6;
+  static constexpr int kWaveLds = 0;
   __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) {
     LimbQ6K::load_x(lds, cols, u, o);
+  }
+};
+template <>
+struct LimbX<LimbQ6KRow> {
+  using T = XLimbsQ6Row;
+  static constexpr int kWaveLds = LimbQ6KRow::kRowBytes;
+  __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) {
+    LimbQ6K::load_x(lds, cols, u, o);
+    o.buf = const_cast<uint8_t*>(lds) + limb_lds_bytes(cols) + int(threadIdx.x >> 6) * LimbQ6KRow::kRowBytes;
   }
 };
 
