@@ -170,6 +170,10 @@ struct LimbQ4K {
     L.a = ld16(row + o.h + o.q);
     L.b = ld16(row + o.h + o.q + 16);
   }
+  // unit `lane` of a window copied to LDS (blocks on 16-byte boundaries)
+  __device__ static __forceinline__ void load_lds(const uint8_t* win, int lane, Load& L) {
+    load(win, offsets(lane), L);
+  }
   __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
     const int g = lane & 3;
     const uint32_t sh = (g & 1) << 4;
@@ -213,6 +217,10 @@ struct LimbQ5K {
     L.h1 = ld16(row + o.h + 32);
     L.a = ld16(row + o.h + o.q);
     L.b = ld16(row + o.h + o.q + 16);
+  }
+  // unit `lane` of a window copied to LDS (blocks on 16-byte boundaries)
+  __device__ static __forceinline__ void load_lds(const uint8_t* win, int lane, Load& L) {
+    load(win, offsets(lane), L);
   }
   __device__ static __forceinline__ float dot(const Load& L, const XLimbs& x, int lane, int) {
     const int g = lane & 3;
@@ -401,6 +409,12 @@ struct LimbQ6K {
     const uint32_t shift = uint32_t(reinterpret_cast<uintptr_t>(blk)) & 3u;
     load_at<false>(blk - shift, shift, o.q >> 1, o.q & 1, L);
   }
+  // unit `lane` of a window copied to LDS from a 16-byte boundary
+  __device__ static __forceinline__ void load_lds(const uint8_t* win, int lane, Load& L) {
+    const int sbo = (lane >> 2) * 210;
+    const uint32_t shift = uint32_t(sbo) & 3u;
+    load_at<true>(win + sbo - int(shift), shift, (lane >> 1) & 1, lane & 1, L);
+  }
   // Limb words and sums of unit u's columns: group i lies in the 64-column
   // LDS unit 2 (u >> 1) + (i >> 1), at byte 32 (i & 1) + 16 t of it, and
   // in x block 4 (u >> 1) + i (half t of its two 16-column sums).
@@ -454,46 +468,49 @@ struct LimbQ6K {
   }
 };
 
-// Q6_K rows of 4096 columns (3360 bytes, 16-byte aligned), the unit of
-// LimbQ6K read a whole row at a time: the wave's loads take the row in
-// contiguous 16-byte pieces (lane i: bytes 16 i + 1024 k), which the memory
-// system serves as whole lines, and each lane then gathers its unit's bytes
-// from a per-wave LDS copy of the row. LimbQ6K's own loads are ten partial-
-// line reads a row (151936-row head: 104 -> 97 us).
-struct XLimbsQ6Row : XLimbsQ6 {
-  uint8_t* buf;  // the wave's row buffer in LDS
-};
-
-struct LimbQ6KRow {
-  static constexpr uint32_t kQuant = kQ6_K;
-  static constexpr int kRowBytes = 3360;
-  static constexpr int kPieces = (kRowBytes + 1023) / 1024;
+// A unit F read a whole 4096-column window at a time: the wave's loads take
+// the window's bytes in contiguous 16-byte pieces (lane i: bytes 16 i +
+// 1024 k), which the memory system serves as whole lines, and each lane then
+// reads its unit's bytes (F::load_lds) from a per-wave LDS copy of the window.
+// F's own per-unit loads touch partial lines: Q6_K's are ten reads a row (the
+// 151936x4096 head: 103 -> 92 us). Rows of whole windows on 16-byte
+// boundaries only (the launcher checks).
+template <class F>
+struct LimbWin {
+  static constexpr uint32_t kQuant = F::kQuant;
+  static constexpr int kWinBytes = F::kWinBytes;
+  static constexpr int kPieces = (kWinBytes + 1023) / 1024;
+  static_assert(kWinBytes % 16 == 0, "windows of whole 16-byte pieces");
   struct Load {
     u32x4 p[kPieces];
   };
-  static constexpr int kWinBytes = kRowBytes;
-  using Off = LimbQ6K::Off;
-  __device__ static __forceinline__ Off offsets(int u) { return {0, u & 3}; }  // rows of one window
-  __device__ static __forceinline__ void load(const uint8_t* row, Off, Load& L) {
-    const int ln = threadIdx.x & 63;
+  using Off = typename F::Off;
+  // h: the window's byte offset in the row, q: the lane's unit in it
+  __device__ static __forceinline__ Off offsets(int u) { return {(u >> 6) * kWinBytes, u & 63}; }
+  __device__ static __forceinline__ void load(const uint8_t* row, Off o, Load& L) {
+    const uint8_t* win = row + o.h;
 #pragma unroll
-    for (int k = 0; k < kPieces; ++k) L.p[k] = ld16(row + min(16 * ln + 1024 * k, kRowBytes - 16));
+    for (int k = 0; k < kPieces; ++k) L.p[k] = ld16(win + min(16 * o.q + 1024 * k, kWinBytes - 16));
   }
-  __device__ static __forceinline__ float dot(const Load& L, const XLimbsQ6Row& x, int lane, int q6_signed) {
-    // the row into LDS (a wave's LDS operations run in order, so the reads
-    // below see every lane's piece, and the next row's writes come after
-    // them), then the unit's bytes from it: block lane / 4, 2-byte aligned
+  template <class X>
+  __device__ static __forceinline__ float dot(const Load& L, const X& x, int lane, int flags) {
+    // the window into LDS (a wave's LDS operations run in order, so the
+    // reads below see every lane's piece, and the next window's writes come
+    // after them), then the unit's bytes from it
 #pragma unroll
     for (int k = 0; k < kPieces; ++k) {
       const int off = 16 * lane + 1024 * k;
-      if (off < kRowBytes) *reinterpret_cast<u32x4*>(x.buf + off) = L.p[k];
+      if (off < kWinBytes) *reinterpret_cast<u32x4*>(x.buf + off) = L.p[k];
     }
-    const int sbo = (lane >> 2) * 210;
-    const uint32_t shift = uint32_t(sbo) & 3u;
-    LimbQ6K::Load q;
-    LimbQ6K::load_at<true>(x.buf + sbo - int(shift), shift, (lane >> 1) & 1, lane & 1, q);
-    return LimbQ6K::dot(q, x, lane, q6_signed);
+    typename F::Load q;
+    F::load_lds(x.buf, lane, q);
+    return F::dot(q, x, lane, flags);
   }
+};
+
+template <class XT>
+struct XWithBuf : XT {
+  uint8_t* buf;  // the wave's window buffer in LDS
 };
 
 // The x limbs a unit of F reads, and how it reads them; LDS bytes per wave
@@ -512,13 +529,13 @@ struct LimbX<LimbQ6K> {
     LimbQ6K::load_x(lds, cols, u, o);
   }
 };
-template <>
-struct LimbX<LimbQ6KRow> {
-  using T = XLimbsQ6Row;
-  static constexpr int kWaveLds = LimbQ6KRow::kRowBytes;
+template <class F>
+struct LimbX<LimbWin<F>> {
+  using T = XWithBuf<typename LimbX<F>::T>;
+  static constexpr int kWaveLds = F::kWinBytes;
   __device__ static __forceinline__ void load(const uint8_t* lds, int cols, int u, T& o) {
-    LimbQ6K::load_x(lds, cols, u, o);
-    o.buf = const_cast<uint8_t*>(lds) + limb_lds_bytes(cols) + int(threadIdx.x >> 6) * LimbQ6KRow::kRowBytes;
+    LimbX<F>::load(lds, cols, u, o);
+    o.buf = const_cast<uint8_t*>(lds) + limb_lds_bytes(cols) + int(threadIdx.x >> 6) * F::kWinBytes;
   }
 };
 

@@ -52,6 +52,7 @@ def check(got, want, x):
     ((8, 8, 8), 2048, 4096, 1, False),       # fused Q8_0
     ((13, 13, 13), 2048, 4096, 1, False),    # fused Q5_K
     ((14, 14, 14), 2048, 4096, 1, False),    # fused Q6_K
+    ((14, 14, 14), 4096, 2048, 1, False),    # fused Q6_K, gate/up rows of one whole window (read whole)
     ((12, 12, 12), 8192, 1024, 1, False),    # fused, rows of two windows: h formed in down's staging
     ((14, 14, 14), 8192, 1024, 1, True),
 ])
