@@ -211,6 +211,31 @@ def test_gemv_dev_pointers_on_torch_stream(oracle):
     check(yd.cpu().numpy(), oracle.gemv(12, rows, cols, w, x, threads=8))
 
 
+@pytest.mark.parametrize("cols", [4096, 12288])
+@pytest.mark.parametrize("offset", [0, 2, 8, 16])
+def test_gemv_q6k_base_offsets(oracle, cols, offset):
+    """Q6_K rows of whole 4096-column windows from weight buffers starting 0,
+    2, 8 and 16 bytes into an allocation: 16-byte boundaries read each window
+    whole through LDS, the others the unit loads (2: every other block two
+    bytes below a dword boundary); both readings of the scales."""
+    import torch
+    rows = 300
+    say("gemv_dev Q6_K offset", rows, cols, offset)
+    w = S.matrix(14, 57 + offset, rows, cols)
+    x = S.normal_f32(58, cols)
+    buf = torch.zeros(w.nbytes + 64, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + w.nbytes] = torch.from_numpy(w).cuda()
+    xd = torch.from_numpy(x).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    for signed in (False, True):
+        yd = torch.empty(rows, dtype=torch.float32, device="cuda")
+        flags = H.FLAG_Q6K_SIGNED_SCALES if signed else 0
+        H.gemv_dev(14, buf.data_ptr() + offset, rows, cols, xd.data_ptr(), yd.data_ptr(), 1, s, flags)
+        torch.cuda.synchronize()
+        mode = oracle.SCALE_I8 if signed else oracle.SCALE_U8
+        check(yd.cpu().numpy(), oracle.gemv(14, rows, cols, w, x, scale_mode=mode), f"signed {signed}")
+
+
 def plain_matrix(quant, seed, rows, cols):
     """F32 / F16 / BF16 rows of N(0, 1) values, as packed bytes."""
     v = S.normal_f32(seed, rows * cols)
