@@ -300,8 +300,9 @@ __global__ void __launch_bounds__(512) gemv1_kernel(const uint8_t* __restrict__ 
 // as row q of w (gate) and row q of w2 (up) and stores y[q] = silu(g) * u,
 // the same f32 expression kLimbSiluX stages, so the down launch stages one
 // vector instead of two.
-// kLimbFine stages x in the 23-bit limbs (limb.hpp), as the modes that take
-// a silu(g) * u input (kLimbSiluX, kLimbResid, the shared expert's down) do.
+// kLimbFine stages x in the 23-bit limbs (limb.hpp), as the modes of the
+// silu(g) * u chain (kLimbTwoMat, kLimbPairSilu, kLimbSiluX, kLimbResid, the
+// shared expert's down) do.
 constexpr int kLimbTwoMat = 1, kLimbSiluX = 2, kLimbResid = 4, kLimbPairSilu = 8, kLimbFine = 16;
 
 // silu(g) * u in f32, g / (1 + exp(-g)) * u without contraction
@@ -322,7 +323,9 @@ __global__ void __launch_bounds__(512) gemv_limb_kernel(const uint8_t* __restric
                                                         const float* xres) {  // xres may be y (in place)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
   constexpr bool kLow = F::kQuant == kQ8_0 || F::kQuant == kIQ4_XS;  // signed codes: the low-limb sums
-  constexpr bool kFine = (MODE & (kLimbSiluX | kLimbResid | kLimbFine)) != 0;
+  // 23-bit limbs for every step of the silu(g) * u chain: the gate / up
+  // inputs whose sums form it and the inputs formed from it
+  constexpr bool kFine = (MODE & (kLimbTwoMat | kLimbPairSilu | kLimbSiluX | kLimbResid | kLimbFine)) != 0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (tid >> 6));
   const int units = cols >> 6;

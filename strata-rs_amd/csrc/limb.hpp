@@ -17,9 +17,10 @@ namespace sh {
 // each element within 2^-23 of its block's maximum; with FINE a in
 // [-128, 127] (a value that rounds up to 2^23 is held at 2^23 - 1), within
 // 2^-24, at two more instructions per element. Near the block maximum either
-// is as close to x as the f32 activations themselves; FINE serves inputs that
-// went through a chain of products (silu(g) * u), whose rounding the next
-// matvec passes on. Weight codes are
+// is as close to x as the f32 activations themselves; FINE serves the steps
+// of a chain of products (the gate / up sums that form silu(g) * u and the
+// matvec that takes it), whose rounding the next matvec passes on. Weight
+// codes are
 // small non-negative integers, so the per-block dot products are exact
 // integer sums on v_dot4_i32_i8 (a) and v_dot4_u32_u8 (b, c), four weights
 // per instruction:
