@@ -78,7 +78,7 @@ def elem_rel_err(got, want, floor=1e-3):
 # scale scores O(1).
 NORM_TOL = 1e-3
 STRICT_TOL = 2e-3
-METRICS = []  # (test, label, normwise, strict) of every check_parity call
+METRICS = []  # (test, label, normwise, strict, strict asserted) of every check_parity call
 
 
 def check_parity(got, want, label="", norm_tol=NORM_TOL, strict_tol=STRICT_TOL):
@@ -86,7 +86,7 @@ def check_parity(got, want, label="", norm_tol=NORM_TOL, strict_tol=STRICT_TOL):
     n = rel_err(got, want)
     st = elem_rel_err(got, want)
     test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
-    METRICS.append((test, label, n, st))
+    METRICS.append((test, label, n, st, strict_tol is not None))
     assert n <= norm_tol, f"{label}: normwise error {n:.3e} > {norm_tol:g}"
     if strict_tol is not None:  # None: recorded only (operands rounded on purpose, e.g. bf16)
         assert st <= strict_tol, f"{label}: per-element error {st:.3e} > {strict_tol:g}"
@@ -98,15 +98,21 @@ def pytest_terminal_summary(terminalreporter):
     if not METRICS:
         return
     worst = {}
-    for test, _label, n, st in METRICS:
+    for test, _label, n, st, asserted in METRICS:
         f = test.split("::")[0]
-        a, b, c = worst.get(f, (0.0, 0.0, 0))
-        worst[f] = (max(a, n), max(b, st), c + 1)
+        a, b, r, c = worst.get(f, (0.0, 0.0, None, 0))
+        if asserted:
+            b = max(b, st)
+        else:  # operands rounded on purpose (bf16, Q8): the per-element figure is recorded, not held to the bar
+            r = max(r or 0.0, st)
+        worst[f] = (max(a, n), b, r, c + 1)
     terminalreporter.write_sep("-", "parity metrics (worst per file: normwise, per-element with 1e-3 rms floor)")
-    for f, (n, st, c) in sorted(worst.items()):
-        terminalreporter.write_line(f"{f}: {c} checks, normwise {n:.2e}, per-element {st:.2e}")
+    for f, (n, st, r, c) in sorted(worst.items()):
+        extra = "" if r is None else f"; per-element of the checks against unrounded f32 (not asserted) {r:.2e}"
+        terminalreporter.write_line(f"{f}: {c} checks, normwise {n:.2e}, per-element {st:.2e}{extra}")
     out = os.environ.get("STRATA_PARITY_JSON")
     if out:
         import json
         with open(out, "w") as fh:
-            json.dump([{"test": t, "label": l, "normwise": n, "per_element": st} for t, l, n, st in METRICS], fh)
+            json.dump([{"test": t, "label": l, "normwise": n, "per_element": st, "per_element_asserted": a}
+                       for t, l, n, st, a in METRICS], fh)
