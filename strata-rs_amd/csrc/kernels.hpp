@@ -137,9 +137,11 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
 hipError_t launch_moe_route(const MoePlan& p, const float* logits, void* workspace, hipStream_t s);
 // out[t] = sum over t's experts in ascending id with w != 0 of w * (the
 // sum of the pair's nch_b down chunk sums at o_part_b), plus the shared
-// expert's gated output when `shared` is given.
+// expert's gated output when `shared` is given. `pairs_in_order`: token t's
+// a-th expert is pair t * top_k + a (one token routed inside gate/up), so
+// the pair table is not read.
 hipError_t launch_moe_combine(const MoePlan& p, const uint8_t* ws, float* out, const MoeShared* shared,
-                              hipStream_t s);
+                              hipStream_t s, bool pairs_in_order = false);
 // The one-token in-major path (moe_one.hip): fills p's one-token fields
 // and sets p.one when the shape allows it; the launches (gate/up, down,
 // then launch_moe_combine over its sums).

@@ -519,15 +519,17 @@ __device__ __forceinline__ void combine_cols(const MoePlan& plan, const float* _
 // after the routed sum.
 __global__ void __launch_bounds__(256) moe_combine_kernel(MoePlan plan, const uint8_t* ws,
                                                           float* __restrict__ out, const float* __restrict__ sh_d,
-                                                          const float* __restrict__ sh_s) {
+                                                          const float* __restrict__ sh_s, int pairs_in_order) {
   __shared__ float dsum[kMoeMaxTopK][32];
   __shared__ float wsh[kMoeMaxTopK];
   __shared__ int qsh[kMoeMaxTopK];
   const int blocks_per_tok = plan.n_embd / 32;
   const int t = blockIdx.x / blocks_per_tok, col0 = (blockIdx.x - t * blocks_per_tok) * 32;
-  // the token's pairs, once for the workgroup (each expert lane reads its own)
+  // the token's pairs, once for the workgroup (each expert lane reads its
+  // own); in order, the table is not read: one memory round trip fewer
   const int* tp = reinterpret_cast<const int*>(ws + plan.o_tokpair) + t * plan.top_k;
-  if (int(threadIdx.x) < plan.top_k) qsh[threadIdx.x] = tp[threadIdx.x];
+  if (int(threadIdx.x) < plan.top_k)
+    qsh[threadIdx.x] = pairs_in_order ? t * plan.top_k + int(threadIdx.x) : tp[threadIdx.x];
   __syncthreads();
   combine_cols(plan, reinterpret_cast<const float*>(ws + plan.o_part_b), qsh,
                reinterpret_cast<const float*>(ws + plan.o_wts) + t * plan.top_k, t, col0, out, dsum, wsh, sh_d,
@@ -705,17 +707,17 @@ hipError_t launch_moe(const MoePlan& p, uint32_t qg, uint32_t qu, uint32_t qd, c
         else launch_down<HxIQ4XS<false>>(p, down, ws, q6d, s);
     }
   }
-  return launch_moe_combine(p, ws, out, shared, s);
+  return launch_moe_combine(p, ws, out, shared, s, fused_route);
 }
 
 hipError_t launch_moe_combine(const MoePlan& p, const uint8_t* ws, float* out, const MoeShared* shared,
-                              hipStream_t s) {
+                              hipStream_t s, bool pairs_in_order) {
   if (shared && shared->join) {
     const hipError_t e = hipStreamWaitEvent(s, shared->join, 0);
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned(p.n_tok * (p.n_embd / 32))), dim3(256), 0, s, p,
-                     ws, out, shared ? shared->d : nullptr, shared ? shared->s : nullptr);
+                     ws, out, shared ? shared->d : nullptr, shared ? shared->s : nullptr, int(pairs_in_order));
   return hipGetLastError();
 }
 

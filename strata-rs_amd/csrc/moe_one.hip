@@ -384,7 +384,7 @@ hipError_t launch_moe_one(const MoePlan& p, uint32_t qg, uint32_t qd, const void
   MoePlan pc = p;
   pc.o_part_b = p.o_p1b;
   pc.nch_b = p.b1_nrc;
-  return launch_moe_combine(pc, ws, out, shared, s);
+  return launch_moe_combine(pc, ws, out, shared, s, fused_route);
 }
 
 }  // namespace sh
